@@ -1,0 +1,251 @@
+"""Benchmark: OAL grouped quadratic attention fwd+bwd on one MI355X.
+
+Workload: B=4, Hq=14, Hkv=2, N=4096, d=64, bf16, causal,
+8 uneven groups, fwd+bwd through the grouped autograd Function in
+oal_amd.hd_block_gemm_autograd, upstream dO ~ N(0,1) bf16, gradients for q, k, v
+and the coefficients (c0, lam, Gam). Inputs are synthetic and already resident
+in HBM when the timed region starts.
+
+One JSON line on stdout:
+  value      = B*N / (seconds per fwd+bwd step)  [tokens/s]
+  roofline   = dominant kernel's credited state-contraction FLOPs per launch
+               / its average launch time (HIP events on its launch stream,
+               recorded by the library during a second pass of the same K steps)
+               against the MI355X dense bf16 MFMA peak
+  cpu_baseline = the CPU oracle (oracle/grouped_oracle.py chunked fwd+bwd) on a
+               bounded sample of the same workload, on this host's cores
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+import torch  # noqa: E402
+
+F_LOGICAL = 2145  # 1 + 64 + 2080 features
+DA = 65  # value columns + the denominator column
+BF16_PEAK_TFLOPS = 2516.6  # MI355X dense bf16 MFMA (256 CU x 2.4 GHz x 4096 FLOP/clk)
+METRIC = "OAL attn fwd+bwd tokens/s at N=4096 d=64 bf16; % bf16 MFMA peak"
+
+
+def credited_flops(kernel: str, b: int, hq: int, hkv: int, n: int) -> float:
+    """Chunk-independent dense state-contraction FLOPs one launch performs.
+
+    fwd:  T_c update 2*F*DA per kv token; readout 2*F*DA per query token
+    bwd:  dCarry and dphi_Q 2*F*DA each per query token; dphi_K and dU
+          2*F*DA each per kv token.   Sum = 6*F*DA*B*N*(Hq+Hkv).
+    """
+    unit = 2.0 * F_LOGICAL * DA
+    q_tok = b * hq * n
+    kv_tok = b * hkv * n
+    return {
+        "k_state_fwd": unit * kv_tok,
+        "k_out_fwd": unit * q_tok,
+        "k_state_bwd": unit * q_tok,
+        "k_q_bwd": unit * q_tok,
+        "k_kv_bwd": 2 * unit * kv_tok,
+    }.get(kernel, 0.0)
+
+
+def make_inputs(b: int, n: int, device: torch.device, seed: int = 0):
+    from oal_amd.hd_block_gemm_autograd import pad_labels
+
+    gen = torch.Generator().manual_seed(seed)
+    hq, hkv, d = 14, 2, 64
+    q = torch.randn((b, hq, n, d), generator=gen)
+    k = torch.randn((b, hkv, n, d), generator=gen)
+    v = torch.randn((b, hkv, n, d), generator=gen)
+    for t, heads in ((q, hq), (k, hkv), (v, hkv)):
+        for h in range(heads):
+            dims = torch.randperm(d, generator=gen)[:2]
+            t[:, h, :, dims] *= 8.0
+    sizes = (2, 4, 6, 8, 10, 10, 12, 12)
+    perm = torch.randperm(d, generator=gen)
+    labels = torch.empty(d, dtype=torch.int32)
+    start = 0
+    for gid, size in enumerate(sizes):
+        labels[perm[start:start + size]] = gid
+        start += size
+    g = len(sizes)
+    lam = 0.5 + torch.rand((hq, g), generator=gen)
+    upper = torch.triu(0.5 * torch.rand((hq, g, g), generator=gen))
+    gam = 0.5 * (upper + upper.transpose(-1, -2))
+    c0 = torch.ones(hq)
+    dout = torch.randn((b, hq, n, d), generator=gen)
+    to = dict(device=device)
+    return dict(
+        q=q.to(torch.bfloat16).to(**to).requires_grad_(),
+        k=k.to(torch.bfloat16).to(**to).requires_grad_(),
+        v=v.to(torch.bfloat16).to(**to).requires_grad_(),
+        c0=c0.to(**to).requires_grad_(),
+        lam=lam.to(**to).requires_grad_(),
+        gam=gam.to(**to).requires_grad_(),
+        labels=pad_labels(labels, hq).to(device),
+        dout=dout.to(torch.bfloat16).to(**to),
+        scale=d ** -0.5,
+    )
+
+
+def step(inp) -> None:
+    from oal_amd.hd_block_gemm_autograd import _GroupedOALFunction
+
+    for name in ("q", "k", "v", "c0", "lam", "gam"):
+        inp[name].grad = None
+    out, _, _ = _GroupedOALFunction.apply(
+        inp["q"], inp["k"], inp["v"], inp["c0"], inp["lam"], inp["gam"], inp["labels"], inp["scale"], 0.0
+    )
+    out.backward(inp["dout"])
+
+
+def cpu_baseline(seconds: float = 12.0) -> dict:
+    """Time the oracle's chunked fwd+bwd (fp32, all host threads) on a bounded sample."""
+    from oracle import grouped_oracle as go
+
+    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    threads = min(threads, 16)
+    torch.set_num_threads(threads)
+    b, n = 1, 1024
+    inp = go.config_inputs(2, batch=b, seq_len=n)
+    wq = go.feature_coefficients(inp["groups"], inp["c0"], inp["lam"], inp["gam"], scale=inp["scale"], head_dim=64)
+    dout = torch.randn((b, 14, n, 64), generator=torch.Generator().manual_seed(1))
+    reps = 0
+    t0 = time.perf_counter()
+    while True:
+        _, num, den = go.chunked_forward(inp["q"], inp["k"], inp["v"], wq, chunk=64)
+        go.chunked_backward(inp["q"], inp["k"], inp["v"], wq, num, den, dout, chunk=64)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or reps >= 1000:
+            break
+    cpu_model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    cpu_model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {
+        "value": b * n * reps / el,
+        "unit": "tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (
+            f"oracle chunked fwd+bwd (fp32, torch CPU) at the config-2 head shape with B={b}, N={n}, "
+            f"{reps} reps in {el:.1f}s on {cpu_model}; tokens/s is linear in N for this algorithm"
+        ),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--batch", type=int, default=4)
+    ap.add_argument("--seq-len", type=int, default=4096)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(
+            f"bench.py measures one GPU: the operator shards over independent (batch, kv-head) units "
+            f"with no exchange, so --gpus {args.gpus} is not run here (see DESIGN.md)",
+            file=sys.stderr,
+        )
+        return 2
+
+    from oal_amd import _native
+
+    dev = torch.device("cuda:0")
+    b, n = args.batch, args.seq_len
+    inp = make_inputs(b, n, dev)
+    for _ in range(args.warmup):
+        step(inp)
+    torch.cuda.synchronize()
+
+    # timed region for `value`
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step(inp)
+    torch.cuda.synchronize()
+    sec = (time.perf_counter() - t0) / args.steps
+
+    # the same K steps again with per-kernel HIP events on the launch stream
+    _native.profile_collect()
+    _native.profile_enable(True)
+    torch.cuda.synchronize()
+    for _ in range(args.steps):
+        step(inp)
+    torch.cuda.synchronize()
+    _native.profile_enable(False)
+    kernels = _native.profile_collect()
+
+    per_kernel = {}
+    for name, (count, total_ms) in kernels.items():
+        avg_ms = total_ms / max(count, 1)
+        fl = credited_flops(name, b, 14, 2, n)
+        per_kernel[name] = {
+            "launches": count,
+            "avg_ms": round(avg_ms, 4),
+            "tflops": round(fl / (avg_ms * 1e-3) / 1e12, 3) if fl else None,
+        }
+    dominant = max(kernels, key=lambda k_: kernels[k_][1])
+    dom_avg_s = kernels[dominant][1] / kernels[dominant][0] * 1e-3
+    dom_flops = credited_flops(dominant, b, 14, 2, n)
+    achieved = dom_flops / dom_avg_s / 1e12
+    total_credited = 6.0 * F_LOGICAL * DA * b * n * (14 + 2)
+
+    result = {
+        "metric": METRIC,
+        "value": round(b * n / sec, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(sec * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (BASELINE config 2 distributions: N(0,1) with 2 outlier dims x8 per head, "
+                "8 uneven groups, c0=1, a~U(0.5,1.5), b~U(0,0.5))",
+        "config": {
+            "workload": "OAL causal attention fwd+bwd, BASELINE config 2",
+            "batch": b,
+            "q_heads": 14,
+            "kv_heads": 2,
+            "seq_len": n,
+            "head_dim": 64,
+            "groups": 8,
+        },
+        "roofline": {
+            "bound": "mfma",
+            "kernel": dominant,
+            "achieved": round(achieved, 3),
+            "peak": BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / BF16_PEAK_TFLOPS, 5),
+            "traffic": None,
+            "step_credited_tflops": round(total_credited / sec / 1e12, 3),
+            "step_frac": round(total_credited / sec / 1e12 / BF16_PEAK_TFLOPS, 5),
+        },
+        "kernels": per_kernel,
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

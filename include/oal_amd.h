@@ -1,0 +1,109 @@
+/*
+ * oal_amd.h -- C ABI of the MI355X (gfx950) OAL grouped quadratic attention library.
+ *
+ * One shared library, liboal_amd.so, built with hipcc for gfx950. Every entry point
+ * takes plain device pointers and sizes; no framework types cross this boundary.
+ * Callers own every buffer (inputs, outputs, the forward's saved state and the
+ * backward's workspace; sizes come from the *_bytes queries). Work is enqueued on
+ * the caller's HIP stream and nothing is synchronized. The library allocates no
+ * device memory.
+ *
+ * Operator (reference oal_attention/grouped_reference.py:102-211):
+ *   s_g(i,j)   = scale * sum_{d: labels[h][d] == g} q[i][d] * k[j][d]
+ *   kappa(i,j) = c0[h] + sum_g lam[h][g] s_g + sum_{g,g'} gam[h][g][g'] s_g s_g'
+ *   num[i] = sum_{j<=i} kappa(i,j) v[j],  den[i] = sum_{j<=i} kappa(i,j)
+ *   out[i] = num[i] / max(den[i], floor)        (floor <= 0: plain num / den)
+ * gam must be symmetric. The head dimension and value dimension are 64 (callers
+ * with smaller dimensions pad q, k, v with zeros). Query head h reads KV head
+ * h / (q_heads / kv_heads).
+ *
+ * Layouts (row-major, contiguous):
+ *   q [B][Hq][N][64], k and v [B][Hkv][N][64]    dtype OAL_DTYPE_F32 or OAL_DTYPE_BF16
+ *   out [B][Hq][N][64] (dtype);  num [B][Hq][N][64] f32;  den [B][Hq][N] f32
+ *   labels [Hq][64] int32 in [0, groups);  c0 [Hq];  lam [Hq][groups];
+ *   gam [Hq][groups][groups]  (all f32);  1 <= groups <= 64
+ *
+ * Return value: 0 on success, nonzero on invalid arguments or a launch error;
+ * oal_last_error() then describes the failure (thread-local string).
+ */
+#ifndef OAL_AMD_H_
+#define OAL_AMD_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define OAL_DTYPE_F32 0
+#define OAL_DTYPE_BF16 1
+
+/* ABI revision of this header. */
+int oal_abi_version(void);
+
+/* Message for the last nonzero return on the calling thread. */
+const char* oal_last_error(void);
+
+/* Opt-in per-kernel timing. While enabled, every kernel launch is bracketed by
+ * HIP events recorded on the launch stream. oal_profile_collect() waits for the
+ * recorded events, writes one line "kernel_name launches total_ms" per kernel
+ * into buf (NUL-terminated, truncated to buflen) and clears the records. This
+ * replaces the reference's CUDA-event stage timing
+ * (oal_attention/hd_block_gemm_profiling.py:195-226). */
+int oal_profile_enable(int enable);
+int oal_profile_collect(char* buf, size_t buflen);
+
+/* Logical feature count 1 + 64 + 64*65/2 = 2145 (reference
+ * hd_block_gemm_cache.py:105-121 pair layout) and the padded stride used in
+ * the saved state. */
+int oal_feature_count(void);
+int oal_feature_stride(void);
+
+/* Token block (chunk) the kernels use; results do not depend on it. */
+int oal_chunk_size(void);
+
+/* Bytes of the forward's saved state (per-chunk exclusive prefix states and
+ * feature coefficients), needed by oal_backward. */
+size_t oal_forward_saved_bytes(int batch, int q_heads, int kv_heads, int seq_len, int dtype);
+
+/* Bytes of scratch oal_backward needs. */
+size_t oal_backward_workspace_bytes(int batch, int q_heads, int kv_heads, int seq_len, int dtype);
+
+/*
+ * Causal chunked forward. Replaces the forward of the reference's HD Block-GEMM
+ * core, oal_attention/hd_block_gemm_runtime.py:617-805 (_hd_parallel_block_gemm_impl,
+ * called through hd_block_gemm_autograd.py:85-204), and of the legacy Triton
+ * route oal_attention/triton/grouped_quadratic_causal_forward_kernels.py:1155-1386.
+ * Writes out, num, den and the saved state.
+ */
+int oal_forward(const void* q, const void* k, const void* v,
+                const int32_t* labels, const float* c0, const float* lam, const float* gam,
+                int groups, int batch, int q_heads, int kv_heads, int seq_len, int dtype,
+                float scale, float floor,
+                void* out, float* num, float* den, void* saved, void* stream);
+
+/*
+ * First-order VJP. Replaces oal_attention/hd_block_gemm_autograd.py:207-347
+ * (_hd_parallel_block_gemm_autograd_backward_impl) and the legacy
+ * grouped_causal_first_order_vjp (triton/grouped_quadratic_causal_backward.py:1807-1869).
+ * dout (dtype), dnum [B][Hq][N][64] f32 and dden [B][Hq][N] f32 may each be NULL
+ * (no upstream gradient). dq, dk, dv (dtype) and the coefficient gradients
+ * dc0 [Hq], dlam [Hq][groups], dgam [Hq][groups][groups] (f32, overwritten) may be
+ * NULL when not requested. dgam[h][g(r)][g(c)] accumulates pair (r, c) with r >= c
+ * only, the reference's gather routing (grouped_reference.py:89-93).
+ */
+int oal_backward(const void* q, const void* k, const void* v,
+                 const int32_t* labels, const float* c0, const float* lam, const float* gam,
+                 int groups, int batch, int q_heads, int kv_heads, int seq_len, int dtype,
+                 float scale, float floor,
+                 const float* num, const float* den, const void* saved,
+                 const void* dout, const float* dnum, const float* dden,
+                 void* dq, void* dk, void* dv, float* dc0, float* dlam, float* dgam,
+                 void* workspace, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* OAL_AMD_H_ */

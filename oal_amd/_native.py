@@ -1,0 +1,200 @@
+"""ctypes binding of liboal_amd.so (the C ABI declared in include/oal_amd.h).
+
+PyTorch supplies device memory and the current HIP stream; every byte of the
+operator's arithmetic runs in the HIP kernels behind this library. There is no
+fallback: if the library is missing or the tensors are not on a ROCm device,
+the call raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+_LIB_NAME = "liboal_amd.so"
+_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), _LIB_NAME)
+_LOCK = threading.Lock()
+_LIB = None
+
+DTYPE_F32 = 0
+DTYPE_BF16 = 1
+HEAD_DIM = 64
+
+_vp = ctypes.c_void_p
+_i = ctypes.c_int
+_f = ctypes.c_float
+_sz = ctypes.c_size_t
+
+_SIGNATURES = {
+    "oal_abi_version": ([], _i),
+    "oal_last_error": ([], ctypes.c_char_p),
+    "oal_profile_enable": ([_i], _i),
+    "oal_profile_collect": ([ctypes.c_char_p, _sz], _i),
+    "oal_feature_count": ([], _i),
+    "oal_feature_stride": ([], _i),
+    "oal_chunk_size": ([], _i),
+    "oal_forward_saved_bytes": ([_i, _i, _i, _i, _i], _sz),
+    "oal_backward_workspace_bytes": ([_i, _i, _i, _i, _i], _sz),
+    "oal_forward": (
+        [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _f, _f, _vp, _vp, _vp, _vp, _vp],
+        _i,
+    ),
+    "oal_backward": (
+        [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _f, _f, _vp, _vp, _vp, _vp, _vp, _vp,
+         _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
+        _i,
+    ),
+}
+
+EXPORTED_SYMBOLS = tuple(_SIGNATURES)
+
+
+def library_path() -> str:
+    return _LIB_PATH
+
+
+def load_library(path: str | None = None) -> ctypes.CDLL:
+    """Load liboal_amd.so once; raise if it has not been built."""
+    global _LIB
+    with _LOCK:
+        if _LIB is not None and path is None:
+            return _LIB
+        target = path or _LIB_PATH
+        if not os.path.exists(target):
+            raise RuntimeError(
+                f"{_LIB_NAME} is not built ({target}); run __graft_entry__.build() "
+                "(hipcc --offload-arch=gfx950) before using oal_amd"
+            )
+        lib = ctypes.CDLL(target)
+        for name, (args, res) in _SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.argtypes = args
+            fn.restype = res
+        if lib.oal_abi_version() != 1:
+            raise RuntimeError("liboal_amd.so ABI version mismatch")
+        if path is None:
+            _LIB = lib
+        return lib
+
+
+def _check(rc: int, lib: ctypes.CDLL, what: str) -> None:
+    if rc != 0:
+        msg = lib.oal_last_error().decode("utf-8", "replace")
+        raise RuntimeError(f"{what} failed: {msg}")
+
+
+def _ptr(t: torch.Tensor | None):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _dtype_code(dtype: torch.dtype) -> int:
+    if dtype == torch.float32:
+        return DTYPE_F32
+    if dtype == torch.bfloat16:
+        return DTYPE_BF16
+    raise TypeError("the HIP kernels take float32 or bfloat16 q, k, v")
+
+
+def _require_device(*tensors: torch.Tensor) -> None:
+    for t in tensors:
+        if t is None:
+            continue
+        if t.device.type != "cuda" or torch.version.hip is None:
+            raise RuntimeError("oal_amd runs only on a ROCm (HIP) device; got a tensor on " + str(t.device))
+
+
+def _stream(device: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def profile_enable(enable: bool) -> None:
+    load_library().oal_profile_enable(1 if enable else 0)
+
+
+def profile_collect() -> dict[str, tuple[int, float]]:
+    """{kernel: (launches, total_ms)} for launches since the last collect."""
+    lib = load_library()
+    buf = ctypes.create_string_buffer(1 << 16)
+    _check(lib.oal_profile_collect(buf, len(buf)), lib, "oal_profile_collect")
+    result = {}
+    for line in buf.value.decode().splitlines():
+        name, count, total = line.split()
+        result[name] = (int(count), float(total))
+    return result
+
+
+def chunk_size() -> int:
+    return load_library().oal_chunk_size()
+
+
+def forward(q, k, v, labels, c0, lam, gam, *, scale: float, floor: float):
+    """Run the HIP forward. q [B,Hq,N,64], k/v [B,Hkv,N,64] contiguous, same dtype.
+
+    Returns (out [dtype], num f32, den f32 [B,Hq,N,1], saved uint8).
+    """
+    lib = load_library()
+    _require_device(q, k, v, labels, c0, lam, gam)
+    b, hq, n, d = q.shape
+    hkv = k.shape[1]
+    assert d == HEAD_DIM and v.shape[-1] == HEAD_DIM
+    code = _dtype_code(q.dtype)
+    groups = lam.shape[1]
+    dev = q.device
+    with torch.cuda.device(dev):
+        nbytes = lib.oal_forward_saved_bytes(b, hq, hkv, n, code)
+        if nbytes == 0:
+            _check(1, lib, "oal_forward_saved_bytes")
+        out = torch.empty((b, hq, n, d), dtype=q.dtype, device=dev)
+        num = torch.empty((b, hq, n, d), dtype=torch.float32, device=dev)
+        den = torch.empty((b, hq, n, 1), dtype=torch.float32, device=dev)
+        saved = torch.empty((nbytes,), dtype=torch.uint8, device=dev)
+        rc = lib.oal_forward(
+            _ptr(q), _ptr(k), _ptr(v), _ptr(labels), _ptr(c0), _ptr(lam), _ptr(gam), groups,
+            b, hq, hkv, n, code, float(scale), float(floor),
+            _ptr(out), _ptr(num), _ptr(den), _ptr(saved), _stream(dev),
+        )
+        _check(rc, lib, "oal_forward")
+    return out, num, den, saved
+
+
+def backward(q, k, v, labels, c0, lam, gam, num, den, saved, dout, dnum, dden, *, scale: float, floor: float,
+             need_q: bool, need_k: bool, need_v: bool, need_coef: bool):
+    """Run the HIP VJP; returns (dq, dk, dv, dc0, dlam, dgam) with None where not requested."""
+    lib = load_library()
+    _require_device(q, k, v, num, den, saved, dout, dnum, dden)
+    b, hq, n, d = q.shape
+    hkv = k.shape[1]
+    code = _dtype_code(q.dtype)
+    groups = lam.shape[1]
+    dev = q.device
+    with torch.cuda.device(dev):
+        wbytes = lib.oal_backward_workspace_bytes(b, hq, hkv, n, code)
+        if wbytes == 0:
+            _check(1, lib, "oal_backward_workspace_bytes")
+        work = torch.empty((wbytes,), dtype=torch.uint8, device=dev)
+        dq = torch.empty_like(q) if need_q else None
+        dk = torch.empty_like(k) if need_k else None
+        dv = torch.empty_like(v) if need_v else None
+        if need_coef:
+            dc0 = torch.empty_like(c0)
+            dlam = torch.empty_like(lam)
+            dgam = torch.empty_like(gam)
+        else:
+            dc0 = dlam = dgam = None
+        if dout is not None:
+            dout = dout.to(q.dtype).contiguous()
+        if dnum is not None:
+            dnum = dnum.to(torch.float32).contiguous()
+        if dden is not None:
+            dden = dden.to(torch.float32).contiguous()
+        rc = lib.oal_backward(
+            _ptr(q), _ptr(k), _ptr(v), _ptr(labels), _ptr(c0), _ptr(lam), _ptr(gam), groups,
+            b, hq, hkv, n, code, float(scale), float(floor),
+            _ptr(num), _ptr(den), _ptr(saved), _ptr(dout), _ptr(dnum), _ptr(dden),
+            _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dc0), _ptr(dlam), _ptr(dgam), _ptr(work), _stream(dev),
+        )
+        _check(rc, lib, "oal_backward")
+    return dq, dk, dv, dc0, dlam, dgam

@@ -1,0 +1,56 @@
+"""Builds liboal_amd.so in-tree with hipcc for gfx950.
+
+Usage: ``python -m oal_amd.build`` (``__graft_entry__.build()`` calls it).
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(PKG)
+SOURCES = [os.path.join(PKG, "csrc", "oal_kernels.hip")]
+HEADERS = [os.path.join(PKG, "csrc", "oal_common.hpp"), os.path.join(ROOT, "include", "oal_amd.h")]
+OUTPUT = os.path.join(PKG, "liboal_amd.so")
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and os.path.exists(cand):
+            return cand
+    raise RuntimeError("hipcc not found (ROCm is required to build oal_amd)")
+
+
+def compile_flags() -> list[str]:
+    return [
+        "--offload-arch=gfx950",
+        "-O3",
+        "-std=c++17",
+        "-fPIC",
+        "-shared",
+        "-I" + os.path.join(ROOT, "include"),
+        "-I" + os.path.join(PKG, "csrc"),
+        # packed FP32 VALU instructions stay off (numerics)
+        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    ]
+
+
+def build(verbose: bool = False) -> str:
+    """Compile every HIP source into oal_amd/liboal_amd.so; returns its path."""
+    tmp = OUTPUT + ".tmp"
+    cmd = [hipcc(), *compile_flags(), *SOURCES, "-o", tmp]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        sys.stderr.write(proc.stdout + proc.stderr)
+        raise RuntimeError(f"hipcc failed with exit code {proc.returncode}")
+    os.replace(tmp, OUTPUT)
+    return OUTPUT
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

@@ -1,0 +1,221 @@
+"""Autograd boundary of the HIP operator.
+
+Two ``torch.autograd.Function`` classes share the same HIP forward/VJP:
+
+* :class:`_GroupedOALFunction` takes the grouped coefficients (c0, lam, Gam and
+  dimension labels) that ``oal_attention`` and the HD adapters derive from the
+  packed factor. Its gradients are (dq, dk, dv, dc0, dlam, dGam), with dGam
+  routed exactly like the reference gather (pair (r, c), r >= c, to
+  Gam[g(r), g(c)]; ``grouped_reference.py:89-93``).
+* :class:`_HDParallelBlockGemmFunction` keeps the reference contract of
+  ``oal_attention/hd_block_gemm_autograd.py:85-204``:
+  forward(q, k, v, a, b, c, scale, eps, layout, plan) -> (out, num, den) with
+  logical per-dimension b [Hq, D] and per-pair c [Hq, D(D+1)/2]; backward
+  returns 6 gradients + 4 ``None``, no double backward, gradients cast to the
+  input dtypes (:333-347). It runs the same kernels with one group per
+  dimension (labels = d, lam = b, Gam = symmetric fill of c).
+
+Both pad D and DV up to 64 with zeros (padding contributes nothing) and slice
+the results back.
+"""
+
+from __future__ import annotations
+
+from typing import Any
+
+import torch
+
+from . import _native
+
+HEAD_DIM = _native.HEAD_DIM
+
+
+def _pad_last(x: torch.Tensor, size: int = HEAD_DIM) -> torch.Tensor:
+    if x.shape[-1] == size:
+        return x.contiguous()
+    if x.shape[-1] > size:
+        raise ValueError(f"the HIP kernels support head and value dimensions up to {size}")
+    return torch.nn.functional.pad(x, (0, size - x.shape[-1])).contiguous()
+
+
+def _kernel_dtype(dtype: torch.dtype) -> torch.dtype:
+    if dtype in (torch.float32, torch.bfloat16):
+        return dtype
+    if dtype == torch.float16:
+        return torch.float32
+    raise TypeError("HIP execution supports float16, bfloat16 and float32 q, k, v")
+
+
+def pad_labels(labels: torch.Tensor, query_heads: int) -> torch.Tensor:
+    """[D] or [Hq, D] integer labels -> contiguous int32 [Hq, 64] (pad dims -> group 0)."""
+    lab = labels if labels.ndim == 2 else labels.unsqueeze(0).expand(query_heads, -1)
+    lab = lab.to(torch.int32)
+    if lab.shape[-1] < HEAD_DIM:
+        lab = torch.nn.functional.pad(lab, (0, HEAD_DIM - lab.shape[-1]))
+    return lab.contiguous()
+
+
+class _GroupedOALFunction(torch.autograd.Function):
+    """(q, k, v, c0, lam, gam, labels, scale, floor) -> (out, num, den).
+
+    q, k, v must already be [B, H, N, 64] contiguous float32 or bfloat16 on one
+    ROCm device; c0 [Hq], lam [Hq, G], gam [Hq, G, G] float32, gam symmetric.
+    """
+
+    @staticmethod
+    def forward(ctx: Any, q, k, v, c0, lam, gam, labels, scale: float, floor: float):
+        ctx.set_materialize_grads(False)
+        c0c, lamc, gamc = (t.detach().to(torch.float32).contiguous() for t in (c0, lam, gam))
+        out, num, den, saved = _native.forward(q, k, v, labels, c0c, lamc, gamc, scale=scale, floor=floor)
+        ctx.save_for_backward(q, k, v, c0c, lamc, gamc, labels, num, den, saved)
+        ctx.scale = float(scale)
+        ctx.floor = float(floor)
+        ctx.coef_dtypes = (c0.dtype, lam.dtype, gam.dtype)
+        return out, num, den
+
+    @staticmethod
+    def backward(ctx: Any, dout, dnum, dden):
+        if torch.is_grad_enabled():
+            raise RuntimeError("the OAL HIP operator does not support double backward")
+        q, k, v, c0, lam, gam, labels, num, den, saved = ctx.saved_tensors
+        needs = ctx.needs_input_grad
+        if dout is None and dnum is None and dden is None:
+            return (None,) * 9
+        dq, dk, dv, dc0, dlam, dgam = _native.backward(
+            q, k, v, labels, c0, lam, gam, num, den, saved, dout, dnum, dden,
+            scale=ctx.scale, floor=ctx.floor,
+            need_q=needs[0], need_k=needs[1], need_v=needs[2], need_coef=any(needs[3:6]),
+        )
+        cd = ctx.coef_dtypes
+        return (
+            dq,
+            dk,
+            dv,
+            dc0.to(cd[0]) if needs[3] else None,
+            dlam.to(cd[1]) if needs[4] else None,
+            dgam.to(cd[2]) if needs[5] else None,
+            None,
+            None,
+            None,
+        )
+
+
+def grouped_oal(q, k, v, labels, c0, lam, gam, *, scale: float, floor: float):
+    """Differentiable grouped operator on [B, H, N, D<=64] tensors of any float dtype.
+
+    Returns (out, num, den) with out in q's dtype, num [B, Hq, N, DV] and
+    den [B, Hq, N, 1] in float32.
+    """
+    dv_orig = v.shape[-1]
+    kd = _kernel_dtype(q.dtype)
+    qp, kp, vp = (_pad_last(t.to(kd)) for t in (q, k, v))
+    lab = pad_labels(labels, q.shape[1])
+    out, num, den = _GroupedOALFunction.apply(qp, kp, vp, c0, lam, gam, lab, float(scale), float(floor))
+    if dv_orig != HEAD_DIM:
+        out = out[..., :dv_orig]
+        num = num[..., :dv_orig]
+    return out.to(q.dtype), num, den
+
+
+def _pair_rows_cols(d: int, device) -> tuple[torch.Tensor, torch.Tensor]:
+    rows, cols = torch.tril_indices(d, d, device=device)
+    return rows, cols
+
+
+def logical_to_grouped(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, head_dim: int):
+    """Logical (a [Hq], b [Hq, D], c [Hq, D(D+1)/2]) -> one group per dimension.
+
+    labels = d, lam = b, Gam[r][c] = Gam[c][r] = c_p(r, c) (D padded to 64).
+    """
+    hq = a.shape[0]
+    dev = a.device
+    rows, cols = _pair_rows_cols(head_dim, dev)
+    gam = torch.zeros((hq, HEAD_DIM, HEAD_DIM), dtype=torch.float32, device=dev)
+    cf = c.to(torch.float32)
+    gam[:, rows, cols] = cf
+    gam[:, cols, rows] = cf
+    lam = torch.zeros((hq, HEAD_DIM), dtype=torch.float32, device=dev)
+    lam[:, :head_dim] = b.to(torch.float32)
+    labels = torch.arange(HEAD_DIM, dtype=torch.int32, device=dev).unsqueeze(0).expand(hq, -1).contiguous()
+    return a.to(torch.float32).contiguous(), lam.contiguous(), gam.contiguous(), labels
+
+
+class _HDParallelBlockGemmFunction(torch.autograd.Function):
+    """Reference-contract Function over logical coefficients (see module doc)."""
+
+    @staticmethod
+    def forward(ctx: Any, q, k, v, a, b, c, scale: float, eps: float, layout, plan):
+        gradient_mask = tuple(bool(x) for x in ctx.needs_input_grad[:6])
+        if (
+            plan is not None
+            and torch.is_grad_enabled()
+            and tuple(plan.requested_gradient_mask) != gradient_mask
+        ):
+            raise ValueError("plan gradient mask must exactly match the six tensor inputs")
+        ctx.set_materialize_grads(False)
+        d, dv = q.shape[-1], v.shape[-1]
+        kd = _kernel_dtype(q.dtype)
+        qp, kp, vp = (_pad_last(t.detach().to(kd)) for t in (q, k, v))
+        c0g, lam, gam, labels = logical_to_grouped(a.detach(), b.detach(), c.detach(), d)
+        out, num, den, saved = _native.forward(qp, kp, vp, labels, c0g, lam, gam, scale=scale, floor=eps)
+        if plan is not None and getattr(plan, "require_positive_denominator", True):
+            _require_positive_denominator(den)
+        ctx.save_for_backward(qp, kp, vp, c0g, lam, gam, labels, num, den, saved)
+        ctx.meta = (float(scale), float(eps), d, dv, gradient_mask)
+        ctx.input_dtypes = tuple(t.dtype for t in (q, k, v, a, b, c))
+        out = out[..., :dv].to(q.dtype)
+        return out, num[..., :dv], den
+
+    @staticmethod
+    def backward(ctx: Any, dout, dnum, dden):
+        if torch.is_grad_enabled():
+            raise RuntimeError("HD Block-GEMM does not support double backward")
+        qp, kp, vp, c0g, lam, gam, labels, num, den, saved = ctx.saved_tensors
+        scale, eps, d, dv, mask = ctx.meta
+        if dout is None and dnum is None and dden is None:
+            return (None,) * 10
+        if dout is not None:
+            dout = _pad_last(dout)
+        if dnum is not None:
+            dnum = _pad_last(dnum.to(torch.float32))
+        need_q, need_k, need_v, need_a, need_b, need_c = mask
+        dq, dk, dvv, dc0, dlam, dgam = _native.backward(
+            qp, kp, vp, labels, c0g, lam, gam, num, den, saved, dout, dnum, dden,
+            scale=scale, floor=eps, need_q=need_q, need_k=need_k, need_v=need_v,
+            need_coef=need_a or need_b or need_c,
+        )
+        rows, cols = _pair_rows_cols(d, qp.device)
+        grads = [
+            dq[..., :d] if need_q else None,
+            dk[..., :d] if need_k else None,
+            dvv[..., :dv] if need_v else None,
+            dc0 if need_a else None,
+            dlam[:, :d] if need_b else None,
+            dgam[:, rows, cols] if need_c else None,
+        ]
+        out = [g.to(dt) if g is not None else None for g, dt in zip(grads, ctx.input_dtypes)]
+        return (*out, None, None, None, None)
+
+
+def _require_positive_denominator(den: torch.Tensor) -> None:
+    """Raise unless every denominator is finite and positive (two host syncs).
+
+    Mirrors ``hd_block_gemm_runtime.py:392-408``.
+    """
+    lo, hi = torch.aminmax(den)
+    if not (bool(torch.isfinite(lo)) and bool(torch.isfinite(hi))):
+        raise RuntimeError("HD Block-GEMM denominator must be finite")
+    if float(lo) <= 0.0:
+        raise RuntimeError("HD Block-GEMM denominator must be strictly positive")
+
+
+def _hd_parallel_block_gemm_autograd(q, k, v, a, b, c, *, scale, eps, layout, plan):
+    return _HDParallelBlockGemmFunction.apply(q, k, v, a, b, c, scale, eps, layout, plan)
+
+
+def _hd_parallel_block_gemm(q, k, v, a, b, c, *, scale, eps, layout, plan):
+    with torch.no_grad():
+        return _HDParallelBlockGemmFunction.apply(q, k, v, a, b, c, scale, eps, layout, plan)
+
+
+__all__: tuple[str, ...] = ()
