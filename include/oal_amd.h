@@ -39,6 +39,14 @@ extern "C" {
 #define OAL_DTYPE_F32 0
 #define OAL_DTYPE_BF16 1
 
+/* Arithmetic precision (reference HD planner "precision", hd_block_gemm.py:132-153):
+ * OAL_PRECISION_FP32  fp32 arithmetic throughout (VALU kernels), any group count.
+ * OAL_PRECISION_BF16  bf16 operands, fp32 accumulation on the gfx950 matrix cores
+ *                     (MFMA) when groups <= 8; larger group counts use the fp32
+ *                     kernels. */
+#define OAL_PRECISION_FP32 0
+#define OAL_PRECISION_BF16 1
+
 /* ABI revision of this header. */
 int oal_abi_version(void);
 
@@ -65,10 +73,12 @@ int oal_chunk_size(void);
 
 /* Bytes of the forward's saved state (per-chunk exclusive prefix states and
  * feature coefficients), needed by oal_backward. */
-size_t oal_forward_saved_bytes(int batch, int q_heads, int kv_heads, int seq_len, int dtype);
+size_t oal_forward_saved_bytes(int batch, int q_heads, int kv_heads, int seq_len, int groups, int dtype,
+                               int precision);
 
 /* Bytes of scratch oal_backward needs. */
-size_t oal_backward_workspace_bytes(int batch, int q_heads, int kv_heads, int seq_len, int dtype);
+size_t oal_backward_workspace_bytes(int batch, int q_heads, int kv_heads, int seq_len, int groups, int dtype,
+                                    int precision);
 
 /*
  * Causal chunked forward. Replaces the forward of the reference's HD Block-GEMM
@@ -80,7 +90,7 @@ size_t oal_backward_workspace_bytes(int batch, int q_heads, int kv_heads, int se
 int oal_forward(const void* q, const void* k, const void* v,
                 const int32_t* labels, const float* c0, const float* lam, const float* gam,
                 int groups, int batch, int q_heads, int kv_heads, int seq_len, int dtype,
-                float scale, float floor,
+                int precision, float scale, float floor,
                 void* out, float* num, float* den, void* saved, void* stream);
 
 /*
@@ -96,11 +106,19 @@ int oal_forward(const void* q, const void* k, const void* v,
 int oal_backward(const void* q, const void* k, const void* v,
                  const int32_t* labels, const float* c0, const float* lam, const float* gam,
                  int groups, int batch, int q_heads, int kv_heads, int seq_len, int dtype,
-                 float scale, float floor,
+                 int precision, float scale, float floor,
                  const float* num, const float* den, const void* saved,
                  const void* dout, const float* dnum, const float* dden,
                  void* dq, void* dk, void* dv, float* dc0, float* dlam, float* dgam,
                  void* workspace, void* stream);
+
+/*
+ * Matrix-core self-test: one wave checks the MFMA accumulator layouts the bf16
+ * kernels assume and adds the number of mismatching elements to
+ * *device_errors (a device int the caller zeroed). No counterpart in the
+ * reference; it lets a deployment verify the device before trusting results.
+ */
+int oal_selftest(int* device_errors, void* stream);
 
 #ifdef __cplusplus
 }

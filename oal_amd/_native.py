@@ -21,6 +21,8 @@ _LIB = None
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
+PRECISION_FP32 = 0
+PRECISION_BF16 = 1
 HEAD_DIM = 64
 
 _vp = ctypes.c_void_p
@@ -36,17 +38,18 @@ _SIGNATURES = {
     "oal_feature_count": ([], _i),
     "oal_feature_stride": ([], _i),
     "oal_chunk_size": ([], _i),
-    "oal_forward_saved_bytes": ([_i, _i, _i, _i, _i], _sz),
-    "oal_backward_workspace_bytes": ([_i, _i, _i, _i, _i], _sz),
+    "oal_forward_saved_bytes": ([_i, _i, _i, _i, _i, _i, _i], _sz),
+    "oal_backward_workspace_bytes": ([_i, _i, _i, _i, _i, _i, _i], _sz),
     "oal_forward": (
-        [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _f, _f, _vp, _vp, _vp, _vp, _vp],
+        [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _f, _f, _vp, _vp, _vp, _vp, _vp],
         _i,
     ),
     "oal_backward": (
-        [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _f, _f, _vp, _vp, _vp, _vp, _vp, _vp,
+        [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _f, _f, _vp, _vp, _vp, _vp, _vp, _vp,
          _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
         _i,
     ),
+    "oal_selftest": ([_vp, _vp], _i),
 }
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)
@@ -73,7 +76,7 @@ def load_library(path: str | None = None) -> ctypes.CDLL:
             fn = getattr(lib, name)
             fn.argtypes = args
             fn.restype = res
-        if lib.oal_abi_version() != 1:
+        if lib.oal_abi_version() != 2:
             raise RuntimeError("liboal_amd.so ABI version mismatch")
         if path is None:
             _LIB = lib
@@ -130,7 +133,24 @@ def chunk_size() -> int:
     return load_library().oal_chunk_size()
 
 
-def forward(q, k, v, labels, c0, lam, gam, *, scale: float, floor: float):
+def _precision_code(precision: str) -> int:
+    if precision == "fp32":
+        return PRECISION_FP32
+    if precision == "bf16":
+        return PRECISION_BF16
+    raise ValueError("precision must be 'fp32' or 'bf16'")
+
+
+def selftest() -> int:
+    """Run the matrix-core layout self-test on the current device; returns mismatches."""
+    lib = load_library()
+    dev = torch.device("cuda", torch.cuda.current_device())
+    errors = torch.zeros(1, dtype=torch.int32, device=dev)
+    _check(lib.oal_selftest(_ptr(errors), _stream(dev)), lib, "oal_selftest")
+    return int(errors.item())
+
+
+def forward(q, k, v, labels, c0, lam, gam, *, scale: float, floor: float, precision: str = "fp32"):
     """Run the HIP forward. q [B,Hq,N,64], k/v [B,Hkv,N,64] contiguous, same dtype.
 
     Returns (out [dtype], num f32, den f32 [B,Hq,N,1], saved uint8).
@@ -144,7 +164,8 @@ def forward(q, k, v, labels, c0, lam, gam, *, scale: float, floor: float):
     groups = lam.shape[1]
     dev = q.device
     with torch.cuda.device(dev):
-        nbytes = lib.oal_forward_saved_bytes(b, hq, hkv, n, code)
+        pcode = _precision_code(precision)
+        nbytes = lib.oal_forward_saved_bytes(b, hq, hkv, n, groups, code, pcode)
         if nbytes == 0:
             _check(1, lib, "oal_forward_saved_bytes")
         out = torch.empty((b, hq, n, d), dtype=q.dtype, device=dev)
@@ -153,7 +174,7 @@ def forward(q, k, v, labels, c0, lam, gam, *, scale: float, floor: float):
         saved = torch.empty((nbytes,), dtype=torch.uint8, device=dev)
         rc = lib.oal_forward(
             _ptr(q), _ptr(k), _ptr(v), _ptr(labels), _ptr(c0), _ptr(lam), _ptr(gam), groups,
-            b, hq, hkv, n, code, float(scale), float(floor),
+            b, hq, hkv, n, code, pcode, float(scale), float(floor),
             _ptr(out), _ptr(num), _ptr(den), _ptr(saved), _stream(dev),
         )
         _check(rc, lib, "oal_forward")
@@ -161,7 +182,7 @@ def forward(q, k, v, labels, c0, lam, gam, *, scale: float, floor: float):
 
 
 def backward(q, k, v, labels, c0, lam, gam, num, den, saved, dout, dnum, dden, *, scale: float, floor: float,
-             need_q: bool, need_k: bool, need_v: bool, need_coef: bool):
+             need_q: bool, need_k: bool, need_v: bool, need_coef: bool, precision: str = "fp32"):
     """Run the HIP VJP; returns (dq, dk, dv, dc0, dlam, dgam) with None where not requested."""
     lib = load_library()
     _require_device(q, k, v, num, den, saved, dout, dnum, dden)
@@ -171,7 +192,8 @@ def backward(q, k, v, labels, c0, lam, gam, num, den, saved, dout, dnum, dden, *
     groups = lam.shape[1]
     dev = q.device
     with torch.cuda.device(dev):
-        wbytes = lib.oal_backward_workspace_bytes(b, hq, hkv, n, code)
+        pcode = _precision_code(precision)
+        wbytes = lib.oal_backward_workspace_bytes(b, hq, hkv, n, groups, code, pcode)
         if wbytes == 0:
             _check(1, lib, "oal_backward_workspace_bytes")
         work = torch.empty((wbytes,), dtype=torch.uint8, device=dev)
@@ -192,7 +214,7 @@ def backward(q, k, v, labels, c0, lam, gam, num, den, saved, dout, dnum, dden, *
             dden = dden.to(torch.float32).contiguous()
         rc = lib.oal_backward(
             _ptr(q), _ptr(k), _ptr(v), _ptr(labels), _ptr(c0), _ptr(lam), _ptr(gam), groups,
-            b, hq, hkv, n, code, float(scale), float(floor),
+            b, hq, hkv, n, code, pcode, float(scale), float(floor),
             _ptr(num), _ptr(den), _ptr(saved), _ptr(dout), _ptr(dnum), _ptr(dden),
             _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dc0), _ptr(dlam), _ptr(dgam), _ptr(work), _stream(dev),
         )

@@ -28,6 +28,7 @@
 
 #include "oal_amd.h"
 #include "oal_common.hpp"
+#include "oal_internal.hpp"
 
 namespace oal {
 
@@ -698,6 +699,14 @@ void timed(const char* name, hipStream_t st, F&& launch) {
   if (a && b) g_prof_records.push_back({name, a, b});
 }
 
+bool use_mfma(int precision, int groups) { return precision == OAL_PRECISION_BF16 && groups <= 8; }
+
+oal::LaunchGeom launch_geom(const Geometry& g) { return oal::LaunchGeom{g.B, g.Hq, g.Hkv, g.N, g.NB, g.U, g.R}; }
+
+oal::Timer make_timer() {
+  return [](const char* name, hipStream_t st, const std::function<void()>& launch) { timed(name, st, launch); };
+}
+
 template <typename T, int GMAX>
 int forward_impl(const Geometry& g, const void* q, const void* k, const void* v, const int32_t* labels,
                  const float* c0, const float* lam, const float* gam, int groups, float scale, float floor,
@@ -757,7 +766,7 @@ int backward_impl(const Geometry& g, const void* q, const void* k, const void* v
 
 extern "C" {
 
-int oal_abi_version(void) { return 1; }
+int oal_abi_version(void) { return 2; }
 
 int oal_profile_enable(int enable) {
   std::lock_guard<std::mutex> lock(g_prof_mu);
@@ -811,28 +820,48 @@ int oal_feature_stride(void) { return oal::kFP; }
 
 int oal_chunk_size(void) { return oal::kC; }
 
-size_t oal_forward_saved_bytes(int batch, int q_heads, int kv_heads, int seq_len, int dtype) {
+static int check_common(int groups, int precision) {
+  if (groups < 1 || groups > 64) return fail("groups must be in [1, 64]");
+  if (precision != OAL_PRECISION_FP32 && precision != OAL_PRECISION_BF16)
+    return fail("precision must be OAL_PRECISION_FP32 or OAL_PRECISION_BF16");
+  return 0;
+}
+
+size_t oal_forward_saved_bytes(int batch, int q_heads, int kv_heads, int seq_len, int groups, int dtype,
+                               int precision) {
   Geometry g;
-  if (check_geometry(batch, q_heads, kv_heads, seq_len, dtype, &g)) return 0;
+  if (check_geometry(batch, q_heads, kv_heads, seq_len, dtype, &g) || check_common(groups, precision)) return 0;
+  if (use_mfma(precision, groups)) return oal::mfma_saved_bytes(g.Hq, g.U, g.NB);
   return saved_bytes(g);
 }
 
-size_t oal_backward_workspace_bytes(int batch, int q_heads, int kv_heads, int seq_len, int dtype) {
+size_t oal_backward_workspace_bytes(int batch, int q_heads, int kv_heads, int seq_len, int groups, int dtype,
+                                    int precision) {
   Geometry g;
-  if (check_geometry(batch, q_heads, kv_heads, seq_len, dtype, &g)) return 0;
+  if (check_geometry(batch, q_heads, kv_heads, seq_len, dtype, &g) || check_common(groups, precision)) return 0;
   return work_view(g, nullptr).bytes;
 }
 
 int oal_forward(const void* q, const void* k, const void* v, const int32_t* labels, const float* c0,
                 const float* lam, const float* gam, int groups, int batch, int q_heads, int kv_heads, int seq_len,
-                int dtype, float scale, float floor, void* out, float* num, float* den, void* saved,
+                int dtype, int precision, float scale, float floor, void* out, float* num, float* den, void* saved,
                 void* stream) {
   Geometry g;
   if (check_geometry(batch, q_heads, kv_heads, seq_len, dtype, &g)) return 1;
   if (!q || !k || !v || !labels || !c0 || !lam || !gam || !out || !num || !den || !saved)
     return fail("oal_forward: null pointer argument");
-  if (groups < 1 || groups > 64) return fail("groups must be in [1, 64]");
+  if (check_common(groups, precision)) return 1;
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (use_mfma(precision, groups)) {
+    const oal::LaunchGeom lg = launch_geom(g);
+    if (dtype == OAL_DTYPE_F32)
+      oal::launch_mfma_forward<float>(lg, q, k, v, labels, c0, lam, gam, groups, scale, floor, out, num, den, saved,
+                                      st, make_timer());
+    else
+      oal::launch_mfma_forward<uint16_t>(lg, q, k, v, labels, c0, lam, gam, groups, scale, floor, out, num, den,
+                                         saved, st, make_timer());
+    return launch_status("oal_forward launch");
+  }
   if (dtype == OAL_DTYPE_F32) {
     if (groups <= 8)
       return forward_impl<float, 8>(g, q, k, v, labels, c0, lam, gam, groups, scale, floor, out, num, den, saved, st);
@@ -845,14 +874,15 @@ int oal_forward(const void* q, const void* k, const void* v, const int32_t* labe
 
 int oal_backward(const void* q, const void* k, const void* v, const int32_t* labels, const float* c0,
                  const float* lam, const float* gam, int groups, int batch, int q_heads, int kv_heads, int seq_len,
-                 int dtype, float scale, float floor, const float* num, const float* den, const void* saved,
-                 const void* dout, const float* dnum, const float* dden, void* dq, void* dk, void* dv, float* dc0,
-                 float* dlam, float* dgam, void* workspace, void* stream) {
+                 int dtype, int precision, float scale, float floor, const float* num, const float* den,
+                 const void* saved, const void* dout, const float* dnum, const float* dden, void* dq, void* dk,
+                 void* dv, float* dc0, float* dlam, float* dgam, void* workspace, void* stream) {
   Geometry g;
   if (check_geometry(batch, q_heads, kv_heads, seq_len, dtype, &g)) return 1;
   if (!q || !k || !v || !labels || !c0 || !lam || !gam || !num || !den || !saved || !workspace)
     return fail("oal_backward: null pointer argument");
-  if (groups < 1 || groups > 64) return fail("groups must be in [1, 64]");
+  if (check_common(groups, precision)) return 1;
+  if (use_mfma(precision, groups)) return fail("oal_backward: the bf16 matrix-core backward is not available yet");
   hipStream_t st = static_cast<hipStream_t>(stream);
 #define OAL_BWD_ARGS                                                                                       \
   g, q, k, v, labels, c0, lam, gam, groups, scale, floor, num, den, saved, dout, dnum, dden, dq, dk, dv, dc0, \
@@ -864,6 +894,13 @@ int oal_backward(const void* q, const void* k, const void* v, const int32_t* lab
   if (groups <= 8) return backward_impl<uint16_t, 8>(OAL_BWD_ARGS);
   return backward_impl<uint16_t, 64>(OAL_BWD_ARGS);
 #undef OAL_BWD_ARGS
+}
+
+int oal_selftest(int* device_errors, void* stream) {
+  if (!device_errors) return fail("oal_selftest: null pointer argument");
+  if (oal::run_mfma_selftest(device_errors, static_cast<hipStream_t>(stream)))
+    return fail("oal_selftest: launch failed");
+  return 0;
 }
 
 }  // extern "C"

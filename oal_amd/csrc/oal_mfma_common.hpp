@@ -1,0 +1,186 @@
+// MFMA fragment types and the rotated feature-slot order used by the bf16
+// (matrix-core) kernels on gfx950.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <utility>
+
+#include "oal_common.hpp"
+
+namespace oal {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// v_mfma_f32_32x32x16_bf16: lane l supplies A[l%32][8*(l/32) + j] and
+// B[8*(l/32) + j][l%32] (j < 8); accumulator register i of lane l holds
+// C[8*(i/4) + 4*(l/32) + i%4][l%32].
+__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+// v_mfma_f32_16x16x32_bf16: lane l supplies A[l%16][8*(l/16) + j],
+// B[8*(l/16) + j][l%16]; register i holds C[4*(l/16) + i][l%16].
+__device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ constexpr int c32_row(int i, int lane) { return 8 * (i / 4) + 4 * (lane / 32) + (i % 4); }
+__device__ __forceinline__ constexpr int c16_row(int i, int lane) { return 4 * (lane / 16) + i; }
+
+// ---------------------------------------------------------------------------
+// Rotated slot order.
+// The 32x32x16 MFMA splits K into two lane groups (s = lane/32) of 8 slots.
+// Lane group s keeps its token's row rotated by 32*s: xrot[m] = x[(m + 32 s) % 64]
+// (xrot[64] = 1, xrot[65] = 0). A base (rb, cb) evaluated on xrot is the
+// feature x[(rb+32s)%64] * x[(cb+32s)%64]: one static register pair serves
+// both lane groups. Slot sigma = 16 t + 8 s + j belongs to k-step t, lane
+// group s and base 8 t + j. Bases: 32 linear (d, one), 1 constant (one, one),
+// 1056 pair orbits under the +32 rotation, then padding (zero, zero).
+// Slots whose rotated pair repeats the s = 0 pair (pairs {r, r+32}) and the
+// constant's s = 1 slot are invalid: their state rows are zero.
+// ---------------------------------------------------------------------------
+constexpr int kS = 2208;         // slots (138 k-steps of 16, 69 tiles of 32)
+constexpr int kBases = kS / 2;   // 1104
+constexpr int kKS = kS / 16;     // 138
+
+struct SlotTable {
+  uint8_t rb[kBases];
+  uint8_t cb[kBases];
+  uint8_t ar[kS];   // actual row index (64 = one, 65 = zero)
+  uint8_t ac[kS];   // actual column index
+  int16_t nat[kS];  // natural feature index (grouped_reference pair order), -1 if invalid
+};
+
+constexpr int pair_index(int r, int c) { return r * (r + 1) / 2 + c; }
+
+constexpr SlotTable make_slot_table() {
+  SlotTable t{};
+  bool assigned[kD * (kD + 1) / 2] = {};
+  int b = 0;
+  for (int d = 0; d < kD / 2; ++d) {
+    t.rb[b] = static_cast<uint8_t>(d);
+    t.cb[b] = 64;
+    ++b;
+  }
+  t.rb[b] = 64;
+  t.cb[b] = 64;
+  ++b;
+  for (int r = 0; r < kD; ++r) {
+    for (int c = 0; c <= r; ++c) {
+      if (assigned[pair_index(r, c)]) continue;
+      t.rb[b] = static_cast<uint8_t>(r);
+      t.cb[b] = static_cast<uint8_t>(c);
+      ++b;
+      assigned[pair_index(r, c)] = true;
+      const int r2 = (r + 32) % 64, c2 = (c + 32) % 64;
+      const int hi = r2 > c2 ? r2 : c2, lo = r2 > c2 ? c2 : r2;
+      assigned[pair_index(hi, lo)] = true;
+    }
+  }
+  for (; b < kBases; ++b) {
+    t.rb[b] = 65;
+    t.cb[b] = 65;
+  }
+  for (int sg = 0; sg < kS; ++sg) {
+    const int tt = sg / 16, s = (sg % 16) / 8, j = sg % 8, base = 8 * tt + j;
+    const int rb = t.rb[base], cb = t.cb[base];
+    int nat = -1, ar = 65, ac = 65;
+    if (rb == 64) {
+      if (s == 0) {
+        nat = 0;
+        ar = 64;
+        ac = 64;
+      }
+    } else if (rb < 64 && cb == 64) {
+      const int d = (rb + 32 * s) % 64;
+      nat = 1 + d;
+      ar = d;
+      ac = 64;
+    } else if (rb < 64) {
+      const int r = (rb + 32 * s) % 64, c = (cb + 32 * s) % 64;
+      const int hi = r > c ? r : c, lo = r > c ? c : r;
+      const bool dup = s == 1 && hi == (rb > cb ? rb : cb) && lo == (rb > cb ? cb : rb);
+      if (!dup) {
+        nat = 1 + kD + pair_index(hi, lo);
+        ar = hi;
+        ac = lo;
+      }
+    }
+    t.nat[sg] = static_cast<int16_t>(nat);
+    t.ar[sg] = static_cast<uint8_t>(ar);
+    t.ac[sg] = static_cast<uint8_t>(ac);
+  }
+  return t;
+}
+
+constexpr SlotTable kSlotHost = make_slot_table();
+
+constexpr bool slot_table_is_a_permutation() {
+  bool seen[kFeat] = {};
+  int valid = 0;
+  for (int s = 0; s < kS; ++s) {
+    const int n = kSlotHost.nat[s];
+    if (n < 0) continue;
+    if (n >= kFeat || seen[n]) return false;
+    seen[n] = true;
+    ++valid;
+  }
+  return valid == kFeat;
+}
+static_assert(slot_table_is_a_permutation(), "every feature must occupy exactly one valid slot");
+
+// Value of base B on a rotated row (static register indices).
+template <int B>
+__device__ __forceinline__ float base_value(const float (&x)[kD]) {
+  constexpr int rb = kSlotHost.rb[B], cb = kSlotHost.cb[B];
+  if constexpr (rb == 65) {
+    return 0.f;
+  } else if constexpr (rb == 64) {
+    return 1.f;
+  } else if constexpr (cb == 64) {
+    return x[rb];
+  } else {
+    return x[rb] * x[cb];
+  }
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  bf16x2 v = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+__device__ __forceinline__ bf16x8 pack8(const float (&v)[8]) {
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  u32x4 u = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7])};
+  return __builtin_bit_cast(bf16x8, u);
+}
+
+// A fragment of k-step T: features of bases 8T..8T+7 on the rotated row,
+// scaled by the lane group's slot coefficients w[0..7].
+template <int T, int... J>
+__device__ __forceinline__ bf16x8 feature_fragment_impl(const float (&x)[kD], const float (&w)[8],
+                                                        std::integer_sequence<int, J...>) {
+  float v[8] = {(base_value<8 * T + J>(x) * w[J])...};
+  return pack8(v);
+}
+template <int T>
+__device__ __forceinline__ bf16x8 feature_fragment(const float (&x)[kD], const float (&w)[8]) {
+  return feature_fragment_impl<T>(x, w, std::make_integer_sequence<int, 8>{});
+}
+template <int T, int... J>
+__device__ __forceinline__ bf16x8 raw_fragment_impl(const float (&x)[kD], std::integer_sequence<int, J...>) {
+  float v[8] = {base_value<8 * T + J>(x)...};
+  return pack8(v);
+}
+template <int T>
+__device__ __forceinline__ bf16x8 raw_fragment(const float (&x)[kD]) {
+  return raw_fragment_impl<T>(x, std::make_integer_sequence<int, 8>{});
+}
+
+__device__ __forceinline__ float bf16_to_f(uint16_t x) { return __uint_as_float(uint32_t(x) << 16); }
+
+}  // namespace oal

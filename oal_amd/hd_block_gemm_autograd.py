@@ -63,13 +63,16 @@ class _GroupedOALFunction(torch.autograd.Function):
     """
 
     @staticmethod
-    def forward(ctx: Any, q, k, v, c0, lam, gam, labels, scale: float, floor: float):
+    def forward(ctx: Any, q, k, v, c0, lam, gam, labels, scale: float, floor: float, precision: str = "fp32"):
         ctx.set_materialize_grads(False)
         c0c, lamc, gamc = (t.detach().to(torch.float32).contiguous() for t in (c0, lam, gam))
-        out, num, den, saved = _native.forward(q, k, v, labels, c0c, lamc, gamc, scale=scale, floor=floor)
+        out, num, den, saved = _native.forward(
+            q, k, v, labels, c0c, lamc, gamc, scale=scale, floor=floor, precision=precision
+        )
         ctx.save_for_backward(q, k, v, c0c, lamc, gamc, labels, num, den, saved)
         ctx.scale = float(scale)
         ctx.floor = float(floor)
+        ctx.precision = precision
         ctx.coef_dtypes = (c0.dtype, lam.dtype, gam.dtype)
         return out, num, den
 
@@ -80,10 +83,10 @@ class _GroupedOALFunction(torch.autograd.Function):
         q, k, v, c0, lam, gam, labels, num, den, saved = ctx.saved_tensors
         needs = ctx.needs_input_grad
         if dout is None and dnum is None and dden is None:
-            return (None,) * 9
+            return (None,) * 10
         dq, dk, dv, dc0, dlam, dgam = _native.backward(
             q, k, v, labels, c0, lam, gam, num, den, saved, dout, dnum, dden,
-            scale=ctx.scale, floor=ctx.floor,
+            scale=ctx.scale, floor=ctx.floor, precision=ctx.precision,
             need_q=needs[0], need_k=needs[1], need_v=needs[2], need_coef=any(needs[3:6]),
         )
         cd = ctx.coef_dtypes
@@ -97,20 +100,25 @@ class _GroupedOALFunction(torch.autograd.Function):
             None,
             None,
             None,
+            None,
         )
 
 
-def grouped_oal(q, k, v, labels, c0, lam, gam, *, scale: float, floor: float):
+def grouped_oal(q, k, v, labels, c0, lam, gam, *, scale: float, floor: float, precision: str = "fp32"):
     """Differentiable grouped operator on [B, H, N, D<=64] tensors of any float dtype.
 
-    Returns (out, num, den) with out in q's dtype, num [B, Hq, N, DV] and
-    den [B, Hq, N, 1] in float32.
+    ``precision`` "fp32" runs fp32 arithmetic throughout; "bf16" runs bf16
+    operands with fp32 accumulation on the matrix cores (reference HD
+    ``bf16_tensorcore``). Returns (out, num, den) with out in q's dtype,
+    num [B, Hq, N, DV] and den [B, Hq, N, 1] in float32.
     """
     dv_orig = v.shape[-1]
     kd = _kernel_dtype(q.dtype)
     qp, kp, vp = (_pad_last(t.to(kd)) for t in (q, k, v))
     lab = pad_labels(labels, q.shape[1])
-    out, num, den = _GroupedOALFunction.apply(qp, kp, vp, c0, lam, gam, lab, float(scale), float(floor))
+    out, num, den = _GroupedOALFunction.apply(
+        qp, kp, vp, c0, lam, gam, lab, float(scale), float(floor), precision
+    )
     if dv_orig != HEAD_DIM:
         out = out[..., :dv_orig]
         num = num[..., :dv_orig]

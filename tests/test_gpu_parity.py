@@ -212,3 +212,29 @@ def test_bf16_config2_shape_backward_matches_fp32_oracle():
     for got, want in ((qb.grad, dq_r), (kb.grad, dk_r), (vb.grad, dv_r), (c0.grad, dc0_r), (lam.grad, dlam_r),
                       (gam.grad, dgam_r)):
         assert rel(got, want) <= BF16_TOL, rel(got, want)
+
+
+def test_matrix_core_layout_selftest():
+    from oal_amd import _native
+
+    _dev()
+    assert _native.selftest() == 0
+
+
+@pytest.mark.parametrize("n", [256, 200, 1024])
+def test_bf16_matrix_core_forward_matches_fp32_oracle(n):
+    from oal_amd.hd_block_gemm_autograd import grouped_oal
+
+    dev = _dev()
+    inp = _bf16_case(1, n, seed=4)
+    qb, kb, vb = (inp[nm].to(torch.bfloat16) for nm in ("q", "k", "v"))
+    args = [t.to(dev) for t in (qb, kb, vb)] + [inp[nm].to(dev) for nm in ("groups", "c0", "lam", "gam")]
+    out, num, den = grouped_oal(*args, scale=inp["scale"], floor=0.0, precision="bf16")
+    q32, k32, v32 = (t.float() for t in (qb, kb, vb))
+    wq = go.feature_coefficients(inp["groups"], inp["c0"], inp["lam"], inp["gam"], scale=inp["scale"], head_dim=64)
+    out_r, num_r, den_r = go.chunked_forward(q32, k32, v32, wq, chunk=64)
+    e_num, e_den = rel(num, num_r), rel(den, den_r)
+    ok = den_r.abs() > 1.0
+    e_out = rel(out.float().cpu()[ok.expand_as(out_r)], out_r[ok.expand_as(out_r)])
+    print(f"bf16 mfma forward N={n}: num {e_num:.2e} den {e_den:.2e} out {e_out:.2e}")
+    assert e_num <= BF16_TOL and e_den <= BF16_TOL and e_out <= BF16_TOL

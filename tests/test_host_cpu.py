@@ -41,14 +41,20 @@ def test_size_queries_and_argument_errors_without_a_gpu():
     if not os.path.exists(_native.library_path()):
         pytest.skip("liboal_amd.so not built")
     lib = _native.load_library()
-    assert lib.oal_forward_saved_bytes(1, 14, 2, 4096, 1) > 0
-    assert lib.oal_backward_workspace_bytes(4, 14, 2, 4096, 1) > 0
-    assert lib.oal_forward_saved_bytes(1, 14, 3, 4096, 1) == 0  # Hq % Hkv != 0
+    fp32 = lib.oal_forward_saved_bytes(1, 14, 2, 4096, 8, 1, 0)
+    mfma = lib.oal_forward_saved_bytes(1, 14, 2, 4096, 8, 1, 1)
+    assert fp32 > 0 and mfma > 0 and mfma != fp32
+    # more than 8 groups keeps the fp32 kernels (and their saved layout)
+    assert lib.oal_forward_saved_bytes(1, 14, 2, 4096, 64, 1, 1) == fp32
+    assert lib.oal_backward_workspace_bytes(4, 14, 2, 4096, 8, 1, 1) > 0
+    assert lib.oal_forward_saved_bytes(1, 14, 3, 4096, 8, 1, 0) == 0  # Hq % Hkv != 0
     assert b"divisible" in lib.oal_last_error()
-    rc = lib.oal_forward(None, None, None, None, None, None, None, 8, 1, 1, 1, 64, 0, 0.1, 0.0,
+    assert lib.oal_forward_saved_bytes(1, 14, 2, 4096, 8, 1, 5) == 0
+    assert b"precision" in lib.oal_last_error()
+    rc = lib.oal_forward(None, None, None, None, None, None, None, 8, 1, 1, 1, 64, 0, 0, 0.1, 0.0,
                          None, None, None, None, None)
     assert rc != 0 and b"null" in lib.oal_last_error()
-    rc = lib.oal_forward(None, None, None, None, None, None, None, 8, 1, 1, 1, 64, 7, 0.1, 0.0,
+    rc = lib.oal_forward(None, None, None, None, None, None, None, 8, 1, 1, 1, 64, 7, 0, 0.1, 0.0,
                          None, None, None, None, None)
     assert rc != 0 and b"dtype" in lib.oal_last_error()
 
