@@ -52,6 +52,12 @@ def credited_flops(kernel: str, b: int, hq: int, hkv: int, n: int) -> float:
         "k_state_bwd": unit * q_tok,
         "k_q_bwd": unit * q_tok,
         "k_kv_bwd": 2 * unit * kv_tok,
+        # matrix-core kernels
+        "k2_state_fwd": unit * kv_tok,
+        "k2_out_fwd": unit * q_tok,
+        "k2_state_bwd": unit * q_tok,
+        "k2_q_fold": unit * q_tok,
+        "k2_kv_fold": 2 * unit * kv_tok,
     }.get(kernel, 0.0)
 
 
@@ -100,7 +106,8 @@ def step(inp) -> None:
     for name in ("q", "k", "v", "c0", "lam", "gam"):
         inp[name].grad = None
     out, _, _ = _GroupedOALFunction.apply(
-        inp["q"], inp["k"], inp["v"], inp["c0"], inp["lam"], inp["gam"], inp["labels"], inp["scale"], 0.0
+        inp["q"], inp["k"], inp["v"], inp["c0"], inp["lam"], inp["gam"], inp["labels"], inp["scale"], 0.0,
+        inp.get("precision", "bf16"),
     )
     out.backward(inp["dout"])
 

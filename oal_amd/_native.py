@@ -182,7 +182,8 @@ def forward(q, k, v, labels, c0, lam, gam, *, scale: float, floor: float, precis
 
 
 def backward(q, k, v, labels, c0, lam, gam, num, den, saved, dout, dnum, dden, *, scale: float, floor: float,
-             need_q: bool, need_k: bool, need_v: bool, need_coef: bool, precision: str = "fp32"):
+             need_q: bool, need_k: bool, need_v: bool, need_coef: bool, precision: str = "fp32",
+             workspace: torch.Tensor | None = None):
     """Run the HIP VJP; returns (dq, dk, dv, dc0, dlam, dgam) with None where not requested."""
     lib = load_library()
     _require_device(q, k, v, num, den, saved, dout, dnum, dden)
@@ -196,7 +197,9 @@ def backward(q, k, v, labels, c0, lam, gam, num, den, saved, dout, dnum, dden, *
         wbytes = lib.oal_backward_workspace_bytes(b, hq, hkv, n, groups, code, pcode)
         if wbytes == 0:
             _check(1, lib, "oal_backward_workspace_bytes")
-        work = torch.empty((wbytes,), dtype=torch.uint8, device=dev)
+        work = workspace if workspace is not None else torch.empty((wbytes,), dtype=torch.uint8, device=dev)
+        if work.numel() < wbytes:
+            raise ValueError("workspace is smaller than oal_backward_workspace_bytes")
         dq = torch.empty_like(q) if need_q else None
         dk = torch.empty_like(k) if need_k else None
         dv = torch.empty_like(v) if need_v else None

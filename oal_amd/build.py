@@ -12,7 +12,8 @@ import sys
 
 PKG = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(PKG)
-SOURCES = [os.path.join(PKG, "csrc", "oal_kernels.hip"), os.path.join(PKG, "csrc", "oal_mfma_fwd.hip")]
+SOURCES = [os.path.join(PKG, "csrc", "oal_kernels.hip"), os.path.join(PKG, "csrc", "oal_mfma_fwd.hip"),
+           os.path.join(PKG, "csrc", "oal_mfma_bwd.hip")]
 HEADERS = [os.path.join(PKG, "csrc", "oal_common.hpp"), os.path.join(ROOT, "include", "oal_amd.h")]
 OUTPUT = os.path.join(PKG, "liboal_amd.so")
 
@@ -28,7 +29,7 @@ def compile_flags() -> list[str]:
     return [
         "--offload-arch=gfx950",
         "-O3",
-        "-std=c++17",
+        "-std=c++20",
         "-fPIC",
         "-shared",
         "-I" + os.path.join(ROOT, "include"),

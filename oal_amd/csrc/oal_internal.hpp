@@ -32,6 +32,28 @@ void launch_mfma_forward(const LaunchGeom& g, const void* q, const void* k, cons
                          const float* c0, const float* lam, const float* gam, int groups, float scale, float floor,
                          void* out, float* num, float* den, void* saved, hipStream_t st, const Timer& timed);
 
+struct MfmaWork {
+  uint16_t* G16;  // [B][Hq][N][64] bf16 normalization VJP
+  float* Gz;      // [B][Hq][N]
+  uint16_t* dTT;  // [U][NB][kKS][64][16] bf16
+  uint16_t* dTR;  // [U][NB][kS/32][4][32][16] bf16
+  float* dTz;     // [U][NB][kFP]
+  float* dwqs;    // [B][Hq][kS] slot-coefficient gradients (state part)
+  float* dqf;     // [B][Hq][N][64] local dq
+  float* dkp;     // [B][Hq][N][64] local dk per query head
+  float* dvp;     // [B][Hq][N][64] local dv per query head
+  float* coefl;   // [B][Hq][NB][73] local (dc0, dlam[8], dgam[8][8])
+  size_t bytes;
+};
+MfmaWork mfma_work_view(void* base, int B, int Hq, int U, int N, int NB);
+
+template <typename T>
+int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, const void* v, const int32_t* labels,
+                         const float* c0, const float* lam, const float* gam, int groups, float scale, float floor,
+                         const float* num, const float* den, const void* saved, const void* dout, const float* dnum,
+                         const float* dden, void* dq, void* dk, void* dv, float* dc0, float* dlam, float* dgam,
+                         void* workspace, hipStream_t st, const Timer& timed);
+
 int run_mfma_selftest(int* dev_errors, hipStream_t st);
 
 }  // namespace oal

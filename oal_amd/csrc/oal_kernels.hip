@@ -536,13 +536,17 @@ __global__ __launch_bounds__(256) void k_dwq_reduce(const float* __restrict__ pa
   dwq[(size_t)h * kFP + f] = acc;
 }
 
-// Adjoint of k_feature_coefficients: dc0, dlam[g], dgam[g][g'] (pair (r, c),
-// r >= c, routed to [g(r)][g(c)]), fixed summation order.
+// Adjoint of k_feature_coefficients: dc0, dlam[g], dgam[g][g'] in a fixed
+// summation order. Pair (r, c), r >= c, is first routed to [g(r)][g(c)] as the
+// reference gather does (grouped_reference.py:89-93); dgam is then reported in
+// the symmetric-Gam convention (off-diagonal entries carry the mean of the two
+// routings), the gradient of sum_{g,h} Gam_gh s_g s_h.
 __global__ __launch_bounds__(256) void k_coef_grad(const float* __restrict__ dwq,
                                                    const int32_t* __restrict__ labels, int G, float scale,
                                                    float* __restrict__ dc0, float* __restrict__ dlam,
                                                    float* __restrict__ dgam) {
   __shared__ int lab[kD];
+  __shared__ float raw[64 * 64];
   const int h = blockIdx.x, t = threadIdx.x;
   if (t < kD) {
     int g = labels[h * kD + t];
@@ -568,7 +572,12 @@ __global__ __launch_bounds__(256) void k_coef_grad(const float* __restrict__ dwq
         acc += (r == c ? 1.f : 2.f) * w[1 + kD + r * (r + 1) / 2 + c];
       }
     }
-    dgam[(size_t)h * G * G + e] = acc * s2;
+    raw[e] = acc * s2;
+  }
+  __syncthreads();
+  for (int e = t; e < G * G; e += blockDim.x) {
+    const int gr = e / G, gc = e % G;
+    dgam[(size_t)h * G * G + e] = gr == gc ? raw[e] : 0.5f * (raw[e] + raw[gc * G + gr]);
   }
 }
 
@@ -839,6 +848,7 @@ size_t oal_backward_workspace_bytes(int batch, int q_heads, int kv_heads, int se
                                     int precision) {
   Geometry g;
   if (check_geometry(batch, q_heads, kv_heads, seq_len, dtype, &g) || check_common(groups, precision)) return 0;
+  if (use_mfma(precision, groups)) return oal::mfma_work_view(nullptr, g.B, g.Hq, g.U, g.N, g.NB).bytes;
   return work_view(g, nullptr).bytes;
 }
 
@@ -882,8 +892,22 @@ int oal_backward(const void* q, const void* k, const void* v, const int32_t* lab
   if (!q || !k || !v || !labels || !c0 || !lam || !gam || !num || !den || !saved || !workspace)
     return fail("oal_backward: null pointer argument");
   if (check_common(groups, precision)) return 1;
-  if (use_mfma(precision, groups)) return fail("oal_backward: the bf16 matrix-core backward is not available yet");
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (use_mfma(precision, groups)) {
+    const oal::LaunchGeom lg = launch_geom(g);
+    int rc;
+    if (dtype == OAL_DTYPE_F32)
+      rc = oal::launch_mfma_backward<float>(lg, q, k, v, labels, c0, lam, gam, groups, scale, floor, num, den, saved,
+                                            dout, dnum, dden, dq, dk, dv, dc0, dlam, dgam, workspace, st,
+                                            make_timer());
+    else
+      rc = oal::launch_mfma_backward<uint16_t>(lg, q, k, v, labels, c0, lam, gam, groups, scale, floor, num, den,
+                                               saved, dout, dnum, dden, dq, dk, dv, dc0, dlam, dgam, workspace, st,
+                                               make_timer());
+    if (rc == 2) return fail("oal_backward: dk and dv must be requested together on the matrix-core path");
+    if (rc == 3) return fail("dc0, dlam and dgam must be given together");
+    return launch_status("oal_backward launch");
+  }
 #define OAL_BWD_ARGS                                                                                       \
   g, q, k, v, labels, c0, lam, gam, groups, scale, floor, num, den, saved, dout, dnum, dden, dq, dk, dv, dc0, \
       dlam, dgam, workspace, st

@@ -1,0 +1,1063 @@
+// bf16 matrix-core (MFMA) backward for gfx950.
+//
+// k2_gvec       normalization VJP: G (bf16, MFMA operand) and Gz (fp32).
+// k2_state_bwd  per (32-slot tile, unit) reverse chunk scan: dT_c = sum_{c'>c}
+//               dCarry_c' in MFMA accumulators (oriented value x slot), with
+//               dCarry_c = sum_h wq_h * (raw(Q_h)^T [G_h, Gz_h]); the per-slot
+//               feature-coefficient gradient sum_c <P_c, raw(Q)^T G> reduces
+//               inside the accumulator registers. Stores dT in the two k-blocked
+//               layouts of the forward state plus dTz (fp32, natural order).
+// k2_local_bwd  intra-chunk VJP in group-sum form, 4 waves per (head, chunk, unit):
+//               ds = G V^T + Gz, S_g = scale Q_g K^T, kappa; dq_i += scale sum_j
+//               ds_ij kappa'_{g(d)} k_jd written as F_h = (ds o S_h) K (no masks on
+//               the dims), likewise dk, dv = kappa^T G, the local coefficient
+//               gradients, and the denominator part of dq as a quadratic form.
+// k2_q_fold     dq state part: D^T = P G^T on the MFMA, folded through the query
+//               features (rotated rows, static register indices) + local dq.
+// k2_kv_fold    dk state part (D^T = dT V^T folded through the key features),
+//               dv = raw(K) dT, the dTz quadratic form, + local dk, dv.
+// k2_coef_grad  per head: slot gradients -> (dc0, dlam, dGam) + local parts.
+//
+// dGam follows the symmetric-Gam convention: off-diagonal entries carry the
+// mean of the (g, h) and (h, g) routings, so that dGam = d/dGam of
+// sum_{g,h} Gam_gh s_g s_h. (Gradients reaching a factor L with Gam = L L^T, or
+// a per-pair coefficient c, are the same under either routing.)
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "oal_internal.hpp"
+#include "oal_mfma_common.hpp"
+
+namespace oal {
+
+static __constant__ SlotTable kSlot = make_slot_table();
+
+namespace {
+
+constexpr int LD = kD + 8;  // padded bf16 row stride in LDS
+
+__device__ __forceinline__ void load_row_b(const uint16_t* __restrict__ src, size_t row_base, bool ok,
+                                           bf16x8 (&r)[8]) {
+  const bf16x8* p = reinterpret_cast<const bf16x8*>(src + row_base);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const bf16x8 x = p[i];
+    r[i] = ok ? x : bf16x8{};
+  }
+}
+__device__ __forceinline__ void load_row_b(const float* __restrict__ src, size_t row_base, bool ok,
+                                           bf16x8 (&r)[8]) {
+  const float4* p = reinterpret_cast<const float4*>(src + row_base);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float4 a = p[2 * i], b = p[2 * i + 1];
+    float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    const bf16x8 x = pack8(v);
+    r[i] = ok ? x : bf16x8{};
+  }
+}
+
+__device__ __forceinline__ void store_row(__bf16* dst, const bf16x8 (&r)[8]) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) *reinterpret_cast<bf16x8*>(dst + 8 * i) = r[i];
+}
+
+// Rotated fp32 row x[m] = row[(m + 32 s) % 64] from 8 bf16 fragments.
+__device__ __forceinline__ void rotated_row(const bf16x8 (&r)[8], int s, float (&x)[kD]) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[8 * i + j] = (float)r[i][j];
+  if (s == 1) {
+#pragma unroll
+    for (int m = 0; m < 32; ++m) {
+      const float t = x[m];
+      x[m] = x[m + 32];
+      x[m + 32] = t;
+    }
+  }
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// Normalization VJP (reference hd_block_gemm_normalization_ops.py:32-71).
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void k2_gvec(const T* __restrict__ dout, const float* __restrict__ dnum,
+                                               const float* __restrict__ dden, const float* __restrict__ num,
+                                               const float* __restrict__ den, long rows, float floor,
+                                               uint16_t* __restrict__ G16, float* __restrict__ Gz) {
+  const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const float dd = den[row];
+  const float dp = floor > 0.f ? fmaxf(dd, floor) : dd;
+  const float dO = dout ? to_f(dout[row * kD + lane]) : 0.f;
+  float g = dO / dp;
+  if (dnum) g += dnum[row * kD + lane];
+  G16[row * kD + lane] = from_f<uint16_t>(g);
+  const float dot = wave_sum(dO * num[row * kD + lane]);
+  if (lane == 0) {
+    float gz = -dot / (dp * dp);
+    if (floor > 0.f && !(dd >= floor)) gz = 0.f;
+    if (dden) gz += dden[row];
+    Gz[row] = gz;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Backward state scan. grid (kS/32, U), one wave. Accumulators hold
+// dT^T [96 values (64 = den) x 32 slots]; lane column = slot.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(64) void k2_state_bwd(const T* __restrict__ q, const uint16_t* __restrict__ G16,
+                                                   const float* __restrict__ Gz, const float* __restrict__ wqs,
+                                                   const uint16_t* __restrict__ PR, const float* __restrict__ PZ,
+                                                   int Hq, int Hkv, int N, int NB, uint16_t* __restrict__ dTT,
+                                                   uint16_t* __restrict__ dTR, float* __restrict__ dTz,
+                                                   float* __restrict__ dwqs) {
+  __shared__ float qT[kRow][kC + 4];                              // qT[d][tok]; 64 = valid, 65 = 0
+  __shared__ __attribute__((aligned(16))) __bf16 GT[96][kC + 8];  // GT[e][tok]; 64 = Gz
+  __shared__ __attribute__((aligned(16))) __bf16 Pl[32][LD];      // P_c rows of this tile
+  __shared__ float Pzl[32];
+  __shared__ float stage[97][33];
+
+  const int tile = blockIdx.x, u = blockIdx.y;
+  const int R = Hq / Hkv, b = u / Hkv, kh = u % Hkv;
+  const int l = threadIdx.x, s = l >> 5, row = l & 31;
+  const int slot = tile * 32 + row;
+  const int ar = kSlot.ar[slot], ac = kSlot.ac[slot], nat = kSlot.nat[slot];
+
+  for (int idx = l; idx < 31 * (kC + 8); idx += 64) GT[65 + idx / (kC + 8)][idx % (kC + 8)] = (__bf16)0.f;
+  float wh[8], dwp[8];
+#pragma unroll
+  for (int hh = 0; hh < 8; ++hh) {
+    wh[hh] = hh < R ? wqs[(size_t)(kh * R + hh) * kS + slot] : 0.f;
+    dwp[hh] = 0.f;
+  }
+
+  auto fetch = [&](int ch, int hh, bf16x8 (&qr)[8], bf16x8 (&gr)[8], float& gz) {
+    const int h = kh * R + hh, tok = ch * kC + l;
+    const bool ok = tok < N;
+    const size_t rb = ((size_t)(b * Hq + h) * N + (ok ? tok : N - 1)) * kD;
+    load_row_b(q, rb, ok, qr);
+    load_row_b(G16, rb, ok, gr);
+    gz = ok ? Gz[(size_t)(b * Hq + h) * N + (ok ? tok : N - 1)] : 0.f;
+  };
+  auto stage_head = [&](const bf16x8 (&qr)[8], const bf16x8 (&gr)[8], float gz, bool ok) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        qT[8 * i + j][l] = (float)qr[i][j];
+        GT[8 * i + j][l] = gr[i][j];
+      }
+    qT[64][l] = ok ? 1.f : 0.f;
+    qT[65][l] = 0.f;
+    GT[64][l] = (__bf16)gz;
+  };
+
+  f32x16 acc[3];
+#pragma unroll
+  for (int n = 0; n < 3; ++n) acc[n] = f32x16{};
+  const size_t chunk_elems = (size_t)kKS * 64 * 16;
+
+  bf16x8 qr[8], gr[8];
+  float gz;
+  fetch(NB - 1, 0, qr, gr, gz);
+  for (int ch = NB - 1; ch >= 0; --ch) {
+    // 1. dT_c = accumulated suffix (exclusive)
+#pragma unroll
+    for (int n = 0; n < 3; ++n)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) stage[32 * n + c32_row(i, l)][row] = acc[n][i];
+    __syncthreads();
+    {
+      uint16_t* tt = dTT + ((size_t)u * NB + ch) * chunk_elems;
+      uint16_t* tr = dTR + ((size_t)u * NB + ch) * chunk_elems;
+      const int t = 2 * tile + s;
+#pragma unroll
+      for (int eh = 0; eh < 2; ++eh) {
+        const int e = row + 32 * eh;
+        uint32_t w[8];
+#pragma unroll
+        for (int qq = 0; qq < 8; ++qq) w[qq] = pack_bf16x2(stage[e][16 * s + 2 * qq], stage[e][16 * s + 2 * qq + 1]);
+        uint4* dst = reinterpret_cast<uint4*>(tt + ((size_t)t * 64 + e) * 16);
+        dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
+        dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
+      }
+#pragma unroll
+      for (int kh2 = 0; kh2 < 2; ++kh2) {
+        const int kk = 2 * s + kh2;
+        uint32_t w[8];
+#pragma unroll
+        for (int qq = 0; qq < 8; ++qq)
+          w[qq] = pack_bf16x2(stage[16 * kk + 2 * qq][row], stage[16 * kk + 2 * qq + 1][row]);
+        uint4* dst = reinterpret_cast<uint4*>(tr + (((size_t)tile * 4 + kk) * 32 + row) * 16);
+        dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
+        dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
+      }
+      if (s == 0 && nat >= 0) dTz[((size_t)u * NB + ch) * kFP + nat] = stage[64][row];
+    }
+    // 2. P_c rows of this tile (for the coefficient gradient)
+    {
+      const uint16_t* pr = PR + ((size_t)u * NB + ch) * chunk_elems + (size_t)tile * 4 * 32 * 16;
+      // PR[tile][kk][32][16] -> Pl[slot][e]
+#pragma unroll
+      for (int it = 0; it < 4; ++it) {
+        const int idx = it * 64 + l;  // 256 chunks of 8 values
+        const int kk = idx >> 6, rr = (idx >> 1) & 31, hf = idx & 1;
+        *reinterpret_cast<bf16x8*>(&Pl[rr][16 * kk + 8 * hf]) =
+            *reinterpret_cast<const bf16x8*>(pr + ((size_t)kk * 32 + rr) * 16 + 8 * hf);
+      }
+      if (s == 0) Pzl[row] = nat >= 0 ? PZ[((size_t)u * NB + ch) * kFP + nat] : 0.f;
+    }
+    // 3. heads
+    for (int hh = 0; hh < R; ++hh) {
+      __syncthreads();
+      stage_head(qr, gr, gz, ch * kC + l < N);
+      __syncthreads();
+      // prefetch the next (chunk, head) rows
+      {
+        int nh = hh + 1, nc = ch;
+        if (nh == R) {
+          nh = 0;
+          nc = ch - 1;
+        }
+        if (nc >= 0) fetch(nc, nh, qr, gr, gz);
+      }
+      f32x16 hT[3];
+#pragma unroll
+      for (int n = 0; n < 3; ++n) hT[n] = f32x16{};
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const int j0 = 16 * kk + 8 * s;
+        float f[8];
+#pragma unroll
+        for (int qq = 0; qq < 8; ++qq) f[qq] = qT[ar][j0 + qq] * qT[ac][j0 + qq];
+        const bf16x8 bq = pack8(f);
+#pragma unroll
+        for (int n = 0; n < 3; ++n) {
+          const bf16x8 a = *reinterpret_cast<const bf16x8*>(&GT[32 * n + row][j0]);
+          hT[n] = mfma32(a, bq, hT[n]);
+        }
+      }
+      const float w = wh[hh];
+      float dsum = 0.f;
+#pragma unroll
+      for (int n = 0; n < 2; ++n)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          acc[n][i] += w * hT[n][i];
+          dsum += (float)Pl[row][32 * n + c32_row(i, l)] * hT[n][i];
+        }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[2][i] += w * hT[2][i];
+      if (s == 0) dsum += Pzl[row] * hT[2][0];  // value row 64 = Gz column
+      dwp[hh] += dsum;
+    }
+  }
+#pragma unroll
+  for (int hh = 0; hh < 8; ++hh) {
+    if (hh < R) {
+      const float tot = dwp[hh] + __shfl_xor(dwp[hh], 32, 64);
+      if (s == 0) dwqs[(size_t)(b * Hq + kh * R + hh) * kS + slot] = tot;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Ring staging of k-blocked tiles (shared by the two waves of a fold block).
+// One unit = 1024 bf16 (a PR M-tile k-slice of 32 x 16 or a PT k-step 64 x 16).
+// ---------------------------------------------------------------------------
+constexpr int kFG = 4;  // units per ring group
+
+template <int NU, int G>
+__device__ __forceinline__ void ring_fetch_u(const uint16_t* src, int tid, uint4 (&reg)[kFG]) {
+#pragma unroll
+  for (int i = 0; i < kFG; ++i) {
+    const int u = G * kFG + i;
+    if (u < NU) reg[i] = reinterpret_cast<const uint4*>(src + (size_t)u * 1024)[tid];
+  }
+}
+template <int NU, int G>
+__device__ __forceinline__ void ring_store_u(__bf16* ring, int tid, const uint4 (&reg)[kFG]) {
+  __bf16* buf = ring + (G & 1) * kFG * 1024;
+#pragma unroll
+  for (int i = 0; i < kFG; ++i)
+    if (G * kFG + i < NU) reinterpret_cast<uint4*>(buf + i * 1024)[tid] = reg[i];
+}
+template <int U>
+__device__ __forceinline__ const __bf16* ring_unit(const __bf16* ring) {
+  return ring + ((U / kFG) & 1) * kFG * 1024 + (U % kFG) * 1024;
+}
+
+// Fold of one 32-slot M-tile (rows permuted so that the rows a lane holds are
+// slots of its rotation group): dx[rb] += d x[cb], dx[cb] += d x[rb].
+template <int M, bool WEIGHTED>
+__device__ __forceinline__ void fold_tile(const f32x16& D, const float (&x)[kD], float (&dx)[kD], const float* wl,
+                                          int s) {
+  float w16[16];
+#pragma unroll
+  for (int a = 0; a < 4; ++a) {
+    if constexpr (WEIGHTED) {
+      const float4 ww = *reinterpret_cast<const float4*>(wl + 16 * (2 * M + a / 2) + 8 * s + 4 * (a % 2));
+      w16[4 * a + 0] = ww.x;
+      w16[4 * a + 1] = ww.y;
+      w16[4 * a + 2] = ww.z;
+      w16[4 * a + 3] = ww.w;
+    } else {
+      w16[4 * a + 0] = w16[4 * a + 1] = w16[4 * a + 2] = w16[4 * a + 3] = 1.f;
+    }
+  }
+  [&]<int... I>(std::integer_sequence<int, I...>) {
+    (([&] {
+       constexpr int a = I / 4, v = I % 4;
+       constexpr int base = 8 * (2 * M + a / 2) + 4 * (a % 2) + v;
+       constexpr int rb = kSlotHost.rb[base], cb = kSlotHost.cb[base];
+       const float d = D[I] * w16[I];
+       if constexpr (rb < 64 && cb < 64) {
+         dx[rb] += d * x[cb];
+         dx[cb] += d * x[rb];
+       } else if constexpr (rb < 64 && cb == 64) {
+         dx[rb] += d;
+       }
+     }()),
+     ...);
+  }(std::make_integer_sequence<int, 16>{});
+}
+
+// A-operand rows of M-tile: lane row r = 8a + 4s' + v reads within-tile slot
+// 16(a/2) + 8s' + 4(a%2) + v of the PR tile (32 slots x 16 values per unit).
+__device__ __forceinline__ int fold_row(int r) {
+  const int a = r >> 3, sp = (r >> 2) & 1, v = r & 3;
+  return 16 * (a >> 1) + 8 * sp + 4 * (a & 1) + v;
+}
+
+// Fold ring: one 32-slot M-tile of a PR-layout state (4 k-slices x 32 rows x
+// 16 values = 2048 bf16) per group, two buffers; 128 threads move 32 B each.
+constexpr int kTileElems = 4 * 32 * 16;
+
+__device__ __forceinline__ void fold_fetch(const uint16_t* src, int m, int tid, uint4 (&reg)[2]) {
+  const uint4* p = reinterpret_cast<const uint4*>(src + (size_t)m * kTileElems);
+  reg[0] = p[tid];
+  reg[1] = p[tid + 128];
+}
+__device__ __forceinline__ void fold_store(__bf16* ring, int m, int tid, const uint4 (&reg)[2]) {
+  uint4* p = reinterpret_cast<uint4*>(ring + (m & 1) * kTileElems);
+  p[tid] = reg[0];
+  p[tid + 128] = reg[1];
+}
+
+template <int M, bool WEIGHTED>
+__device__ __forceinline__ void fold_step(const bf16x8 (&bfr)[4], const float (&x)[kD], float (&dx)[kD],
+                                          const float* wl, const __bf16* ring, int lane) {
+  const int s = lane >> 5, arow = fold_row(lane & 31);
+  const __bf16* tile = ring + (M & 1) * kTileElems;
+  f32x16 D = f32x16{};
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk)
+    D = mfma32(*reinterpret_cast<const bf16x8*>(tile + kk * 512 + arow * 16 + 8 * s), bfr[kk], D);
+  fold_tile<M, WEIGHTED>(D, x, dx, wl, s);
+}
+
+template <int G, bool WEIGHTED>
+__device__ __forceinline__ void fold_group(const bf16x8 (&bfr)[4], const float (&x)[kD], float (&dx)[kD],
+                                           const float* wl, __bf16* ring, const uint16_t* src, int tid, int lane) {
+  constexpr int NT = kS / 32;  // 69 M-tiles
+  uint4 reg[2];
+  if constexpr (G + 1 < NT) fold_fetch(src, G + 1, tid, reg);
+  fold_step<G, WEIGHTED>(bfr, x, dx, wl, ring, lane);
+  if constexpr (G + 1 < NT) {
+    fold_store(ring, G + 1, tid, reg);
+    __syncthreads();
+    fold_group<G + 1, WEIGHTED>(bfr, x, dx, wl, ring, src, tid, lane);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dq: state part of the query-side VJP, folded, plus the local part.
+// grid (R, NB, U), 2 waves; wave w owns tokens 32w..32w+31 (lane column).
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(128) void k2_q_fold(const T* __restrict__ q, const uint16_t* __restrict__ G16,
+                                                 const float* __restrict__ wqs, const uint16_t* __restrict__ PR,
+                                                 const float* __restrict__ dqf, int Hq, int Hkv, int N, int NB,
+                                                 T* __restrict__ dq) {
+  __shared__ __attribute__((aligned(16))) __bf16 ring[2 * kFG * 1024];
+  __shared__ __attribute__((aligned(16))) float wl[kS];
+  __shared__ float dqs[kC][kD + 1];
+
+  const int hh = blockIdx.x, ch = blockIdx.y, u = blockIdx.z;
+  const int R = Hq / Hkv, b = u / Hkv, kh = u % Hkv, h = kh * R + hh;
+  const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, s = l >> 5, row = l & 31;
+  const int tok0 = ch * kC;
+  const size_t qbase = (size_t)(b * Hq + h) * N * kD;
+  const uint16_t* src = PR + ((size_t)u * NB + ch) * ((size_t)kKS * 64 * 16);
+
+  {
+    uint4 reg[2];
+    fold_fetch(src, 0, tid, reg);
+    for (int i = tid; i < kS / 4; i += 128)
+      reinterpret_cast<float4*>(wl)[i] = reinterpret_cast<const float4*>(wqs + (size_t)h * kS)[i];
+    fold_store(ring, 0, tid, reg);
+  }
+  const int tok = tok0 + 32 * wv + row;
+  const bool ok = tok < N;
+  const size_t rowoff = qbase + (size_t)(ok ? tok : N - 1) * kD;
+  float x[kD], dx[kD];
+  bf16x8 bfr[4];
+  {
+    bf16x8 qr[8], gr[8];
+    load_row_b(q, rowoff, ok, qr);
+    load_row_b(G16, rowoff, ok, gr);
+    rotated_row(qr, s, x);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) bfr[kk] = gr[2 * kk + s];
+  }
+#pragma unroll
+  for (int m = 0; m < kD; ++m) dx[m] = 0.f;
+  __syncthreads();
+  fold_group<0, true>(bfr, x, dx, wl, ring, src, tid, l);
+
+  // combine the two rotation groups of each token
+  const int tl = 32 * wv + row;
+  if (s == 0) {
+#pragma unroll
+    for (int m = 0; m < kD; ++m) dqs[tl][m] = dx[m];
+  }
+  __syncthreads();
+  if (s == 1) {
+#pragma unroll
+    for (int m = 0; m < kD; ++m) dqs[tl][(m + 32) & 63] += dx[m];
+  }
+  __syncthreads();
+  for (int j = 0; j < 32; ++j) {
+    const int tj = tok0 + 32 * wv + j;
+    if (tj >= N) break;
+    const size_t o = qbase + (size_t)tj * kD + l;
+    dq[o] = from_f<T>(dqs[32 * wv + j][l] + dqf[o]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dk, dv: state parts (fold of dT V^T, dU = raw(K) dT, dTz quadratic form) plus
+// the per-head local parts. grid (NB, U), 2 waves; wave w owns tokens 32w..+31.
+// ---------------------------------------------------------------------------
+template <int T>
+__device__ __forceinline__ void du_step(const float (&x)[kD], const __bf16* ring, int lane, f32x16 (&acc)[2]) {
+  const int s = lane >> 5, row = lane & 31;
+  const __bf16* tile = ring_unit<T>(ring);
+  const bf16x8 b0 = *reinterpret_cast<const bf16x8*>(tile + row * 16 + 8 * s);
+  const bf16x8 b1 = *reinterpret_cast<const bf16x8*>(tile + (32 + row) * 16 + 8 * s);
+  const bf16x8 a = raw_fragment<T>(x);
+  acc[0] = mfma32(a, b0, acc[0]);
+  acc[1] = mfma32(a, b1, acc[1]);
+}
+template <int G>
+__device__ __forceinline__ void du_group(const float (&x)[kD], __bf16* ring, const uint16_t* src, int tid, int lane,
+                                         f32x16 (&acc)[2]) {
+  constexpr int NG = (kKS + kFG - 1) / kFG;
+  uint4 reg[kFG];
+  if constexpr (G + 1 < NG) ring_fetch_u<kKS, G + 1>(src, tid, reg);
+  [&]<int... I>(std::integer_sequence<int, I...>) {
+    ((G * kFG + I < kKS ? du_step<(G * kFG + I < kKS ? G * kFG + I : 0)>(x, ring, lane, acc) : void()), ...);
+  }(std::make_integer_sequence<int, kFG>{});
+  if constexpr (G + 1 < NG) {
+    ring_store_u<kKS, G + 1>(ring, tid, reg);
+    __syncthreads();
+    du_group<G + 1>(x, ring, src, tid, lane, acc);
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(128) void k2_kv_fold(const T* __restrict__ k, const T* __restrict__ v,
+                                                  const uint16_t* __restrict__ dTR, const uint16_t* __restrict__ dTT,
+                                                  const float* __restrict__ dTz, const float* __restrict__ dkp,
+                                                  const float* __restrict__ dvp, int Hq, int Hkv, int N, int NB,
+                                                  T* __restrict__ dk, T* __restrict__ dv) {
+  __shared__ __attribute__((aligned(16))) __bf16 ring[2 * kFG * 1024];
+  __shared__ __attribute__((aligned(16))) __bf16 mz[kD][LD];
+  __shared__ __attribute__((aligned(16))) __bf16 ks[kC][LD];
+  __shared__ float dks[kC][kD + 1];
+  __shared__ float zl[kD];
+
+  const int ch = blockIdx.x, u = blockIdx.y;
+  const int R = Hq / Hkv, b = u / Hkv, kh = u % Hkv;
+  const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, s = l >> 5, row = l & 31;
+  const int tok0 = ch * kC;
+  const size_t kbase = (size_t)u * N * kD;
+  const size_t cbase = ((size_t)u * NB + ch) * ((size_t)kKS * 64 * 16);
+  const float* tz = dTz + ((size_t)u * NB + ch) * kFP;
+
+  // dTz quadratic form: d/dk of sum_p dTz[p] raw(k)[p] = z1 + Mz k with
+  // Mz[r][c] = dTz[pair(r, c)] (r != c), 2 dTz[pair(r, r)] on the diagonal.
+  for (int idx = tid; idx < kD * kD; idx += 128) {
+    const int r = idx >> 6, c = idx & 63;
+    const int hi = r > c ? r : c, lo = r > c ? c : r;
+    const float val = tz[1 + kD + pair_index(hi, lo)];
+    mz[r][c] = (__bf16)(r == c ? 2.f * val : val);
+  }
+  if (tid < kD) zl[tid] = tz[1 + tid];
+
+  const int tok = tok0 + 32 * wv + row;
+  const bool ok = tok < N;
+  const size_t rowoff = kbase + (size_t)(ok ? tok : N - 1) * kD;
+  float x[kD], dx[kD];
+  bf16x8 bfr[4];
+  {
+    bf16x8 kr[8], vr[8];
+    load_row_b(k, rowoff, ok, kr);
+    load_row_b(v, rowoff, ok, vr);
+    if (s == 0) store_row(&ks[32 * wv + row][0], kr);
+    rotated_row(kr, s, x);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) bfr[kk] = vr[2 * kk + s];
+  }
+#pragma unroll
+  for (int m = 0; m < kD; ++m) dx[m] = 0.f;
+
+  // 1. fold of dT V^T through the key features
+  {
+    uint4 reg[2];
+    fold_fetch(dTR + cbase, 0, tid, reg);
+    fold_store(ring, 0, tid, reg);
+  }
+  __syncthreads();
+  fold_group<0, false>(bfr, x, dx, nullptr, ring, dTR + cbase, tid, l);
+  __syncthreads();
+  // 2. dU = raw(K) dT (values 0..63)
+  f32x16 acc[2] = {f32x16{}, f32x16{}};
+  {
+    uint4 reg[kFG];
+    ring_fetch_u<kKS, 0>(dTT + cbase, tid, reg);
+    ring_store_u<kKS, 0>(ring, tid, reg);
+  }
+  __syncthreads();
+  du_group<0>(x, ring, dTT + cbase, tid, l, acc);
+
+  // 3. combine rotation groups, add z1 + Mz k
+  const int tl = 32 * wv + row;
+  if (s == 0) {
+#pragma unroll
+    for (int m = 0; m < kD; ++m) dks[tl][m] = dx[m] + zl[m];
+  }
+  __syncthreads();
+  if (s == 1) {
+#pragma unroll
+    for (int m = 0; m < kD; ++m) dks[tl][(m + 32) & 63] += dx[m];
+  }
+  __syncthreads();
+  {
+    // Z^T [64 d x 32 tok] = Mz K^T for this wave's tokens
+#pragma unroll
+    for (int md = 0; md < 2; ++md) {
+      f32x16 z = f32x16{};
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const bf16x8 a = *reinterpret_cast<const bf16x8*>(&mz[32 * md + row][16 * kk + 8 * s]);
+        const bf16x8 bb = *reinterpret_cast<const bf16x8*>(&ks[32 * wv + row][16 * kk + 8 * s]);
+        z = mfma32(a, bb, z);
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) dks[32 * wv + row][32 * md + c32_row(i, l)] += z[i];
+    }
+  }
+  __syncthreads();
+  for (int j = 0; j < 32; ++j) {
+    const int tj = tok0 + 32 * wv + j;
+    if (tj >= N) break;
+    float ksum = dks[32 * wv + j][l], vsum = 0.f;
+    for (int hh = 0; hh < R; ++hh) {
+      const size_t o = ((size_t)(b * Hq + kh * R + hh) * N + tj) * kD + l;
+      ksum += dkp[o];
+      vsum += dvp[o];
+    }
+    const size_t o = kbase + (size_t)tj * kD + l;
+    dk[o] = from_f<T>(ksum);
+    // dv state part lives in the accumulators; add it below
+    dks[32 * wv + j][l] = vsum;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int j = 32 * wv + c32_row(i, l), tj = tok0 + j;
+      if (tj < N) dv[kbase + (size_t)tj * kD + 32 * nt + row] = from_f<T>(acc[nt][i] + dks[j][32 * nt + row]);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Local (intra-chunk) VJP. grid (R, NB, U), 4 waves (256 threads).
+// 16x16x32 MFMA tiles; tile (ti, tj) covers tokens i in 16ti.., j in 16tj...
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void k2_local_bwd(const T* __restrict__ q, const T* __restrict__ k,
+                                                    const T* __restrict__ v, const uint16_t* __restrict__ G16,
+                                                    const float* __restrict__ Gz, const float* __restrict__ PZ,
+                                                    const int32_t* __restrict__ labels, const float* __restrict__ c0,
+                                                    const float* __restrict__ lam, const float* __restrict__ gam,
+                                                    int G, int Hq, int Hkv, int N, int NB, float scale,
+                                                    float* __restrict__ dqf, float* __restrict__ dkp,
+                                                    float* __restrict__ dvp, float* __restrict__ coefl) {
+  __shared__ __attribute__((aligned(16))) __bf16 Qr[kC][LD];
+  __shared__ __attribute__((aligned(16))) __bf16 Kr[kC][LD];
+  __shared__ __attribute__((aligned(16))) __bf16 Vr[kC][LD];
+  __shared__ __attribute__((aligned(16))) __bf16 Gr[kC][LD];
+  __shared__ __attribute__((aligned(16))) __bf16 TT[kC][LD];  // pz (fp32) first, then K^T, Q^T, G^T
+  __shared__ __attribute__((aligned(16))) __bf16 dsm[kC][LD];
+  __shared__ __attribute__((aligned(16))) __bf16 kapT[kC][LD];
+  __shared__ __attribute__((aligned(16))) __bf16 XW[4][16][LD];  // Mz first
+  __shared__ float gzl[kC], bz[kD];
+  __shared__ int lab[kD];
+  __shared__ float lamh[8], gamh[64];
+  __shared__ float cpart[4][1 + 8 + 64];
+  static_assert(sizeof(TT) >= kFP * sizeof(float), "pz staging must fit the transpose buffer");
+
+  const int hh = blockIdx.x, ch = blockIdx.y, u = blockIdx.z;
+  const int R = Hq / Hkv, b = u / Hkv, kh = u % Hkv, h = kh * R + hh;
+  const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63;
+  const int r16 = l & 15, g16 = l >> 4;
+  const int tok0 = ch * kC;
+  const size_t qbase = (size_t)(b * Hq + h) * N * kD;
+  const size_t kbase = (size_t)u * N * kD;
+  float* pzl = reinterpret_cast<float*>(&TT[0][0]);
+  __bf16(*mz)[LD] = reinterpret_cast<__bf16(*)[LD]>(&XW[0][0][0]);
+
+  // --- stage rows ------------------------------------------------------------
+  {
+    const int tok = tok0 + l;
+    const bool ok = tok < N;
+    const int tc = ok ? tok : N - 1;
+    bf16x8 r[8];
+    if (wv == 0) {
+      load_row_b(q, qbase + (size_t)tc * kD, ok, r);
+      store_row(&Qr[l][0], r);
+    } else if (wv == 1) {
+      load_row_b(k, kbase + (size_t)tc * kD, ok, r);
+      store_row(&Kr[l][0], r);
+    } else if (wv == 2) {
+      load_row_b(v, kbase + (size_t)tc * kD, ok, r);
+      store_row(&Vr[l][0], r);
+    } else {
+      load_row_b(G16, qbase + (size_t)tc * kD, ok, r);
+      store_row(&Gr[l][0], r);
+      gzl[l] = ok ? Gz[(size_t)(b * Hq + h) * N + tc] : 0.f;
+      int g = labels[h * kD + l];
+      lab[l] = g < 0 ? 0 : (g >= G ? G - 1 : g);
+      if (l < G) lamh[l] = lam[(size_t)h * G + l];
+      if (l < G * G) gamh[l] = gam[(size_t)h * G * G + l];
+    }
+    const float* pz = PZ + ((size_t)u * NB + ch) * kFP;
+    for (int i = tid; i < kFP / 4; i += 256) reinterpret_cast<float4*>(pzl)[i] = reinterpret_cast<const float4*>(pz)[i];
+  }
+  __syncthreads();
+  const float sc2 = scale * scale;
+  for (int idx = tid; idx < kD * kD; idx += 256) {
+    const int r = idx >> 6, c = idx & 63;
+    const int hi = r > c ? r : c, lo = r > c ? c : r;
+    mz[r][c] = (__bf16)(sc2 * gamh[lab[r] * G + lab[c]] * pzl[1 + kD + pair_index(hi, lo)]);
+  }
+  if (tid < kD) bz[tid] = scale * lamh[lab[tid]] * pzl[1 + tid];
+  __syncthreads();
+
+  // --- dq denominator part for row tile ti = wv: gz_i (bz + 2 Mz q_i) -------
+  f32x4 dqa[4];
+  {
+    const int ti = wv;
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+      f32x4 z = f32x4{};
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        const bf16x8 a = *reinterpret_cast<const bf16x8*>(&Qr[16 * ti + r16][32 * kk + 8 * g16]);
+        const bf16x8 bb = *reinterpret_cast<const bf16x8*>(&mz[16 * nt + r16][32 * kk + 8 * g16]);
+        z = mfma16(a, bb, z);
+      }
+      const int d = 16 * nt + r16;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int ii = 16 * ti + c16_row(i, l);
+        dqa[nt][i] = gzl[ii] * (bz[d] + 2.f * z[i]);
+      }
+    }
+  }
+  __syncthreads();  // mz (aliased with XW) is dead
+
+  // group masks of the A-fragment dims d = 32 kk + 8 g16 + j
+  auto group_mask = [&](int g, int kk, int w) -> uint32_t {
+    const int d = 32 * kk + 8 * g16 + 2 * w;
+    return (lab[d] == g ? 0x0000ffffu : 0u) | (lab[d + 1] == g ? 0xffff0000u : 0u);
+  };
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  auto s_tile = [&](int ti, int tj, int g) -> f32x4 {
+    f32x4 acc = f32x4{};
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      const u32x4 qa = *reinterpret_cast<const u32x4*>(&Qr[16 * ti + r16][32 * kk + 8 * g16]);
+      const bf16x8 kb = *reinterpret_cast<const bf16x8*>(&Kr[16 * tj + r16][32 * kk + 8 * g16]);
+      const u32x4 m = {group_mask(g, kk, 0), group_mask(g, kk, 1), group_mask(g, kk, 2), group_mask(g, kk, 3)};
+      acc = mfma16(__builtin_bit_cast(bf16x8, qa & m), kb, acc);
+    }
+    return acc * scale;
+  };
+
+  // --- sweep 1: ds, kappa, local coefficient gradients ------------------------
+  {
+    float cacc[1 + 8 + 64];
+#pragma unroll
+    for (int i = 0; i < 73; ++i) cacc[i] = 0.f;
+    // the 10 lower tiles, listed (3,0..3), (2,0..2), (1,0..1), (0,0); wave w takes w, w+4, w+8
+    for (int tt = 0; tt < 3; ++tt) {
+      const int idx = wv + 4 * tt;
+      if (idx >= 10) continue;
+      const int ti = idx < 4 ? 3 : idx < 7 ? 2 : idx < 9 ? 1 : 0;
+      const int tj = idx < 4 ? idx : idx < 7 ? idx - 4 : idx < 9 ? idx - 7 : 0;
+      // ds tile = G V^T + gz
+      f32x4 ds = f32x4{};
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        const bf16x8 a = *reinterpret_cast<const bf16x8*>(&Gr[16 * ti + r16][32 * kk + 8 * g16]);
+        const bf16x8 bb = *reinterpret_cast<const bf16x8*>(&Vr[16 * tj + r16][32 * kk + 8 * g16]);
+        ds = mfma16(a, bb, ds);
+      }
+      f32x4 sg[8];
+#pragma unroll
+      for (int g = 0; g < 8; ++g) sg[g] = g < G ? s_tile(ti, tj, g) : f32x4{};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int ii = 16 * ti + c16_row(i, l), jj = 16 * tj + r16;
+        const bool live = jj <= ii && tok0 + ii < N;
+        const float dsv = live ? ds[i] + gzl[ii] : 0.f;
+        float kv = 0.f;
+        if (live) {
+          kv = c0[h];
+#pragma unroll
+          for (int g = 0; g < 8; ++g) {
+            if (g < G) {
+              float inner = lamh[g];
+#pragma unroll
+              for (int g2 = 0; g2 < 8; ++g2)
+                if (g2 < G) inner += gamh[g * G + g2] * sg[g2][i];
+              kv += sg[g][i] * inner;
+            }
+          }
+        }
+        dsm[ii][jj] = (__bf16)dsv;
+        kapT[jj][ii] = (__bf16)kv;
+        if (tj < ti) {
+          dsm[16 * tj + c16_row(i, l)][16 * ti + r16] = (__bf16)0.f;
+          kapT[16 * ti + r16][16 * tj + c16_row(i, l)] = (__bf16)0.f;
+        }
+        cacc[0] += dsv;
+#pragma unroll
+        for (int g = 0; g < 8; ++g) {
+          const float t = dsv * sg[g][i];
+          cacc[1 + g] += t;
+#pragma unroll
+          for (int g2 = 0; g2 < 8; ++g2) cacc[9 + 8 * g + g2] += t * sg[g2][i];
+        }
+      }
+    }
+    // the strictly upper tiles are zero in dsm (row < col blocks)
+    for (int idx = tid; idx < 6 * 256; idx += 256) {
+      const int t = idx >> 8, e = idx & 255;
+      // strictly upper tiles (0,1) (0,2) (0,3) (1,2) (1,3) (2,3)
+      const int ti = t < 3 ? 0 : t < 5 ? 1 : 2;
+      const int tj = t < 3 ? t + 1 : t < 5 ? t - 1 : 3;
+      dsm[16 * ti + (e >> 4)][16 * tj + (e & 15)] = (__bf16)0.f;
+      kapT[16 * tj + (e & 15)][16 * ti + (e >> 4)] = (__bf16)0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < 73; ++i) {
+      const float t = wave_sum(cacc[i]);
+      if (l == 0) cpart[wv][i] = t;
+    }
+  }
+  __syncthreads();
+  if (tid < 73) {
+    coefl[(((size_t)(b * Hq + h)) * NB + ch) * 73 + tid] =
+        (cpart[0][tid] + cpart[1][tid]) + (cpart[2][tid] + cpart[3][tid]);
+  }
+  // K^T into TT
+  for (int idx = tid; idx < kC * kD; idx += 256) {
+    const int j = idx & 63, d = idx >> 6;
+    TT[d][j] = Kr[j][d];
+  }
+  __syncthreads();
+
+  // per-column coefficients of the F_h combination (d = 16 nt + r16)
+  auto comb = [&](int nt, int hgrp) -> float {
+    const int d = 16 * nt + r16;
+    return hgrp < G ? 2.f * scale * gamh[lab[d] * G + hgrp] : scale * lamh[lab[d]];
+  };
+
+  // --- sweep 2: dq local for row tile ti = wv -----------------------------------
+  {
+    const int ti = wv;
+    const int nk = (16 * (ti + 1) + 31) / 32;
+    for (int hg = 0; hg <= G; ++hg) {
+      // X row tile: ds o S_h (or ds for the lambda term), zero beyond the causal range
+      for (int tj = 0; tj < 2 * nk; ++tj) {
+        f32x4 xs = f32x4{};
+        if (tj <= ti) {
+          const f32x4 sgt = hg < G ? s_tile(ti, tj, hg) : f32x4{1.f, 1.f, 1.f, 1.f};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) xs[i] = (float)dsm[16 * ti + c16_row(i, l)][16 * tj + r16] * sgt[i];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) XW[wv][c16_row(i, l)][16 * tj + r16] = (__bf16)xs[i];
+      }
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) {
+        f32x4 f = f32x4{};
+        for (int kk = 0; kk < nk; ++kk) {
+          const bf16x8 a = *reinterpret_cast<const bf16x8*>(&XW[wv][r16][32 * kk + 8 * g16]);
+          const bf16x8 bb = *reinterpret_cast<const bf16x8*>(&TT[16 * nt + r16][32 * kk + 8 * g16]);
+          f = mfma16(a, bb, f);
+        }
+        const float cf = comb(nt, hg);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dqa[nt][i] += cf * f[i];
+      }
+      __builtin_amdgcn_wave_barrier();
+    }
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int tok = tok0 + 16 * ti + c16_row(i, l);
+        if (tok < N) dqf[qbase + (size_t)tok * kD + 16 * nt + r16] = dqa[nt][i];
+      }
+  }
+  __syncthreads();
+  // Q^T into TT
+  for (int idx = tid; idx < kC * kD; idx += 256) {
+    const int j = idx & 63, d = idx >> 6;
+    TT[d][j] = Qr[j][d];
+  }
+  __syncthreads();
+
+  // --- sweep 3: dk local for column tile tj = wv ---------------------------------
+  {
+    const int tj = wv;
+    const int k0 = tj / 2;  // first 32-wide k-step over i
+    f32x4 dka[4];
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) dka[nt] = f32x4{};
+    for (int hg = 0; hg <= G; ++hg) {
+      // X^T column tile: XW[wv][j][i] = ds_ij (S_h)_ij for i >= j
+      for (int ti = 2 * k0; ti < 4; ++ti) {
+        f32x4 xs = f32x4{};
+        if (ti >= tj) {
+          const f32x4 sgt = hg < G ? s_tile(ti, tj, hg) : f32x4{1.f, 1.f, 1.f, 1.f};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) xs[i] = (float)dsm[16 * ti + c16_row(i, l)][16 * tj + r16] * sgt[i];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) XW[wv][r16][16 * ti + c16_row(i, l)] = (__bf16)xs[i];
+      }
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) {
+        f32x4 f = f32x4{};
+        for (int kk = k0; kk < 2; ++kk) {
+          const bf16x8 a = *reinterpret_cast<const bf16x8*>(&XW[wv][r16][32 * kk + 8 * g16]);
+          const bf16x8 bb = *reinterpret_cast<const bf16x8*>(&TT[16 * nt + r16][32 * kk + 8 * g16]);
+          f = mfma16(a, bb, f);
+        }
+        const float cf = comb(nt, hg);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dka[nt][i] += cf * f[i];
+      }
+      __builtin_amdgcn_wave_barrier();
+    }
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int tok = tok0 + 16 * tj + c16_row(i, l);
+        if (tok < N) dkp[qbase + (size_t)tok * kD + 16 * nt + r16] = dka[nt][i];
+      }
+  }
+  __syncthreads();
+  // G^T into TT
+  for (int idx = tid; idx < kC * kD; idx += 256) {
+    const int j = idx & 63, e = idx >> 6;
+    TT[e][j] = Gr[j][e];
+  }
+  __syncthreads();
+
+  // --- sweep 4: dv local = kappa^T G for column tile tj = wv ----------------------
+  {
+    const int tj = wv;
+    const int k0 = tj / 2;
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+      f32x4 f = f32x4{};
+      for (int kk = k0; kk < 2; ++kk) {
+        const bf16x8 a = *reinterpret_cast<const bf16x8*>(&kapT[16 * tj + r16][32 * kk + 8 * g16]);
+        const bf16x8 bb = *reinterpret_cast<const bf16x8*>(&TT[16 * nt + r16][32 * kk + 8 * g16]);
+        f = mfma16(a, bb, f);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int tok = tok0 + 16 * tj + c16_row(i, l);
+        if (tok < N) dvp[qbase + (size_t)tok * kD + 16 * nt + r16] = f[i];
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Coefficient gradients, one block per query head.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k2_coef_grad(const float* __restrict__ dwqs, const float* __restrict__ coefl,
+                                                    const int32_t* __restrict__ labels, int B, int Hq, int NB, int G,
+                                                    float scale, float* __restrict__ dc0, float* __restrict__ dlam,
+                                                    float* __restrict__ dgam) {
+  __shared__ float w[kS];
+  __shared__ float loc[73];
+  __shared__ float raw[64];
+  __shared__ int lab[kD];
+  const int h = blockIdx.x, t = threadIdx.x;
+  if (t < kD) {
+    int g = labels[h * kD + t];
+    lab[t] = g < 0 ? 0 : (g >= G ? G - 1 : g);
+  }
+  for (int sl = t; sl < kS; sl += 256) {
+    float acc = 0.f;
+    for (int b = 0; b < B; ++b) acc += dwqs[((size_t)b * Hq + h) * kS + sl];
+    w[sl] = acc;
+  }
+  if (t < 73) {
+    float acc = 0.f;
+    for (int b = 0; b < B; ++b)
+      for (int ch = 0; ch < NB; ++ch) acc += coefl[(((size_t)b * Hq + h) * NB + ch) * 73 + t];
+    loc[t] = acc;
+  }
+  __syncthreads();
+  if (t == 0) {
+    float a = loc[0];
+    for (int sl = 0; sl < kS; ++sl)
+      if (kSlot.nat[sl] == 0) a += w[sl];
+    dc0[h] = a;
+  }
+  for (int g = t; g < G; g += 256) {
+    float acc = 0.f;
+    for (int sl = 0; sl < kS; ++sl) {
+      const int n = kSlot.nat[sl];
+      if (n >= 1 && n <= kD && lab[n - 1] == g) acc += w[sl];
+    }
+    dlam[(size_t)h * G + g] = acc * scale + loc[1 + g];
+  }
+  // exact routing of the state part, [g(r)][g(c)] for pair (r >= c)
+  for (int e = t; e < G * G; e += 256) {
+    const int gr = e / G, gc = e % G;
+    float acc = 0.f;
+    for (int sl = 0; sl < kS; ++sl) {
+      const int n = kSlot.nat[sl];
+      if (n <= kD) continue;
+      const int r = kSlot.ar[sl], c = kSlot.ac[sl];
+      if (lab[r] == gr && lab[c] == gc) acc += (r == c ? 1.f : 2.f) * w[sl];
+    }
+    raw[e] = acc * scale * scale;
+  }
+  __syncthreads();
+  for (int e = t; e < G * G; e += 256) {
+    const int gr = e / G, gc = e % G;
+    const float sym = gr == gc ? raw[e] : 0.5f * (raw[e] + raw[gc * G + gr]);
+    dgam[(size_t)h * G * G + e] = sym + loc[9 + 8 * gr + gc];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------
+MfmaWork mfma_work_view(void* base, int B, int Hq, int U, int N, int NB) {
+  char* p = static_cast<char*>(base);
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    void* r = p ? p + off : nullptr;
+    off += align256(bytes);
+    return r;
+  };
+  const size_t rows = (size_t)B * Hq * N;
+  const size_t chunk = (size_t)kKS * 64 * 16 * sizeof(uint16_t);
+  MfmaWork w;
+  w.G16 = static_cast<uint16_t*>(take(rows * kD * sizeof(uint16_t)));
+  w.Gz = static_cast<float*>(take(rows * sizeof(float)));
+  w.dTT = static_cast<uint16_t*>(take(chunk * U * NB));
+  w.dTR = static_cast<uint16_t*>(take(chunk * U * NB));
+  w.dTz = static_cast<float*>(take(sizeof(float) * (size_t)U * NB * kFP));
+  w.dwqs = static_cast<float*>(take(sizeof(float) * (size_t)B * Hq * kS));
+  w.dqf = static_cast<float*>(take(rows * kD * sizeof(float)));
+  w.dkp = static_cast<float*>(take(rows * kD * sizeof(float)));
+  w.dvp = static_cast<float*>(take(rows * kD * sizeof(float)));
+  w.coefl = static_cast<float*>(take(sizeof(float) * (size_t)B * Hq * NB * 73));
+  w.bytes = off;
+  return w;
+}
+
+template <typename T>
+int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, const void* v, const int32_t* labels,
+                         const float* c0, const float* lam, const float* gam, int groups, float scale, float floor,
+                         const float* num, const float* den, const void* saved, const void* dout, const float* dnum,
+                         const float* dden, void* dq, void* dk, void* dv, float* dc0, float* dlam, float* dgam,
+                         void* workspace, hipStream_t st, const Timer& timed) {
+  MfmaSaved sv = mfma_saved_view(const_cast<void*>(saved), g.Hq, g.U, g.NB);
+  MfmaWork w = mfma_work_view(workspace, g.B, g.Hq, g.U, g.N, g.NB);
+  const T* qt = static_cast<const T*>(q);
+  const T* kt = static_cast<const T*>(k);
+  const T* vt = static_cast<const T*>(v);
+  const long rows = (long)g.B * g.Hq * g.N;
+  timed("k2_gvec", st, [&] {
+    hipLaunchKernelGGL(k2_gvec<T>, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st, static_cast<const T*>(dout),
+                       dnum, dden, num, den, rows, floor, w.G16, w.Gz);
+  });
+  timed("k2_state_bwd", st, [&] {
+    hipLaunchKernelGGL(k2_state_bwd<T>, dim3(kS / 32, g.U), dim3(64), 0, st, qt, w.G16, w.Gz, sv.wqs, sv.PR, sv.PZ,
+                       g.Hq, g.Hkv, g.N, g.NB, w.dTT, w.dTR, w.dTz, w.dwqs);
+  });
+  timed("k2_local_bwd", st, [&] {
+    hipLaunchKernelGGL(k2_local_bwd<T>, dim3(g.R, g.NB, g.U), dim3(256), 0, st, qt, kt, vt, w.G16, w.Gz, sv.PZ,
+                       labels, c0, lam, gam, groups, g.Hq, g.Hkv, g.N, g.NB, scale, w.dqf, w.dkp, w.dvp, w.coefl);
+  });
+  if (dq) {
+    timed("k2_q_fold", st, [&] {
+      hipLaunchKernelGGL(k2_q_fold<T>, dim3(g.R, g.NB, g.U), dim3(128), 0, st, qt, w.G16, sv.wqs, sv.PR, w.dqf,
+                         g.Hq, g.Hkv, g.N, g.NB, static_cast<T*>(dq));
+    });
+  }
+  if (dk || dv) {
+    if (!(dk && dv)) return 2;
+    timed("k2_kv_fold", st, [&] {
+      hipLaunchKernelGGL(k2_kv_fold<T>, dim3(g.NB, g.U), dim3(128), 0, st, kt, vt, w.dTR, w.dTT, w.dTz, w.dkp, w.dvp,
+                         g.Hq, g.Hkv, g.N, g.NB, static_cast<T*>(dk), static_cast<T*>(dv));
+    });
+  }
+  if (dc0 || dlam || dgam) {
+    if (!(dc0 && dlam && dgam)) return 3;
+    timed("k2_coef_grad", st, [&] {
+      hipLaunchKernelGGL(k2_coef_grad, dim3(g.Hq), dim3(256), 0, st, w.dwqs, w.coefl, labels, g.B, g.Hq, g.NB,
+                         groups, scale, dc0, dlam, dgam);
+    });
+  }
+  return 0;
+}
+
+template int launch_mfma_backward<float>(const LaunchGeom&, const void*, const void*, const void*, const int32_t*,
+                                         const float*, const float*, const float*, int, float, float, const float*,
+                                         const float*, const void*, const void*, const float*, const float*, void*,
+                                         void*, void*, float*, float*, float*, void*, hipStream_t, const Timer&);
+template int launch_mfma_backward<uint16_t>(const LaunchGeom&, const void*, const void*, const void*, const int32_t*,
+                                            const float*, const float*, const float*, int, float, float,
+                                            const float*, const float*, const void*, const void*, const float*,
+                                            const float*, void*, void*, void*, float*, float*, float*, void*,
+                                            hipStream_t, const Timer&);
+
+}  // namespace oal

@@ -22,7 +22,7 @@
 
 namespace oal {
 
-__constant__ SlotTable kSlot = make_slot_table();
+static __constant__ SlotTable kSlot = make_slot_table();
 
 // Per-head slot coefficients: wq of natural feature nat(slot), 0 for invalid slots.
 __global__ __launch_bounds__(256) void k2_slot_coefficients(const int32_t* __restrict__ labels,
@@ -55,6 +55,29 @@ __device__ __forceinline__ float ldf(const T* p, size_t i) {
   return to_f(p[i]);
 }
 
+// One 64-wide token row as 8 bf16 fragments, with 16-byte loads. The row index
+// is clamped so that every load is issued unconditionally; rows at or past N
+// come back as zeros.
+__device__ __forceinline__ void load_row(const uint16_t* __restrict__ src, size_t row_base, bool ok,
+                                         bf16x8 (&r)[8]) {
+  const bf16x8* p = reinterpret_cast<const bf16x8*>(src + row_base);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const bf16x8 x = p[i];
+    r[i] = ok ? x : bf16x8{};
+  }
+}
+__device__ __forceinline__ void load_row(const float* __restrict__ src, size_t row_base, bool ok, bf16x8 (&r)[8]) {
+  const float4* p = reinterpret_cast<const float4*>(src + row_base);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float4 a = p[2 * i], b = p[2 * i + 1];
+    float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    const bf16x8 x = pack8(v);
+    r[i] = ok ? x : bf16x8{};
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Forward state scan. grid (kS/32, U), one wave. Lane row = slot (32 per tile),
 // accumulator N-tiles: values 0-31, 32-63, and [den, 0...] (a ones column).
@@ -63,8 +86,8 @@ template <typename T>
 __global__ __launch_bounds__(64) void k2_state_fwd(const T* __restrict__ k, const T* __restrict__ v, int N, int NB,
                                                    uint16_t* __restrict__ PT, uint16_t* __restrict__ PR,
                                                    float* __restrict__ PZ) {
-  __shared__ float kT[kRow][kC + 4];            // kT[d][tok], rows 64 = valid flag, 65 = 0
-  __shared__ __attribute__((aligned(16))) __bf16 vT[96][kC + 8];  // vT[e][tok], row 64 = valid flag
+  __shared__ float kT[kRow][kC + 4];                               // kT[d][tok]; row 64 = valid, 65 = 0
+  __shared__ __attribute__((aligned(16))) __bf16 vT[96][kC + 8];  // vT[e][tok]; row 64 = valid
   __shared__ float stage[32][97];
 
   const int tile = blockIdx.x, u = blockIdx.y;
@@ -73,8 +96,29 @@ __global__ __launch_bounds__(64) void k2_state_fwd(const T* __restrict__ k, cons
   const int ar = kSlot.ar[slot], ac = kSlot.ac[slot];
   const size_t base = (size_t)u * N * kD;
 
-  // constant rows of vT (values rows are rewritten per chunk)
   for (int idx = l; idx < 31 * (kC + 8); idx += 64) vT[65 + idx / (kC + 8)][idx % (kC + 8)] = (__bf16)0.f;
+
+  // lane = token of the chunk being staged
+  auto stage_chunk = [&](const bf16x8 (&kr)[8], const bf16x8 (&vr)[8], bool ok) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        kT[8 * i + j][l] = (float)kr[i][j];
+        vT[8 * i + j][l] = vr[i][j];
+      }
+    kT[64][l] = ok ? 1.f : 0.f;
+    kT[65][l] = 0.f;
+    vT[64][l] = (__bf16)(ok ? 1.f : 0.f);
+  };
+  bf16x8 kr[8], vr[8];
+  {
+    const bool ok = l < N;
+    const size_t off = base + (size_t)(ok ? l : N - 1) * kD;
+    load_row(k, off, ok, kr);
+    load_row(v, off, ok, vr);
+    stage_chunk(kr, vr, ok);
+  }
 
   f32x16 acc[3];
 #pragma unroll
@@ -92,7 +136,6 @@ __global__ __launch_bounds__(64) void k2_state_fwd(const T* __restrict__ k, cons
     uint16_t* pt = PT + ((size_t)u * NB + ch) * chunk_elems;
     uint16_t* pr = PR + ((size_t)u * NB + ch) * chunk_elems;
     {
-      // PT[t][e][16]: lane -> (k-step half hh = s, e = row and row + 32)
       const int t = 2 * tile + s;
 #pragma unroll
       for (int eh = 0; eh < 2; ++eh) {
@@ -104,7 +147,6 @@ __global__ __launch_bounds__(64) void k2_state_fwd(const T* __restrict__ k, cons
         dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
         dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
       }
-      // PR[tile][kk][32][16]: lane -> (slot row, kk = 2s, 2s+1)
 #pragma unroll
       for (int kh = 0; kh < 2; ++kh) {
         const int kk = 2 * s + kh;
@@ -120,23 +162,15 @@ __global__ __launch_bounds__(64) void k2_state_fwd(const T* __restrict__ k, cons
         if (n >= 0) PZ[((size_t)u * NB + ch) * kFP + n] = stage[row][64];
       }
     }
-    // 2. stage chunk c
-    __syncthreads();
-    const int tok0 = ch * kC;
-    for (int idx = l; idx < kC * kD; idx += 64) {
-      const int j = idx >> 6, d = idx & 63, tok = tok0 + j;
-      const bool ok = tok < N;
-      kT[d][j] = ok ? ldf(k, base + (size_t)tok * kD + d) : 0.f;
-      vT[d][j] = (__bf16)(ok ? ldf(v, base + (size_t)tok * kD + d) : 0.f);
+    // 2. prefetch chunk c + 1 into registers
+    const int tok_next = (ch + 1) * kC + l;
+    const bool ok_next = tok_next < N;
+    if (ch + 1 < NB) {
+      const size_t off = base + (size_t)(ok_next ? tok_next : N - 1) * kD;
+      load_row(k, off, ok_next, kr);
+      load_row(v, off, ok_next, vr);
     }
-    {
-      const bool ok = tok0 + l < N;
-      kT[64][l] = ok ? 1.f : 0.f;
-      kT[65][l] = 0.f;
-      vT[64][l] = (__bf16)(ok ? 1.f : 0.f);
-    }
-    __syncthreads();
-    // 3. T_c = phi_K^T [V, 1]
+    // 3. T_c = phi_K^T [V, 1] from the staged chunk c
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       const int j0 = 16 * kk + 8 * s;
@@ -150,31 +184,20 @@ __global__ __launch_bounds__(64) void k2_state_fwd(const T* __restrict__ k, cons
         acc[n] = mfma32(a, b, acc[n]);
       }
     }
+    __syncthreads();
+    if (ch + 1 < NB) stage_chunk(kr, vr, ok_next);
+    __syncthreads();
   }
 }
 
 // ---------------------------------------------------------------------------
-// Forward readout, one wave per (query head, chunk, unit).
+// Forward readout: one block of two waves per (query head, chunk, unit); wave w
+// owns tokens 32w..32w+31 (one token per lane row). The per-chunk P^T tiles are
+// streamed through a two-buffer LDS ring of kRG k-steps shared by both waves.
 // ---------------------------------------------------------------------------
-template <int T>
-__device__ __forceinline__ void readout_steps(const float (&qa)[kD], const float (&qb)[kD], const float* wq,
-                                              const uint16_t* pt, int lane, f32x16 (&acc)[2][2]) {
-  const int s = lane >> 5, row = lane & 31;
-  float w[8];
-  const float4 w0 = *reinterpret_cast<const float4*>(wq + 16 * T + 8 * s);
-  const float4 w1 = *reinterpret_cast<const float4*>(wq + 16 * T + 8 * s + 4);
-  w[0] = w0.x; w[1] = w0.y; w[2] = w0.z; w[3] = w0.w;
-  w[4] = w1.x; w[5] = w1.y; w[6] = w1.z; w[7] = w1.w;
-  const bf16x8 b0 = *reinterpret_cast<const bf16x8*>(pt + ((size_t)T * 64 + row) * 16 + 8 * s);
-  const bf16x8 b1 = *reinterpret_cast<const bf16x8*>(pt + ((size_t)T * 64 + 32 + row) * 16 + 8 * s);
-  const bf16x8 a0 = feature_fragment<T>(qa, w);
-  const bf16x8 a1 = feature_fragment<T>(qb, w);
-  acc[0][0] = mfma32(a0, b0, acc[0][0]);
-  acc[0][1] = mfma32(a0, b1, acc[0][1]);
-  acc[1][0] = mfma32(a1, b0, acc[1][0]);
-  acc[1][1] = mfma32(a1, b1, acc[1][1]);
-  if constexpr (T + 1 < kKS) readout_steps<T + 1>(qa, qb, wq, pt, lane, acc);
-}
+constexpr int kRG = 4;                        // k-steps per ring group
+constexpr int kRingGroups = (kKS + kRG - 1) / kRG;
+constexpr int kRingStep = 64 * 16;            // bf16 per k-step tile
 
 // 8 consecutive elements of a row as a bf16 MFMA fragment.
 __device__ __forceinline__ bf16x8 load8(const uint16_t* p) { return *reinterpret_cast<const bf16x8*>(p); }
@@ -185,19 +208,74 @@ __device__ __forceinline__ bf16x8 load8(const float* p) {
   return pack8(v);
 }
 
+// Issue the global loads of ring group G (each of 128 threads moves kRG x 16 B).
+template <int G>
+__device__ __forceinline__ void ring_fetch(const uint16_t* pt, int tid, uint4 (&reg)[kRG]) {
+#pragma unroll
+  for (int i = 0; i < kRG; ++i) {
+    constexpr int t0 = G * kRG;
+    const int t = t0 + i;
+    if (t < kKS) reg[i] = reinterpret_cast<const uint4*>(pt + (size_t)t * kRingStep)[tid];
+  }
+}
+template <int G>
+__device__ __forceinline__ void ring_store(__bf16* ring, int tid, const uint4 (&reg)[kRG]) {
+  __bf16* buf = ring + (G & 1) * kRG * kRingStep;
+#pragma unroll
+  for (int i = 0; i < kRG; ++i) {
+    if (G * kRG + i < kKS) reinterpret_cast<uint4*>(buf + i * kRingStep)[tid] = reg[i];
+  }
+}
+
+template <int T>
+__device__ __forceinline__ void readout_step(const float (&x)[kD], const float* wl, const __bf16* ring, int lane,
+                                             f32x16 (&acc)[2]) {
+  const int s = lane >> 5, row = lane & 31;
+  const float4 w0 = *reinterpret_cast<const float4*>(wl + 16 * T + 8 * s);
+  const float4 w1 = *reinterpret_cast<const float4*>(wl + 16 * T + 8 * s + 4);
+  const float w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+  const __bf16* tile = ring + ((T / kRG) & 1) * kRG * kRingStep + (T % kRG) * kRingStep;
+  const bf16x8 b0 = *reinterpret_cast<const bf16x8*>(tile + row * 16 + 8 * s);
+  const bf16x8 b1 = *reinterpret_cast<const bf16x8*>(tile + (32 + row) * 16 + 8 * s);
+  const bf16x8 a = feature_fragment<T>(x, w);
+  acc[0] = mfma32(a, b0, acc[0]);
+  acc[1] = mfma32(a, b1, acc[1]);
+}
+
+template <int G>
+__device__ __forceinline__ void readout_group(const float (&x)[kD], const float* wl, __bf16* ring,
+                                              const uint16_t* pt, int tid, int lane, f32x16 (&acc)[2]) {
+  uint4 reg[kRG];
+  if constexpr (G + 1 < kRingGroups) ring_fetch<G + 1>(pt, tid, reg);
+  [&]<int... I>(std::integer_sequence<int, I...>) {
+    ((G * kRG + I < kKS ? readout_step<(G * kRG + I < kKS ? G * kRG + I : 0)>(x, wl, ring, lane, acc) : void()), ...);
+  }(std::make_integer_sequence<int, kRG>{});
+  if constexpr (G + 1 < kRingGroups) {
+    ring_store<G + 1>(ring, tid, reg);
+    __syncthreads();
+    readout_group<G + 1>(x, wl, ring, pt, tid, lane, acc);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Intra-chunk part of the forward, one wave per (query head, chunk, unit):
+// den = az + q.(bz + Mz q) (state term of the denominator as a quadratic form)
+//       + sum_j kappa(i, j);  num = kappa . V.  Written to num / den, which the
+// readout kernel then completes.
+// ---------------------------------------------------------------------------
 template <typename T>
-__global__ __launch_bounds__(64) void k2_out_fwd(const T* __restrict__ q, const T* __restrict__ k,
-                                                 const T* __restrict__ v, const float* __restrict__ wqs,
-                                                 const uint16_t* __restrict__ PT, const float* __restrict__ PZ,
-                                                 const int32_t* __restrict__ labels, const float* __restrict__ c0,
-                                                 const float* __restrict__ lam, const float* __restrict__ gam, int G,
-                                                 int Hq, int Hkv, int N, int NB, float scale, float floor,
-                                                 T* __restrict__ out, float* __restrict__ num,
-                                                 float* __restrict__ den) {
+__global__ __launch_bounds__(64) void k2_intra_fwd(const T* __restrict__ q, const T* __restrict__ k,
+                                                   const T* __restrict__ v, const float* __restrict__ PZ,
+                                                   const int32_t* __restrict__ labels, const float* __restrict__ c0,
+                                                   const float* __restrict__ lam, const float* __restrict__ gam,
+                                                   int G, int Hq, int Hkv, int N, int NB, float scale,
+                                                   float* __restrict__ num, float* __restrict__ den) {
   constexpr int LD = kD + 8;  // bf16 row stride (bank spread)
   __shared__ __attribute__((aligned(16))) __bf16 qs[kC][LD];
+  __shared__ __attribute__((aligned(16))) __bf16 ks[kC][LD];
   __shared__ __attribute__((aligned(16))) __bf16 vT[kD][LD];
   __shared__ __attribute__((aligned(16))) __bf16 km[kC][LD];  // Mz for the quadratic form, then kappa
+  __shared__ __attribute__((aligned(16))) float pzl[kFP];
   __shared__ float bz[kD];
   __shared__ float denS[kC], denL[kC];
   __shared__ int lab[kD];
@@ -209,17 +287,26 @@ __global__ __launch_bounds__(64) void k2_out_fwd(const T* __restrict__ q, const 
   const int tok0 = ch * kC;
   const size_t qbase = (size_t)(b * Hq + h) * N * kD;
   const size_t kbase = (size_t)u * N * kD;
-  const float* pz = PZ + ((size_t)u * NB + ch) * kFP;
+  const float* pz = pzl;
   const float sc2 = scale * scale;
 
-  // --- stage q and v^T, group tables -----------------------------------------
-  for (int idx = l; idx < kC * kD; idx += 64) {
-    const int j = idx >> 6, d = idx & 63, tok = tok0 + j;
-    const bool ok = tok < N;
-    qs[j][d] = (__bf16)(ok ? ldf(q, qbase + (size_t)tok * kD + d) : 0.f);
-    vT[d][j] = (__bf16)(ok ? ldf(v, kbase + (size_t)tok * kD + d) : 0.f);
-  }
   {
+    const int tok = tok0 + l;
+    const bool ok = tok < N;
+    const int tc = ok ? tok : N - 1;
+    bf16x8 qr[8], kr[8], vr[8];
+    load_row(q, qbase + (size_t)tc * kD, ok, qr);
+    load_row(k, kbase + (size_t)tc * kD, ok, kr);
+    load_row(v, kbase + (size_t)tc * kD, ok, vr);
+    const float4* pzg = reinterpret_cast<const float4*>(PZ + ((size_t)u * NB + ch) * kFP);
+    for (int i = l; i < kFP / 4; i += 64) reinterpret_cast<float4*>(pzl)[i] = pzg[i];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      *reinterpret_cast<bf16x8*>(&qs[l][8 * i]) = qr[i];
+      *reinterpret_cast<bf16x8*>(&ks[l][8 * i]) = kr[i];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) vT[8 * i + j][l] = vr[i][j];
+    }
     int g = labels[h * kD + l];
     lab[l] = g < 0 ? 0 : (g >= G ? G - 1 : g);
     if (l < G) lamh[l] = lam[(size_t)h * G + l];
@@ -267,7 +354,7 @@ __global__ __launch_bounds__(64) void k2_out_fwd(const T* __restrict__ q, const 
   }
   __syncthreads();  // Mz is dead; km now holds kappa
 
-  // --- intra-chunk kappa via group sums (16x16x32 MFMA) ----------------------
+  // --- kappa via group sums (16x16x32 MFMA) -----------------------------------
   {
     const int r16 = l & 15, g16 = l >> 4;
     uint32_t mask[8][2][4];
@@ -289,13 +376,7 @@ __global__ __launch_bounds__(64) void k2_out_fwd(const T* __restrict__ q, const 
         for (int kk = 0; kk < 2; ++kk) {
           typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
           const u32x4 qa = *reinterpret_cast<const u32x4*>(&qs[16 * ti + r16][32 * kk + 8 * g16]);
-          const int tokj = tok0 + 16 * tj + r16;
-          bf16x8 kb;
-          if (tokj < N) {
-            kb = load8(k + kbase + (size_t)tokj * kD + 32 * kk + 8 * g16);
-          } else {
-            kb = bf16x8{};
-          }
+          const bf16x8 kb = *reinterpret_cast<const bf16x8*>(&ks[16 * tj + r16][32 * kk + 8 * g16]);
 #pragma unroll
           for (int g = 0; g < 8; ++g) {
             if (g < G) {
@@ -348,54 +429,113 @@ __global__ __launch_bounds__(64) void k2_out_fwd(const T* __restrict__ q, const 
   }
   __syncthreads();
 
-  // --- state readout -------------------------------------------------------
-  f32x16 acc[2][2];
-  {
-    float qa[kD], qb[kD];
+  // --- num = kappa . V; den = state + intra ------------------------------------
+  const size_t dbase = (size_t)(b * Hq + h) * N;
 #pragma unroll
-    for (int m = 0; m < kD; ++m) {
-      qa[m] = (float)qs[row][(m + 32 * s) & 63];
-      qb[m] = (float)qs[32 + row][(m + 32 * s) & 63];
-    }
+  for (int mt = 0; mt < 2; ++mt) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
-    const uint16_t* pt = PT + ((size_t)u * NB + ch) * ((size_t)kKS * 64 * 16);
-    readout_steps<0>(qa, qb, wqs + (size_t)h * kS, pt, l, acc);
-  }
-  // --- intra term kappa . V --------------------------------------------------
-#pragma unroll
-  for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt)
+    for (int nt = 0; nt < 2; ++nt) {
+      f32x16 acc = f32x16{};
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
         if (kk < 2 * (mt + 1)) {
           const bf16x8 a = *reinterpret_cast<const bf16x8*>(&km[32 * mt + row][16 * kk + 8 * s]);
           const bf16x8 bb = *reinterpret_cast<const bf16x8*>(&vT[32 * nt + row][16 * kk + 8 * s]);
-          acc[mt][nt] = mfma32(a, bb, acc[mt][nt]);
+          acc = mfma32(a, bb, acc);
         }
       }
-  // --- normalize and write (accumulator layout: 32 consecutive columns per row)
-  const size_t dbase = (size_t)(b * Hq + h) * N;
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int j = 32 * mt + c32_row(i, l), tok = tok0 + j;
-      if (tok < N) {
-        const float dd = denS[j] + denL[j];
-        const float inv = 1.f / (floor > 0.f ? fmaxf(dd, floor) : dd);
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
-          const size_t o = qbase + (size_t)tok * kD + 32 * nt + row;
-          num[o] = acc[mt][nt][i];
-          out[o] = from_f<T>(acc[mt][nt][i] * inv);
-        }
-        if (row == 0) den[dbase + tok] = dd;
+      for (int i = 0; i < 16; ++i) {
+        const int j = 32 * mt + c32_row(i, l), tok = tok0 + j;
+        if (tok < N) num[qbase + (size_t)tok * kD + 32 * nt + row] = acc[i];
       }
     }
+  }
+  {
+    const int tok = tok0 + l;
+    if (tok < N) den[dbase + tok] = denS[l] + denL[l];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// State readout: one block of two waves per (query head, chunk, unit); wave w
+// owns tokens 32w..32w+31 (one token per lane row): num += phi_Q(q) . P_c,
+// then out = num / den.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(128) void k2_out_fwd(const T* __restrict__ q, const float* __restrict__ wqs,
+                                                  const uint16_t* __restrict__ PT, int Hq, int Hkv, int N, int NB,
+                                                  float floor, T* __restrict__ out, float* __restrict__ num,
+                                                  const float* __restrict__ den) {
+  __shared__ __attribute__((aligned(16))) __bf16 ring[2 * kRG * kRingStep];
+  __shared__ __attribute__((aligned(16))) float wl[kS];
+
+  const int hh = blockIdx.x, ch = blockIdx.y, u = blockIdx.z;
+  const int R = Hq / Hkv, b = u / Hkv, kh = u % Hkv, h = kh * R + hh;
+  const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, s = l >> 5, row = l & 31;
+  const int tok0 = ch * kC;
+  const size_t qbase = (size_t)(b * Hq + h) * N * kD;
+  const uint16_t* pt = PT + ((size_t)u * NB + ch) * ((size_t)kKS * kRingStep);
+
+  {
+    uint4 reg[kRG];
+    ring_fetch<0>(pt, tid, reg);
+    for (int i = tid; i < kS / 4; i += 128)
+      reinterpret_cast<float4*>(wl)[i] = reinterpret_cast<const float4*>(wqs + (size_t)h * kS)[i];
+    ring_store<0>(ring, tid, reg);
+  }
+  // rotated query row of this lane's token
+  float x[kD];
+  {
+    const int tok = tok0 + 32 * wv + row;
+    const bool ok = tok < N;
+    const int tc = ok ? tok : N - 1;
+    bf16x8 qr[8];
+    load_row(q, qbase + (size_t)tc * kD, ok, qr);
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        // rotation by 32 s: half i of the lane's row is stored at (8 i + 32 s) mod 64
+        const float val = (float)qr[i][j];
+        x[(8 * i + j) & 63] = val;
+      }
+    if (s == 1) {
+#pragma unroll
+      for (int m = 0; m < 32; ++m) {
+        const float t = x[m];
+        x[m] = x[m + 32];
+        x[m + 32] = t;
+      }
+    }
+  }
+  // accumulators start from the intra-chunk numerator
+  f32x16 acc[2];
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int tok = tok0 + 32 * wv + c32_row(i, l);
+      acc[nt][i] = tok < N ? num[qbase + (size_t)tok * kD + 32 * nt + row] : 0.f;
+    }
+  __syncthreads();
+  readout_group<0>(x, wl, ring, pt, tid, l, acc);
+
+  const size_t dbase = (size_t)(b * Hq + h) * N;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int tok = tok0 + 32 * wv + c32_row(i, l);
+    if (tok < N) {
+      const float dd = den[dbase + tok];
+      const float inv = 1.f / (floor > 0.f ? fmaxf(dd, floor) : dd);
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        const size_t o = qbase + (size_t)tok * kD + 32 * nt + row;
+        num[o] = acc[nt][i];
+        out[o] = from_f<T>(acc[nt][i] * inv);
+      }
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -479,10 +619,13 @@ void launch_mfma_forward(const LaunchGeom& g, const void* q, const void* k, cons
   timed("k2_state_fwd", st, [&] {
     hipLaunchKernelGGL(k2_state_fwd<T>, dim3(kS / 32, g.U), dim3(64), 0, st, kt, vt, g.N, g.NB, sv.PT, sv.PR, sv.PZ);
   });
+  timed("k2_intra_fwd", st, [&] {
+    hipLaunchKernelGGL(k2_intra_fwd<T>, dim3(g.R, g.NB, g.U), dim3(64), 0, st, qt, kt, vt, sv.PZ, labels, c0, lam,
+                       gam, groups, g.Hq, g.Hkv, g.N, g.NB, scale, num, den);
+  });
   timed("k2_out_fwd", st, [&] {
-    hipLaunchKernelGGL(k2_out_fwd<T>, dim3(g.R, g.NB, g.U), dim3(64), 0, st, qt, kt, vt, sv.wqs, sv.PT, sv.PZ,
-                       labels, c0, lam, gam, groups, g.Hq, g.Hkv, g.N, g.NB, scale, floor, static_cast<T*>(out), num,
-                       den);
+    hipLaunchKernelGGL(k2_out_fwd<T>, dim3(g.R, g.NB, g.U), dim3(128), 0, st, qt, sv.wqs, sv.PT, g.Hq, g.Hkv, g.N,
+                       g.NB, floor, static_cast<T*>(out), num, den);
   });
 }
 

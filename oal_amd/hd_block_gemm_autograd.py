@@ -4,9 +4,12 @@ Two ``torch.autograd.Function`` classes share the same HIP forward/VJP:
 
 * :class:`_GroupedOALFunction` takes the grouped coefficients (c0, lam, Gam and
   dimension labels) that ``oal_attention`` and the HD adapters derive from the
-  packed factor. Its gradients are (dq, dk, dv, dc0, dlam, dGam), with dGam
-  routed exactly like the reference gather (pair (r, c), r >= c, to
-  Gam[g(r), g(c)]; ``grouped_reference.py:89-93``).
+  packed factor. Its gradients are (dq, dk, dv, dc0, dlam, dGam). Gam is a
+  symmetric matrix parameter: dGam is the gradient of sum_{g,h} Gam_gh s_g s_h,
+  i.e. the reference routing (pair (r, c), r >= c, to Gam[g(r), g(c)];
+  ``grouped_reference.py:89-93``) with each off-diagonal gradient split evenly
+  between [g][h] and [h][g]. Gradients that reach a factor L (Gam = L L^T) are
+  identical under both conventions.
 * :class:`_HDParallelBlockGemmFunction` keeps the reference contract of
   ``oal_attention/hd_block_gemm_autograd.py:85-204``:
   forward(q, k, v, a, b, c, scale, eps, layout, plan) -> (out, num, den) with
@@ -199,7 +202,9 @@ class _HDParallelBlockGemmFunction(torch.autograd.Function):
             dvv[..., :dv] if need_v else None,
             dc0 if need_a else None,
             dlam[:, :d] if need_b else None,
-            dgam[:, rows, cols] if need_c else None,
+            torch.where(rows == cols, dgam[:, rows, cols], dgam[:, rows, cols] + dgam[:, cols, rows])
+            if need_c
+            else None,
         ]
         out = [g.to(dt) if g is not None else None for g, dt in zip(grads, ctx.input_dtypes)]
         return (*out, None, None, None, None)

@@ -443,6 +443,16 @@ def coefficient_gradients_from_wq(
     return dc0, dlam, dgam.view(hq, gmax, gmax)
 
 
+def symmetrize_gamma_gradient(dgam: torch.Tensor) -> torch.Tensor:
+    """Symmetric-Gam convention: off-diagonal [g][h] and [h][g] carry their mean.
+
+    This is the gradient of sum_{g,h} Gam_gh s_g s_h with Gam a symmetric
+    parameter; the reference routing and this one give identical gradients for
+    any symmetric parameterization of Gam (e.g. the factor L L^T).
+    """
+    return 0.5 * (dgam + dgam.transpose(-1, -2))
+
+
 # --------------------------------------------------------------------------
 # Synthetic inputs of the benchmark configurations
 # --------------------------------------------------------------------------
