@@ -708,7 +708,11 @@ void timed(const char* name, hipStream_t st, F&& launch) {
   if (a && b) g_prof_records.push_back({name, a, b});
 }
 
-bool use_mfma(int precision, int groups) { return precision == OAL_PRECISION_BF16 && groups <= 8; }
+// The matrix-core kernels keep up to 8 groups and up to 8 query heads per KV head
+// in registers; other shapes run the fp32 kernels.
+bool use_mfma(int precision, int groups, const Geometry& g) {
+  return precision == OAL_PRECISION_BF16 && groups <= 8 && g.R <= 8;
+}
 
 oal::LaunchGeom launch_geom(const Geometry& g) { return oal::LaunchGeom{g.B, g.Hq, g.Hkv, g.N, g.NB, g.U, g.R}; }
 
@@ -840,7 +844,7 @@ size_t oal_forward_saved_bytes(int batch, int q_heads, int kv_heads, int seq_len
                                int precision) {
   Geometry g;
   if (check_geometry(batch, q_heads, kv_heads, seq_len, dtype, &g) || check_common(groups, precision)) return 0;
-  if (use_mfma(precision, groups)) return oal::mfma_saved_bytes(g.Hq, g.U, g.NB);
+  if (use_mfma(precision, groups, g)) return oal::mfma_saved_bytes(g.Hq, g.U, g.NB);
   return saved_bytes(g);
 }
 
@@ -848,7 +852,7 @@ size_t oal_backward_workspace_bytes(int batch, int q_heads, int kv_heads, int se
                                     int precision) {
   Geometry g;
   if (check_geometry(batch, q_heads, kv_heads, seq_len, dtype, &g) || check_common(groups, precision)) return 0;
-  if (use_mfma(precision, groups)) return oal::mfma_work_view(nullptr, g.B, g.Hq, g.U, g.N, g.NB).bytes;
+  if (use_mfma(precision, groups, g)) return oal::mfma_work_view(nullptr, g.B, g.Hq, g.U, g.N, g.NB).bytes;
   return work_view(g, nullptr).bytes;
 }
 
@@ -862,7 +866,7 @@ int oal_forward(const void* q, const void* k, const void* v, const int32_t* labe
     return fail("oal_forward: null pointer argument");
   if (check_common(groups, precision)) return 1;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (use_mfma(precision, groups)) {
+  if (use_mfma(precision, groups, g)) {
     const oal::LaunchGeom lg = launch_geom(g);
     if (dtype == OAL_DTYPE_F32)
       oal::launch_mfma_forward<float>(lg, q, k, v, labels, c0, lam, gam, groups, scale, floor, out, num, den, saved,
@@ -893,7 +897,7 @@ int oal_backward(const void* q, const void* k, const void* v, const int32_t* lab
     return fail("oal_backward: null pointer argument");
   if (check_common(groups, precision)) return 1;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (use_mfma(precision, groups)) {
+  if (use_mfma(precision, groups, g)) {
     const oal::LaunchGeom lg = launch_geom(g);
     int rc;
     if (dtype == OAL_DTYPE_F32)
