@@ -42,7 +42,7 @@ struct MfmaWork {
   float* dqf;     // [B][Hq][N][64] local dq
   float* dkp;     // [B][Hq][N][64] local dk per query head
   float* dvp;     // [B][Hq][N][64] local dv per query head
-  float* coefl;   // [B][Hq][NB][73] local (dc0, dlam[8], dgam[8][8])
+  float* coefl;   // [Hq][73][B * NB] local (dc0, dlam[8], dgam[8][8]) per chunk
   size_t bytes;
 };
 MfmaWork mfma_work_view(void* base, int B, int Hq, int U, int N, int NB);

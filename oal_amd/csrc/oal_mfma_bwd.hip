@@ -390,7 +390,8 @@ __global__ __launch_bounds__(128) void k2_q_fold(const T* __restrict__ q, const 
   __shared__ __attribute__((aligned(16))) float wl[kS];
   __shared__ float dqs[kC][kD + 1];
 
-  const int hh = blockIdx.x, ch = blockIdx.y, u = blockIdx.z;
+  int hh, ch, u;
+  head_chunk_unit(Hq / Hkv, NB, (int)(gridDim.x / ((Hq / Hkv) * NB)), hh, ch, u);
   const int R = Hq / Hkv, b = u / Hkv, kh = u % Hkv, h = kh * R + hh;
   const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, s = l >> 5, row = l & 31;
   const int tok0 = ch * kC;
@@ -617,7 +618,8 @@ __global__ __launch_bounds__(256) void k2_local_bwd(const T* __restrict__ q, con
   __shared__ float cpart[4][1 + 8 + 64];
   static_assert(sizeof(TT) >= kFP * sizeof(float), "pz staging must fit the transpose buffer");
 
-  const int hh = blockIdx.x, ch = blockIdx.y, u = blockIdx.z;
+  int hh, ch, u;
+  head_chunk_unit(Hq / Hkv, NB, (int)(gridDim.x / ((Hq / Hkv) * NB)), hh, ch, u);
   const int R = Hq / Hkv, b = u / Hkv, kh = u % Hkv, h = kh * R + hh;
   const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63;
   const int r16 = l & 15, g16 = l >> 4;
@@ -779,7 +781,10 @@ __global__ __launch_bounds__(256) void k2_local_bwd(const T* __restrict__ q, con
   }
   __syncthreads();
   if (tid < 73) {
-    coefl[(((size_t)(b * Hq + h)) * NB + ch) * 73 + tid] =
+    // column-major partials [Hq][73][B * NB] so that the final reduction reads
+    // each column contiguously
+    const size_t bn = (size_t)(gridDim.x / ((Hq / Hkv) * NB) / Hkv) * NB;
+    coefl[((size_t)h * 73 + tid) * bn + (size_t)b * NB + ch] =
         (cpart[0][tid] + cpart[1][tid]) + (cpart[2][tid] + cpart[3][tid]);
   }
   // K^T into TT
@@ -914,64 +919,75 @@ __global__ __launch_bounds__(256) void k2_local_bwd(const T* __restrict__ q, con
 }
 
 // ---------------------------------------------------------------------------
-// Coefficient gradients, one block per query head.
+// Coefficient gradients, one block per query head, every sum in a fixed order.
+// State part: the per-slot gradients (summed over the batch) are laid out in
+// natural feature order wn[f]; dc0 = wn[0], dlam[g] = scale sum_{g(d)=g} wn[1+d],
+// and the pair part routes pair (r >= c) to [g(r)][g(c)] through
+// X[r][g] = sum_{c <= r, g(c) = g} m_rc wn[pair(r, c)], raw = E^T X with E the
+// one-hot label matrix. Local part: column sums of the per-chunk partials.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void k2_coef_grad(const float* __restrict__ dwqs, const float* __restrict__ coefl,
                                                     const int32_t* __restrict__ labels, int B, int Hq, int NB, int G,
                                                     float scale, float* __restrict__ dc0, float* __restrict__ dlam,
                                                     float* __restrict__ dgam) {
-  __shared__ float w[kS];
+  __shared__ float wn[kFeat];
   __shared__ float loc[73];
+  __shared__ float xr[kD][9];
   __shared__ float raw[64];
   __shared__ int lab[kD];
-  const int h = blockIdx.x, t = threadIdx.x;
+  const int h = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
   if (t < kD) {
     int g = labels[h * kD + t];
     lab[t] = g < 0 ? 0 : (g >= G ? G - 1 : g);
   }
   for (int sl = t; sl < kS; sl += 256) {
-    float acc = 0.f;
-    for (int b = 0; b < B; ++b) acc += dwqs[((size_t)b * Hq + h) * kS + sl];
-    w[sl] = acc;
+    const int n = kSlot.nat[sl];
+    if (n >= 0) {
+      float acc = 0.f;
+      for (int b = 0; b < B; ++b) acc += dwqs[((size_t)b * Hq + h) * kS + sl];
+      wn[n] = acc;
+    }
   }
-  if (t < 73) {
+  const int bn = B * NB;
+  for (int j = wave; j < 73; j += 4) {
+    const float* col = coefl + ((size_t)h * 73 + j) * bn;
     float acc = 0.f;
-    for (int b = 0; b < B; ++b)
-      for (int ch = 0; ch < NB; ++ch) acc += coefl[(((size_t)b * Hq + h) * NB + ch) * 73 + t];
-    loc[t] = acc;
+    for (int r = lane; r < bn; r += 64) acc += col[r];
+    acc = wave_sum(acc);
+    if (lane == 0) loc[j] = acc;
   }
   __syncthreads();
-  if (t == 0) {
-    float a = loc[0];
-    for (int sl = 0; sl < kS; ++sl)
-      if (kSlot.nat[sl] == 0) a += w[sl];
-    dc0[h] = a;
-  }
-  for (int g = t; g < G; g += 256) {
+  for (int e = t; e < kD * 8; e += 256) {
+    const int r = e >> 3, g = e & 7;
     float acc = 0.f;
-    for (int sl = 0; sl < kS; ++sl) {
-      const int n = kSlot.nat[sl];
-      if (n >= 1 && n <= kD && lab[n - 1] == g) acc += w[sl];
+    if (g < G) {
+      const float* row = wn + 1 + kD + pair_index(r, 0);
+      for (int c = 0; c <= r; ++c)
+        if (lab[c] == g) acc += (c == r ? 1.f : 2.f) * row[c];
     }
+    xr[r][g] = acc;
+  }
+  __syncthreads();
+  if (t < G * G) {
+    const int gr = t / G, gc = t % G;
+    float acc = 0.f;
+    for (int r = 0; r < kD; ++r)
+      if (lab[r] == gr) acc += xr[r][gc];
+    raw[t] = acc * scale * scale;
+  }
+  if (t == 64) dc0[h] = wn[0] + loc[0];
+  if (t >= 128 && t < 128 + G) {
+    const int g = t - 128;
+    float acc = 0.f;
+    for (int d = 0; d < kD; ++d)
+      if (lab[d] == g) acc += wn[1 + d];
     dlam[(size_t)h * G + g] = acc * scale + loc[1 + g];
   }
-  // exact routing of the state part, [g(r)][g(c)] for pair (r >= c)
-  for (int e = t; e < G * G; e += 256) {
-    const int gr = e / G, gc = e % G;
-    float acc = 0.f;
-    for (int sl = 0; sl < kS; ++sl) {
-      const int n = kSlot.nat[sl];
-      if (n <= kD) continue;
-      const int r = kSlot.ar[sl], c = kSlot.ac[sl];
-      if (lab[r] == gr && lab[c] == gc) acc += (r == c ? 1.f : 2.f) * w[sl];
-    }
-    raw[e] = acc * scale * scale;
-  }
   __syncthreads();
-  for (int e = t; e < G * G; e += 256) {
-    const int gr = e / G, gc = e % G;
-    const float sym = gr == gc ? raw[e] : 0.5f * (raw[e] + raw[gc * G + gr]);
-    dgam[(size_t)h * G * G + e] = sym + loc[9 + 8 * gr + gc];
+  if (t < G * G) {
+    const int gr = t / G, gc = t % G;
+    const float sym = gr == gc ? raw[t] : 0.5f * (raw[t] + raw[gc * G + gr]);
+    dgam[(size_t)h * G * G + t] = sym + loc[9 + 8 * gr + gc];
   }
 }
 
@@ -1024,12 +1040,12 @@ int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, cons
                        g.Hq, g.Hkv, g.N, g.NB, w.dTT, w.dTR, w.dTz, w.dwqs);
   });
   timed("k2_local_bwd", st, [&] {
-    hipLaunchKernelGGL(k2_local_bwd<T>, dim3(g.R, g.NB, g.U), dim3(256), 0, st, qt, kt, vt, w.G16, w.Gz, sv.PZ,
+    hipLaunchKernelGGL(k2_local_bwd<T>, dim3(g.R * g.NB * g.U), dim3(256), 0, st, qt, kt, vt, w.G16, w.Gz, sv.PZ,
                        labels, c0, lam, gam, groups, g.Hq, g.Hkv, g.N, g.NB, scale, w.dqf, w.dkp, w.dvp, w.coefl);
   });
   if (dq) {
     timed("k2_q_fold", st, [&] {
-      hipLaunchKernelGGL(k2_q_fold<T>, dim3(g.R, g.NB, g.U), dim3(128), 0, st, qt, w.G16, sv.wqs, sv.PR, w.dqf,
+      hipLaunchKernelGGL(k2_q_fold<T>, dim3(g.R * g.NB * g.U), dim3(128), 0, st, qt, w.G16, sv.wqs, sv.PR, w.dqf,
                          g.Hq, g.Hkv, g.N, g.NB, static_cast<T*>(dq));
     });
   }

@@ -184,3 +184,22 @@ __device__ __forceinline__ bf16x8 raw_fragment(const float (&x)[kD]) {
 __device__ __forceinline__ float bf16_to_f(uint16_t x) { return __uint_as_float(uint32_t(x) << 16); }
 
 }  // namespace oal
+
+namespace oal {
+
+// Work item of a 1-D grid over (query head in group, chunk, unit), ordered so
+// that the query heads of one (chunk, unit) run on one XCD and share its L2:
+// workgroups are dispatched round-robin over the 8 XCDs, so workgroup id goes
+// to XCD id % 8; item w = (id % 8) * (total / 8) + id / 8 gives each XCD a
+// contiguous range of items (head fastest). Falls back to w = id when the
+// item count is not a multiple of 8.
+__device__ __forceinline__ void head_chunk_unit(int R, int NB, int U, int& hh, int& ch, int& u) {
+  const int total = R * NB * U;
+  const int id = blockIdx.x;
+  const int w = (total & 7) == 0 ? (id & 7) * (total >> 3) + (id >> 3) : id;
+  hh = w % R;
+  ch = (w / R) % NB;
+  u = w / (R * NB);
+}
+
+}  // namespace oal

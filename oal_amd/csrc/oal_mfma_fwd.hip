@@ -281,7 +281,8 @@ __global__ __launch_bounds__(64) void k2_intra_fwd(const T* __restrict__ q, cons
   __shared__ int lab[kD];
   __shared__ float lamh[8], gamh[64];
 
-  const int hh = blockIdx.x, ch = blockIdx.y, u = blockIdx.z;
+  int hh, ch, u;
+  head_chunk_unit(Hq / Hkv, NB, (int)(gridDim.x / ((Hq / Hkv) * NB)), hh, ch, u);
   const int R = Hq / Hkv, b = u / Hkv, kh = u % Hkv, h = kh * R + hh;
   const int l = threadIdx.x, s = l >> 5, row = l & 31;
   const int tok0 = ch * kC;
@@ -470,7 +471,8 @@ __global__ __launch_bounds__(128) void k2_out_fwd(const T* __restrict__ q, const
   __shared__ __attribute__((aligned(16))) __bf16 ring[2 * kRG * kRingStep];
   __shared__ __attribute__((aligned(16))) float wl[kS];
 
-  const int hh = blockIdx.x, ch = blockIdx.y, u = blockIdx.z;
+  int hh, ch, u;
+  head_chunk_unit(Hq / Hkv, NB, (int)(gridDim.x / ((Hq / Hkv) * NB)), hh, ch, u);
   const int R = Hq / Hkv, b = u / Hkv, kh = u % Hkv, h = kh * R + hh;
   const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, s = l >> 5, row = l & 31;
   const int tok0 = ch * kC;
@@ -620,11 +622,11 @@ void launch_mfma_forward(const LaunchGeom& g, const void* q, const void* k, cons
     hipLaunchKernelGGL(k2_state_fwd<T>, dim3(kS / 32, g.U), dim3(64), 0, st, kt, vt, g.N, g.NB, sv.PT, sv.PR, sv.PZ);
   });
   timed("k2_intra_fwd", st, [&] {
-    hipLaunchKernelGGL(k2_intra_fwd<T>, dim3(g.R, g.NB, g.U), dim3(64), 0, st, qt, kt, vt, sv.PZ, labels, c0, lam,
+    hipLaunchKernelGGL(k2_intra_fwd<T>, dim3(g.R * g.NB * g.U), dim3(64), 0, st, qt, kt, vt, sv.PZ, labels, c0, lam,
                        gam, groups, g.Hq, g.Hkv, g.N, g.NB, scale, num, den);
   });
   timed("k2_out_fwd", st, [&] {
-    hipLaunchKernelGGL(k2_out_fwd<T>, dim3(g.R, g.NB, g.U), dim3(128), 0, st, qt, sv.wqs, sv.PT, g.Hq, g.Hkv, g.N,
+    hipLaunchKernelGGL(k2_out_fwd<T>, dim3(g.R * g.NB * g.U), dim3(128), 0, st, qt, sv.wqs, sv.PT, g.Hq, g.Hkv, g.N,
                        g.NB, floor, static_cast<T*>(out), num, den);
   });
 }
