@@ -161,6 +161,11 @@ def main() -> int:
     ap.add_argument("--batch", type=int, default=4)
     ap.add_argument("--seq-len", type=int, default=4096)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument(
+        "--copy-calibration-mib", type=int, default=0,
+        help="first run one plain device copy of this many MiB (reads and writes that many bytes), "
+             "the reference point that scales rocprofv3 FETCH_SIZE / WRITE_SIZE counters to bytes",
+    )
     args = ap.parse_args()
     if args.gpus != 1:
         print(
@@ -174,6 +179,13 @@ def main() -> int:
 
     dev = torch.device("cuda:0")
     b, n = args.batch, args.seq_len
+    if args.copy_calibration_mib > 0:
+        nbytes = args.copy_calibration_mib << 20
+        src = torch.ones(nbytes // 4, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     inp = make_inputs(b, n, dev)
     for _ in range(args.warmup):
         step(inp)

@@ -83,6 +83,20 @@ def load_library(path: str | None = None) -> ctypes.CDLL:
         return lib
 
 
+def load_hd_cublas_compat(manifest_path=None, runtime_probe_path=None, device=None, *, identity_policy=None):
+    """Setup hook with the signature of the reference's bf16 loader
+    (``oal_attention/hd_cublas_compat.py:688-799``): loads liboal_amd.so and
+    checks that ``device`` is a ROCm device. The manifest and probe paths of
+    the cuBLAS artifact have no meaning here and are ignored.
+    """
+    lib = load_library()
+    if device is not None:
+        dev = torch.device(device)
+        if dev.type != "cuda" or torch.version.hip is None:
+            raise RuntimeError("oal_amd runs only on a ROCm (HIP) device; got " + str(dev))
+    return lib
+
+
 def _check(rc: int, lib: ctypes.CDLL, what: str) -> None:
     if rc != 0:
         msg = lib.oal_last_error().decode("utf-8", "replace")

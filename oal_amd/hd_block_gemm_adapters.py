@@ -60,6 +60,16 @@ def _resolve_scale(scale: float | None, head_dimension: int) -> float:
     return resolved
 
 
+def kernel_precision(plan_precision: str) -> str:
+    """Planner precision -> kernel arithmetic.
+
+    ``bf16_tensorcore`` (bf16 operands, fp32 accumulation on the matrix cores;
+    reference ``hd_block_gemm.py:132-153``) runs the gfx950 MFMA kernels;
+    ``fp32_ieee`` runs the fp32 kernels.
+    """
+    return "bf16" if plan_precision == "bf16_tensorcore" else "fp32"
+
+
 def _expand_factor_coefficients_tensorcore(factor, *, query_heads: int, gmax: int, kernel_eps: float):
     """FP32 pointwise PSD expansion (hd_block_gemm_adapters.py:57-95)."""
     return _expand_factor_coefficients(
@@ -137,7 +147,8 @@ def run_prepared_grouped_hd_block_gemm(prepared, q, k, v, factor):
         factor, query_heads=plan.query_heads, gmax=prepared.gmax, kernel_eps=prepared.kernel_eps
     )
     out, num, den = grouped_oal(
-        q, k, v, prepared.groups, a, lam, gam, scale=prepared.scale, floor=prepared.normalization_floor
+        q, k, v, prepared.groups, a, lam, gam, scale=prepared.scale, floor=prepared.normalization_floor,
+        precision=kernel_precision(plan.precision),
     )
     if plan.require_positive_denominator:
         _require_positive_denominator(den)
