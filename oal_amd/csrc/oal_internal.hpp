@@ -17,11 +17,22 @@ struct LaunchGeom {
 // Runs `launch`, bracketed by HIP events on `stream` when profiling is on.
 using Timer = std::function<void(const char*, hipStream_t, const std::function<void()>&)>;
 
+// Per-head coefficient pack of the intra-chunk kernels: c0, scale * lam[g]
+// (g < 8, zero padded), scale^2 * Gam[g][h] (8 x 8, zero padded).
+constexpr int kIC = 80;
+constexpr int kIcLam = 1;
+constexpr int kIcGam = 9;
+
 struct MfmaSaved {
   float* wqs;     // [Hq][kS] slot coefficients
+  float* ic;      // [Hq][kIC] intra-chunk coefficient pack
+  float* gm;      // [Hq][64][64] scale^2 Gam[g(r)][g(c)]
+  float* lb;      // [Hq][64] scale lam[g(d)]
   uint16_t* PT;   // [U][NB][kKS][64][16] bf16
   uint16_t* PR;   // [U][NB][kS/32][4][32][16] bf16
   float* PZ;      // [U][NB][kFP] denominator column, natural order
+  float* PZm;     // [U][NB][64][64] denominator column as a symmetric pair matrix
+  size_t bytes;
 };
 
 size_t mfma_saved_bytes(int Hq, int U, int NB);

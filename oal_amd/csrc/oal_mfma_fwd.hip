@@ -24,30 +24,55 @@ namespace oal {
 
 static __constant__ SlotTable kSlot = make_slot_table();
 
-// Per-head slot coefficients: wq of natural feature nat(slot), 0 for invalid slots.
+// Per-head coefficients, one block per query head:
+//   wqs[h][slot]  wq of natural feature nat(slot) (0 for invalid slots);
+//   ic[h]         c0, scale*lam[g], scale^2*Gam[g][g'] padded to 8 groups;
+//   gm[h][r][c]   scale^2 * Gam[g(r)][g(c)]  (denominator quadratic form);
+//   lb[h][d]      scale * lam[g(d)].
 __global__ __launch_bounds__(256) void k2_slot_coefficients(const int32_t* __restrict__ labels,
                                                             const float* __restrict__ c0,
                                                             const float* __restrict__ lam,
                                                             const float* __restrict__ gam, int G, float scale,
-                                                            float* __restrict__ wqs) {
-  const int h = blockIdx.x;
-  auto label = [&](int d) {
-    int g = labels[h * kD + d];
-    return g < 0 ? 0 : (g >= G ? G - 1 : g);
-  };
-  for (int s = threadIdx.x; s < kS; s += blockDim.x) {
+                                                            float* __restrict__ wqs, float* __restrict__ ic,
+                                                            float* __restrict__ gm, float* __restrict__ lb) {
+  __shared__ int lab[kD];
+  const int h = blockIdx.x, t = threadIdx.x;
+  if (t < kD) {
+    const int g = labels[h * kD + t];
+    lab[t] = g < 0 ? 0 : (g >= G ? G - 1 : g);
+  }
+  __syncthreads();
+  for (int s = t; s < kS; s += blockDim.x) {
     const int n = kSlot.nat[s];
     const int r = kSlot.ar[s], c = kSlot.ac[s];
     float w = 0.f;
     if (n == 0) {
       w = c0[h];
     } else if (n > 0 && n <= kD) {
-      w = scale * lam[(size_t)h * G + label(r)];
+      w = scale * lam[(size_t)h * G + lab[r]];
     } else if (n > kD) {
-      w = (r == c ? 1.f : 2.f) * scale * scale * gam[((size_t)h * G + label(r)) * G + label(c)];
+      w = (r == c ? 1.f : 2.f) * scale * scale * gam[((size_t)h * G + lab[r]) * G + lab[c]];
     }
     wqs[(size_t)h * kS + s] = w;
   }
+  if (t < kIC) {
+    float x = 0.f;
+    if (t == 0) {
+      x = c0[h];
+    } else if (t < kIcGam) {
+      const int g = t - kIcLam;
+      x = g < G ? scale * lam[(size_t)h * G + g] : 0.f;
+    } else if (t < kIcGam + 64) {
+      const int g = (t - kIcGam) >> 3, g2 = (t - kIcGam) & 7;
+      x = (g < G && g2 < G) ? scale * scale * gam[((size_t)h * G + g) * G + g2] : 0.f;
+    }
+    ic[(size_t)h * kIC + t] = x;
+  }
+  for (int e = t; e < kD * kD; e += blockDim.x) {
+    const int r = e >> 6, c = e & 63;
+    gm[(size_t)h * kD * kD + e] = scale * scale * gam[((size_t)h * G + lab[r]) * G + lab[c]];
+  }
+  if (t < kD) lb[(size_t)h * kD + t] = scale * lam[(size_t)h * G + lab[t]];
 }
 
 template <typename T>
@@ -85,7 +110,7 @@ __device__ __forceinline__ void load_row(const float* __restrict__ src, size_t r
 template <typename T>
 __global__ __launch_bounds__(64) void k2_state_fwd(const T* __restrict__ k, const T* __restrict__ v, int N, int NB,
                                                    uint16_t* __restrict__ PT, uint16_t* __restrict__ PR,
-                                                   float* __restrict__ PZ) {
+                                                   float* __restrict__ PZ, float* __restrict__ PZm) {
   __shared__ float kT[kRow][kC + 4];                               // kT[d][tok]; row 64 = valid, 65 = 0
   __shared__ __attribute__((aligned(16))) __bf16 vT[96][kC + 8];  // vT[e][tok]; row 64 = valid
   __shared__ float stage[32][97];
@@ -159,7 +184,15 @@ __global__ __launch_bounds__(64) void k2_state_fwd(const T* __restrict__ k, cons
       }
       if (s == 0) {
         const int n = kSlot.nat[slot];
-        if (n >= 0) PZ[((size_t)u * NB + ch) * kFP + n] = stage[row][64];
+        if (n >= 0) {
+          const float z = stage[row][64];
+          PZ[((size_t)u * NB + ch) * kFP + n] = z;
+          if (n > kD) {
+            float* pm = PZm + ((size_t)u * NB + ch) * kD * kD;
+            pm[ar * kD + ac] = z;
+            pm[ac * kD + ar] = z;
+          }
+        }
       }
     }
     // 2. prefetch chunk c + 1 into registers
@@ -257,204 +290,222 @@ __device__ __forceinline__ void readout_group(const float (&x)[kD], const float*
   }
 }
 
+// 16 consecutive elements of a row as two bf16 fragments (16-byte loads).
+__device__ __forceinline__ void load16(const uint16_t* __restrict__ src, size_t off, bool ok, bf16x8 (&r)[2]) {
+  const bf16x8* p = reinterpret_cast<const bf16x8*>(src + off);
+  const bf16x8 a = p[0], b = p[1];
+  r[0] = ok ? a : bf16x8{};
+  r[1] = ok ? b : bf16x8{};
+}
+__device__ __forceinline__ void load16(const float* __restrict__ src, size_t off, bool ok, bf16x8 (&r)[2]) {
+  const float4* p = reinterpret_cast<const float4*>(src + off);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const float4 a = p[2 * i], b = p[2 * i + 1];
+    float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    const bf16x8 y = pack8(x);
+    r[i] = ok ? y : bf16x8{};
+  }
+}
+
 // ---------------------------------------------------------------------------
-// Intra-chunk part of the forward, one wave per (query head, chunk, unit):
-// den = az + q.(bz + Mz q) (state term of the denominator as a quadratic form)
-//       + sum_j kappa(i, j);  num = kappa . V.  Written to num / den, which the
-// readout kernel then completes.
+// Intra-chunk forward, one block of 4 waves per (query head, chunk, unit).
+// Waves 0-2 each own one lower 32x32 tile of kappa^T (rows j = key token,
+// columns i = query token), (j-tile, i-tile) = (0,0), (0,1), (1,1):
+//   s_g^T = (K o mask_g) Q^T on v_mfma_f32_32x32x16_bf16 (8 groups x 4 k-steps),
+//   kappa = c0 + sum_g s_g (lam'_g + Gam'_gg s_g + 2 sum_{h>g} Gam'_gh s_h)
+// (lam' = scale lam, Gam' = scale^2 Gam, padded to 8 groups with zeros), then
+// num^T = V^T kappa^T with kappa^T handed to the MFMA straight from the
+// accumulators, and the denominator row sums. Wave 3 evaluates the state part
+// of the denominator as the quadratic form az + q . (bz + Mz q), Mz = gm o PZm.
+// Writes the intra part of num and the full den; k2_out_fwd adds the readout.
 // ---------------------------------------------------------------------------
 template <typename T>
-__global__ __launch_bounds__(64) void k2_intra_fwd(const T* __restrict__ q, const T* __restrict__ k,
-                                                   const T* __restrict__ v, const float* __restrict__ PZ,
-                                                   const int32_t* __restrict__ labels, const float* __restrict__ c0,
-                                                   const float* __restrict__ lam, const float* __restrict__ gam,
-                                                   int G, int Hq, int Hkv, int N, int NB, float scale,
-                                                   float* __restrict__ num, float* __restrict__ den) {
+__global__ __launch_bounds__(256) void k2_intra_fwd(const T* __restrict__ q, const T* __restrict__ k,
+                                                    const T* __restrict__ v, const float* __restrict__ PZ,
+                                                    const float* __restrict__ PZm, const int32_t* __restrict__ labels,
+                                                    const float* __restrict__ ic, const float* __restrict__ gm,
+                                                    const float* __restrict__ lb, int G, int Hq, int Hkv, int N,
+                                                    int NB, float* __restrict__ num, float* __restrict__ den) {
   constexpr int LD = kD + 8;  // bf16 row stride (bank spread)
-  __shared__ __attribute__((aligned(16))) __bf16 qs[kC][LD];
-  __shared__ __attribute__((aligned(16))) __bf16 ks[kC][LD];
-  __shared__ __attribute__((aligned(16))) __bf16 vT[kD][LD];
-  __shared__ __attribute__((aligned(16))) __bf16 km[kC][LD];  // Mz for the quadratic form, then kappa
-  __shared__ __attribute__((aligned(16))) float pzl[kFP];
-  __shared__ float bz[kD];
-  __shared__ float denS[kC], denL[kC];
-  __shared__ int lab[kD];
-  __shared__ float lamh[8], gamh[64];
+  __shared__ __attribute__((aligned(16))) __bf16 Qs[kC][LD];
+  __shared__ __attribute__((aligned(16))) __bf16 Ks[kC][LD];
+  __shared__ __attribute__((aligned(16))) __bf16 VT[kD][LD];
+  __shared__ __attribute__((aligned(16))) __bf16 Mz[kD][LD];
+  __shared__ __attribute__((aligned(16))) uint32_t mk[4][8][2][4];
+  __shared__ float red[2][16][64];
+  __shared__ float bz[kD], dsS[kC], dp2[32];
 
   int hh, ch, u;
   head_chunk_unit(Hq / Hkv, NB, (int)(gridDim.x / ((Hq / Hkv) * NB)), hh, ch, u);
   const int R = Hq / Hkv, b = u / Hkv, kh = u % Hkv, h = kh * R + hh;
-  const int l = threadIdx.x, s = l >> 5, row = l & 31;
+  const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, s = l >> 5, row = l & 31;
   const int tok0 = ch * kC;
   const size_t qbase = (size_t)(b * Hq + h) * N * kD;
   const size_t kbase = (size_t)u * N * kD;
-  const float* pz = pzl;
-  const float sc2 = scale * scale;
+  const size_t cbase = (size_t)u * NB + ch;
+  const float* cf = ic + (size_t)h * kIC;
 
+  // --- staging ------------------------------------------------------------
   {
-    const int tok = tok0 + l;
+    const int r = tid >> 2, qq = tid & 3;
+    const int tok = tok0 + r;
     const bool ok = tok < N;
-    const int tc = ok ? tok : N - 1;
-    bf16x8 qr[8], kr[8], vr[8];
-    load_row(q, qbase + (size_t)tc * kD, ok, qr);
-    load_row(k, kbase + (size_t)tc * kD, ok, kr);
-    load_row(v, kbase + (size_t)tc * kD, ok, vr);
-    const float4* pzg = reinterpret_cast<const float4*>(PZ + ((size_t)u * NB + ch) * kFP);
-    for (int i = l; i < kFP / 4; i += 64) reinterpret_cast<float4*>(pzl)[i] = pzg[i];
+    const size_t roff = (size_t)(ok ? tok : N - 1) * kD + 16 * qq;
+    bf16x8 x[2];
+    load16(q, qbase + roff, ok, x);
+    *reinterpret_cast<bf16x8*>(&Qs[r][16 * qq]) = x[0];
+    *reinterpret_cast<bf16x8*>(&Qs[r][16 * qq + 8]) = x[1];
+    load16(k, kbase + roff, ok, x);
+    *reinterpret_cast<bf16x8*>(&Ks[r][16 * qq]) = x[0];
+    *reinterpret_cast<bf16x8*>(&Ks[r][16 * qq + 8]) = x[1];
+    load16(v, kbase + roff, ok, x);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      *reinterpret_cast<bf16x8*>(&qs[l][8 * i]) = qr[i];
-      *reinterpret_cast<bf16x8*>(&ks[l][8 * i]) = kr[i];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) vT[8 * i + j][l] = vr[i][j];
+    for (int e = 0; e < 8; ++e) {
+      VT[16 * qq + e][r] = x[0][e];
+      VT[16 * qq + 8 + e][r] = x[1][e];
     }
-    int g = labels[h * kD + l];
-    lab[l] = g < 0 ? 0 : (g >= G ? G - 1 : g);
-    if (l < G) lamh[l] = lam[(size_t)h * G + l];
-    if (l < G * G) gamh[l] = gam[(size_t)h * G * G + l];
-    denL[l] = 0.f;
+    // Mz[r][c] = gm[h][r][c] * PZm[r][c], c = 16 qq .. 16 qq + 15
+    const float4* gp = reinterpret_cast<const float4*>(gm + ((size_t)h * kD + r) * kD + 16 * qq);
+    const float4* zp = reinterpret_cast<const float4*>(PZm + (cbase * kD + r) * kD + 16 * qq);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const float4 g0 = gp[2 * i], g1 = gp[2 * i + 1], z0 = zp[2 * i], z1 = zp[2 * i + 1];
+      float y[8] = {g0.x * z0.x, g0.y * z0.y, g0.z * z0.z, g0.w * z0.w,
+                    g1.x * z1.x, g1.y * z1.y, g1.z * z1.z, g1.w * z1.w};
+      *reinterpret_cast<bf16x8*>(&Mz[r][16 * qq + 8 * i]) = pack8(y);
+    }
+    // group masks: entry (kk, g, ss, w) covers dims d, d + 1 with d = 16 kk + 8 ss + 2 w
+    {
+      const int kk = tid >> 6, g = (tid >> 3) & 7, ss = (tid >> 2) & 1, w = tid & 3;
+      const int d = 16 * kk + 8 * ss + 2 * w;
+      int g0 = labels[h * kD + d], g1 = labels[h * kD + d + 1];
+      g0 = g0 < 0 ? 0 : (g0 >= G ? G - 1 : g0);
+      g1 = g1 < 0 ? 0 : (g1 >= G ? G - 1 : g1);
+      mk[kk][g][ss][w] = (g0 == g ? 0x0000ffffu : 0u) | (g1 == g ? 0xffff0000u : 0u);
+    }
+    if (tid < kD) bz[tid] = lb[(size_t)h * kD + tid] * PZ[cbase * kFP + 1 + tid];
   }
-  __syncthreads();
-  const float c0h = c0[h];
-  for (int idx = l; idx < kD * kD; idx += 64) {
-    const int r = idx >> 6, c = idx & 63;
-    const int hi = r > c ? r : c, lo = r > c ? c : r;
-    km[r][c] = (__bf16)(sc2 * gamh[lab[r] * G + lab[c]] * pz[1 + kD + pair_index(hi, lo)]);
-  }
-  bz[l] = scale * lamh[lab[l]] * pz[1 + l];
-  const float az = c0h * pz[0];
   __syncthreads();
 
-  // --- denominator state term: den_i = az + q_i . (bz + Mz q_i) -------------
-  {
-    float part[2] = {0.f, 0.f};
+  f32x16 acc[2] = {f32x16{}, f32x16{}};
+  float dsum = 0.f;
+  if (wv < 3) {
+    const int tj = wv == 2 ? 1 : 0, ti = wv == 0 ? 0 : 1;
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    f32x16 sg[8];
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
+    for (int g = 0; g < 8; ++g) sg[g] = f32x16{};
 #pragma unroll
-      for (int md = 0; md < 2; ++md) {
+    for (int kk = 0; kk < 4; ++kk) {
+      const u32x4 kf = *reinterpret_cast<const u32x4*>(&Ks[32 * tj + row][16 * kk + 8 * s]);
+      const bf16x8 qf = *reinterpret_cast<const bf16x8*>(&Qs[32 * ti + row][16 * kk + 8 * s]);
+#pragma unroll
+      for (int g = 0; g < 8; ++g) {
+        const u32x4 m = *reinterpret_cast<const u32x4*>(&mk[kk][g][s][0]);
+        sg[g] = mfma32(__builtin_bit_cast(bf16x8, kf & m), qf, sg[g]);
+      }
+    }
+    float lamc[8], gd[8], g2[8][8];
+    const float c0h = cf[0];
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+      lamc[g] = cf[kIcLam + g];
+      gd[g] = cf[kIcGam + 9 * g];
+#pragma unroll
+      for (int h2 = 0; h2 < 8; ++h2) g2[g][h2] = 2.f * cf[kIcGam + 8 * g + h2];
+    }
+    const int i = 32 * ti + row;
+    const bool irow = tok0 + i < N;
+    float kap[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int j = 32 * tj + c32_row(r, l);
+      float kv = c0h;
+#pragma unroll
+      for (int g = 0; g < 8; ++g) {
+        float inner = fmaf(gd[g], sg[g][r], lamc[g]);
+#pragma unroll
+        for (int h2 = g + 1; h2 < 8; ++h2) inner = fmaf(g2[g][h2], sg[h2][r], inner);
+        kv = fmaf(sg[g][r], inner, kv);
+      }
+      kap[r] = (j <= i && irow) ? kv : 0.f;
+      dsum += kap[r];
+    }
+    dsum += __shfl_xor(dsum, 32, 64);
+    // kappa^T as the B operand of num^T = V^T kappa^T: k-step t covers
+    // j = 16 t .. 16 t + 15; lane group s must hold j = 16 t + 8 s .. + 7, the
+    // accumulators give it j = 16 t + 4 s + (0..3) and 16 t + 8 + 4 s + (0..3).
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const uint32_t a0 = pack_bf16x2(kap[8 * t + 0], kap[8 * t + 1]);
+      const uint32_t a1 = pack_bf16x2(kap[8 * t + 2], kap[8 * t + 3]);
+      const uint32_t b0 = pack_bf16x2(kap[8 * t + 4], kap[8 * t + 5]);
+      const uint32_t b1 = pack_bf16x2(kap[8 * t + 6], kap[8 * t + 7]);
+      const uint32_t r0 = __shfl_xor(s ? a0 : b0, 32, 64);
+      const uint32_t r1 = __shfl_xor(s ? a1 : b1, 32, 64);
+      const u32x4 fr = s ? u32x4{r0, r1, b0, b1} : u32x4{a0, a1, r0, r1};
+      const bf16x8 bfr = __builtin_bit_cast(bf16x8, fr);
+#pragma unroll
+      for (int et = 0; et < 2; ++et) {
+        const bf16x8 af = *reinterpret_cast<const bf16x8*>(&VT[32 * et + row][32 * tj + 16 * t + 8 * s]);
+        acc[et] = mfma32(af, bfr, acc[et]);
+      }
+    }
+    if (wv == 2) {
+#pragma unroll
+      for (int et = 0; et < 2; ++et)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) red[et][r][l] = acc[et][r];
+      if (s == 0) dp2[row] = dsum;
+    }
+  } else {
+    // state part of the denominator: Z[d][i] = (Mz Q^T)[d][i]
+    const float az = cf[0] * PZ[cbase * kFP];
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+      float part = 0.f;
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt) {
         f32x16 z = f32x16{};
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
-          const bf16x8 a = *reinterpret_cast<const bf16x8*>(&km[32 * md + row][16 * kk + 8 * s]);
-          const bf16x8 bb = *reinterpret_cast<const bf16x8*>(&qs[32 * nt + row][16 * kk + 8 * s]);
-          z = mfma32(a, bb, z);
-        }
-        const int tok = 32 * nt + row;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int d = 32 * md + c32_row(i, l);
-          part[nt] += (float)qs[tok][d] * (z[i] + bz[d]);
-        }
-      }
-    }
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      const float tot = part[nt] + __shfl_xor(part[nt], 32, 64);
-      if (s == 0) denS[32 * nt + row] = az + tot;
-    }
-  }
-  __syncthreads();  // Mz is dead; km now holds kappa
-
-  // --- kappa via group sums (16x16x32 MFMA) -----------------------------------
-  {
-    const int r16 = l & 15, g16 = l >> 4;
-    uint32_t mask[8][2][4];
-#pragma unroll
-    for (int g = 0; g < 8; ++g)
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          const int d = 32 * kk + 8 * g16 + 2 * w;
-          mask[g][kk][w] = (lab[d] == g ? 0x0000ffffu : 0u) | (lab[d + 1] == g ? 0xffff0000u : 0u);
-        }
-    for (int ti = 0; ti < 4; ++ti) {
-      for (int tj = 0; tj <= ti; ++tj) {
-        f32x4 sg[8];
-#pragma unroll
-        for (int g = 0; g < 8; ++g) sg[g] = f32x4{};
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-          typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-          const u32x4 qa = *reinterpret_cast<const u32x4*>(&qs[16 * ti + r16][32 * kk + 8 * g16]);
-          const bf16x8 kb = *reinterpret_cast<const bf16x8*>(&ks[16 * tj + r16][32 * kk + 8 * g16]);
-#pragma unroll
-          for (int g = 0; g < 8; ++g) {
-            if (g < G) {
-              const u32x4 m = {mask[g][kk][0], mask[g][kk][1], mask[g][kk][2], mask[g][kk][3]};
-              sg[g] = mfma16(__builtin_bit_cast(bf16x8, qa & m), kb, sg[g]);
-            }
-          }
-        }
-        float rs[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int ii = 16 * ti + c16_row(i, l), jj = 16 * tj + r16;
-          float kv = 0.f;
-          if (jj <= ii && tok0 + ii < N) {
-            kv = c0h;
-#pragma unroll
-            for (int g = 0; g < 8; ++g) {
-              if (g < G) {
-                float inner = lamh[g];
-#pragma unroll
-                for (int g2 = 0; g2 < 8; ++g2)
-                  if (g2 < G) inner += gamh[g * G + g2] * (sg[g2][i] * scale);
-                kv += (sg[g][i] * scale) * inner;
-              }
-            }
-          }
-          const __bf16 kb16 = (__bf16)kv;
-          km[ii][jj] = kb16;
-          rs[i] = (float)kb16;
-        }
-        if (tj < ti) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) km[16 * tj + c16_row(i, l)][16 * ti + r16] = (__bf16)0.f;
+          const bf16x8 a = *reinterpret_cast<const bf16x8*>(&Mz[32 * dt + row][16 * kk + 8 * s]);
+          const bf16x8 bq = *reinterpret_cast<const bf16x8*>(&Qs[32 * it + row][16 * kk + 8 * s]);
+          z = mfma32(a, bq, z);
         }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          float x = rs[i];
-          x += __shfl_xor(x, 1, 64);
-          x += __shfl_xor(x, 2, 64);
-          x += __shfl_xor(x, 4, 64);
-          x += __shfl_xor(x, 8, 64);
-          rs[i] = x;
-        }
-        if (r16 == 0) {
+        for (int a = 0; a < 4; ++a) {
+          const int d0 = 32 * dt + 8 * a + 4 * s;
+          const bf16x4 q4 = *reinterpret_cast<const bf16x4*>(&Qs[32 * it + row][d0]);
 #pragma unroll
-          for (int i = 0; i < 4; ++i) denL[16 * ti + c16_row(i, l)] += rs[i];
+          for (int vv = 0; vv < 4; ++vv) part = fmaf((float)q4[vv], bz[d0 + vv] + z[4 * a + vv], part);
         }
       }
+      part += __shfl_xor(part, 32, 64);
+      if (s == 0) dsS[32 * it + row] = az + part;
     }
   }
   __syncthreads();
-
-  // --- num = kappa . V; den = state + intra ------------------------------------
-  const size_t dbase = (size_t)(b * Hq + h) * N;
+  if (wv < 2) {
+    const int i = 32 * wv + row, tok = tok0 + i;
+    if (wv == 1) {
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt) {
+      for (int et = 0; et < 2; ++et)
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      f32x16 acc = f32x16{};
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        if (kk < 2 * (mt + 1)) {
-          const bf16x8 a = *reinterpret_cast<const bf16x8*>(&km[32 * mt + row][16 * kk + 8 * s]);
-          const bf16x8 bb = *reinterpret_cast<const bf16x8*>(&vT[32 * nt + row][16 * kk + 8 * s]);
-          acc = mfma32(a, bb, acc);
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int j = 32 * mt + c32_row(i, l), tok = tok0 + j;
-        if (tok < N) num[qbase + (size_t)tok * kD + 32 * nt + row] = acc[i];
-      }
+        for (int r = 0; r < 16; ++r) acc[et][r] += red[et][r][l];
+      dsum += dp2[row];
     }
-  }
-  {
-    const int tok = tok0 + l;
-    if (tok < N) den[dbase + tok] = denS[l] + denL[l];
+    if (tok < N) {
+      float* o = num + qbase + (size_t)tok * kD;
+#pragma unroll
+      for (int et = 0; et < 2; ++et)
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+          *reinterpret_cast<float4*>(o + 32 * et + 8 * a + 4 * s) =
+              make_float4(acc[et][4 * a], acc[et][4 * a + 1], acc[et][4 * a + 2], acc[et][4 * a + 3]);
+      if (s == 0) den[(size_t)(b * Hq + h) * N + tok] = dsS[i] + dsum;
+    }
   }
 }
 
@@ -586,25 +637,30 @@ __global__ __launch_bounds__(64) void k2_selftest(int* __restrict__ errors) {
 // ---------------------------------------------------------------------------
 // Host launchers
 // ---------------------------------------------------------------------------
-size_t mfma_saved_bytes(int Hq, int U, int NB) {
-  const size_t chunk = (size_t)kKS * 64 * 16 * sizeof(uint16_t);
-  return align256(sizeof(float) * (size_t)Hq * kS) + 2 * align256(chunk * U * NB) +
-         align256(sizeof(float) * (size_t)U * NB * kFP);
-}
-
 MfmaSaved mfma_saved_view(void* base, int Hq, int U, int NB) {
   char* p = static_cast<char*>(base);
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    void* r = p ? p + off : nullptr;
+    off += align256(bytes);
+    return r;
+  };
   const size_t chunk = (size_t)kKS * 64 * 16 * sizeof(uint16_t);
+  const size_t units = (size_t)U * NB;
   MfmaSaved v;
-  v.wqs = reinterpret_cast<float*>(p);
-  p += align256(sizeof(float) * (size_t)Hq * kS);
-  v.PT = reinterpret_cast<uint16_t*>(p);
-  p += align256(chunk * U * NB);
-  v.PR = reinterpret_cast<uint16_t*>(p);
-  p += align256(chunk * U * NB);
-  v.PZ = reinterpret_cast<float*>(p);
+  v.wqs = static_cast<float*>(take(sizeof(float) * (size_t)Hq * kS));
+  v.ic = static_cast<float*>(take(sizeof(float) * (size_t)Hq * kIC));
+  v.gm = static_cast<float*>(take(sizeof(float) * (size_t)Hq * kD * kD));
+  v.lb = static_cast<float*>(take(sizeof(float) * (size_t)Hq * kD));
+  v.PT = static_cast<uint16_t*>(take(chunk * units));
+  v.PR = static_cast<uint16_t*>(take(chunk * units));
+  v.PZ = static_cast<float*>(take(sizeof(float) * units * kFP));
+  v.PZm = static_cast<float*>(take(sizeof(float) * units * kD * kD));
+  v.bytes = off;
   return v;
 }
+
+size_t mfma_saved_bytes(int Hq, int U, int NB) { return mfma_saved_view(nullptr, Hq, U, NB).bytes; }
 
 template <typename T>
 void launch_mfma_forward(const LaunchGeom& g, const void* q, const void* k, const void* v, const int32_t* labels,
@@ -616,14 +672,15 @@ void launch_mfma_forward(const LaunchGeom& g, const void* q, const void* k, cons
   const T* vt = static_cast<const T*>(v);
   timed("k2_slot_coefficients", st, [&] {
     hipLaunchKernelGGL(k2_slot_coefficients, dim3(g.Hq), dim3(256), 0, st, labels, c0, lam, gam, groups, scale,
-                       sv.wqs);
+                       sv.wqs, sv.ic, sv.gm, sv.lb);
   });
   timed("k2_state_fwd", st, [&] {
-    hipLaunchKernelGGL(k2_state_fwd<T>, dim3(kS / 32, g.U), dim3(64), 0, st, kt, vt, g.N, g.NB, sv.PT, sv.PR, sv.PZ);
+    hipLaunchKernelGGL(k2_state_fwd<T>, dim3(kS / 32, g.U), dim3(64), 0, st, kt, vt, g.N, g.NB, sv.PT, sv.PR, sv.PZ,
+                       sv.PZm);
   });
   timed("k2_intra_fwd", st, [&] {
-    hipLaunchKernelGGL(k2_intra_fwd<T>, dim3(g.R * g.NB * g.U), dim3(64), 0, st, qt, kt, vt, sv.PZ, labels, c0, lam,
-                       gam, groups, g.Hq, g.Hkv, g.N, g.NB, scale, num, den);
+    hipLaunchKernelGGL(k2_intra_fwd<T>, dim3(g.R * g.NB * g.U), dim3(256), 0, st, qt, kt, vt, sv.PZ, sv.PZm, labels,
+                       sv.ic, sv.gm, sv.lb, groups, g.Hq, g.Hkv, g.N, g.NB, num, den);
   });
   timed("k2_out_fwd", st, [&] {
     hipLaunchKernelGGL(k2_out_fwd<T>, dim3(g.R * g.NB * g.U), dim3(128), 0, st, qt, sv.wqs, sv.PT, g.Hq, g.Hkv, g.N,
