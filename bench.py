@@ -56,6 +56,7 @@ def credited_flops(kernel: str, b: int, hq: int, hkv: int, n: int) -> float:
         "k2_state_fwd": unit * kv_tok,
         "k2_out_fwd": unit * q_tok,
         "k2_state_bwd": unit * q_tok,
+        "k2_state_bwd_totals": unit * q_tok,
         "k2_q_fold": unit * q_tok,
         "k2_kv_fold": 2 * unit * kv_tok,
     }.get(kernel, 0.0)

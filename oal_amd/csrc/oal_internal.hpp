@@ -46,14 +46,20 @@ void launch_mfma_forward(const LaunchGeom& g, const void* q, const void* k, cons
 struct MfmaWork {
   uint16_t* G16;  // [B][Hq][N][64] bf16 normalization VJP
   float* Gz;      // [B][Hq][N]
+  uint16_t* GT16; // [B][Hq][66][NB * 64] bf16: G^T, Gz, 0
+  uint16_t* QT16; // [B][Hq][66][NB * 64] bf16: q^T, 1 (token < N), 0
   uint16_t* dTT;  // [U][NB][kKS][64][16] bf16
   uint16_t* dTR;  // [U][NB][kS/32][4][32][16] bf16
   float* dTz;     // [U][NB][kFP]
-  float* dwqs;    // [B][Hq][kS] slot-coefficient gradients (state part)
+  float* dwqs;    // [S][B][Hq][kS] slot-coefficient gradients (state part) per segment
+  float* dwq;     // [Hq][kS] their sum
+  float* segtot;  // [U][S][kS][65] per-segment dCarry totals
+  float* carry;   // [U][S][kS][65] suffix of later segments
   float* dqf;     // [B][Hq][N][64] local dq
   float* dkp;     // [B][Hq][N][64] local dk per query head
   float* dvp;     // [B][Hq][N][64] local dv per query head
   float* coefl;   // [Hq][73][B * NB] local (dc0, dlam[8], dgam[8][8]) per chunk
+  int S, SL;      // segments of the backward state scan and chunks per segment
   size_t bytes;
 };
 MfmaWork mfma_work_view(void* base, int B, int Hq, int U, int N, int NB);

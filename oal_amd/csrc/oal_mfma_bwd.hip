@@ -1,6 +1,6 @@
 // bf16 matrix-core (MFMA) backward for gfx950.
 //
-// k2_gvec       normalization VJP: G (bf16, MFMA operand) and Gz (fp32).
+// k2_bwd_prep   normalization VJP: G (bf16 token rows and transposed), Gz; transposed q.
 // k2_state_bwd  per (32-slot tile, unit) reverse chunk scan: dT_c = sum_{c'>c}
 //               dCarry_c' in MFMA accumulators (oriented value x slot), with
 //               dCarry_c = sum_h wq_h * (raw(Q_h)^T [G_h, Gz_h]); the per-slot
@@ -25,6 +25,7 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <stdlib.h>
 
 #include "oal_internal.hpp"
 #include "oal_mfma_common.hpp"
@@ -81,190 +82,379 @@ __device__ __forceinline__ void rotated_row(const bf16x8 (&r)[8], int s, float (
 
 }  // namespace
 
+// 16 consecutive elements of a row as fp32 (zeros when !ok).
+__device__ __forceinline__ void load16f(const uint16_t* __restrict__ src, size_t off, bool ok, float (&x)[16]) {
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4* p = reinterpret_cast<const u32x4*>(src + off);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const u32x4 w = ok ? p[i] : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      x[8 * i + 2 * j] = __uint_as_float(w[j] << 16);
+      x[8 * i + 2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+    }
+  }
+}
+__device__ __forceinline__ void load16f(const float* __restrict__ src, size_t off, bool ok, float (&x)[16]) {
+  const float4* p = reinterpret_cast<const float4*>(src + off);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float4 a = ok ? p[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    x[4 * i] = a.x;
+    x[4 * i + 1] = a.y;
+    x[4 * i + 2] = a.z;
+    x[4 * i + 3] = a.w;
+  }
+}
+
+// Rows of the transposed per-head operands (QT16 / GT16): 64 feature or value
+// rows, then row 64 (QT: 1 for tokens < N; GT: Gz) and row 65 (zeros).
+constexpr int kTRows = kD + 2;
+
 // ---------------------------------------------------------------------------
-// Normalization VJP (reference hd_block_gemm_normalization_ops.py:32-71).
+// Backward preparation, one block per (batch, query head, chunk):
+// normalization VJP (reference hd_block_gemm_normalization_ops.py:32-71)
+//   G = dO / den' + dnum,  Gz = -(dO . num) / den'^2 [den >= floor] + dden,
+// den' = max(den, floor) (floor <= 0: den' = den, no mask), written as G16
+// (token rows, bf16) and Gz (f32), plus the transposed bf16 operands of the
+// backward state scan, GT16 = [G^T; Gz; 0] and QT16 = [q^T; 1; 0], each
+// [B][Hq][66][NB * 64].
 // ---------------------------------------------------------------------------
 template <typename T>
-__global__ __launch_bounds__(256) void k2_gvec(const T* __restrict__ dout, const float* __restrict__ dnum,
-                                               const float* __restrict__ dden, const float* __restrict__ num,
-                                               const float* __restrict__ den, long rows, float floor,
-                                               uint16_t* __restrict__ G16, float* __restrict__ Gz) {
-  const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  if (row >= rows) return;
-  const float dd = den[row];
+__global__ __launch_bounds__(256) void k2_bwd_prep(const T* __restrict__ q, const T* __restrict__ dout,
+                                                   const float* __restrict__ dnum, const float* __restrict__ dden,
+                                                   const float* __restrict__ num, const float* __restrict__ den, int N,
+                                                   int NB, float floor, uint16_t* __restrict__ G16,
+                                                   float* __restrict__ Gz, uint16_t* __restrict__ GT16,
+                                                   uint16_t* __restrict__ QT16) {
+  constexpr int LT = kC + 8;
+  __shared__ __attribute__((aligned(16))) __bf16 gT[kTRows][LT];
+  __shared__ __attribute__((aligned(16))) __bf16 qT[kTRows][LT];
+  const int bh = blockIdx.x / NB, ch = blockIdx.x % NB;
+  const int tid = threadIdx.x, j = tid >> 2, qq = tid & 3;
+  const int tok = ch * kC + j;
+  const bool ok = tok < N;
+  const size_t roff = ((size_t)bh * N + (ok ? tok : N - 1)) * kD + 16 * qq;
+  float dO[16], nm[16], qv[16];
+  if (dout) {
+    load16f(dout, roff, ok, dO);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) dO[e] = 0.f;
+  }
+  load16f(num, roff, ok, nm);
+  load16f(q, roff, ok, qv);
+  const float dd = ok ? den[(size_t)bh * N + tok] : 1.f;
   const float dp = floor > 0.f ? fmaxf(dd, floor) : dd;
-  const float dO = dout ? to_f(dout[row * kD + lane]) : 0.f;
-  float g = dO / dp;
-  if (dnum) g += dnum[row * kD + lane];
-  G16[row * kD + lane] = from_f<uint16_t>(g);
-  const float dot = wave_sum(dO * num[row * kD + lane]);
-  if (lane == 0) {
-    float gz = -dot / (dp * dp);
-    if (floor > 0.f && !(dd >= floor)) gz = 0.f;
-    if (dden) gz += dden[row];
-    Gz[row] = gz;
+  const float inv = 1.f / dp;
+  float g[16], dot = 0.f;
+  if (dnum) {
+    float dn[16];
+    load16f(dnum, roff, ok, dn);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) g[e] = dO[e] * inv + dn[e];
+  } else {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) g[e] = dO[e] * inv;
+  }
+#pragma unroll
+  for (int e = 0; e < 16; ++e) dot = fmaf(dO[e], nm[e], dot);
+  dot += __shfl_xor(dot, 1, 64);
+  dot += __shfl_xor(dot, 2, 64);
+  float gz = -dot / (dp * dp);
+  if (floor > 0.f && !(dd >= floor)) gz = 0.f;
+  if (dden && ok) gz += dden[(size_t)bh * N + tok];
+  if (!ok) gz = 0.f;
+  {
+    float y0[8], y1[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      y0[e] = ok ? g[e] : 0.f;
+      y1[e] = ok ? g[8 + e] : 0.f;
+    }
+    const bf16x8 p0 = pack8(y0), p1 = pack8(y1);
+    if (ok) {
+      bf16x8* dst = reinterpret_cast<bf16x8*>(G16 + roff);
+      dst[0] = p0;
+      dst[1] = p1;
+      if (qq == 0) Gz[(size_t)bh * N + tok] = gz;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      gT[16 * qq + e][j] = p0[e];
+      gT[16 * qq + 8 + e][j] = p1[e];
+      qT[16 * qq + e][j] = (__bf16)qv[e];
+      qT[16 * qq + 8 + e][j] = (__bf16)qv[8 + e];
+    }
+    if (qq == 0) {
+      gT[kD][j] = (__bf16)gz;
+      gT[kD + 1][j] = (__bf16)0.f;
+      qT[kD][j] = (__bf16)(ok ? 1.f : 0.f);
+      qT[kD + 1][j] = (__bf16)0.f;
+    }
+  }
+  __syncthreads();
+  const size_t np = (size_t)NB * kC;
+  for (int idx = tid; idx < kTRows * 8; idx += 256) {
+    const int r = idx >> 3, c8 = idx & 7;
+    const size_t o = ((size_t)bh * kTRows + r) * np + (size_t)ch * kC + 8 * c8;
+    *reinterpret_cast<bf16x8*>(GT16 + o) = *reinterpret_cast<const bf16x8*>(&gT[r][8 * c8]);
+    *reinterpret_cast<bf16x8*>(QT16 + o) = *reinterpret_cast<const bf16x8*>(&qT[r][8 * c8]);
   }
 }
 
 // ---------------------------------------------------------------------------
-// Backward state scan. grid (kS/32, U), one wave. Accumulators hold
-// dT^T [96 values (64 = den) x 32 slots]; lane column = slot.
+// Backward state scan over one segment of chunks (reverse order).
+// grid (ceil(69 / 4) tile groups, U, S segments), 4 waves; wave w owns the
+// 32-slot tile 4 * blockIdx.x + w. Accumulators hold dT^T [96 value rows
+// (row 64 = denominator) x 32 slots] (lane column = slot):
+//   dT_c = carry + sum_{c' > c in segment} dCarry_c',
+//   dCarry_c = sum_h wq_h o (raw(Q_h)^T [G_h, Gz_h])   (reference
+//   hd_block_gemm_backward.py:764-908, _query_dcarry + _exclusive_right_scan).
+// The per-(head, chunk) operands QT16 / GT16 are staged once per block into a
+// double-buffered LDS ring shared by the four tiles; raw features come from
+// v_dot2_f32_bf16 on masked bf16 pairs.
+// MODE 0: segment totals + coefficient partials (no dT outputs);
+// MODE 1: replay from the carry of later segments, emit dT;
+// MODE 2: single segment, emit dT and coefficient partials.
+// Coefficient partial: dwq_h[slot] += sum_c <P_c[slot], raw(Q_h,c)^T G_h,c [slot]>.
 // ---------------------------------------------------------------------------
-template <typename T>
-__global__ __launch_bounds__(64) void k2_state_bwd(const T* __restrict__ q, const uint16_t* __restrict__ G16,
-                                                   const float* __restrict__ Gz, const float* __restrict__ wqs,
-                                                   const uint16_t* __restrict__ PR, const float* __restrict__ PZ,
-                                                   int Hq, int Hkv, int N, int NB, uint16_t* __restrict__ dTT,
-                                                   uint16_t* __restrict__ dTR, float* __restrict__ dTz,
-                                                   float* __restrict__ dwqs) {
-  __shared__ float qT[kRow][kC + 4];                              // qT[d][tok]; 64 = valid, 65 = 0
-  __shared__ __attribute__((aligned(16))) __bf16 GT[96][kC + 8];  // GT[e][tok]; 64 = Gz
-  __shared__ __attribute__((aligned(16))) __bf16 Pl[32][LD];      // P_c rows of this tile
-  __shared__ float Pzl[32];
-  __shared__ float stage[97][33];
+constexpr int kSB_TILES = 4;
+constexpr int kSB_ROW = kC + 8;                     // LDS row stride of G^T (bf16)
+constexpr int kSB_QROW = kC + 4;                    // LDS row stride of q^T (f32)
+constexpr int kSB_BUF = kTRows * kSB_ROW;           // one staged G^T
+constexpr int kSB_QBUF = kTRows * kSB_QROW;         // one staged q^T
+constexpr int kSB_UNITS = kTRows * kC / 8;          // 16-byte bf16 units per matrix (528)
 
-  const int tile = blockIdx.x, u = blockIdx.y;
+template <int MODE>
+__global__ __launch_bounds__(256) void k2_state_bwd(const uint16_t* __restrict__ QT16,
+                                                    const uint16_t* __restrict__ GT16, const float* __restrict__ wqs,
+                                                    const uint16_t* __restrict__ PR, const float* __restrict__ PZ,
+                                                    const float* __restrict__ carry, int Hq, int Hkv, int N, int NB,
+                                                    int SL, int Sg, uint16_t* __restrict__ dTT,
+                                                    uint16_t* __restrict__ dTR,
+                                                    float* __restrict__ dTz, float* __restrict__ segtot,
+                                                    float* __restrict__ dwqs) {
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  __shared__ __attribute__((aligned(16))) float Qs[2][kSB_QBUF];
+  __shared__ __attribute__((aligned(16))) __bf16 Gs[2][kSB_BUF];
+  __shared__ __attribute__((aligned(16))) __bf16 em[kSB_TILES][32][kSB_ROW];
+
+  // 1-D grid ordered so that the tile groups of one (unit, segment), which read
+  // the same operands, run on one XCD (workgroup id -> XCD id % 8)
+  constexpr int TG = (kS / 32 + kSB_TILES - 1) / kSB_TILES;
+  const int total = gridDim.x;
+  int u, seg, tgi;
+  {
+    const int id = blockIdx.x;
+    const int w = (total & 7) == 0 ? (id & 7) * (total >> 3) + (id >> 3) : id;
+    tgi = w % TG;
+    seg = (w / TG) % Sg;
+    u = w / (TG * Sg);
+  }
   const int R = Hq / Hkv, b = u / Hkv, kh = u % Hkv;
-  const int l = threadIdx.x, s = l >> 5, row = l & 31;
-  const int slot = tile * 32 + row;
-  const int ar = kSlot.ar[slot], ac = kSlot.ac[slot], nat = kSlot.nat[slot];
+  const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, s = l >> 5, row = l & 31;
+  const int tile = kSB_TILES * tgi + wv;
+  const bool live = tile < kS / 32;
+  const int slot = live ? tile * 32 + row : 0;
+  const int ar = kSlot.ar[slot], ac = kSlot.ac[slot], nat = live ? kSlot.nat[slot] : -1;
+  const int c_lo = seg * SL, c_hi = min(NB, c_lo + SL);
+  const size_t np = (size_t)NB * kC;
+  const size_t chunk_elems = (size_t)kKS * 64 * 16;
 
-  for (int idx = l; idx < 31 * (kC + 8); idx += 64) GT[65 + idx / (kC + 8)][idx % (kC + 8)] = (__bf16)0.f;
   float wh[8], dwp[8];
 #pragma unroll
   for (int hh = 0; hh < 8; ++hh) {
-    wh[hh] = hh < R ? wqs[(size_t)(kh * R + hh) * kS + slot] : 0.f;
+    wh[hh] = (live && hh < R) ? wqs[(size_t)(kh * R + hh) * kS + slot] : 0.f;
     dwp[hh] = 0.f;
   }
-
-  auto fetch = [&](int ch, int hh, bf16x8 (&qr)[8], bf16x8 (&gr)[8], float& gz) {
-    const int h = kh * R + hh, tok = ch * kC + l;
-    const bool ok = tok < N;
-    const size_t rb = ((size_t)(b * Hq + h) * N + (ok ? tok : N - 1)) * kD;
-    load_row_b(q, rb, ok, qr);
-    load_row_b(G16, rb, ok, gr);
-    gz = ok ? Gz[(size_t)(b * Hq + h) * N + (ok ? tok : N - 1)] : 0.f;
-  };
-  auto stage_head = [&](const bf16x8 (&qr)[8], const bf16x8 (&gr)[8], float gz, bool ok) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        qT[8 * i + j][l] = (float)qr[i][j];
-        GT[8 * i + j][l] = gr[i][j];
-      }
-    qT[64][l] = ok ? 1.f : 0.f;
-    qT[65][l] = 0.f;
-    GT[64][l] = (__bf16)gz;
-  };
 
   f32x16 acc[3];
 #pragma unroll
   for (int n = 0; n < 3; ++n) acc[n] = f32x16{};
-  const size_t chunk_elems = (size_t)kKS * 64 * 16;
-
-  bf16x8 qr[8], gr[8];
-  float gz;
-  fetch(NB - 1, 0, qr, gr, gz);
-  for (int ch = NB - 1; ch >= 0; --ch) {
-    // 1. dT_c = accumulated suffix (exclusive)
-#pragma unroll
-    for (int n = 0; n < 3; ++n)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) stage[32 * n + c32_row(i, l)][row] = acc[n][i];
-    __syncthreads();
-    {
-      uint16_t* tt = dTT + ((size_t)u * NB + ch) * chunk_elems;
-      uint16_t* tr = dTR + ((size_t)u * NB + ch) * chunk_elems;
-      const int t = 2 * tile + s;
-#pragma unroll
-      for (int eh = 0; eh < 2; ++eh) {
-        const int e = row + 32 * eh;
-        uint32_t w[8];
-#pragma unroll
-        for (int qq = 0; qq < 8; ++qq) w[qq] = pack_bf16x2(stage[e][16 * s + 2 * qq], stage[e][16 * s + 2 * qq + 1]);
-        uint4* dst = reinterpret_cast<uint4*>(tt + ((size_t)t * 64 + e) * 16);
-        dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
-        dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
-      }
-#pragma unroll
-      for (int kh2 = 0; kh2 < 2; ++kh2) {
-        const int kk = 2 * s + kh2;
-        uint32_t w[8];
-#pragma unroll
-        for (int qq = 0; qq < 8; ++qq)
-          w[qq] = pack_bf16x2(stage[16 * kk + 2 * qq][row], stage[16 * kk + 2 * qq + 1][row]);
-        uint4* dst = reinterpret_cast<uint4*>(tr + (((size_t)tile * 4 + kk) * 32 + row) * 16);
-        dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
-        dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
-      }
-      if (s == 0 && nat >= 0) dTz[((size_t)u * NB + ch) * kFP + nat] = stage[64][row];
-    }
-    // 2. P_c rows of this tile (for the coefficient gradient)
-    {
-      const uint16_t* pr = PR + ((size_t)u * NB + ch) * chunk_elems + (size_t)tile * 4 * 32 * 16;
-      // PR[tile][kk][32][16] -> Pl[slot][e]
-#pragma unroll
-      for (int it = 0; it < 4; ++it) {
-        const int idx = it * 64 + l;  // 256 chunks of 8 values
-        const int kk = idx >> 6, rr = (idx >> 1) & 31, hf = idx & 1;
-        *reinterpret_cast<bf16x8*>(&Pl[rr][16 * kk + 8 * hf]) =
-            *reinterpret_cast<const bf16x8*>(pr + ((size_t)kk * 32 + rr) * 16 + 8 * hf);
-      }
-      if (s == 0) Pzl[row] = nat >= 0 ? PZ[((size_t)u * NB + ch) * kFP + nat] : 0.f;
-    }
-    // 3. heads
-    for (int hh = 0; hh < R; ++hh) {
-      __syncthreads();
-      stage_head(qr, gr, gz, ch * kC + l < N);
-      __syncthreads();
-      // prefetch the next (chunk, head) rows
-      {
-        int nh = hh + 1, nc = ch;
-        if (nh == R) {
-          nh = 0;
-          nc = ch - 1;
-        }
-        if (nc >= 0) fetch(nc, nh, qr, gr, gz);
-      }
-      f32x16 hT[3];
-#pragma unroll
-      for (int n = 0; n < 3; ++n) hT[n] = f32x16{};
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        const int j0 = 16 * kk + 8 * s;
-        float f[8];
-#pragma unroll
-        for (int qq = 0; qq < 8; ++qq) f[qq] = qT[ar][j0 + qq] * qT[ac][j0 + qq];
-        const bf16x8 bq = pack8(f);
-#pragma unroll
-        for (int n = 0; n < 3; ++n) {
-          const bf16x8 a = *reinterpret_cast<const bf16x8*>(&GT[32 * n + row][j0]);
-          hT[n] = mfma32(a, bq, hT[n]);
-        }
-      }
-      const float w = wh[hh];
-      float dsum = 0.f;
+  if constexpr (MODE == 1) {
+    if (live) {
+      const float* cr = carry + (((size_t)u * Sg + seg) * kS + slot) * 65;
 #pragma unroll
       for (int n = 0; n < 2; ++n)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          acc[n][i] += w * hT[n][i];
-          dsum += (float)Pl[row][32 * n + c32_row(i, l)] * hT[n][i];
-        }
-#pragma unroll
-      for (int i = 0; i < 16; ++i) acc[2][i] += w * hT[2][i];
-      if (s == 0) dsum += Pzl[row] * hT[2][0];  // value row 64 = Gz column
-      dwp[hh] += dsum;
+        for (int i = 0; i < 16; ++i) acc[n][i] = cr[32 * n + c32_row(i, l)];
+      acc[2][0] = s == 0 ? cr[64] : 0.f;
     }
   }
-#pragma unroll
-  for (int hh = 0; hh < 8; ++hh) {
-    if (hh < R) {
-      const float tot = dwp[hh] + __shfl_xor(dwp[hh], 32, 64);
-      if (s == 0) dwqs[(size_t)(b * Hq + kh * R + hh) * kS + slot] = tot;
+
+  // staging of item (chunk, head): 528 16-byte units per matrix; thread t
+  // moves units t and t + 256 of each, threads t < 16 also unit t + 512.
+  uint4 rq0, rq1, rq2, rg0, rg1, rg2;
+  rq2 = rg2 = make_uint4(0u, 0u, 0u, 0u);
+  const bool third = tid < kSB_UNITS - 512;
+  const size_t u0 = (size_t)(tid >> 3) * np + 8 * (tid & 7);
+  const size_t u1 = (size_t)((tid + 256) >> 3) * np + 8 * (tid & 7);
+  const size_t u2 = (size_t)((tid + 512) >> 3) * np + 8 * (tid & 7);
+  auto fetch = [&](int ch, int hh) {
+    const size_t base = ((size_t)(b * Hq + kh * R + hh) * kTRows) * np + (size_t)ch * kC;
+    rq0 = *reinterpret_cast<const uint4*>(QT16 + base + u0);
+    rg0 = *reinterpret_cast<const uint4*>(GT16 + base + u0);
+    rq1 = *reinterpret_cast<const uint4*>(QT16 + base + u1);
+    rg1 = *reinterpret_cast<const uint4*>(GT16 + base + u1);
+    if (third) {
+      rq2 = *reinterpret_cast<const uint4*>(QT16 + base + u2);
+      rg2 = *reinterpret_cast<const uint4*>(GT16 + base + u2);
     }
+  };
+  auto put = [&](int buf, int idx, const uint4& wq, const uint4& wg) {
+    const int r = idx >> 3, c8 = idx & 7;
+    float4* qd = reinterpret_cast<float4*>(&Qs[buf][r * kSB_QROW + 8 * c8]);
+    qd[0] = make_float4(__uint_as_float(wq.x << 16), __uint_as_float(wq.x & 0xffff0000u),
+                        __uint_as_float(wq.y << 16), __uint_as_float(wq.y & 0xffff0000u));
+    qd[1] = make_float4(__uint_as_float(wq.z << 16), __uint_as_float(wq.z & 0xffff0000u),
+                        __uint_as_float(wq.w << 16), __uint_as_float(wq.w & 0xffff0000u));
+    *reinterpret_cast<uint4*>(&Gs[buf][r * kSB_ROW + 8 * c8]) = wg;
+  };
+  auto store = [&](int buf) {
+    put(buf, tid, rq0, rg0);
+    put(buf, tid + 256, rq1, rg1);
+    if (third) put(buf, tid + 512, rq2, rg2);
+  };
+
+  fetch(c_hi - 1, 0);
+  store(0);
+  __syncthreads();
+  int buf = 0;
+  float pf[2][16];
+  float pz = 0.f;
+  for (int ch = c_hi - 1; ch >= c_lo; --ch) {
+    const size_t cb = (size_t)u * NB + ch;
+    if constexpr (MODE != 0) {
+      // emit dT_c = acc (exclusive suffix)
+      if (live) {
+        uint16_t* tr = dTR + cb * chunk_elems + (size_t)tile * 4 * 32 * 16;
+#pragma unroll
+        for (int n = 0; n < 2; ++n)
+#pragma unroll
+          for (int a = 0; a < 4; ++a) {
+            const uint32_t w0 = pack_bf16x2(acc[n][4 * a], acc[n][4 * a + 1]);
+            const uint32_t w1 = pack_bf16x2(acc[n][4 * a + 2], acc[n][4 * a + 3]);
+            const int kk = 2 * n + (a >> 1), pos = 8 * (a & 1) + 4 * s;
+            *reinterpret_cast<uint2*>(tr + ((size_t)kk * 32 + row) * 16 + pos) = make_uint2(w0, w1);
+            *reinterpret_cast<uint2*>(&em[wv][row][32 * n + 8 * a + 4 * s]) = make_uint2(w0, w1);
+          }
+        if (s == 0 && nat >= 0) dTz[cb * kFP + nat] = acc[2][0];
+        __builtin_amdgcn_wave_barrier();
+        // dTT [kstep][64 values][16 slots]: lane l = value row
+        uint16_t* tt = dTT + cb * chunk_elems;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          uint32_t w[8];
+#pragma unroll
+          for (int q2 = 0; q2 < 8; ++q2)
+            w[q2] = uint32_t(__builtin_bit_cast(uint16_t, em[wv][16 * ks + 2 * q2][l])) |
+                    (uint32_t(__builtin_bit_cast(uint16_t, em[wv][16 * ks + 2 * q2 + 1][l])) << 16);
+          uint4* dst = reinterpret_cast<uint4*>(tt + ((size_t)(2 * tile + ks) * 64 + l) * 16);
+          dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
+          dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
+        }
+        __builtin_amdgcn_wave_barrier();
+      }
+    }
+    if constexpr (MODE != 1) {
+      // P_c rows of this lane's slot, values e = 32 n + 8 a + 4 s + v
+      if (live) {
+        const uint16_t* pr = PR + cb * chunk_elems + (size_t)tile * 4 * 32 * 16;
+#pragma unroll
+        for (int n = 0; n < 2; ++n)
+#pragma unroll
+          for (int a = 0; a < 4; ++a) {
+            const int kk = 2 * n + (a >> 1), pos = 8 * (a & 1) + 4 * s;
+            const uint2 w = *reinterpret_cast<const uint2*>(pr + ((size_t)kk * 32 + row) * 16 + pos);
+            pf[n][4 * a] = __uint_as_float(w.x << 16);
+            pf[n][4 * a + 1] = __uint_as_float(w.x & 0xffff0000u);
+            pf[n][4 * a + 2] = __uint_as_float(w.y << 16);
+            pf[n][4 * a + 3] = __uint_as_float(w.y & 0xffff0000u);
+          }
+        pz = (s == 0 && nat >= 0) ? PZ[cb * kFP + nat] : 0.f;
+      }
+    }
+#pragma unroll
+    for (int hh = 0; hh < 8; ++hh) {
+      if (hh < R) {
+        const bool more = hh + 1 < R || ch > c_lo;
+        if (more) fetch(hh + 1 < R ? ch : ch - 1, hh + 1 < R ? hh + 1 : 0);
+        if (live) {
+          const float* qs = Qs[buf];
+          const __bf16* gs = Gs[buf];
+          f32x16 hT[3] = {f32x16{}, f32x16{}, f32x16{}};
+#pragma unroll
+          for (int kk = 0; kk < 4; ++kk) {
+            const float4* pa = reinterpret_cast<const float4*>(qs + ar * kSB_QROW + 16 * kk + 8 * s);
+            const float4* pc = reinterpret_cast<const float4*>(qs + ac * kSB_QROW + 16 * kk + 8 * s);
+            const float4 a0 = pa[0], a1 = pa[1], c0v = pc[0], c1v = pc[1];
+            const float f[8] = {a0.x * c0v.x, a0.y * c0v.y, a0.z * c0v.z, a0.w * c0v.w,
+                                a1.x * c1v.x, a1.y * c1v.y, a1.z * c1v.z, a1.w * c1v.w};
+            const bf16x8 bq = pack8(f);
+#pragma unroll
+            for (int n = 0; n < 3; ++n) {
+              const int gr = n < 2 ? 32 * n + row : (row == 0 ? kD : kD + 1);
+              const bf16x8 a = *reinterpret_cast<const bf16x8*>(gs + gr * kSB_ROW + 16 * kk + 8 * s);
+              hT[n] = mfma32(a, bq, hT[n]);
+            }
+          }
+          const float w = wh[hh];
+#pragma unroll
+          for (int n = 0; n < 2; ++n)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[n][i] = fmaf(w, hT[n][i], acc[n][i]);
+          acc[2][0] = fmaf(w, hT[2][0], acc[2][0]);
+          if constexpr (MODE != 1) {
+            float d = pz * hT[2][0];
+#pragma unroll
+            for (int n = 0; n < 2; ++n)
+#pragma unroll
+              for (int i = 0; i < 16; ++i) d = fmaf(pf[n][i], hT[n][i], d);
+            dwp[hh] += d;
+          }
+        }
+        if (more) store(buf ^ 1);
+        __syncthreads();
+        buf ^= 1;
+      }
+    }
+  }
+  if constexpr (MODE == 0) {
+    if (live) {
+      float* st = segtot + (((size_t)u * Sg + seg) * kS + slot) * 65;
+#pragma unroll
+      for (int n = 0; n < 2; ++n)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) st[32 * n + c32_row(i, l)] = acc[n][i];
+      if (s == 0) st[64] = acc[2][0];
+    }
+  }
+  if constexpr (MODE != 1) {
+    const int B = (int)(gridDim.x / (TG * Sg)) / Hkv;
+#pragma unroll
+    for (int hh = 0; hh < 8; ++hh) {
+      if (hh < R) {
+        const float tot = dwp[hh] + __shfl_xor(dwp[hh], 32, 64);
+        if (live && s == 0) dwqs[(((size_t)seg * B + b) * Hq + kh * R + hh) * kS + slot] = tot;
+      }
+    }
+  }
+}
+
+// carry[u][seg] = sum_{seg' > seg} segtot[u][seg'] (fixed order), elementwise.
+__global__ __launch_bounds__(256) void k2_seg_carry(const float* __restrict__ segtot, int S,
+                                                    float* __restrict__ carry) {
+  const size_t per = (size_t)kS * 65;
+  const size_t e = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (e >= per) return;
+  const size_t ub = (size_t)blockIdx.y * S * per;
+  float run = 0.f;
+  for (int sg = S - 1; sg >= 0; --sg) {
+    carry[ub + (size_t)sg * per + e] = run;
+    run += segtot[ub + (size_t)sg * per + e];
   }
 }
 
@@ -918,6 +1108,16 @@ __global__ __launch_bounds__(256) void k2_local_bwd(const T* __restrict__ q, con
   }
 }
 
+// dwq[h][slot] = sum over (segment, batch) of the state-scan partials, fixed order.
+__global__ __launch_bounds__(256) void k2_dwq_reduce(const float* __restrict__ dwqs, int rowsets, int Hq,
+                                                     float* __restrict__ dwq) {
+  const int h = blockIdx.y, sl = blockIdx.x * 256 + threadIdx.x;
+  if (sl >= kS) return;
+  float acc = 0.f;
+  for (int r = 0; r < rowsets; ++r) acc += dwqs[((size_t)r * Hq + h) * kS + sl];
+  dwq[(size_t)h * kS + sl] = acc;
+}
+
 // ---------------------------------------------------------------------------
 // Coefficient gradients, one block per query head, every sum in a fixed order.
 // State part: the per-slot gradients (summed over the batch) are laid out in
@@ -926,8 +1126,8 @@ __global__ __launch_bounds__(256) void k2_local_bwd(const T* __restrict__ q, con
 // X[r][g] = sum_{c <= r, g(c) = g} m_rc wn[pair(r, c)], raw = E^T X with E the
 // one-hot label matrix. Local part: column sums of the per-chunk partials.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k2_coef_grad(const float* __restrict__ dwqs, const float* __restrict__ coefl,
-                                                    const int32_t* __restrict__ labels, int B, int Hq, int NB, int G,
+__global__ __launch_bounds__(256) void k2_coef_grad(const float* __restrict__ dwq, const float* __restrict__ coefl,
+                                                    const int32_t* __restrict__ labels, int Hq, int bn, int G,
                                                     float scale, float* __restrict__ dc0, float* __restrict__ dlam,
                                                     float* __restrict__ dgam) {
   __shared__ float wn[kFeat];
@@ -942,13 +1142,8 @@ __global__ __launch_bounds__(256) void k2_coef_grad(const float* __restrict__ dw
   }
   for (int sl = t; sl < kS; sl += 256) {
     const int n = kSlot.nat[sl];
-    if (n >= 0) {
-      float acc = 0.f;
-      for (int b = 0; b < B; ++b) acc += dwqs[((size_t)b * Hq + h) * kS + sl];
-      wn[n] = acc;
-    }
+    if (n >= 0) wn[n] = dwq[(size_t)h * kS + sl];
   }
-  const int bn = B * NB;
   for (int j = wave; j < 73; j += 4) {
     const float* col = coefl + ((size_t)h * 73 + j) * bn;
     float acc = 0.f;
@@ -994,6 +1189,20 @@ __global__ __launch_bounds__(256) void k2_coef_grad(const float* __restrict__ dw
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
+// Segments of the backward state scan: enough (tile group, unit, segment)
+// blocks to give every SIMD about four waves; one segment when that already
+// holds. OAL_BWD_SEGMENTS overrides (for tuning).
+static void bwd_segments(int U, int NB, int& S, int& SL) {
+  const int tg = (kS / 32 + kSB_TILES - 1) / kSB_TILES;
+  const int per_seg_waves = tg * U * kSB_TILES;
+  int want = (4096 + per_seg_waves - 1) / per_seg_waves;
+  if (const char* env = getenv("OAL_BWD_SEGMENTS")) want = atoi(env);
+  if (want < 1) want = 1;
+  if (want > NB) want = NB;
+  SL = (NB + want - 1) / want;
+  S = (NB + SL - 1) / SL;
+}
+
 MfmaWork mfma_work_view(void* base, int B, int Hq, int U, int N, int NB) {
   char* p = static_cast<char*>(base);
   size_t off = 0;
@@ -1003,14 +1212,22 @@ MfmaWork mfma_work_view(void* base, int B, int Hq, int U, int N, int NB) {
     return r;
   };
   const size_t rows = (size_t)B * Hq * N;
+  const size_t trows = (size_t)B * Hq * kTRows * NB * kC;
   const size_t chunk = (size_t)kKS * 64 * 16 * sizeof(uint16_t);
   MfmaWork w;
+  bwd_segments(U, NB, w.S, w.SL);
   w.G16 = static_cast<uint16_t*>(take(rows * kD * sizeof(uint16_t)));
   w.Gz = static_cast<float*>(take(rows * sizeof(float)));
+  w.GT16 = static_cast<uint16_t*>(take(trows * sizeof(uint16_t)));
+  w.QT16 = static_cast<uint16_t*>(take(trows * sizeof(uint16_t)));
   w.dTT = static_cast<uint16_t*>(take(chunk * U * NB));
   w.dTR = static_cast<uint16_t*>(take(chunk * U * NB));
   w.dTz = static_cast<float*>(take(sizeof(float) * (size_t)U * NB * kFP));
-  w.dwqs = static_cast<float*>(take(sizeof(float) * (size_t)B * Hq * kS));
+  w.dwqs = static_cast<float*>(take(sizeof(float) * (size_t)w.S * B * Hq * kS));
+  w.dwq = static_cast<float*>(take(sizeof(float) * (size_t)Hq * kS));
+  const size_t seg = w.S > 1 ? sizeof(float) * (size_t)U * w.S * kS * 65 : 0;
+  w.segtot = static_cast<float*>(take(seg));
+  w.carry = static_cast<float*>(take(seg));
   w.dqf = static_cast<float*>(take(rows * kD * sizeof(float)));
   w.dkp = static_cast<float*>(take(rows * kD * sizeof(float)));
   w.dvp = static_cast<float*>(take(rows * kD * sizeof(float)));
@@ -1025,20 +1242,37 @@ int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, cons
                          const float* num, const float* den, const void* saved, const void* dout, const float* dnum,
                          const float* dden, void* dq, void* dk, void* dv, float* dc0, float* dlam, float* dgam,
                          void* workspace, hipStream_t st, const Timer& timed) {
+  if ((dk != nullptr) != (dv != nullptr)) return 2;
+  const bool need_coef = dc0 || dlam || dgam;
+  if (need_coef && !(dc0 && dlam && dgam)) return 3;
   MfmaSaved sv = mfma_saved_view(const_cast<void*>(saved), g.Hq, g.U, g.NB);
   MfmaWork w = mfma_work_view(workspace, g.B, g.Hq, g.U, g.N, g.NB);
   const T* qt = static_cast<const T*>(q);
   const T* kt = static_cast<const T*>(k);
   const T* vt = static_cast<const T*>(v);
-  const long rows = (long)g.B * g.Hq * g.N;
-  timed("k2_gvec", st, [&] {
-    hipLaunchKernelGGL(k2_gvec<T>, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st, static_cast<const T*>(dout),
-                       dnum, dden, num, den, rows, floor, w.G16, w.Gz);
+  timed("k2_bwd_prep", st, [&] {
+    hipLaunchKernelGGL(k2_bwd_prep<T>, dim3(g.B * g.Hq * g.NB), dim3(256), 0, st, qt, static_cast<const T*>(dout),
+                       dnum, dden, num, den, g.N, g.NB, floor, w.G16, w.Gz, w.GT16, w.QT16);
   });
-  timed("k2_state_bwd", st, [&] {
-    hipLaunchKernelGGL(k2_state_bwd<T>, dim3(kS / 32, g.U), dim3(64), 0, st, qt, w.G16, w.Gz, sv.wqs, sv.PR, sv.PZ,
-                       g.Hq, g.Hkv, g.N, g.NB, w.dTT, w.dTR, w.dTz, w.dwqs);
-  });
+  const dim3 sgrid((unsigned)(((kS / 32 + kSB_TILES - 1) / kSB_TILES) * g.U * w.S));
+  if (w.S == 1) {
+    timed("k2_state_bwd", st, [&] {
+      hipLaunchKernelGGL(k2_state_bwd<2>, sgrid, dim3(256), 0, st, w.QT16, w.GT16, sv.wqs, sv.PR, sv.PZ, nullptr,
+                         g.Hq, g.Hkv, g.N, g.NB, w.SL, w.S, w.dTT, w.dTR, w.dTz, nullptr, w.dwqs);
+    });
+  } else {
+    timed("k2_state_bwd_totals", st, [&] {
+      hipLaunchKernelGGL(k2_state_bwd<0>, sgrid, dim3(256), 0, st, w.QT16, w.GT16, sv.wqs, sv.PR, sv.PZ, nullptr,
+                         g.Hq, g.Hkv, g.N, g.NB, w.SL, w.S, nullptr, nullptr, nullptr, w.segtot, w.dwqs);
+    });
+    timed("k2_seg_carry", st, [&] {
+      hipLaunchKernelGGL(k2_seg_carry, dim3((kS * 65 + 255) / 256, g.U), dim3(256), 0, st, w.segtot, w.S, w.carry);
+    });
+    timed("k2_state_bwd", st, [&] {
+      hipLaunchKernelGGL(k2_state_bwd<1>, sgrid, dim3(256), 0, st, w.QT16, w.GT16, sv.wqs, sv.PR, sv.PZ, w.carry,
+                         g.Hq, g.Hkv, g.N, g.NB, w.SL, w.S, w.dTT, w.dTR, w.dTz, nullptr, nullptr);
+    });
+  }
   timed("k2_local_bwd", st, [&] {
     hipLaunchKernelGGL(k2_local_bwd<T>, dim3(g.R * g.NB * g.U), dim3(256), 0, st, qt, kt, vt, w.G16, w.Gz, sv.PZ,
                        labels, c0, lam, gam, groups, g.Hq, g.Hkv, g.N, g.NB, scale, w.dqf, w.dkp, w.dvp, w.coefl);
@@ -1049,17 +1283,19 @@ int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, cons
                          g.Hq, g.Hkv, g.N, g.NB, static_cast<T*>(dq));
     });
   }
-  if (dk || dv) {
-    if (!(dk && dv)) return 2;
+  if (dk) {
     timed("k2_kv_fold", st, [&] {
       hipLaunchKernelGGL(k2_kv_fold<T>, dim3(g.NB, g.U), dim3(128), 0, st, kt, vt, w.dTR, w.dTT, w.dTz, w.dkp, w.dvp,
                          g.Hq, g.Hkv, g.N, g.NB, static_cast<T*>(dk), static_cast<T*>(dv));
     });
   }
-  if (dc0 || dlam || dgam) {
-    if (!(dc0 && dlam && dgam)) return 3;
+  if (need_coef) {
+    timed("k2_dwq_reduce", st, [&] {
+      hipLaunchKernelGGL(k2_dwq_reduce, dim3((kS + 255) / 256, g.Hq), dim3(256), 0, st, w.dwqs, g.B * w.S, g.Hq,
+                         w.dwq);
+    });
     timed("k2_coef_grad", st, [&] {
-      hipLaunchKernelGGL(k2_coef_grad, dim3(g.Hq), dim3(256), 0, st, w.dwqs, w.coefl, labels, g.B, g.Hq, g.NB,
+      hipLaunchKernelGGL(k2_coef_grad, dim3(g.Hq), dim3(256), 0, st, w.dwq, w.coefl, labels, g.Hq, g.B * g.NB,
                          groups, scale, dc0, dlam, dgam);
     });
   }

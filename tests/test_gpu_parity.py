@@ -284,3 +284,35 @@ def test_bf16_matrix_core_backward_matches_fp32_oracle(batch, n, upstream):
         errs[name] = rel(got, want)
     print(f"bf16 mfma backward B={batch} N={n} {upstream}: " + " ".join(f"{k_}={e:.2e}" for k_, e in errs.items()))
     assert all(e <= BF16_TOL for e in errs.values()), errs
+
+
+@pytest.mark.parametrize("segments", ["1", "3"])
+def test_bf16_backward_state_scan_segmentation_is_invisible(segments, monkeypatch):
+    """The backward state scan runs in S segments (totals, carry, replay) or in
+    one pass; both must give the oracle's gradients (N = 320: 5 chunks, so 3
+    segments are uneven)."""
+    from oal_amd.hd_block_gemm_autograd import grouped_oal
+
+    dev = _dev()
+    monkeypatch.setenv("OAL_BWD_SEGMENTS", segments)
+    inp = _bf16_case(1, 320, seed=9)
+    qb, kb, vb = (inp[nm].to(torch.bfloat16).to(dev).requires_grad_() for nm in ("q", "k", "v"))
+    c0, lam, gam = (inp[nm].to(dev).requires_grad_() for nm in ("c0", "lam", "gam"))
+    out, num, den = grouped_oal(qb, kb, vb, inp["groups"].to(dev), c0, lam, gam, scale=inp["scale"], floor=0.0,
+                                precision="bf16")
+    gen = torch.Generator().manual_seed(10)
+    dnum = torch.randn(num.shape, generator=gen)
+    dden = torch.randn(den.shape, generator=gen)
+    ((num * dnum.to(dev)).sum() + (den * dden.to(dev)).sum()).backward()
+    q32, k32, v32 = (inp[nm].to(torch.bfloat16).float() for nm in ("q", "k", "v"))
+    wq = go.feature_coefficients(inp["groups"], inp["c0"], inp["lam"], inp["gam"], scale=inp["scale"], head_dim=64)
+    _, num_r, den_r = go.chunked_forward(q32, k32, v32, wq, chunk=64)
+    dq_r, dk_r, dv_r, dwq_r = go.chunked_backward(q32, k32, v32, wq, num_r, den_r, None, dnum, dden)
+    dc0_r, dlam_r, dgam_r = go.coefficient_gradients_from_wq(dwq_r, inp["groups"], 8, scale=inp["scale"],
+                                                             head_dim=64)
+    dgam_r = go.symmetrize_gamma_gradient(dgam_r)
+    errs = {name: rel(got, want) for name, got, want in (
+        ("dq", qb.grad, dq_r), ("dk", kb.grad, dk_r), ("dv", vb.grad, dv_r), ("dc0", c0.grad, dc0_r),
+        ("dlam", lam.grad, dlam_r), ("dgam", gam.grad, dgam_r))}
+    print(f"bf16 backward segments={segments}: " + " ".join(f"{k_}={e:.2e}" for k_, e in errs.items()))
+    assert all(e <= BF16_TOL for e in errs.values()), errs
