@@ -55,9 +55,10 @@ struct MfmaWork {
   float* dwq;     // [Hq][kS] their sum
   float* segtot;  // [U][S][kS][65] per-segment dCarry totals
   float* carry;   // [U][S][kS][65] suffix of later segments
+  uint16_t* KT16; // [U][64][NB * 64] bf16 k^T
   float* dqf;     // [B][Hq][N][64] local dq
-  float* dkp;     // [B][Hq][N][64] local dk per query head
-  float* dvp;     // [B][Hq][N][64] local dv per query head
+  float* dkl;     // [U][N][64] local dk, summed over the unit's query heads
+  float* dvl;     // [U][N][64] local dv, summed over the unit's query heads
   float* coefl;   // [Hq][73][B * NB] local (dc0, dlam[8], dgam[8][8]) per chunk
   int S, SL;      // segments of the backward state scan and chunks per segment
   size_t bytes;
@@ -70,6 +71,32 @@ int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, cons
                          const float* num, const float* den, const void* saved, const void* dout, const float* dnum,
                          const float* dden, void* dq, void* dk, void* dv, float* dc0, float* dlam, float* dgam,
                          void* workspace, hipStream_t st, const Timer& timed);
+
+struct LocalBwdArgs {
+  const uint16_t* G16;
+  const float* Gz;
+  const uint16_t* QT16;
+  const uint16_t* GT16;
+  uint16_t* KT16;
+  const float* PZ;
+  const float* PZm;
+  const int32_t* labels;
+  const float* lam;
+  const float* gam;
+  const float* ic;
+  const float* gm;
+  const float* lb;
+  int groups;
+  float scale;
+  float* dqf;
+  float* dkl;
+  float* dvl;
+  float* coefl;  // nullptr when the coefficient gradients are not requested
+};
+
+template <typename T>
+void launch_local_bwd(const LaunchGeom& g, const T* q, const T* k, const T* v, const LocalBwdArgs& a, bool need_dq,
+                      bool need_dkv, hipStream_t st, const Timer& timed);
 
 int run_mfma_selftest(int* dev_errors, hipStream_t st);
 

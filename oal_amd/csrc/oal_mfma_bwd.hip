@@ -1,21 +1,19 @@
 // bf16 matrix-core (MFMA) backward for gfx950.
 //
 // k2_bwd_prep   normalization VJP: G (bf16 token rows and transposed), Gz; transposed q.
-// k2_state_bwd  per (32-slot tile, unit) reverse chunk scan: dT_c = sum_{c'>c}
-//               dCarry_c' in MFMA accumulators (oriented value x slot), with
+// k2_state_bwd  reverse chunk scan per (4 slot tiles, unit, segment):
+//               dT_c = sum_{c'>c} dCarry_c' in MFMA accumulators (value x slot),
 //               dCarry_c = sum_h wq_h * (raw(Q_h)^T [G_h, Gz_h]); the per-slot
 //               feature-coefficient gradient sum_c <P_c, raw(Q)^T G> reduces
 //               inside the accumulator registers. Stores dT in the two k-blocked
 //               layouts of the forward state plus dTz (fp32, natural order).
-// k2_local_bwd  intra-chunk VJP in group-sum form, 4 waves per (head, chunk, unit):
-//               ds = G V^T + Gz, S_g = scale Q_g K^T, kappa; dq_i += scale sum_j
-//               ds_ij kappa'_{g(d)} k_jd written as F_h = (ds o S_h) K (no masks on
-//               the dims), likewise dk, dv = kappa^T G, the local coefficient
-//               gradients, and the denominator part of dq as a quadratic form.
+//               Segments run as totals, carry, replay (k2_seg_carry).
+// (the intra-chunk VJP, k2_local_dq / k2_local_dkv, is in oal_mfma_local.hip)
 // k2_q_fold     dq state part: D^T = P G^T on the MFMA, folded through the query
 //               features (rotated rows, static register indices) + local dq.
 // k2_kv_fold    dk state part (D^T = dT V^T folded through the key features),
 //               dv = raw(K) dT, the dTz quadratic form, + local dk, dv.
+// k2_dwq_reduce sum of the per-segment slot-coefficient partials.
 // k2_coef_grad  per head: slot gradients -> (dc0, dlam, dGam) + local parts.
 //
 // dGam follows the symmetric-Gam convention: off-diagonal entries carry the
@@ -666,8 +664,8 @@ __device__ __forceinline__ void du_group(const float (&x)[kD], __bf16* ring, con
 template <typename T>
 __global__ __launch_bounds__(128) void k2_kv_fold(const T* __restrict__ k, const T* __restrict__ v,
                                                   const uint16_t* __restrict__ dTR, const uint16_t* __restrict__ dTT,
-                                                  const float* __restrict__ dTz, const float* __restrict__ dkp,
-                                                  const float* __restrict__ dvp, int Hq, int Hkv, int N, int NB,
+                                                  const float* __restrict__ dTz, const float* __restrict__ dkl,
+                                                  const float* __restrict__ dvl, int Hq, int Hkv, int N, int NB,
                                                   T* __restrict__ dk, T* __restrict__ dv) {
   __shared__ __attribute__((aligned(16))) __bf16 ring[2 * kFG * 1024];
   __shared__ __attribute__((aligned(16))) __bf16 mz[kD][LD];
@@ -760,13 +758,8 @@ __global__ __launch_bounds__(128) void k2_kv_fold(const T* __restrict__ k, const
   for (int j = 0; j < 32; ++j) {
     const int tj = tok0 + 32 * wv + j;
     if (tj >= N) break;
-    float ksum = dks[32 * wv + j][l], vsum = 0.f;
-    for (int hh = 0; hh < R; ++hh) {
-      const size_t o = ((size_t)(b * Hq + kh * R + hh) * N + tj) * kD + l;
-      ksum += dkp[o];
-      vsum += dvp[o];
-    }
     const size_t o = kbase + (size_t)tj * kD + l;
+    const float ksum = dks[32 * wv + j][l] + dkl[o], vsum = dvl[o];
     dk[o] = from_f<T>(ksum);
     // dv state part lives in the accumulators; add it below
     dks[32 * wv + j][l] = vsum;
@@ -779,333 +772,6 @@ __global__ __launch_bounds__(128) void k2_kv_fold(const T* __restrict__ k, const
       const int j = 32 * wv + c32_row(i, l), tj = tok0 + j;
       if (tj < N) dv[kbase + (size_t)tj * kD + 32 * nt + row] = from_f<T>(acc[nt][i] + dks[j][32 * nt + row]);
     }
-}
-
-// ---------------------------------------------------------------------------
-// Local (intra-chunk) VJP. grid (R, NB, U), 4 waves (256 threads).
-// 16x16x32 MFMA tiles; tile (ti, tj) covers tokens i in 16ti.., j in 16tj...
-// ---------------------------------------------------------------------------
-template <typename T>
-__global__ __launch_bounds__(256) void k2_local_bwd(const T* __restrict__ q, const T* __restrict__ k,
-                                                    const T* __restrict__ v, const uint16_t* __restrict__ G16,
-                                                    const float* __restrict__ Gz, const float* __restrict__ PZ,
-                                                    const int32_t* __restrict__ labels, const float* __restrict__ c0,
-                                                    const float* __restrict__ lam, const float* __restrict__ gam,
-                                                    int G, int Hq, int Hkv, int N, int NB, float scale,
-                                                    float* __restrict__ dqf, float* __restrict__ dkp,
-                                                    float* __restrict__ dvp, float* __restrict__ coefl) {
-  __shared__ __attribute__((aligned(16))) __bf16 Qr[kC][LD];
-  __shared__ __attribute__((aligned(16))) __bf16 Kr[kC][LD];
-  __shared__ __attribute__((aligned(16))) __bf16 Vr[kC][LD];
-  __shared__ __attribute__((aligned(16))) __bf16 Gr[kC][LD];
-  __shared__ __attribute__((aligned(16))) __bf16 TT[kC][LD];  // pz (fp32) first, then K^T, Q^T, G^T
-  __shared__ __attribute__((aligned(16))) __bf16 dsm[kC][LD];
-  __shared__ __attribute__((aligned(16))) __bf16 kapT[kC][LD];
-  __shared__ __attribute__((aligned(16))) __bf16 XW[4][16][LD];  // Mz first
-  __shared__ float gzl[kC], bz[kD];
-  __shared__ int lab[kD];
-  __shared__ float lamh[8], gamh[64];
-  __shared__ float cpart[4][1 + 8 + 64];
-  static_assert(sizeof(TT) >= kFP * sizeof(float), "pz staging must fit the transpose buffer");
-
-  int hh, ch, u;
-  head_chunk_unit(Hq / Hkv, NB, (int)(gridDim.x / ((Hq / Hkv) * NB)), hh, ch, u);
-  const int R = Hq / Hkv, b = u / Hkv, kh = u % Hkv, h = kh * R + hh;
-  const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63;
-  const int r16 = l & 15, g16 = l >> 4;
-  const int tok0 = ch * kC;
-  const size_t qbase = (size_t)(b * Hq + h) * N * kD;
-  const size_t kbase = (size_t)u * N * kD;
-  float* pzl = reinterpret_cast<float*>(&TT[0][0]);
-  __bf16(*mz)[LD] = reinterpret_cast<__bf16(*)[LD]>(&XW[0][0][0]);
-
-  // --- stage rows ------------------------------------------------------------
-  {
-    const int tok = tok0 + l;
-    const bool ok = tok < N;
-    const int tc = ok ? tok : N - 1;
-    bf16x8 r[8];
-    if (wv == 0) {
-      load_row_b(q, qbase + (size_t)tc * kD, ok, r);
-      store_row(&Qr[l][0], r);
-    } else if (wv == 1) {
-      load_row_b(k, kbase + (size_t)tc * kD, ok, r);
-      store_row(&Kr[l][0], r);
-    } else if (wv == 2) {
-      load_row_b(v, kbase + (size_t)tc * kD, ok, r);
-      store_row(&Vr[l][0], r);
-    } else {
-      load_row_b(G16, qbase + (size_t)tc * kD, ok, r);
-      store_row(&Gr[l][0], r);
-      gzl[l] = ok ? Gz[(size_t)(b * Hq + h) * N + tc] : 0.f;
-      int g = labels[h * kD + l];
-      lab[l] = g < 0 ? 0 : (g >= G ? G - 1 : g);
-      if (l < G) lamh[l] = lam[(size_t)h * G + l];
-      if (l < G * G) gamh[l] = gam[(size_t)h * G * G + l];
-    }
-    const float* pz = PZ + ((size_t)u * NB + ch) * kFP;
-    for (int i = tid; i < kFP / 4; i += 256) reinterpret_cast<float4*>(pzl)[i] = reinterpret_cast<const float4*>(pz)[i];
-  }
-  __syncthreads();
-  const float sc2 = scale * scale;
-  for (int idx = tid; idx < kD * kD; idx += 256) {
-    const int r = idx >> 6, c = idx & 63;
-    const int hi = r > c ? r : c, lo = r > c ? c : r;
-    mz[r][c] = (__bf16)(sc2 * gamh[lab[r] * G + lab[c]] * pzl[1 + kD + pair_index(hi, lo)]);
-  }
-  if (tid < kD) bz[tid] = scale * lamh[lab[tid]] * pzl[1 + tid];
-  __syncthreads();
-
-  // --- dq denominator part for row tile ti = wv: gz_i (bz + 2 Mz q_i) -------
-  f32x4 dqa[4];
-  {
-    const int ti = wv;
-#pragma unroll
-    for (int nt = 0; nt < 4; ++nt) {
-      f32x4 z = f32x4{};
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-        const bf16x8 a = *reinterpret_cast<const bf16x8*>(&Qr[16 * ti + r16][32 * kk + 8 * g16]);
-        const bf16x8 bb = *reinterpret_cast<const bf16x8*>(&mz[16 * nt + r16][32 * kk + 8 * g16]);
-        z = mfma16(a, bb, z);
-      }
-      const int d = 16 * nt + r16;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int ii = 16 * ti + c16_row(i, l);
-        dqa[nt][i] = gzl[ii] * (bz[d] + 2.f * z[i]);
-      }
-    }
-  }
-  __syncthreads();  // mz (aliased with XW) is dead
-
-  // group masks of the A-fragment dims d = 32 kk + 8 g16 + j
-  auto group_mask = [&](int g, int kk, int w) -> uint32_t {
-    const int d = 32 * kk + 8 * g16 + 2 * w;
-    return (lab[d] == g ? 0x0000ffffu : 0u) | (lab[d + 1] == g ? 0xffff0000u : 0u);
-  };
-  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-  auto s_tile = [&](int ti, int tj, int g) -> f32x4 {
-    f32x4 acc = f32x4{};
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      const u32x4 qa = *reinterpret_cast<const u32x4*>(&Qr[16 * ti + r16][32 * kk + 8 * g16]);
-      const bf16x8 kb = *reinterpret_cast<const bf16x8*>(&Kr[16 * tj + r16][32 * kk + 8 * g16]);
-      const u32x4 m = {group_mask(g, kk, 0), group_mask(g, kk, 1), group_mask(g, kk, 2), group_mask(g, kk, 3)};
-      acc = mfma16(__builtin_bit_cast(bf16x8, qa & m), kb, acc);
-    }
-    return acc * scale;
-  };
-
-  // --- sweep 1: ds, kappa, local coefficient gradients ------------------------
-  {
-    float cacc[1 + 8 + 64];
-#pragma unroll
-    for (int i = 0; i < 73; ++i) cacc[i] = 0.f;
-    // the 10 lower tiles, listed (3,0..3), (2,0..2), (1,0..1), (0,0); wave w takes w, w+4, w+8
-    for (int tt = 0; tt < 3; ++tt) {
-      const int idx = wv + 4 * tt;
-      if (idx >= 10) continue;
-      const int ti = idx < 4 ? 3 : idx < 7 ? 2 : idx < 9 ? 1 : 0;
-      const int tj = idx < 4 ? idx : idx < 7 ? idx - 4 : idx < 9 ? idx - 7 : 0;
-      // ds tile = G V^T + gz
-      f32x4 ds = f32x4{};
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-        const bf16x8 a = *reinterpret_cast<const bf16x8*>(&Gr[16 * ti + r16][32 * kk + 8 * g16]);
-        const bf16x8 bb = *reinterpret_cast<const bf16x8*>(&Vr[16 * tj + r16][32 * kk + 8 * g16]);
-        ds = mfma16(a, bb, ds);
-      }
-      f32x4 sg[8];
-#pragma unroll
-      for (int g = 0; g < 8; ++g) sg[g] = g < G ? s_tile(ti, tj, g) : f32x4{};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int ii = 16 * ti + c16_row(i, l), jj = 16 * tj + r16;
-        const bool live = jj <= ii && tok0 + ii < N;
-        const float dsv = live ? ds[i] + gzl[ii] : 0.f;
-        float kv = 0.f;
-        if (live) {
-          kv = c0[h];
-#pragma unroll
-          for (int g = 0; g < 8; ++g) {
-            if (g < G) {
-              float inner = lamh[g];
-#pragma unroll
-              for (int g2 = 0; g2 < 8; ++g2)
-                if (g2 < G) inner += gamh[g * G + g2] * sg[g2][i];
-              kv += sg[g][i] * inner;
-            }
-          }
-        }
-        dsm[ii][jj] = (__bf16)dsv;
-        kapT[jj][ii] = (__bf16)kv;
-        if (tj < ti) {
-          dsm[16 * tj + c16_row(i, l)][16 * ti + r16] = (__bf16)0.f;
-          kapT[16 * ti + r16][16 * tj + c16_row(i, l)] = (__bf16)0.f;
-        }
-        cacc[0] += dsv;
-#pragma unroll
-        for (int g = 0; g < 8; ++g) {
-          const float t = dsv * sg[g][i];
-          cacc[1 + g] += t;
-#pragma unroll
-          for (int g2 = 0; g2 < 8; ++g2) cacc[9 + 8 * g + g2] += t * sg[g2][i];
-        }
-      }
-    }
-    // the strictly upper tiles are zero in dsm (row < col blocks)
-    for (int idx = tid; idx < 6 * 256; idx += 256) {
-      const int t = idx >> 8, e = idx & 255;
-      // strictly upper tiles (0,1) (0,2) (0,3) (1,2) (1,3) (2,3)
-      const int ti = t < 3 ? 0 : t < 5 ? 1 : 2;
-      const int tj = t < 3 ? t + 1 : t < 5 ? t - 1 : 3;
-      dsm[16 * ti + (e >> 4)][16 * tj + (e & 15)] = (__bf16)0.f;
-      kapT[16 * tj + (e & 15)][16 * ti + (e >> 4)] = (__bf16)0.f;
-    }
-#pragma unroll
-    for (int i = 0; i < 73; ++i) {
-      const float t = wave_sum(cacc[i]);
-      if (l == 0) cpart[wv][i] = t;
-    }
-  }
-  __syncthreads();
-  if (tid < 73) {
-    // column-major partials [Hq][73][B * NB] so that the final reduction reads
-    // each column contiguously
-    const size_t bn = (size_t)(gridDim.x / ((Hq / Hkv) * NB) / Hkv) * NB;
-    coefl[((size_t)h * 73 + tid) * bn + (size_t)b * NB + ch] =
-        (cpart[0][tid] + cpart[1][tid]) + (cpart[2][tid] + cpart[3][tid]);
-  }
-  // K^T into TT
-  for (int idx = tid; idx < kC * kD; idx += 256) {
-    const int j = idx & 63, d = idx >> 6;
-    TT[d][j] = Kr[j][d];
-  }
-  __syncthreads();
-
-  // per-column coefficients of the F_h combination (d = 16 nt + r16)
-  auto comb = [&](int nt, int hgrp) -> float {
-    const int d = 16 * nt + r16;
-    return hgrp < G ? 2.f * scale * gamh[lab[d] * G + hgrp] : scale * lamh[lab[d]];
-  };
-
-  // --- sweep 2: dq local for row tile ti = wv -----------------------------------
-  {
-    const int ti = wv;
-    const int nk = (16 * (ti + 1) + 31) / 32;
-    for (int hg = 0; hg <= G; ++hg) {
-      // X row tile: ds o S_h (or ds for the lambda term), zero beyond the causal range
-      for (int tj = 0; tj < 2 * nk; ++tj) {
-        f32x4 xs = f32x4{};
-        if (tj <= ti) {
-          const f32x4 sgt = hg < G ? s_tile(ti, tj, hg) : f32x4{1.f, 1.f, 1.f, 1.f};
-#pragma unroll
-          for (int i = 0; i < 4; ++i) xs[i] = (float)dsm[16 * ti + c16_row(i, l)][16 * tj + r16] * sgt[i];
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) XW[wv][c16_row(i, l)][16 * tj + r16] = (__bf16)xs[i];
-      }
-      __builtin_amdgcn_wave_barrier();
-#pragma unroll
-      for (int nt = 0; nt < 4; ++nt) {
-        f32x4 f = f32x4{};
-        for (int kk = 0; kk < nk; ++kk) {
-          const bf16x8 a = *reinterpret_cast<const bf16x8*>(&XW[wv][r16][32 * kk + 8 * g16]);
-          const bf16x8 bb = *reinterpret_cast<const bf16x8*>(&TT[16 * nt + r16][32 * kk + 8 * g16]);
-          f = mfma16(a, bb, f);
-        }
-        const float cf = comb(nt, hg);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) dqa[nt][i] += cf * f[i];
-      }
-      __builtin_amdgcn_wave_barrier();
-    }
-#pragma unroll
-    for (int nt = 0; nt < 4; ++nt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int tok = tok0 + 16 * ti + c16_row(i, l);
-        if (tok < N) dqf[qbase + (size_t)tok * kD + 16 * nt + r16] = dqa[nt][i];
-      }
-  }
-  __syncthreads();
-  // Q^T into TT
-  for (int idx = tid; idx < kC * kD; idx += 256) {
-    const int j = idx & 63, d = idx >> 6;
-    TT[d][j] = Qr[j][d];
-  }
-  __syncthreads();
-
-  // --- sweep 3: dk local for column tile tj = wv ---------------------------------
-  {
-    const int tj = wv;
-    const int k0 = tj / 2;  // first 32-wide k-step over i
-    f32x4 dka[4];
-#pragma unroll
-    for (int nt = 0; nt < 4; ++nt) dka[nt] = f32x4{};
-    for (int hg = 0; hg <= G; ++hg) {
-      // X^T column tile: XW[wv][j][i] = ds_ij (S_h)_ij for i >= j
-      for (int ti = 2 * k0; ti < 4; ++ti) {
-        f32x4 xs = f32x4{};
-        if (ti >= tj) {
-          const f32x4 sgt = hg < G ? s_tile(ti, tj, hg) : f32x4{1.f, 1.f, 1.f, 1.f};
-#pragma unroll
-          for (int i = 0; i < 4; ++i) xs[i] = (float)dsm[16 * ti + c16_row(i, l)][16 * tj + r16] * sgt[i];
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) XW[wv][r16][16 * ti + c16_row(i, l)] = (__bf16)xs[i];
-      }
-      __builtin_amdgcn_wave_barrier();
-#pragma unroll
-      for (int nt = 0; nt < 4; ++nt) {
-        f32x4 f = f32x4{};
-        for (int kk = k0; kk < 2; ++kk) {
-          const bf16x8 a = *reinterpret_cast<const bf16x8*>(&XW[wv][r16][32 * kk + 8 * g16]);
-          const bf16x8 bb = *reinterpret_cast<const bf16x8*>(&TT[16 * nt + r16][32 * kk + 8 * g16]);
-          f = mfma16(a, bb, f);
-        }
-        const float cf = comb(nt, hg);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) dka[nt][i] += cf * f[i];
-      }
-      __builtin_amdgcn_wave_barrier();
-    }
-#pragma unroll
-    for (int nt = 0; nt < 4; ++nt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int tok = tok0 + 16 * tj + c16_row(i, l);
-        if (tok < N) dkp[qbase + (size_t)tok * kD + 16 * nt + r16] = dka[nt][i];
-      }
-  }
-  __syncthreads();
-  // G^T into TT
-  for (int idx = tid; idx < kC * kD; idx += 256) {
-    const int j = idx & 63, e = idx >> 6;
-    TT[e][j] = Gr[j][e];
-  }
-  __syncthreads();
-
-  // --- sweep 4: dv local = kappa^T G for column tile tj = wv ----------------------
-  {
-    const int tj = wv;
-    const int k0 = tj / 2;
-#pragma unroll
-    for (int nt = 0; nt < 4; ++nt) {
-      f32x4 f = f32x4{};
-      for (int kk = k0; kk < 2; ++kk) {
-        const bf16x8 a = *reinterpret_cast<const bf16x8*>(&kapT[16 * tj + r16][32 * kk + 8 * g16]);
-        const bf16x8 bb = *reinterpret_cast<const bf16x8*>(&TT[16 * nt + r16][32 * kk + 8 * g16]);
-        f = mfma16(a, bb, f);
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int tok = tok0 + 16 * tj + c16_row(i, l);
-        if (tok < N) dvp[qbase + (size_t)tok * kD + 16 * nt + r16] = f[i];
-      }
-    }
-  }
 }
 
 // dwq[h][slot] = sum over (segment, batch) of the state-scan partials, fixed order.
@@ -1228,9 +894,10 @@ MfmaWork mfma_work_view(void* base, int B, int Hq, int U, int N, int NB) {
   const size_t seg = w.S > 1 ? sizeof(float) * (size_t)U * w.S * kS * 65 : 0;
   w.segtot = static_cast<float*>(take(seg));
   w.carry = static_cast<float*>(take(seg));
+  w.KT16 = static_cast<uint16_t*>(take((size_t)U * kD * NB * kC * sizeof(uint16_t)));
   w.dqf = static_cast<float*>(take(rows * kD * sizeof(float)));
-  w.dkp = static_cast<float*>(take(rows * kD * sizeof(float)));
-  w.dvp = static_cast<float*>(take(rows * kD * sizeof(float)));
+  w.dkl = static_cast<float*>(take((size_t)U * N * kD * sizeof(float)));
+  w.dvl = static_cast<float*>(take((size_t)U * N * kD * sizeof(float)));
   w.coefl = static_cast<float*>(take(sizeof(float) * (size_t)B * Hq * NB * 73));
   w.bytes = off;
   return w;
@@ -1273,10 +940,11 @@ int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, cons
                          g.Hq, g.Hkv, g.N, g.NB, w.SL, w.S, w.dTT, w.dTR, w.dTz, nullptr, nullptr);
     });
   }
-  timed("k2_local_bwd", st, [&] {
-    hipLaunchKernelGGL(k2_local_bwd<T>, dim3(g.R * g.NB * g.U), dim3(256), 0, st, qt, kt, vt, w.G16, w.Gz, sv.PZ,
-                       labels, c0, lam, gam, groups, g.Hq, g.Hkv, g.N, g.NB, scale, w.dqf, w.dkp, w.dvp, w.coefl);
-  });
+  {
+    LocalBwdArgs la{w.G16, w.Gz, w.QT16, w.GT16, w.KT16, sv.PZ, sv.PZm, labels, lam, gam, sv.ic, sv.gm, sv.lb,
+                    groups, scale, w.dqf, w.dkl, w.dvl, need_coef ? w.coefl : nullptr};
+    launch_local_bwd<T>(g, qt, kt, vt, la, dq != nullptr, dk != nullptr, st, timed);
+  }
   if (dq) {
     timed("k2_q_fold", st, [&] {
       hipLaunchKernelGGL(k2_q_fold<T>, dim3(g.R * g.NB * g.U), dim3(128), 0, st, qt, w.G16, sv.wqs, sv.PR, w.dqf,
@@ -1285,7 +953,7 @@ int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, cons
   }
   if (dk) {
     timed("k2_kv_fold", st, [&] {
-      hipLaunchKernelGGL(k2_kv_fold<T>, dim3(g.NB, g.U), dim3(128), 0, st, kt, vt, w.dTR, w.dTT, w.dTz, w.dkp, w.dvp,
+      hipLaunchKernelGGL(k2_kv_fold<T>, dim3(g.NB, g.U), dim3(128), 0, st, kt, vt, w.dTR, w.dTT, w.dTz, w.dkl, w.dvl,
                          g.Hq, g.Hkv, g.N, g.NB, static_cast<T*>(dk), static_cast<T*>(dv));
     });
   }

@@ -1,0 +1,580 @@
+// Intra-chunk (local) VJP of the bf16 matrix-core backward for gfx950.
+//
+// For one chunk, with s_g(i,j) = scale * sum_{d in g} q_i[d] k_j[d] and
+// ds(i,j) = g_i . v_j + gz_i  (j <= i; g, gz from the normalization VJP):
+//   dq_i[d] += scale lam_g(d) sum_j ds k_j[d] + 2 scale sum_h Gam_g(d)h sum_j ds s_h k_j[d]
+//   dk_j[d] += the same with q_i in place of k_j (summed over the query heads)
+//   dv_j    += sum_i kappa(i,j) g_i
+//   dc0 += sum ds,  dlam_g += sum ds s_g,  dGam_gh += sum ds s_g s_h
+// (reference: closed-form state VJP grouped_reference.py:214-318 and the local
+// score terms of hd_block_gemm_backward_wave.py:253-477, here in group-sum form).
+// The 64x64 chunk is covered by three lower 32x32 tiles (key tile jt, query
+// tile it) = (0,0), (0,1), (1,1). Group sums and ds come from
+// v_mfma_f32_32x32x16_bf16 on row-major operands; their accumulators are fed
+// straight back into the MFMA as the K-major operand of the dq / dk / dv
+// products, whose other operand is the transposed bf16 copy of K, q or G.
+//
+// k2_kt_prep     K^T (bf16) per unit, the B operand of the dq products.
+// k2_local_dq    one block per (query head, chunk): dq local part and the state
+//                part of the denominator's dq (gz_i (bz + 2 Mz q_i)).
+// k2_local_dk    one block per (unit, chunk): dk local part summed over the
+//                unit's query heads in registers (group sums one at a time).
+// k2_local_dv    one block per (unit, chunk): kappa and the dv local part,
+//                summed over the unit's query heads, and the per-(head, chunk)
+//                coefficient partials.
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "oal_internal.hpp"
+#include "oal_mfma_common.hpp"
+
+namespace oal {
+
+namespace {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// 8 consecutive elements of a row as a bf16 fragment (zeros when !ok).
+__device__ __forceinline__ bf16x8 row8(const uint16_t* __restrict__ p, bool ok) {
+  const bf16x8 x = *reinterpret_cast<const bf16x8*>(p);
+  return ok ? x : bf16x8{};
+}
+__device__ __forceinline__ bf16x8 row8(const float* __restrict__ p, bool ok) {
+  const float4 a = reinterpret_cast<const float4*>(p)[0], b = reinterpret_cast<const float4*>(p)[1];
+  float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  const bf16x8 x = pack8(v);
+  return ok ? x : bf16x8{};
+}
+
+// K-step t (rows 16 t .. 16 t + 15) of a 32-row accumulator tile as an MFMA
+// operand whose K index is the accumulator row: lane group s must hold rows
+// 16 t + 8 s .. + 7; the accumulator gives it rows 16 t + 4 s + (0..3) and
+// 16 t + 8 + 4 s + (0..3), so one quad is exchanged with the other lane group.
+__device__ __forceinline__ bf16x8 acc_kfrag(const float (&x)[16], int t, int s) {
+  const uint32_t a0 = pack_bf16x2(x[8 * t + 0], x[8 * t + 1]);
+  const uint32_t a1 = pack_bf16x2(x[8 * t + 2], x[8 * t + 3]);
+  const uint32_t b0 = pack_bf16x2(x[8 * t + 4], x[8 * t + 5]);
+  const uint32_t b1 = pack_bf16x2(x[8 * t + 6], x[8 * t + 7]);
+  const uint32_t r0 = __shfl_xor(s ? a0 : b0, 32, 64);
+  const uint32_t r1 = __shfl_xor(s ? a1 : b1, 32, 64);
+  const u32x4 fr = s ? u32x4{r0, r1, b0, b1} : u32x4{a0, a1, r0, r1};
+  return __builtin_bit_cast(bf16x8, fr);
+}
+
+__device__ __forceinline__ int clamp_label(int g, int G) { return g < 0 ? 0 : (g >= G ? G - 1 : g); }
+
+// Group mask table for fragments covering dims d, d + 1 with
+// d = 16 kk + 8 ss + 2 w: entry [kk][g][ss][w]; 256 entries, one per thread.
+__device__ __forceinline__ void build_masks(uint32_t (*mk)[8][2][4], const int32_t* __restrict__ labels, int h,
+                                            int G, int t0) {
+  for (int t = t0; t < 256; t += blockDim.x) {
+    const int kk = t >> 6, g = (t >> 3) & 7, ss = (t >> 2) & 1, w = t & 3;
+    const int d = 16 * kk + 8 * ss + 2 * w;
+    const int g0 = clamp_label(labels[h * kD + d], G), g1 = clamp_label(labels[h * kD + d + 1], G);
+    mk[kk][g][ss][w] = (g0 == g ? 0x0000ffffu : 0u) | (g1 == g ? 0xffff0000u : 0u);
+  }
+}
+
+__device__ __forceinline__ bf16x8 masked(bf16x8 f, const uint32_t* m) {
+  const u32x4 mm = *reinterpret_cast<const u32x4*>(m);
+  return __builtin_bit_cast(bf16x8, __builtin_bit_cast(u32x4, f) & mm);
+}
+
+// Tile pair tp -> (key tile jt, query tile it).
+__device__ __forceinline__ int tile_jt(int tp) { return tp == 2 ? 1 : 0; }
+__device__ __forceinline__ int tile_it(int tp) { return tp == 0 ? 0 : 1; }
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// K^T per unit: KT16 [U][64][NB * 64] bf16 (tokens >= N are zero).
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void k2_kt_prep(const T* __restrict__ k, int N, int NB,
+                                                  uint16_t* __restrict__ KT16) {
+  __shared__ __attribute__((aligned(16))) __bf16 kT[kD][kC + 8];
+  const int u = blockIdx.x / NB, ch = blockIdx.x % NB;
+  const int tid = threadIdx.x, j = tid >> 2, qq = tid & 3;
+  const int tok = ch * kC + j;
+  const bool ok = tok < N;
+  const T* src = k + ((size_t)u * N + (ok ? tok : N - 1)) * kD + 16 * qq;
+  const bf16x8 a = row8(src, ok), b = row8(src + 8, ok);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    kT[16 * qq + e][j] = a[e];
+    kT[16 * qq + 8 + e][j] = b[e];
+  }
+  __syncthreads();
+  const size_t np = (size_t)NB * kC;
+  for (int idx = tid; idx < kD * 8; idx += 256) {
+    const int r = idx >> 3, c8 = idx & 7;
+    *reinterpret_cast<bf16x8*>(KT16 + ((size_t)u * kD + r) * np + (size_t)ch * kC + 8 * c8) =
+        *reinterpret_cast<const bf16x8*>(&kT[r][8 * c8]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dq local part + denominator-state dq, one block per (query head, chunk),
+// grid R * NB * U (XCD-ordered), 3 waves = tile pairs 0..2 (orientation
+// C[j][i] for the group sums; dq accumulators C[i][d], lane = d):
+//   dq[i][d] = sum_h coef_h(d) sum_j X_h[i][j] K[j][d], X_h = ds o s_h, X_8 = ds
+// with s_h computed one group at a time; waves 0 and 1 (query tiles 0, 1) add
+// gz_i (bz_d + 2 (Mz q_i)_d), Mz = gm o PZm, and write dqf.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(192) void k2_local_dq(const T* __restrict__ q, const T* __restrict__ k,
+                                                   const T* __restrict__ v, const uint16_t* __restrict__ G16,
+                                                   const float* __restrict__ Gz, const uint16_t* __restrict__ KT16,
+                                                   const float* __restrict__ PZ, const float* __restrict__ PZm,
+                                                   const int32_t* __restrict__ labels, const float* __restrict__ lam,
+                                                   const float* __restrict__ gam, const float* __restrict__ gm,
+                                                   const float* __restrict__ lb, int G, int Hq, int Hkv, int N,
+                                                   int NB, float scale, float* __restrict__ dqf) {
+  constexpr int LD = kD + 8;
+  __shared__ __attribute__((aligned(16))) uint32_t mk[4][8][2][4];
+  __shared__ __attribute__((aligned(16))) __bf16 Mz[kD][LD];
+  __shared__ float bz[kD];
+  __shared__ float red[2][16][64];  // wave 2's dq (query tile 1)
+
+  int hh, ch, u;
+  head_chunk_unit(Hq / Hkv, NB, (int)(gridDim.x / ((Hq / Hkv) * NB)), hh, ch, u);
+  const int R = Hq / Hkv, b = u / Hkv, kh = u % Hkv, h = kh * R + hh;
+  const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, s = l >> 5, row = l & 31;
+  const int tok0 = ch * kC;
+  const size_t qbase = (size_t)(b * Hq + h) * N * kD;
+  const size_t kbase = (size_t)u * N * kD;
+  const size_t cbase = (size_t)u * NB + ch;
+  const size_t np = (size_t)NB * kC;
+
+  build_masks(mk, labels, h, G, tid);
+  for (int e = tid; e < kD * 4; e += 192) {
+    // Mz = gm o PZm (bf16): row r = e / 4, columns 16 (e % 4) .. + 15
+    const int r = e >> 2, qq = e & 3;
+    const float4* gp = reinterpret_cast<const float4*>(gm + ((size_t)h * kD + r) * kD + 16 * qq);
+    const float4* zp = reinterpret_cast<const float4*>(PZm + (cbase * kD + r) * kD + 16 * qq);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const float4 g0 = gp[2 * i], g1 = gp[2 * i + 1], z0 = zp[2 * i], z1 = zp[2 * i + 1];
+      float y[8] = {g0.x * z0.x, g0.y * z0.y, g0.z * z0.z, g0.w * z0.w,
+                    g1.x * z1.x, g1.y * z1.y, g1.z * z1.z, g1.w * z1.w};
+      *reinterpret_cast<bf16x8*>(&Mz[r][16 * qq + 8 * i]) = pack8(y);
+    }
+  }
+  if (tid < kD) bz[tid] = lb[(size_t)h * kD + tid] * PZ[cbase * kFP + 1 + tid];
+  __syncthreads();
+
+  const int tp = wv, jt = tile_jt(tp), it = tile_it(tp);
+  const int jr = tok0 + 32 * jt + row, ir = tok0 + 32 * it + row;  // this lane's operand rows
+  const bool jok = jr < N, iok = ir < N;
+  const size_t jo = (size_t)(jok ? jr : N - 1) * kD, io = (size_t)(iok ? ir : N - 1) * kD;
+  bf16x8 kf[4], qf[4];
+  f32x16 ds = f32x16{};
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) {
+    const int c = 16 * kk + 8 * s;
+    kf[kk] = row8(k + kbase + jo + c, jok);
+    qf[kk] = row8(q + qbase + io + c, iok);
+    ds = mfma32(row8(v + kbase + jo + c, jok), row8(G16 + qbase + io + c, iok), ds);
+  }
+  // lane column i = 32 it + row; register rows j = 32 jt + c32_row(r)
+  const int i = 32 * it + row;
+  const bool icol = tok0 + i < N;
+  const float gzi = icol ? Gz[(size_t)(b * Hq + h) * N + tok0 + i] : 0.f;
+  float dsv[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int j = 32 * jt + c32_row(r, l);
+    dsv[r] = (j <= i && icol) ? ds[r] + gzi : 0.f;
+  }
+  bf16x8 kt[2][2];
+#pragma unroll
+  for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+      kt[dt][t] = *reinterpret_cast<const bf16x8*>(KT16 + ((size_t)u * kD + 32 * dt + row) * np + tok0 + 32 * jt +
+                                                    16 * t + 8 * s);
+  float cf[9][2];
+#pragma unroll
+  for (int dt = 0; dt < 2; ++dt) {
+    const int gd = clamp_label(labels[h * kD + 32 * dt + row], G);
+#pragma unroll
+    for (int h2 = 0; h2 < 8; ++h2) cf[h2][dt] = h2 < G ? 2.f * scale * gam[((size_t)h * G + gd) * G + h2] : 0.f;
+    cf[8][dt] = scale * lam[(size_t)h * G + gd];
+  }
+  f32x16 dq[2] = {f32x16{}, f32x16{}};
+#pragma unroll
+  for (int h2 = 0; h2 < 9; ++h2) {
+    float x[16];
+    if (h2 < 8) {
+      f32x16 sh = f32x16{};
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) sh = mfma32(masked(kf[kk], &mk[kk][h2][s][0]), qf[kk], sh);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) x[r] = dsv[r] * (scale * sh[r]);
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) x[r] = dsv[r];
+    }
+    const bf16x8 f0 = acc_kfrag(x, 0, s), f1 = acc_kfrag(x, 1, s);
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt) {
+      f32x16 p = mfma32(f0, kt[dt][0], f32x16{});
+      p = mfma32(f1, kt[dt][1], p);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) dq[dt][r] = fmaf(cf[h2][dt], p[r], dq[dt][r]);
+    }
+  }
+  if (wv == 2) {
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) red[dt][r][l] = dq[dt][r];
+  } else {
+    // den-state dq of query tile it = wv: gz_i (bz_d + 2 Z[i][d]), Z = q Mz; the
+    // query fragments qf are this lane's row i = 32 it + row
+    float gzr[16];
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+      const int i0 = tok0 + 32 * it + 8 * a + 4 * s;
+#pragma unroll
+      for (int vv = 0; vv < 4; ++vv) gzr[4 * a + vv] = i0 + vv < N ? Gz[(size_t)(b * Hq + h) * N + i0 + vv] : 0.f;
+    }
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt) {
+      f32x16 z = f32x16{};
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk)
+        z = mfma32(qf[kk], *reinterpret_cast<const bf16x8*>(&Mz[32 * dt + row][16 * kk + 8 * s]), z);
+      const float bzd = bz[32 * dt + row];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) dq[dt][r] = fmaf(gzr[r], bzd + 2.f * z[r], dq[dt][r]);
+    }
+  }
+  __syncthreads();
+  if (wv < 2) {
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float x = dq[dt][r];
+        if (wv == 1) x += red[dt][r][l];
+        const int tok = tok0 + 32 * wv + c32_row(r, l);
+        if (tok < N) dqf[qbase + (size_t)tok * kD + 32 * dt + row] = x;
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dk and dv local parts, one block per (unit, chunk), 3 waves (tile pairs),
+// summed over the unit's query heads in registers (orientation C[i][j],
+// lane = key token j). Outputs dkl / dvl [U][N][64] (f32).
+// ---------------------------------------------------------------------------
+struct LocalTile {
+  int tp, jt, it, j, ir, jr;
+  bool iok, jok;
+  size_t io, jo;
+};
+
+__device__ __forceinline__ LocalTile local_tile(int tp, int tok0, int N, int row) {
+  LocalTile t;
+  t.tp = tp;
+  t.jt = tile_jt(tp);
+  t.it = tile_it(tp);
+  t.j = 32 * t.jt + row;
+  t.ir = tok0 + 32 * t.it + row;
+  t.jr = tok0 + 32 * t.jt + row;
+  t.iok = t.ir < N;
+  t.jok = t.jr < N;
+  t.io = (size_t)(t.iok ? t.ir : N - 1) * kD;
+  t.jo = (size_t)(t.jok ? t.jr : N - 1) * kD;
+  return t;
+}
+
+__device__ __forceinline__ int unit_chunk_block(int NB, int& ch) {
+  const int total = gridDim.x, id = blockIdx.x;
+  const int wid = (total & 7) == 0 ? (id & 7) * (total >> 3) + (id >> 3) : id;
+  ch = wid % NB;
+  return wid / NB;
+}
+
+// Combine tile pair 1 into tile pair 0 (both key tile 0) and write out[j][e].
+__device__ __forceinline__ void local_write(float (*red)[16][64], const f32x16 (&acc)[2], const LocalTile& t,
+                                           int l, int row, int tok0, int N, size_t kbase, float* __restrict__ out) {
+  if (t.tp == 1) {
+#pragma unroll
+    for (int n = 0; n < 2; ++n)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) red[n][r][l] = acc[n][r];
+  }
+  __syncthreads();
+  if (t.tp != 1) {
+#pragma unroll
+    for (int n = 0; n < 2; ++n)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float x = acc[n][r];
+        if (t.tp == 0) x += red[n][r][l];
+        const int tok = tok0 + 32 * t.jt + c32_row(r, l);
+        if (tok < N) out[kbase + (size_t)tok * kD + 32 * n + row] = x;
+      }
+  }
+}
+
+// dk[j][d] += sum_h coef_h(d) sum_i X_h[i][j] q_i[d], X_h = ds o s_h, X_8 = ds,
+// with s_h computed one group at a time.
+template <typename T>
+__global__ __launch_bounds__(192) void k2_local_dk(const T* __restrict__ q, const T* __restrict__ k,
+                                                   const T* __restrict__ v, const uint16_t* __restrict__ G16,
+                                                   const float* __restrict__ Gz, const uint16_t* __restrict__ QT16,
+                                                   const int32_t* __restrict__ labels, const float* __restrict__ lam,
+                                                   const float* __restrict__ gam, int G, int Hq, int Hkv, int N,
+                                                   int NB, float scale, float* __restrict__ dkl) {
+  __shared__ __attribute__((aligned(16))) uint32_t mk[2][4][8][2][4];
+  __shared__ float red[2][16][64];
+  int ch;
+  const int u = unit_chunk_block(NB, ch);
+  const int R = Hq / Hkv, b = u / Hkv, kh = u % Hkv;
+  const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, s = l >> 5, row = l & 31;
+  const int tok0 = ch * kC;
+  const size_t kbase = (size_t)u * N * kD;
+  const size_t np = (size_t)NB * kC;
+  const LocalTile t = local_tile(wv, tok0, N, row);
+  f32x16 acc[2] = {f32x16{}, f32x16{}};
+
+  build_masks(mk[0], labels, kh * R, G, tid);
+  __syncthreads();
+  for (int hh = 0; hh < R; ++hh) {
+    const int h = kh * R + hh, mb = hh & 1;
+    if (hh + 1 < R) build_masks(mk[mb ^ 1], labels, h + 1, G, tid);
+    const size_t qbase = (size_t)(b * Hq + h) * N * kD;
+    // ds[i][j] = g_i . v_j + gz_i on live (j <= i, i < N) entries
+    f32x16 ds = f32x16{};
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+      ds = mfma32(row8(G16 + qbase + t.io + 16 * kk + 8 * s, t.iok), row8(v + kbase + t.jo + 16 * kk + 8 * s, t.jok),
+                  ds);
+    float dsv[16];
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+      const int i0 = 32 * t.it + 8 * a + 4 * s;
+#pragma unroll
+      for (int vv = 0; vv < 4; ++vv) {
+        const int i = i0 + vv;
+        const float gzi = tok0 + i < N ? Gz[(size_t)(b * Hq + h) * N + tok0 + i] : 0.f;
+        dsv[4 * a + vv] = (t.j <= i && tok0 + i < N) ? ds[4 * a + vv] + gzi : 0.f;
+      }
+    }
+    bf16x8 qt[2][2];
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)
+        qt[dt][tt] = *reinterpret_cast<const bf16x8*>(QT16 + ((size_t)(b * Hq + h) * (kD + 2) + 32 * dt + row) * np +
+                                                       tok0 + 32 * t.it + 16 * tt + 8 * s);
+    float cf[9][2];
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt) {
+      const int gd = clamp_label(labels[h * kD + 32 * dt + row], G);
+#pragma unroll
+      for (int h2 = 0; h2 < 8; ++h2) cf[h2][dt] = h2 < G ? 2.f * scale * gam[((size_t)h * G + gd) * G + h2] : 0.f;
+      cf[8][dt] = scale * lam[(size_t)h * G + gd];
+    }
+#pragma unroll
+    for (int h2 = 0; h2 < 9; ++h2) {
+      float x[16];
+      if (h2 < 8) {
+        f32x16 sh = f32x16{};
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk)
+          sh = mfma32(masked(row8(q + qbase + t.io + 16 * kk + 8 * s, t.iok), &mk[mb][kk][h2][s][0]),
+                      row8(k + kbase + t.jo + 16 * kk + 8 * s, t.jok), sh);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) x[r] = dsv[r] * (scale * sh[r]);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) x[r] = dsv[r];
+      }
+      const bf16x8 f0 = acc_kfrag(x, 0, s), f1 = acc_kfrag(x, 1, s);
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt) {
+        f32x16 p = mfma32(f0, qt[dt][0], f32x16{});
+        p = mfma32(f1, qt[dt][1], p);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[dt][r] = fmaf(cf[h2][dt], p[r], acc[dt][r]);
+      }
+    }
+    __syncthreads();
+  }
+  local_write(red, acc, t, l, row, tok0, N, kbase, dkl);
+}
+
+// kappa[i][j] (quadratic form in the group sums), dv[j][e] += sum_i kappa g_i[e].
+template <typename T>
+__global__ __launch_bounds__(192) void k2_local_dv(const T* __restrict__ q, const T* __restrict__ k,
+                                                   const T* __restrict__ v, const uint16_t* __restrict__ G16,
+                                                   const float* __restrict__ Gz, const uint16_t* __restrict__ GT16,
+                                                   const int32_t* __restrict__ labels, const float* __restrict__ ic,
+                                                   int G, int Hq, int Hkv, int N, int NB, float scale,
+                                                   float* __restrict__ dvl, float* __restrict__ coefl) {
+  __shared__ __attribute__((aligned(16))) uint32_t mk[2][4][8][2][4];
+  __shared__ float red[2][16][64];
+  __shared__ float cp[3 * 64][45];  // per-lane coefficient partials of the 3 tile waves
+  int ch;
+  const int u = unit_chunk_block(NB, ch);
+  const int R = Hq / Hkv, b = u / Hkv, kh = u % Hkv;
+  const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, s = l >> 5, row = l & 31;
+  const int tok0 = ch * kC;
+  const size_t kbase = (size_t)u * N * kD;
+  const size_t np = (size_t)NB * kC;
+  const LocalTile t = local_tile(wv, tok0, N, row);
+  bf16x8 kf[4], vf[4];
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) {
+    kf[kk] = row8(k + kbase + t.jo + 16 * kk + 8 * s, t.jok);
+    vf[kk] = row8(v + kbase + t.jo + 16 * kk + 8 * s, t.jok);
+  }
+  f32x16 acc[2] = {f32x16{}, f32x16{}};
+  const size_t bn = (size_t)(gridDim.x / NB / Hkv) * NB;
+
+  build_masks(mk[0], labels, kh * R, G, tid);
+  __syncthreads();
+  for (int hh = 0; hh < R; ++hh) {
+    const int h = kh * R + hh, mb = hh & 1;
+    if (hh + 1 < R) build_masks(mk[mb ^ 1], labels, h + 1, G, tid);
+    const size_t qbase = (size_t)(b * Hq + h) * N * kD;
+    f32x16 sg[8];
+#pragma unroll
+    for (int g = 0; g < 8; ++g) sg[g] = f32x16{};
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const bf16x8 qf = row8(q + qbase + t.io + 16 * kk + 8 * s, t.iok);
+#pragma unroll
+      for (int g = 0; g < 8; ++g) sg[g] = mfma32(masked(qf, &mk[mb][kk][g][s][0]), kf[kk], sg[g]);
+    }
+    const float* cf = ic + (size_t)h * kIC;
+    const float c0h = cf[0];
+    float kap[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int i = 32 * t.it + c32_row(r, l);
+      float kv = c0h;
+#pragma unroll
+      for (int g = 0; g < 8; ++g) {
+        float inner = fmaf(cf[kIcGam + 9 * g], sg[g][r], cf[kIcLam + g]);
+#pragma unroll
+        for (int h2 = g + 1; h2 < 8; ++h2) inner = fmaf(2.f * cf[kIcGam + 8 * g + h2], sg[h2][r], inner);
+        kv = fmaf(sg[g][r], inner, kv);
+      }
+      kap[r] = (t.j <= i && tok0 + i < N) ? kv : 0.f;
+    }
+    const bf16x8 f0 = acc_kfrag(kap, 0, s), f1 = acc_kfrag(kap, 1, s);
+#pragma unroll
+    for (int et = 0; et < 2; ++et) {
+      const uint16_t* gt = GT16 + ((size_t)(b * Hq + h) * (kD + 2) + 32 * et + row) * np + tok0 + 32 * t.it + 8 * s;
+      acc[et] = mfma32(f0, *reinterpret_cast<const bf16x8*>(gt), acc[et]);
+      acc[et] = mfma32(f1, *reinterpret_cast<const bf16x8*>(gt + 16), acc[et]);
+    }
+    if (coefl) {
+      // ds[i][j] = g_i . v_j + gz_i; partials [0] sum ds, [1 + g] sum ds s_g,
+      // [9 + idx(g <= h)] sum ds s_g s_h (s = scale * group sum)
+      f32x16 ds = f32x16{};
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) ds = mfma32(row8(G16 + qbase + t.io + 16 * kk + 8 * s, t.iok), vf[kk], ds);
+      float ca[45];
+#pragma unroll
+      for (int e = 0; e < 45; ++e) ca[e] = 0.f;
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        const int i0 = 32 * t.it + 8 * a + 4 * s;
+#pragma unroll
+        for (int vv = 0; vv < 4; ++vv) {
+          const int r = 4 * a + vv, i = i0 + vv;
+          const float gzi = tok0 + i < N ? Gz[(size_t)(b * Hq + h) * N + tok0 + i] : 0.f;
+          const float dsv = (t.j <= i && tok0 + i < N) ? ds[r] + gzi : 0.f;
+          float sv[8], tv[8];
+#pragma unroll
+          for (int g = 0; g < 8; ++g) {
+            sv[g] = scale * sg[g][r];
+            tv[g] = dsv * sv[g];
+          }
+          ca[0] += dsv;
+          int e = 9;
+#pragma unroll
+          for (int g = 0; g < 8; ++g) {
+            ca[1 + g] += tv[g];
+#pragma unroll
+            for (int h2 = g; h2 < 8; ++h2) {
+              ca[e] = fmaf(tv[g], sv[h2], ca[e]);
+              ++e;
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 45; ++e) cp[tid][e] = ca[e];
+    }
+    __syncthreads();
+    if (coefl) {
+      // column sums over the 192 lanes (fixed order: 4 interleaved partial
+      // sums per column, then their sum), written in the full symmetric
+      // 8 x 8 layout [0] dc0, [1 + g] dlam, [9 + 8 g + h] dGam
+      if (tid < 180) {
+        const int e = tid % 45, part = tid / 45;
+        float x = 0.f;
+        for (int r = part; r < 192; r += 4) x += cp[r][e];
+        (&red[0][0][0])[tid] = x;  // red is free until the final combine
+      }
+      __syncthreads();
+      if (tid < 73) {
+        int e = tid;
+        if (tid >= 9) {
+          int g = (tid - 9) >> 3, h2 = (tid - 9) & 7;
+          if (h2 < g) {
+            const int t2 = g;
+            g = h2;
+            h2 = t2;
+          }
+          e = 9 + g * 8 - g * (g - 1) / 2 + (h2 - g);
+        }
+        const float* rp = &red[0][0][0];
+        coefl[((size_t)h * 73 + tid) * bn + (size_t)b * NB + ch] = (rp[e] + rp[45 + e]) + (rp[90 + e] + rp[135 + e]);
+      }
+      __syncthreads();
+    }
+  }
+  local_write(red, acc, t, l, row, tok0, N, kbase, dvl);
+}
+
+template <typename T>
+void launch_local_bwd(const LaunchGeom& g, const T* q, const T* k, const T* v, const LocalBwdArgs& a, bool need_dq,
+                      bool need_dkv, hipStream_t st, const Timer& timed) {
+  if (need_dq) {
+    timed("k2_kt_prep", st, [&] {
+      hipLaunchKernelGGL(k2_kt_prep<T>, dim3(g.U * g.NB), dim3(256), 0, st, k, g.N, g.NB, a.KT16);
+    });
+    timed("k2_local_dq", st, [&] {
+      hipLaunchKernelGGL(k2_local_dq<T>, dim3(g.R * g.NB * g.U), dim3(192), 0, st, q, k, v, a.G16, a.Gz, a.KT16, a.PZ,
+                         a.PZm, a.labels, a.lam, a.gam, a.gm, a.lb, a.groups, g.Hq, g.Hkv, g.N, g.NB, a.scale, a.dqf);
+    });
+  }
+  if (need_dkv) {
+    timed("k2_local_dk", st, [&] {
+      hipLaunchKernelGGL(k2_local_dk<T>, dim3(g.NB * g.U), dim3(192), 0, st, q, k, v, a.G16, a.Gz, a.QT16,
+                         a.labels, a.lam, a.gam, a.groups, g.Hq, g.Hkv, g.N, g.NB, a.scale, a.dkl);
+    });
+  }
+  if (need_dkv || a.coefl) {
+    timed("k2_local_dv", st, [&] {
+      hipLaunchKernelGGL(k2_local_dv<T>, dim3(g.NB * g.U), dim3(192), 0, st, q, k, v, a.G16, a.Gz, a.GT16, a.labels,
+                         a.ic, a.groups, g.Hq, g.Hkv, g.N, g.NB, a.scale, a.dvl, a.coefl);
+    });
+  }
+}
+
+template void launch_local_bwd<float>(const LaunchGeom&, const float*, const float*, const float*,
+                                      const LocalBwdArgs&, bool, bool, hipStream_t, const Timer&);
+template void launch_local_bwd<uint16_t>(const LaunchGeom&, const uint16_t*, const uint16_t*, const uint16_t*,
+                                         const LocalBwdArgs&, bool, bool, hipStream_t, const Timer&);
+
+}  // namespace oal
