@@ -461,25 +461,25 @@ __global__ __launch_bounds__(256) void k2_seg_carry(const float* __restrict__ se
 // One unit = 1024 bf16 (a PR M-tile k-slice of 32 x 16 or a PT k-step 64 x 16).
 // ---------------------------------------------------------------------------
 constexpr int kFG = 4;  // units per ring group
+constexpr int kNS = 4;  // LDS stages of a ring
 
+// Group G (units G * kFG ..) of a k-blocked state into LDS stage G % kNS;
+// 128 threads, each unit is 64 rows x 16 bf16 = 128 lanes x 16 bytes.
+// Stage G % kNS holds units G * kFG .. of group G.
+static_assert(kNS == 4, "LdsRing has four stages");
 template <int NU, int G>
-__device__ __forceinline__ void ring_fetch_u(const uint16_t* src, int tid, uint4 (&reg)[kFG]) {
+__device__ __forceinline__ void ring_issue_u(const uint16_t* src, const LdsRing& ring, int tid) {
+  const int wv = tid >> 6;
+  __bf16* st = ring.st[G % kNS];
 #pragma unroll
   for (int i = 0; i < kFG; ++i) {
     const int u = G * kFG + i;
-    if (u < NU) reg[i] = reinterpret_cast<const uint4*>(src + (size_t)u * 1024)[tid];
+    if (u < NU) copy16_to_lds(src + (size_t)u * 1024 + tid * 8, st + i * 1024 + 64 * wv * 8);
   }
 }
-template <int NU, int G>
-__device__ __forceinline__ void ring_store_u(__bf16* ring, int tid, const uint4 (&reg)[kFG]) {
-  __bf16* buf = ring + (G & 1) * kFG * 1024;
-#pragma unroll
-  for (int i = 0; i < kFG; ++i)
-    if (G * kFG + i < NU) reinterpret_cast<uint4*>(buf + i * 1024)[tid] = reg[i];
-}
 template <int U>
-__device__ __forceinline__ const __bf16* ring_unit(const __bf16* ring) {
-  return ring + ((U / kFG) & 1) * kFG * 1024 + (U % kFG) * 1024;
+__device__ __forceinline__ const __bf16* ring_unit(const LdsRing& ring) {
+  return ring.st[(U / kFG) % kNS] + (U % kFG) * 1024;
 }
 
 // Fold of one 32-slot M-tile (rows permuted so that the rows a lane holds are
@@ -525,25 +525,20 @@ __device__ __forceinline__ int fold_row(int r) {
 }
 
 // Fold ring: one 32-slot M-tile of a PR-layout state (4 k-slices x 32 rows x
-// 16 values = 2048 bf16) per group, two buffers; 128 threads move 32 B each.
+// 16 values = 2048 bf16) per stage, kNS stages; 128 threads move 32 B each.
 constexpr int kTileElems = 4 * 32 * 16;
 
-__device__ __forceinline__ void fold_fetch(const uint16_t* src, int m, int tid, uint4 (&reg)[2]) {
-  const uint4* p = reinterpret_cast<const uint4*>(src + (size_t)m * kTileElems);
-  reg[0] = p[tid];
-  reg[1] = p[tid + 128];
-}
-__device__ __forceinline__ void fold_store(__bf16* ring, int m, int tid, const uint4 (&reg)[2]) {
-  uint4* p = reinterpret_cast<uint4*>(ring + (m & 1) * kTileElems);
-  p[tid] = reg[0];
-  p[tid + 128] = reg[1];
+__device__ __forceinline__ void fold_issue(const uint16_t* src, int m, __bf16* st, int tid) {
+  const int wv = tid >> 6;
+  const uint16_t* g = src + (size_t)m * kTileElems;
+  copy16_to_lds(g + tid * 8, st + 64 * wv * 8);
+  copy16_to_lds(g + (tid + 128) * 8, st + (128 + 64 * wv) * 8);
 }
 
 template <int M, bool WEIGHTED>
 __device__ __forceinline__ void fold_step(const bf16x8 (&bfr)[4], const float (&x)[kD], float (&dx)[kD],
-                                          const float* wl, const __bf16* ring, int lane) {
+                                          const float* wl, const __bf16* tile, int lane) {
   const int s = lane >> 5, arow = fold_row(lane & 31);
-  const __bf16* tile = ring + (M & 1) * kTileElems;
   f32x16 D = f32x16{};
 #pragma unroll
   for (int kk = 0; kk < 4; ++kk)
@@ -551,18 +546,26 @@ __device__ __forceinline__ void fold_step(const bf16x8 (&bfr)[4], const float (&
   fold_tile<M, WEIGHTED>(D, x, dx, wl, s);
 }
 
+// Ring pipeline over the 69 M-tiles: tiles G + 1, G + 2 may still be in
+// flight while tile G is folded; tile G + 3 is issued after the barrier that
+// retires every read of its stage.
 template <int G, bool WEIGHTED>
 __device__ __forceinline__ void fold_group(const bf16x8 (&bfr)[4], const float (&x)[kD], float (&dx)[kD],
-                                           const float* wl, __bf16* ring, const uint16_t* src, int tid, int lane) {
+                                           const float* wl, const LdsRing& ring, const uint16_t* src, int tid,
+                                           int lane) {
   constexpr int NT = kS / 32;  // 69 M-tiles
-  uint4 reg[2];
-  if constexpr (G + 1 < NT) fold_fetch(src, G + 1, tid, reg);
-  fold_step<G, WEIGHTED>(bfr, x, dx, wl, ring, lane);
-  if constexpr (G + 1 < NT) {
-    fold_store(ring, G + 1, tid, reg);
-    __syncthreads();
-    fold_group<G + 1, WEIGHTED>(bfr, x, dx, wl, ring, src, tid, lane);
-  }
+  constexpr int after = (G + 2 < NT) ? 2 : ((G + 1 < NT) ? 1 : 0);
+  ring_sync<2 * after>();
+  if constexpr (G + 3 < NT) fold_issue(src, G + 3, ring.st[(G + 3) % kNS], tid);
+  fold_step<G, WEIGHTED>(bfr, x, dx, wl, ring.st[G % kNS], lane);
+  if constexpr (G + 1 < NT) fold_group<G + 1, WEIGHTED>(bfr, x, dx, wl, ring, src, tid, lane);
+}
+
+// Prologue: tiles 0 .. 2 in flight.
+__device__ __forceinline__ void fold_prologue(const uint16_t* src, const LdsRing& ring, int tid) {
+  fold_issue(src, 0, ring.st[0], tid);
+  fold_issue(src, 1, ring.st[1], tid);
+  fold_issue(src, 2, ring.st[2], tid);
 }
 
 // ---------------------------------------------------------------------------
@@ -574,9 +577,11 @@ __global__ __launch_bounds__(128) void k2_q_fold(const T* __restrict__ q, const 
                                                  const float* __restrict__ wqs, const uint16_t* __restrict__ PR,
                                                  const float* __restrict__ dqf, int Hq, int Hkv, int N, int NB,
                                                  T* __restrict__ dq) {
-  __shared__ __attribute__((aligned(16))) __bf16 ring[2 * kFG * 1024];
+  __shared__ __attribute__((aligned(16))) __bf16 ring0[kTileElems], ring1[kTileElems], ring2[kTileElems],
+      ring3[kTileElems];
   __shared__ __attribute__((aligned(16))) float wl[kS];
   __shared__ float dqs[kC][kD + 1];
+  const LdsRing ring{{ring0, ring1, ring2, ring3}};
 
   int hh, ch, u;
   head_chunk_unit(Hq / Hkv, NB, (int)(gridDim.x / ((Hq / Hkv) * NB)), hh, ch, u);
@@ -586,13 +591,8 @@ __global__ __launch_bounds__(128) void k2_q_fold(const T* __restrict__ q, const 
   const size_t qbase = (size_t)(b * Hq + h) * N * kD;
   const uint16_t* src = PR + ((size_t)u * NB + ch) * ((size_t)kKS * 64 * 16);
 
-  {
-    uint4 reg[2];
-    fold_fetch(src, 0, tid, reg);
-    for (int i = tid; i < kS / 4; i += 128)
-      reinterpret_cast<float4*>(wl)[i] = reinterpret_cast<const float4*>(wqs + (size_t)h * kS)[i];
-    fold_store(ring, 0, tid, reg);
-  }
+  for (int i = tid; i < kS / 4; i += 128)
+    reinterpret_cast<float4*>(wl)[i] = reinterpret_cast<const float4*>(wqs + (size_t)h * kS)[i];
   const int tok = tok0 + 32 * wv + row;
   const bool ok = tok < N;
   const size_t rowoff = qbase + (size_t)(ok ? tok : N - 1) * kD;
@@ -608,7 +608,7 @@ __global__ __launch_bounds__(128) void k2_q_fold(const T* __restrict__ q, const 
   }
 #pragma unroll
   for (int m = 0; m < kD; ++m) dx[m] = 0.f;
-  __syncthreads();
+  fold_prologue(src, ring, tid);
   fold_group<0, true>(bfr, x, dx, wl, ring, src, tid, l);
 
   // combine the two rotation groups of each token
@@ -636,7 +636,7 @@ __global__ __launch_bounds__(128) void k2_q_fold(const T* __restrict__ q, const 
 // the per-head local parts. grid (NB, U), 2 waves; wave w owns tokens 32w..+31.
 // ---------------------------------------------------------------------------
 template <int T>
-__device__ __forceinline__ void du_step(const float (&x)[kD], const __bf16* ring, int lane, f32x16 (&acc)[2]) {
+__device__ __forceinline__ void du_step(const float (&x)[kD], const LdsRing& ring, int lane, f32x16 (&acc)[2]) {
   const int s = lane >> 5, row = lane & 31;
   const __bf16* tile = ring_unit<T>(ring);
   const bf16x8 b0 = *reinterpret_cast<const bf16x8*>(tile + row * 16 + 8 * s);
@@ -646,19 +646,17 @@ __device__ __forceinline__ void du_step(const float (&x)[kD], const __bf16* ring
   acc[1] = mfma32(a, b1, acc[1]);
 }
 template <int G>
-__device__ __forceinline__ void du_group(const float (&x)[kD], __bf16* ring, const uint16_t* src, int tid, int lane,
+__device__ __forceinline__ void du_group(const float (&x)[kD], const LdsRing& ring, const uint16_t* src, int tid, int lane,
                                          f32x16 (&acc)[2]) {
   constexpr int NG = (kKS + kFG - 1) / kFG;
-  uint4 reg[kFG];
-  if constexpr (G + 1 < NG) ring_fetch_u<kKS, G + 1>(src, tid, reg);
+  constexpr int n1 = (G + 1 < NG) ? ((G + 1) * kFG + kFG <= kKS ? kFG : kKS - (G + 1) * kFG) : 0;
+  constexpr int n2 = (G + 2 < NG) ? ((G + 2) * kFG + kFG <= kKS ? kFG : kKS - (G + 2) * kFG) : 0;
+  ring_sync<n1 + n2>();
+  if constexpr (G + 3 < NG) ring_issue_u<kKS, G + 3>(src, ring, tid);
   [&]<int... I>(std::integer_sequence<int, I...>) {
     ((G * kFG + I < kKS ? du_step<(G * kFG + I < kKS ? G * kFG + I : 0)>(x, ring, lane, acc) : void()), ...);
   }(std::make_integer_sequence<int, kFG>{});
-  if constexpr (G + 1 < NG) {
-    ring_store_u<kKS, G + 1>(ring, tid, reg);
-    __syncthreads();
-    du_group<G + 1>(x, ring, src, tid, lane, acc);
-  }
+  if constexpr (G + 1 < NG) du_group<G + 1>(x, ring, src, tid, lane, acc);
 }
 
 template <typename T>
@@ -667,7 +665,8 @@ __global__ __launch_bounds__(128) void k2_kv_fold(const T* __restrict__ k, const
                                                   const float* __restrict__ dTz, const float* __restrict__ dkl,
                                                   const float* __restrict__ dvl, int Hq, int Hkv, int N, int NB,
                                                   T* __restrict__ dk, T* __restrict__ dv) {
-  __shared__ __attribute__((aligned(16))) __bf16 ring[2 * kFG * 1024];
+  __shared__ __attribute__((aligned(16))) __bf16 ring0[kFG * 1024], ring1[kFG * 1024], ring2[kFG * 1024],
+      ring3[kFG * 1024];
   __shared__ __attribute__((aligned(16))) __bf16 mz[kD][LD];
   __shared__ __attribute__((aligned(16))) __bf16 ks[kC][LD];
   __shared__ float dks[kC][kD + 1];
@@ -709,22 +708,18 @@ __global__ __launch_bounds__(128) void k2_kv_fold(const T* __restrict__ k, const
   for (int m = 0; m < kD; ++m) dx[m] = 0.f;
 
   // 1. fold of dT V^T through the key features
-  {
-    uint4 reg[2];
-    fold_fetch(dTR + cbase, 0, tid, reg);
-    fold_store(ring, 0, tid, reg);
-  }
-  __syncthreads();
-  fold_group<0, false>(bfr, x, dx, nullptr, ring, dTR + cbase, tid, l);
+  static_assert(kTileElems <= kFG * 1024, "a fold tile fits one dU ring stage");
+  const LdsRing fr{{ring0, ring1, ring2, ring3}};
+  const LdsRing ring{{ring0, ring1, ring2, ring3}};
+  fold_prologue(dTR + cbase, fr, tid);
+  fold_group<0, false>(bfr, x, dx, nullptr, fr, dTR + cbase, tid, l);
   __syncthreads();
   // 2. dU = raw(K) dT (values 0..63)
   f32x16 acc[2] = {f32x16{}, f32x16{}};
-  {
-    uint4 reg[kFG];
-    ring_fetch_u<kKS, 0>(dTT + cbase, tid, reg);
-    ring_store_u<kKS, 0>(ring, tid, reg);
-  }
-  __syncthreads();
+  __syncthreads();  // every read of the fold ring is done before the dU ring reuses it
+  ring_issue_u<kKS, 0>(dTT + cbase, ring, tid);
+  ring_issue_u<kKS, 1>(dTT + cbase, ring, tid);
+  ring_issue_u<kKS, 2>(dTT + cbase, ring, tid);
   du_group<0>(x, ring, dTT + cbase, tid, l, acc);
 
   // 3. combine rotation groups, add z1 + Mz k

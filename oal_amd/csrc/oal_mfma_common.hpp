@@ -203,3 +203,47 @@ __device__ __forceinline__ void head_chunk_unit(int R, int NB, int U, int& hh, i
 }
 
 }  // namespace oal
+
+namespace oal {
+
+// Asynchronous global -> LDS copy (global_load_lds_dwordx4): every lane of the
+// wave moves 16 bytes from its own global address to lds_base + 16 * lane,
+// where lds_base is wave-uniform. Completion is tracked by vmcnt.
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void gbl_void_t;
+__device__ __forceinline__ void copy16_to_lds(const void* gsrc, void* lds_base) {
+  __builtin_amdgcn_global_load_lds((gbl_void_t*)gsrc, (lds_void_t*)lds_base, 16, 0, 0);
+}
+
+// s_waitcnt vmcnt(N) (expcnt and lgkmcnt left free).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit counter");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Four LDS stages of an asynchronous copy ring. The stages are distinct
+// __shared__ objects: the compiler then tells a read of one stage from the
+// copies still in flight into the others, where a single array would make it
+// wait for every copy in flight (vmcnt(0)) before each read.
+struct LdsRing {
+  __bf16* st[4];
+};
+
+// Ring barrier: this wave's copies older than the newest N have landed in LDS
+// (vmcnt(N)), its own LDS reads and writes are done (lgkmcnt(0)), then the
+// workgroup barrier. Unlike __syncthreads() it carries no release fence, which
+// would wait for every asynchronous copy in flight (vmcnt(0)) and empty the
+// ring; the empty asm statements keep the compiler from moving memory accesses
+// across it.
+template <int N>
+__device__ __forceinline__ void ring_sync() {
+  static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit counter");
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+}  // namespace oal
+

@@ -241,33 +241,29 @@ __device__ __forceinline__ bf16x8 load8(const float* p) {
   return pack8(v);
 }
 
-// Issue the global loads of ring group G (each of 128 threads moves kRG x 16 B).
+constexpr int kNSR = 4;  // LDS stages of the readout ring
+
+// Ring group G (k-steps G * kRG ..) into LDS stage G % kNSR; each k-step tile is
+// 64 values x 16 slots = 128 lanes x 16 bytes.
 template <int G>
-__device__ __forceinline__ void ring_fetch(const uint16_t* pt, int tid, uint4 (&reg)[kRG]) {
+__device__ __forceinline__ void ring_issue(const uint16_t* pt, const LdsRing& ring, int tid) {
+  const int wv = tid >> 6;
+  __bf16* st = ring.st[G % kNSR];
 #pragma unroll
   for (int i = 0; i < kRG; ++i) {
-    constexpr int t0 = G * kRG;
-    const int t = t0 + i;
-    if (t < kKS) reg[i] = reinterpret_cast<const uint4*>(pt + (size_t)t * kRingStep)[tid];
-  }
-}
-template <int G>
-__device__ __forceinline__ void ring_store(__bf16* ring, int tid, const uint4 (&reg)[kRG]) {
-  __bf16* buf = ring + (G & 1) * kRG * kRingStep;
-#pragma unroll
-  for (int i = 0; i < kRG; ++i) {
-    if (G * kRG + i < kKS) reinterpret_cast<uint4*>(buf + i * kRingStep)[tid] = reg[i];
+    const int t = G * kRG + i;
+    if (t < kKS) copy16_to_lds(pt + (size_t)t * kRingStep + tid * 8, st + i * kRingStep + 64 * wv * 8);
   }
 }
 
 template <int T>
-__device__ __forceinline__ void readout_step(const float (&x)[kD], const float* wl, const __bf16* ring, int lane,
+__device__ __forceinline__ void readout_step(const float (&x)[kD], const float* wl, const LdsRing& ring, int lane,
                                              f32x16 (&acc)[2]) {
   const int s = lane >> 5, row = lane & 31;
   const float4 w0 = *reinterpret_cast<const float4*>(wl + 16 * T + 8 * s);
   const float4 w1 = *reinterpret_cast<const float4*>(wl + 16 * T + 8 * s + 4);
   const float w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-  const __bf16* tile = ring + ((T / kRG) & 1) * kRG * kRingStep + (T % kRG) * kRingStep;
+  const __bf16* tile = ring.st[(T / kRG) % kNSR] + (T % kRG) * kRingStep;
   const bf16x8 b0 = *reinterpret_cast<const bf16x8*>(tile + row * 16 + 8 * s);
   const bf16x8 b1 = *reinterpret_cast<const bf16x8*>(tile + (32 + row) * 16 + 8 * s);
   const bf16x8 a = feature_fragment<T>(x, w);
@@ -275,19 +271,20 @@ __device__ __forceinline__ void readout_step(const float (&x)[kD], const float* 
   acc[1] = mfma32(a, b1, acc[1]);
 }
 
+// Ring pipeline over the k-step groups: groups G + 1, G + 2 may still be in
+// flight while group G is read; group G + 3 is issued after the barrier that
+// retires every read of its stage.
 template <int G>
-__device__ __forceinline__ void readout_group(const float (&x)[kD], const float* wl, __bf16* ring,
+__device__ __forceinline__ void readout_group(const float (&x)[kD], const float* wl, const LdsRing& ring,
                                               const uint16_t* pt, int tid, int lane, f32x16 (&acc)[2]) {
-  uint4 reg[kRG];
-  if constexpr (G + 1 < kRingGroups) ring_fetch<G + 1>(pt, tid, reg);
+  constexpr int n1 = (G + 1 < kRingGroups) ? ((G + 1) * kRG + kRG <= kKS ? kRG : kKS - (G + 1) * kRG) : 0;
+  constexpr int n2 = (G + 2 < kRingGroups) ? ((G + 2) * kRG + kRG <= kKS ? kRG : kKS - (G + 2) * kRG) : 0;
+  ring_sync<n1 + n2>();
+  if constexpr (G + 3 < kRingGroups) ring_issue<G + 3>(pt, ring, tid);
   [&]<int... I>(std::integer_sequence<int, I...>) {
     ((G * kRG + I < kKS ? readout_step<(G * kRG + I < kKS ? G * kRG + I : 0)>(x, wl, ring, lane, acc) : void()), ...);
   }(std::make_integer_sequence<int, kRG>{});
-  if constexpr (G + 1 < kRingGroups) {
-    ring_store<G + 1>(ring, tid, reg);
-    __syncthreads();
-    readout_group<G + 1>(x, wl, ring, pt, tid, lane, acc);
-  }
+  if constexpr (G + 1 < kRingGroups) readout_group<G + 1>(x, wl, ring, pt, tid, lane, acc);
 }
 
 // 16 consecutive elements of a row as two bf16 fragments (16-byte loads).
@@ -515,11 +512,14 @@ __global__ __launch_bounds__(256) void k2_intra_fwd(const T* __restrict__ q, con
 // then out = num / den.
 // ---------------------------------------------------------------------------
 template <typename T>
-__global__ __launch_bounds__(128) void k2_out_fwd(const T* __restrict__ q, const float* __restrict__ wqs,
+__global__ __launch_bounds__(128, 2) void k2_out_fwd(const T* __restrict__ q, const float* __restrict__ wqs,
                                                   const uint16_t* __restrict__ PT, int Hq, int Hkv, int N, int NB,
                                                   float floor, T* __restrict__ out, float* __restrict__ num,
                                                   const float* __restrict__ den) {
-  __shared__ __attribute__((aligned(16))) __bf16 ring[2 * kRG * kRingStep];
+  static_assert(kNSR == 4, "LdsRing has four stages");
+  __shared__ __attribute__((aligned(16))) __bf16 ring0[kRG * kRingStep], ring1[kRG * kRingStep],
+      ring2[kRG * kRingStep], ring3[kRG * kRingStep];
+  const LdsRing ring{{ring0, ring1, ring2, ring3}};
   __shared__ __attribute__((aligned(16))) float wl[kS];
 
   int hh, ch, u;
@@ -530,13 +530,8 @@ __global__ __launch_bounds__(128) void k2_out_fwd(const T* __restrict__ q, const
   const size_t qbase = (size_t)(b * Hq + h) * N * kD;
   const uint16_t* pt = PT + ((size_t)u * NB + ch) * ((size_t)kKS * kRingStep);
 
-  {
-    uint4 reg[kRG];
-    ring_fetch<0>(pt, tid, reg);
-    for (int i = tid; i < kS / 4; i += 128)
-      reinterpret_cast<float4*>(wl)[i] = reinterpret_cast<const float4*>(wqs + (size_t)h * kS)[i];
-    ring_store<0>(ring, tid, reg);
-  }
+  for (int i = tid; i < kS / 4; i += 128)
+    reinterpret_cast<float4*>(wl)[i] = reinterpret_cast<const float4*>(wqs + (size_t)h * kS)[i];
   // rotated query row of this lane's token
   float x[kD];
   {
@@ -571,7 +566,9 @@ __global__ __launch_bounds__(128) void k2_out_fwd(const T* __restrict__ q, const
       const int tok = tok0 + 32 * wv + c32_row(i, l);
       acc[nt][i] = tok < N ? num[qbase + (size_t)tok * kD + 32 * nt + row] : 0.f;
     }
-  __syncthreads();
+  ring_issue<0>(pt, ring, tid);
+  ring_issue<1>(pt, ring, tid);
+  ring_issue<2>(pt, ring, tid);
   readout_group<0>(x, wl, ring, pt, tid, l, acc);
 
   const size_t dbase = (size_t)(b * Hq + h) * N;
