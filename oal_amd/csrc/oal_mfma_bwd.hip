@@ -57,6 +57,23 @@ __device__ __forceinline__ void load_row_b(const float* __restrict__ src, size_t
   }
 }
 
+// 32 consecutive elements of a row (16-byte stores).
+__device__ __forceinline__ void store32(float* dst, const float (&v)[32]) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    reinterpret_cast<float4*>(dst)[j] = make_float4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
+}
+__device__ __forceinline__ void store32(uint16_t* dst, const float (&v)[32]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      w[i] = uint32_t(from_f<uint16_t>(v[8 * j + 2 * i])) | (uint32_t(from_f<uint16_t>(v[8 * j + 2 * i + 1])) << 16);
+    reinterpret_cast<uint4*>(dst)[j] = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
 __device__ __forceinline__ void store_row(__bf16* dst, const bf16x8 (&r)[8]) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) *reinterpret_cast<bf16x8*>(dst + 8 * i) = r[i];
@@ -466,9 +483,8 @@ constexpr int kNS = 4;  // LDS stages of a ring
 // Group G (units G * kFG ..) of a k-blocked state into LDS stage G % kNS;
 // 128 threads, each unit is 64 rows x 16 bf16 = 128 lanes x 16 bytes.
 // Stage G % kNS holds units G * kFG .. of group G.
-static_assert(kNS == 4, "LdsRing has four stages");
 template <int NU, int G>
-__device__ __forceinline__ void ring_issue_u(const uint16_t* src, const LdsRing& ring, int tid) {
+__device__ __forceinline__ void ring_issue_u(const uint16_t* src, const LdsRing<4>& ring, int tid) {
   const int wv = tid >> 6;
   __bf16* st = ring.st[G % kNS];
 #pragma unroll
@@ -478,7 +494,7 @@ __device__ __forceinline__ void ring_issue_u(const uint16_t* src, const LdsRing&
   }
 }
 template <int U>
-__device__ __forceinline__ const __bf16* ring_unit(const LdsRing& ring) {
+__device__ __forceinline__ const __bf16* ring_unit(const LdsRing<4>& ring) {
   return ring.st[(U / kFG) % kNS] + (U % kFG) * 1024;
 }
 
@@ -535,37 +551,66 @@ __device__ __forceinline__ void fold_issue(const uint16_t* src, int m, __bf16* s
   copy16_to_lds(g + (tid + 128) * 8, st + (128 + 64 * wv) * 8);
 }
 
-template <int M, bool WEIGHTED>
-__device__ __forceinline__ void fold_step(const bf16x8 (&bfr)[4], const float (&x)[kD], float (&dx)[kD],
-                                          const float* wl, const __bf16* tile, int lane) {
+// D^T of M-tile M: 32 slots (rows, fold_row order) x 32 tokens (lane column).
+template <int M>
+__device__ __forceinline__ f32x16 fold_mfma(const bf16x8 (&bfr)[4], const __bf16* tile, int lane) {
   const int s = lane >> 5, arow = fold_row(lane & 31);
   f32x16 D = f32x16{};
 #pragma unroll
   for (int kk = 0; kk < 4; ++kk)
     D = mfma32(*reinterpret_cast<const bf16x8*>(tile + kk * 512 + arow * 16 + 8 * s), bfr[kk], D);
-  fold_tile<M, WEIGHTED>(D, x, dx, wl, s);
+  return D;
 }
 
-// Ring pipeline over the 69 M-tiles: tiles G + 1, G + 2 may still be in
-// flight while tile G is folded; tile G + 3 is issued after the barrier that
-// retires every read of its stage.
-template <int G, bool WEIGHTED>
+// Ring pipeline over the 69 M-tiles with NS LDS stages. Group G enters with
+// the product of tile G in flight (Dc); it waits for tile G + 1, refills the
+// stage of tile G (whose reads ended before the barrier) with tile G + NS,
+// issues the product of tile G + 1, then folds tile G, so the fold's VALU work
+// overlaps the next tile's matrix products. Up to NS - 2 tiles stay in flight.
+template <int G, int NS, bool WEIGHTED>
 __device__ __forceinline__ void fold_group(const bf16x8 (&bfr)[4], const float (&x)[kD], float (&dx)[kD],
-                                           const float* wl, const LdsRing& ring, const uint16_t* src, int tid,
-                                           int lane) {
+                                           const float* wl, const LdsRing<NS>& ring, const uint16_t* src, int tid,
+                                           int lane, const f32x16& Dc) {
   constexpr int NT = kS / 32;  // 69 M-tiles
-  constexpr int after = (G + 2 < NT) ? 2 : ((G + 1 < NT) ? 1 : 0);
-  ring_sync<2 * after>();
-  if constexpr (G + 3 < NT) fold_issue(src, G + 3, ring.st[(G + 3) % kNS], tid);
-  fold_step<G, WEIGHTED>(bfr, x, dx, wl, ring.st[G % kNS], lane);
-  if constexpr (G + 1 < NT) fold_group<G + 1, WEIGHTED>(bfr, x, dx, wl, ring, src, tid, lane);
+  if constexpr (G + 1 < NT) {
+    constexpr int issued = (G + NS - 1 < NT - 1) ? G + NS - 1 : NT - 1;  // last tile issued so far
+    pin64(dx);  // the fold of tile G - 1 stays in group G - 1
+    ring_sync<2 * (issued - (G + 1))>();
+    if constexpr (G + NS < NT) fold_issue(src, G + NS, ring.st[(G + NS) % NS], tid);
+    const f32x16 Dn = fold_mfma<G + 1>(bfr, ring.st[(G + 1) % NS], lane);
+    fold_tile<G, WEIGHTED>(Dc, x, dx, wl, lane >> 5);
+    fold_group<G + 1, NS, WEIGHTED>(bfr, x, dx, wl, ring, src, tid, lane, Dn);
+  } else {
+    fold_tile<G, WEIGHTED>(Dc, x, dx, wl, lane >> 5);
+  }
 }
 
-// Prologue: tiles 0 .. 2 in flight.
-__device__ __forceinline__ void fold_prologue(const uint16_t* src, const LdsRing& ring, int tid) {
-  fold_issue(src, 0, ring.st[0], tid);
-  fold_issue(src, 1, ring.st[1], tid);
-  fold_issue(src, 2, ring.st[2], tid);
+// Whole fold: tiles 0 .. NS - 1 in flight, product of tile 0, then the groups.
+template <int NS, bool WEIGHTED>
+__device__ __forceinline__ void fold_all(const bf16x8 (&bfr)[4], const float (&x)[kD], float (&dx)[kD],
+                                         const float* wl, const LdsRing<NS>& ring, const uint16_t* src, int tid,
+                                         int lane) {
+  static_assert(NS >= 3 && NS <= kS / 32, "ring depth");
+  [&]<int... I>(std::integer_sequence<int, I...>) {
+    (fold_issue(src, I, ring.st[I], tid), ...);
+  }(std::make_integer_sequence<int, NS>{});
+  ring_sync<2 * (NS - 1)>();
+  const f32x16 D0 = fold_mfma<0>(bfr, ring.st[0], lane);
+  fold_group<0, NS, WEIGHTED>(bfr, x, dx, wl, ring, src, tid, lane, D0);
+}
+
+// The two rotation groups of a token (lanes l and l + 32) hold its gradient
+// in rotated order: lane group s has dimension (m + 32 s) % 64 at index m.
+// Returns, in lane group s, the full gradient of dimensions 32 s + m (m < 32).
+__device__ __forceinline__ void combine_rotation_groups(const float (&dx)[kD], int s, float (&out)[32]) {
+#pragma unroll
+  for (int m = 0; m < 32; ++m) {
+    // partner's dx[m + 32]: lanes < 32 receive it in the second result,
+    // lanes >= 32 in the first
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(dx[m + 32]), __float_as_uint(dx[m + 32]),
+                                                    false, false);
+    out[m] = dx[m] + __uint_as_float(s ? r[0] : r[1]);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -573,15 +618,14 @@ __device__ __forceinline__ void fold_prologue(const uint16_t* src, const LdsRing
 // grid (R, NB, U), 2 waves; wave w owns tokens 32w..32w+31 (lane column).
 // ---------------------------------------------------------------------------
 template <typename T>
-__global__ __launch_bounds__(128) void k2_q_fold(const T* __restrict__ q, const uint16_t* __restrict__ G16,
+__global__ __launch_bounds__(128, 2) void k2_q_fold(const T* __restrict__ q, const uint16_t* __restrict__ G16,
                                                  const float* __restrict__ wqs, const uint16_t* __restrict__ PR,
                                                  const float* __restrict__ dqf, int Hq, int Hkv, int N, int NB,
                                                  T* __restrict__ dq) {
   __shared__ __attribute__((aligned(16))) __bf16 ring0[kTileElems], ring1[kTileElems], ring2[kTileElems],
-      ring3[kTileElems];
+      ring3[kTileElems], ring4[kTileElems], ring5[kTileElems];
   __shared__ __attribute__((aligned(16))) float wl[kS];
-  __shared__ float dqs[kC][kD + 1];
-  const LdsRing ring{{ring0, ring1, ring2, ring3}};
+  const LdsRing<6> ring{{ring0, ring1, ring2, ring3, ring4, ring5}};
 
   int hh, ch, u;
   head_chunk_unit(Hq / Hkv, NB, (int)(gridDim.x / ((Hq / Hkv) * NB)), hh, ch, u);
@@ -608,26 +652,23 @@ __global__ __launch_bounds__(128) void k2_q_fold(const T* __restrict__ q, const 
   }
 #pragma unroll
   for (int m = 0; m < kD; ++m) dx[m] = 0.f;
-  fold_prologue(src, ring, tid);
-  fold_group<0, true>(bfr, x, dx, wl, ring, src, tid, l);
+  fold_all<6, true>(bfr, x, dx, wl, ring, src, tid, l);
 
-  // combine the two rotation groups of each token
-  const int tl = 32 * wv + row;
-  if (s == 0) {
+  // lane group s writes dimensions 32 s .. 32 s + 31 of its token
+  float full[32];
+  combine_rotation_groups(dx, s, full);
+  if (ok) {
+    const size_t o = rowoff + 32 * s;
+    const float4* lf = reinterpret_cast<const float4*>(dqf + o);
 #pragma unroll
-    for (int m = 0; m < kD; ++m) dqs[tl][m] = dx[m];
-  }
-  __syncthreads();
-  if (s == 1) {
-#pragma unroll
-    for (int m = 0; m < kD; ++m) dqs[tl][(m + 32) & 63] += dx[m];
-  }
-  __syncthreads();
-  for (int j = 0; j < 32; ++j) {
-    const int tj = tok0 + 32 * wv + j;
-    if (tj >= N) break;
-    const size_t o = qbase + (size_t)tj * kD + l;
-    dq[o] = from_f<T>(dqs[32 * wv + j][l] + dqf[o]);
+    for (int j = 0; j < 8; ++j) {
+      const float4 a = lf[j];
+      full[4 * j] += a.x;
+      full[4 * j + 1] += a.y;
+      full[4 * j + 2] += a.z;
+      full[4 * j + 3] += a.w;
+    }
+    store32(dq + o, full);
   }
 }
 
@@ -636,7 +677,7 @@ __global__ __launch_bounds__(128) void k2_q_fold(const T* __restrict__ q, const 
 // the per-head local parts. grid (NB, U), 2 waves; wave w owns tokens 32w..+31.
 // ---------------------------------------------------------------------------
 template <int T>
-__device__ __forceinline__ void du_step(const float (&x)[kD], const LdsRing& ring, int lane, f32x16 (&acc)[2]) {
+__device__ __forceinline__ void du_step(const float (&x)[kD], const LdsRing<4>& ring, int lane, f32x16 (&acc)[2]) {
   const int s = lane >> 5, row = lane & 31;
   const __bf16* tile = ring_unit<T>(ring);
   const bf16x8 b0 = *reinterpret_cast<const bf16x8*>(tile + row * 16 + 8 * s);
@@ -646,7 +687,7 @@ __device__ __forceinline__ void du_step(const float (&x)[kD], const LdsRing& rin
   acc[1] = mfma32(a, b1, acc[1]);
 }
 template <int G>
-__device__ __forceinline__ void du_group(const float (&x)[kD], const LdsRing& ring, const uint16_t* src, int tid, int lane,
+__device__ __forceinline__ void du_group(const float (&x)[kD], const LdsRing<4>& ring, const uint16_t* src, int tid, int lane,
                                          f32x16 (&acc)[2]) {
   constexpr int NG = (kKS + kFG - 1) / kFG;
   constexpr int n1 = (G + 1 < NG) ? ((G + 1) * kFG + kFG <= kKS ? kFG : kKS - (G + 1) * kFG) : 0;
@@ -709,10 +750,9 @@ __global__ __launch_bounds__(128) void k2_kv_fold(const T* __restrict__ k, const
 
   // 1. fold of dT V^T through the key features
   static_assert(kTileElems <= kFG * 1024, "a fold tile fits one dU ring stage");
-  const LdsRing fr{{ring0, ring1, ring2, ring3}};
-  const LdsRing ring{{ring0, ring1, ring2, ring3}};
-  fold_prologue(dTR + cbase, fr, tid);
-  fold_group<0, false>(bfr, x, dx, nullptr, fr, dTR + cbase, tid, l);
+  const LdsRing<4> fr{{ring0, ring1, ring2, ring3}};
+  const LdsRing<4> ring{{ring0, ring1, ring2, ring3}};
+  fold_all<4, false>(bfr, x, dx, nullptr, fr, dTR + cbase, tid, l);
   __syncthreads();
   // 2. dU = raw(K) dT (values 0..63)
   f32x16 acc[2] = {f32x16{}, f32x16{}};

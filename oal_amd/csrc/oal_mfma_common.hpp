@@ -222,12 +222,27 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// Four LDS stages of an asynchronous copy ring. The stages are distinct
+// Marks the 64 registers of a per-lane array as read and written at this
+// point (no instruction is emitted): arithmetic that updates them cannot be
+// moved past it. Code generation for a fully unrolled pipeline sees one basic
+// block and may otherwise defer whole stages of register arithmetic to the
+// end, holding (and spilling) the operands of every stage in between.
+__device__ __forceinline__ void pin64(float (&a)[64]) {
+#pragma unroll
+  for (int i = 0; i < 64; i += 16)
+    asm volatile(""
+                 : "+v"(a[i]), "+v"(a[i + 1]), "+v"(a[i + 2]), "+v"(a[i + 3]), "+v"(a[i + 4]), "+v"(a[i + 5]),
+                   "+v"(a[i + 6]), "+v"(a[i + 7]), "+v"(a[i + 8]), "+v"(a[i + 9]), "+v"(a[i + 10]),
+                   "+v"(a[i + 11]), "+v"(a[i + 12]), "+v"(a[i + 13]), "+v"(a[i + 14]), "+v"(a[i + 15]));
+}
+
+// NS LDS stages of an asynchronous copy ring. The stages are distinct
 // __shared__ objects: the compiler then tells a read of one stage from the
 // copies still in flight into the others, where a single array would make it
 // wait for every copy in flight (vmcnt(0)) before each read.
+template <int NS>
 struct LdsRing {
-  __bf16* st[4];
+  __bf16* st[NS];
 };
 
 // Ring barrier: this wave's copies older than the newest N have landed in LDS
@@ -235,13 +250,17 @@ struct LdsRing {
 // workgroup barrier. Unlike __syncthreads() it carries no release fence, which
 // would wait for every asynchronous copy in flight (vmcnt(0)) and empty the
 // ring; the empty asm statements keep the compiler from moving memory accesses
-// across it.
+// across it, the scheduling barriers keep each stage's arithmetic between its
+// two ring barriers (so that products of later stages are not hoisted and
+// spilled).
 template <int N>
 __device__ __forceinline__ void ring_sync() {
   static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit counter");
   asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
   __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
   asm volatile("" ::: "memory");
 }
 

@@ -246,7 +246,7 @@ constexpr int kNSR = 4;  // LDS stages of the readout ring
 // Ring group G (k-steps G * kRG ..) into LDS stage G % kNSR; each k-step tile is
 // 64 values x 16 slots = 128 lanes x 16 bytes.
 template <int G>
-__device__ __forceinline__ void ring_issue(const uint16_t* pt, const LdsRing& ring, int tid) {
+__device__ __forceinline__ void ring_issue(const uint16_t* pt, const LdsRing<4>& ring, int tid) {
   const int wv = tid >> 6;
   __bf16* st = ring.st[G % kNSR];
 #pragma unroll
@@ -257,7 +257,7 @@ __device__ __forceinline__ void ring_issue(const uint16_t* pt, const LdsRing& ri
 }
 
 template <int T>
-__device__ __forceinline__ void readout_step(const float (&x)[kD], const float* wl, const LdsRing& ring, int lane,
+__device__ __forceinline__ void readout_step(const float (&x)[kD], const float* wl, const LdsRing<4>& ring, int lane,
                                              f32x16 (&acc)[2]) {
   const int s = lane >> 5, row = lane & 31;
   const float4 w0 = *reinterpret_cast<const float4*>(wl + 16 * T + 8 * s);
@@ -275,7 +275,7 @@ __device__ __forceinline__ void readout_step(const float (&x)[kD], const float* 
 // flight while group G is read; group G + 3 is issued after the barrier that
 // retires every read of its stage.
 template <int G>
-__device__ __forceinline__ void readout_group(const float (&x)[kD], const float* wl, const LdsRing& ring,
+__device__ __forceinline__ void readout_group(const float (&x)[kD], const float* wl, const LdsRing<4>& ring,
                                               const uint16_t* pt, int tid, int lane, f32x16 (&acc)[2]) {
   constexpr int n1 = (G + 1 < kRingGroups) ? ((G + 1) * kRG + kRG <= kKS ? kRG : kKS - (G + 1) * kRG) : 0;
   constexpr int n2 = (G + 2 < kRingGroups) ? ((G + 2) * kRG + kRG <= kKS ? kRG : kKS - (G + 2) * kRG) : 0;
@@ -516,10 +516,9 @@ __global__ __launch_bounds__(128, 2) void k2_out_fwd(const T* __restrict__ q, co
                                                   const uint16_t* __restrict__ PT, int Hq, int Hkv, int N, int NB,
                                                   float floor, T* __restrict__ out, float* __restrict__ num,
                                                   const float* __restrict__ den) {
-  static_assert(kNSR == 4, "LdsRing has four stages");
   __shared__ __attribute__((aligned(16))) __bf16 ring0[kRG * kRingStep], ring1[kRG * kRingStep],
       ring2[kRG * kRingStep], ring3[kRG * kRingStep];
-  const LdsRing ring{{ring0, ring1, ring2, ring3}};
+  const LdsRing<4> ring{{ring0, ring1, ring2, ring3}};
   __shared__ __attribute__((aligned(16))) float wl[kS];
 
   int hh, ch, u;
