@@ -54,6 +54,7 @@ def credited_flops(kernel: str, b: int, hq: int, hkv: int, n: int) -> float:
         "k_kv_bwd": 2 * unit * kv_tok,
         # matrix-core kernels
         "k2_state_fwd": unit * kv_tok,
+        "k2_state_fwd_totals": unit * kv_tok,
         "k2_out_fwd": unit * q_tok,
         "k2_state_bwd": unit * q_tok,
         "k2_state_bwd_totals": unit * q_tok,

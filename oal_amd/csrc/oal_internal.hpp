@@ -32,6 +32,8 @@ struct MfmaSaved {
   uint16_t* PR;   // [U][NB][kS/32][4][32][16] bf16
   float* PZ;      // [U][NB][kFP] denominator column, natural order
   float* PZm;     // [U][NB][64][64] denominator column as a symmetric pair matrix
+  uint16_t* KT16; // [U][64][NB * 64] bf16 k^T (tokens >= N zero)
+  uint16_t* VT16; // [U][65][NB * 64] bf16 [v^T; 1 (token < N)]
   size_t bytes;
 };
 
@@ -53,9 +55,7 @@ struct MfmaWork {
   float* dTz;     // [U][NB][kFP]
   float* dwqs;    // [S][B][Hq][kS] slot-coefficient gradients (state part) per segment
   float* dwq;     // [Hq][kS] their sum
-  float* segtot;  // [U][S][kS][65] per-segment dCarry totals
-  float* carry;   // [U][S][kS][65] suffix of later segments
-  uint16_t* KT16; // [U][64][NB * 64] bf16 k^T
+  float* segtot;  // [U][S][kS][65] per-segment dCarry totals, then (in place) their carries
   float* dqf;     // [B][Hq][N][64] local dq
   float* dkl;     // [U][N][64] local dk, summed over the unit's query heads
   float* dvl;     // [U][N][64] local dv, summed over the unit's query heads
@@ -77,7 +77,7 @@ struct LocalBwdArgs {
   const float* Gz;
   const uint16_t* QT16;
   const uint16_t* GT16;
-  uint16_t* KT16;
+  const uint16_t* KT16;
   const float* PZ;
   const float* PZm;
   const int32_t* labels;
@@ -97,6 +97,38 @@ struct LocalBwdArgs {
 template <typename T>
 void launch_local_bwd(const LaunchGeom& g, const T* q, const T* k, const T* v, const LocalBwdArgs& a, bool need_dq,
                       bool need_dkv, hipStream_t st, const Timer& timed);
+
+// Segmentation of a chunk-state scan: S segments of SL chunks. More than one
+// segment runs as totals, carry, replay and needs seg_bytes of scratch;
+// scratch_bytes caps S ((size_t)-1: no cap). OAL_SCAN_SEGMENTS overrides.
+struct ScanPlan {
+  int S, SL;
+  size_t seg_bytes;
+};
+ScanPlan scan_plan(int U, int NB, size_t scratch_bytes, bool fwd);
+
+// Operands and outputs of one chunk-state scan (oal_mfma_scan.hip).
+struct ScanArgs {
+  const uint16_t* F;  // feature side, [X][frows][NB * 64] bf16 (rows 0..63 used)
+  int frows;
+  const uint16_t* V;  // value side, [X][vrows][NB * 64] bf16 (rows 0..64 used)
+  int vrows;
+  const float* wqs;   // backward: [Hq][kS] slot coefficients
+  const uint16_t* PR; // backward: forward state (R layout), for the coefficient partials
+  const float* PZ;    // backward: forward denominator column
+  int U, Hq, Hkv, N, NB;
+  uint16_t* outT;     // emitted state, T layout
+  uint16_t* outR;     // emitted state, R layout
+  float* outZ;        // emitted denominator column (natural order)
+  float* outZm;       // forward: denominator column as a symmetric pair matrix
+  float* segtot;      // [U][S][kS][65] scratch when S > 1
+  float* dwqs;        // backward: [S][B][Hq][kS] coefficient partials
+};
+template <bool FWD>
+void launch_scan(const ScanPlan& p, const ScanArgs& a, hipStream_t st, const Timer& timed);
+template <typename T>
+void launch_fwd_prep(const LaunchGeom& g, const T* k, const T* v, uint16_t* KT16, uint16_t* VT16, hipStream_t st,
+                     const Timer& timed);
 
 int run_mfma_selftest(int* dev_errors, hipStream_t st);
 

@@ -1,13 +1,8 @@
 // bf16 matrix-core (MFMA) backward for gfx950.
 //
 // k2_bwd_prep   normalization VJP: G (bf16 token rows and transposed), Gz; transposed q.
-// k2_state_bwd  reverse chunk scan per (4 slot tiles, unit, segment):
-//               dT_c = sum_{c'>c} dCarry_c' in MFMA accumulators (value x slot),
-//               dCarry_c = sum_h wq_h * (raw(Q_h)^T [G_h, Gz_h]); the per-slot
-//               feature-coefficient gradient sum_c <P_c, raw(Q)^T G> reduces
-//               inside the accumulator registers. Stores dT in the two k-blocked
-//               layouts of the forward state plus dTz (fp32, natural order).
-//               Segments run as totals, carry, replay (k2_seg_carry).
+// (the reverse chunk scan dT_c = sum_{c' > c} dCarry_c' and the per-slot
+// coefficient partials are in oal_mfma_scan.hip)
 // (the intra-chunk VJP, k2_local_dq / k2_local_dkv, is in oal_mfma_local.hip)
 // k2_q_fold     dq state part: D^T = P G^T on the MFMA, folded through the query
 //               features (rotated rows, static register indices) + local dq.
@@ -216,260 +211,6 @@ __global__ __launch_bounds__(256) void k2_bwd_prep(const T* __restrict__ q, cons
     const size_t o = ((size_t)bh * kTRows + r) * np + (size_t)ch * kC + 8 * c8;
     *reinterpret_cast<bf16x8*>(GT16 + o) = *reinterpret_cast<const bf16x8*>(&gT[r][8 * c8]);
     *reinterpret_cast<bf16x8*>(QT16 + o) = *reinterpret_cast<const bf16x8*>(&qT[r][8 * c8]);
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Backward state scan over one segment of chunks (reverse order).
-// grid (ceil(69 / 4) tile groups, U, S segments), 4 waves; wave w owns the
-// 32-slot tile 4 * blockIdx.x + w. Accumulators hold dT^T [96 value rows
-// (row 64 = denominator) x 32 slots] (lane column = slot):
-//   dT_c = carry + sum_{c' > c in segment} dCarry_c',
-//   dCarry_c = sum_h wq_h o (raw(Q_h)^T [G_h, Gz_h])   (reference
-//   hd_block_gemm_backward.py:764-908, _query_dcarry + _exclusive_right_scan).
-// The per-(head, chunk) operands QT16 / GT16 are staged once per block into a
-// double-buffered LDS ring shared by the four tiles; raw features come from
-// v_dot2_f32_bf16 on masked bf16 pairs.
-// MODE 0: segment totals + coefficient partials (no dT outputs);
-// MODE 1: replay from the carry of later segments, emit dT;
-// MODE 2: single segment, emit dT and coefficient partials.
-// Coefficient partial: dwq_h[slot] += sum_c <P_c[slot], raw(Q_h,c)^T G_h,c [slot]>.
-// ---------------------------------------------------------------------------
-constexpr int kSB_TILES = 4;
-constexpr int kSB_ROW = kC + 8;                     // LDS row stride of G^T (bf16)
-constexpr int kSB_QROW = kC + 4;                    // LDS row stride of q^T (f32)
-constexpr int kSB_BUF = kTRows * kSB_ROW;           // one staged G^T
-constexpr int kSB_QBUF = kTRows * kSB_QROW;         // one staged q^T
-constexpr int kSB_UNITS = kTRows * kC / 8;          // 16-byte bf16 units per matrix (528)
-
-template <int MODE>
-__global__ __launch_bounds__(256) void k2_state_bwd(const uint16_t* __restrict__ QT16,
-                                                    const uint16_t* __restrict__ GT16, const float* __restrict__ wqs,
-                                                    const uint16_t* __restrict__ PR, const float* __restrict__ PZ,
-                                                    const float* __restrict__ carry, int Hq, int Hkv, int N, int NB,
-                                                    int SL, int Sg, uint16_t* __restrict__ dTT,
-                                                    uint16_t* __restrict__ dTR,
-                                                    float* __restrict__ dTz, float* __restrict__ segtot,
-                                                    float* __restrict__ dwqs) {
-  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-  __shared__ __attribute__((aligned(16))) float Qs[2][kSB_QBUF];
-  __shared__ __attribute__((aligned(16))) __bf16 Gs[2][kSB_BUF];
-  __shared__ __attribute__((aligned(16))) __bf16 em[kSB_TILES][32][kSB_ROW];
-
-  // 1-D grid ordered so that the tile groups of one (unit, segment), which read
-  // the same operands, run on one XCD (workgroup id -> XCD id % 8)
-  constexpr int TG = (kS / 32 + kSB_TILES - 1) / kSB_TILES;
-  const int total = gridDim.x;
-  int u, seg, tgi;
-  {
-    const int id = blockIdx.x;
-    const int w = (total & 7) == 0 ? (id & 7) * (total >> 3) + (id >> 3) : id;
-    tgi = w % TG;
-    seg = (w / TG) % Sg;
-    u = w / (TG * Sg);
-  }
-  const int R = Hq / Hkv, b = u / Hkv, kh = u % Hkv;
-  const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, s = l >> 5, row = l & 31;
-  const int tile = kSB_TILES * tgi + wv;
-  const bool live = tile < kS / 32;
-  const int slot = live ? tile * 32 + row : 0;
-  const int ar = kSlot.ar[slot], ac = kSlot.ac[slot], nat = live ? kSlot.nat[slot] : -1;
-  const int c_lo = seg * SL, c_hi = min(NB, c_lo + SL);
-  const size_t np = (size_t)NB * kC;
-  const size_t chunk_elems = (size_t)kKS * 64 * 16;
-
-  float wh[8], dwp[8];
-#pragma unroll
-  for (int hh = 0; hh < 8; ++hh) {
-    wh[hh] = (live && hh < R) ? wqs[(size_t)(kh * R + hh) * kS + slot] : 0.f;
-    dwp[hh] = 0.f;
-  }
-
-  f32x16 acc[3];
-#pragma unroll
-  for (int n = 0; n < 3; ++n) acc[n] = f32x16{};
-  if constexpr (MODE == 1) {
-    if (live) {
-      const float* cr = carry + (((size_t)u * Sg + seg) * kS + slot) * 65;
-#pragma unroll
-      for (int n = 0; n < 2; ++n)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) acc[n][i] = cr[32 * n + c32_row(i, l)];
-      acc[2][0] = s == 0 ? cr[64] : 0.f;
-    }
-  }
-
-  // staging of item (chunk, head): 528 16-byte units per matrix; thread t
-  // moves units t and t + 256 of each, threads t < 16 also unit t + 512.
-  uint4 rq0, rq1, rq2, rg0, rg1, rg2;
-  rq2 = rg2 = make_uint4(0u, 0u, 0u, 0u);
-  const bool third = tid < kSB_UNITS - 512;
-  const size_t u0 = (size_t)(tid >> 3) * np + 8 * (tid & 7);
-  const size_t u1 = (size_t)((tid + 256) >> 3) * np + 8 * (tid & 7);
-  const size_t u2 = (size_t)((tid + 512) >> 3) * np + 8 * (tid & 7);
-  auto fetch = [&](int ch, int hh) {
-    const size_t base = ((size_t)(b * Hq + kh * R + hh) * kTRows) * np + (size_t)ch * kC;
-    rq0 = *reinterpret_cast<const uint4*>(QT16 + base + u0);
-    rg0 = *reinterpret_cast<const uint4*>(GT16 + base + u0);
-    rq1 = *reinterpret_cast<const uint4*>(QT16 + base + u1);
-    rg1 = *reinterpret_cast<const uint4*>(GT16 + base + u1);
-    if (third) {
-      rq2 = *reinterpret_cast<const uint4*>(QT16 + base + u2);
-      rg2 = *reinterpret_cast<const uint4*>(GT16 + base + u2);
-    }
-  };
-  auto put = [&](int buf, int idx, const uint4& wq, const uint4& wg) {
-    const int r = idx >> 3, c8 = idx & 7;
-    float4* qd = reinterpret_cast<float4*>(&Qs[buf][r * kSB_QROW + 8 * c8]);
-    qd[0] = make_float4(__uint_as_float(wq.x << 16), __uint_as_float(wq.x & 0xffff0000u),
-                        __uint_as_float(wq.y << 16), __uint_as_float(wq.y & 0xffff0000u));
-    qd[1] = make_float4(__uint_as_float(wq.z << 16), __uint_as_float(wq.z & 0xffff0000u),
-                        __uint_as_float(wq.w << 16), __uint_as_float(wq.w & 0xffff0000u));
-    *reinterpret_cast<uint4*>(&Gs[buf][r * kSB_ROW + 8 * c8]) = wg;
-  };
-  auto store = [&](int buf) {
-    put(buf, tid, rq0, rg0);
-    put(buf, tid + 256, rq1, rg1);
-    if (third) put(buf, tid + 512, rq2, rg2);
-  };
-
-  fetch(c_hi - 1, 0);
-  store(0);
-  __syncthreads();
-  int buf = 0;
-  float pf[2][16];
-  float pz = 0.f;
-  for (int ch = c_hi - 1; ch >= c_lo; --ch) {
-    const size_t cb = (size_t)u * NB + ch;
-    if constexpr (MODE != 0) {
-      // emit dT_c = acc (exclusive suffix)
-      if (live) {
-        uint16_t* tr = dTR + cb * chunk_elems + (size_t)tile * 4 * 32 * 16;
-#pragma unroll
-        for (int n = 0; n < 2; ++n)
-#pragma unroll
-          for (int a = 0; a < 4; ++a) {
-            const uint32_t w0 = pack_bf16x2(acc[n][4 * a], acc[n][4 * a + 1]);
-            const uint32_t w1 = pack_bf16x2(acc[n][4 * a + 2], acc[n][4 * a + 3]);
-            const int kk = 2 * n + (a >> 1), pos = 8 * (a & 1) + 4 * s;
-            *reinterpret_cast<uint2*>(tr + ((size_t)kk * 32 + row) * 16 + pos) = make_uint2(w0, w1);
-            *reinterpret_cast<uint2*>(&em[wv][row][32 * n + 8 * a + 4 * s]) = make_uint2(w0, w1);
-          }
-        if (s == 0 && nat >= 0) dTz[cb * kFP + nat] = acc[2][0];
-        __builtin_amdgcn_wave_barrier();
-        // dTT [kstep][64 values][16 slots]: lane l = value row
-        uint16_t* tt = dTT + cb * chunk_elems;
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-          uint32_t w[8];
-#pragma unroll
-          for (int q2 = 0; q2 < 8; ++q2)
-            w[q2] = uint32_t(__builtin_bit_cast(uint16_t, em[wv][16 * ks + 2 * q2][l])) |
-                    (uint32_t(__builtin_bit_cast(uint16_t, em[wv][16 * ks + 2 * q2 + 1][l])) << 16);
-          uint4* dst = reinterpret_cast<uint4*>(tt + ((size_t)(2 * tile + ks) * 64 + l) * 16);
-          dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
-          dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
-        }
-        __builtin_amdgcn_wave_barrier();
-      }
-    }
-    if constexpr (MODE != 1) {
-      // P_c rows of this lane's slot, values e = 32 n + 8 a + 4 s + v
-      if (live) {
-        const uint16_t* pr = PR + cb * chunk_elems + (size_t)tile * 4 * 32 * 16;
-#pragma unroll
-        for (int n = 0; n < 2; ++n)
-#pragma unroll
-          for (int a = 0; a < 4; ++a) {
-            const int kk = 2 * n + (a >> 1), pos = 8 * (a & 1) + 4 * s;
-            const uint2 w = *reinterpret_cast<const uint2*>(pr + ((size_t)kk * 32 + row) * 16 + pos);
-            pf[n][4 * a] = __uint_as_float(w.x << 16);
-            pf[n][4 * a + 1] = __uint_as_float(w.x & 0xffff0000u);
-            pf[n][4 * a + 2] = __uint_as_float(w.y << 16);
-            pf[n][4 * a + 3] = __uint_as_float(w.y & 0xffff0000u);
-          }
-        pz = (s == 0 && nat >= 0) ? PZ[cb * kFP + nat] : 0.f;
-      }
-    }
-#pragma unroll
-    for (int hh = 0; hh < 8; ++hh) {
-      if (hh < R) {
-        const bool more = hh + 1 < R || ch > c_lo;
-        if (more) fetch(hh + 1 < R ? ch : ch - 1, hh + 1 < R ? hh + 1 : 0);
-        if (live) {
-          const float* qs = Qs[buf];
-          const __bf16* gs = Gs[buf];
-          f32x16 hT[3] = {f32x16{}, f32x16{}, f32x16{}};
-#pragma unroll
-          for (int kk = 0; kk < 4; ++kk) {
-            const float4* pa = reinterpret_cast<const float4*>(qs + ar * kSB_QROW + 16 * kk + 8 * s);
-            const float4* pc = reinterpret_cast<const float4*>(qs + ac * kSB_QROW + 16 * kk + 8 * s);
-            const float4 a0 = pa[0], a1 = pa[1], c0v = pc[0], c1v = pc[1];
-            const float f[8] = {a0.x * c0v.x, a0.y * c0v.y, a0.z * c0v.z, a0.w * c0v.w,
-                                a1.x * c1v.x, a1.y * c1v.y, a1.z * c1v.z, a1.w * c1v.w};
-            const bf16x8 bq = pack8(f);
-#pragma unroll
-            for (int n = 0; n < 3; ++n) {
-              const int gr = n < 2 ? 32 * n + row : (row == 0 ? kD : kD + 1);
-              const bf16x8 a = *reinterpret_cast<const bf16x8*>(gs + gr * kSB_ROW + 16 * kk + 8 * s);
-              hT[n] = mfma32(a, bq, hT[n]);
-            }
-          }
-          const float w = wh[hh];
-#pragma unroll
-          for (int n = 0; n < 2; ++n)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) acc[n][i] = fmaf(w, hT[n][i], acc[n][i]);
-          acc[2][0] = fmaf(w, hT[2][0], acc[2][0]);
-          if constexpr (MODE != 1) {
-            float d = pz * hT[2][0];
-#pragma unroll
-            for (int n = 0; n < 2; ++n)
-#pragma unroll
-              for (int i = 0; i < 16; ++i) d = fmaf(pf[n][i], hT[n][i], d);
-            dwp[hh] += d;
-          }
-        }
-        if (more) store(buf ^ 1);
-        __syncthreads();
-        buf ^= 1;
-      }
-    }
-  }
-  if constexpr (MODE == 0) {
-    if (live) {
-      float* st = segtot + (((size_t)u * Sg + seg) * kS + slot) * 65;
-#pragma unroll
-      for (int n = 0; n < 2; ++n)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) st[32 * n + c32_row(i, l)] = acc[n][i];
-      if (s == 0) st[64] = acc[2][0];
-    }
-  }
-  if constexpr (MODE != 1) {
-    const int B = (int)(gridDim.x / (TG * Sg)) / Hkv;
-#pragma unroll
-    for (int hh = 0; hh < 8; ++hh) {
-      if (hh < R) {
-        const float tot = dwp[hh] + __shfl_xor(dwp[hh], 32, 64);
-        if (live && s == 0) dwqs[(((size_t)seg * B + b) * Hq + kh * R + hh) * kS + slot] = tot;
-      }
-    }
-  }
-}
-
-// carry[u][seg] = sum_{seg' > seg} segtot[u][seg'] (fixed order), elementwise.
-__global__ __launch_bounds__(256) void k2_seg_carry(const float* __restrict__ segtot, int S,
-                                                    float* __restrict__ carry) {
-  const size_t per = (size_t)kS * 65;
-  const size_t e = (size_t)blockIdx.x * 256 + threadIdx.x;
-  if (e >= per) return;
-  const size_t ub = (size_t)blockIdx.y * S * per;
-  float run = 0.f;
-  for (int sg = S - 1; sg >= 0; --sg) {
-    carry[ub + (size_t)sg * per + e] = run;
-    run += segtot[ub + (size_t)sg * per + e];
   }
 }
 
@@ -814,8 +555,19 @@ __global__ __launch_bounds__(256) void k2_dwq_reduce(const float* __restrict__ d
                                                      float* __restrict__ dwq) {
   const int h = blockIdx.y, sl = blockIdx.x * 256 + threadIdx.x;
   if (sl >= kS) return;
+  // fixed order; eight loads in flight at a time
+  const float* p = dwqs + (size_t)h * kS + sl;
+  const size_t st = (size_t)Hq * kS;
   float acc = 0.f;
-  for (int r = 0; r < rowsets; ++r) acc += dwqs[((size_t)r * Hq + h) * kS + sl];
+  int r = 0;
+  for (; r + 8 <= rowsets; r += 8) {
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = p[(size_t)(r + i) * st];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc += v[i];
+  }
+  for (; r < rowsets; ++r) acc += p[(size_t)r * st];
   dwq[(size_t)h * kS + sl] = acc;
 }
 
@@ -845,12 +597,30 @@ __global__ __launch_bounds__(256) void k2_coef_grad(const float* __restrict__ dw
     const int n = kSlot.nat[sl];
     if (n >= 0) wn[n] = dwq[(size_t)h * kS + sl];
   }
-  for (int j = wave; j < 73; j += 4) {
-    const float* col = coefl + ((size_t)h * 73 + j) * bn;
-    float acc = 0.f;
-    for (int r = lane; r < bn; r += 64) acc += col[r];
-    acc = wave_sum(acc);
-    if (lane == 0) loc[j] = acc;
+  // column sums of the local partials: each wave owns columns wave, wave + 4, ..;
+  // all of a lane's loads for those columns are issued before the sums
+  {
+    constexpr int kCols = (73 + 3) / 4;
+    float part[kCols];
+#pragma unroll
+    for (int i = 0; i < kCols; ++i) part[i] = 0.f;
+    for (int r0 = 0; r0 < bn; r0 += 64) {
+      const int r = r0 + lane;
+      float v[kCols];
+#pragma unroll
+      for (int i = 0; i < kCols; ++i) {
+        const int j = wave + 4 * i;
+        v[i] = (j < 73 && r < bn) ? coefl[((size_t)h * 73 + j) * bn + r] : 0.f;
+      }
+#pragma unroll
+      for (int i = 0; i < kCols; ++i) part[i] += v[i];
+    }
+#pragma unroll
+    for (int i = 0; i < kCols; ++i) {
+      const int j = wave + 4 * i;
+      const float acc = wave_sum(part[i]);
+      if (lane == 0 && j < 73) loc[j] = acc;
+    }
   }
   __syncthreads();
   for (int e = t; e < kD * 8; e += 256) {
@@ -893,17 +663,6 @@ __global__ __launch_bounds__(256) void k2_coef_grad(const float* __restrict__ dw
 // Segments of the backward state scan: enough (tile group, unit, segment)
 // blocks to give every SIMD about four waves; one segment when that already
 // holds. OAL_BWD_SEGMENTS overrides (for tuning).
-static void bwd_segments(int U, int NB, int& S, int& SL) {
-  const int tg = (kS / 32 + kSB_TILES - 1) / kSB_TILES;
-  const int per_seg_waves = tg * U * kSB_TILES;
-  int want = (4096 + per_seg_waves - 1) / per_seg_waves;
-  if (const char* env = getenv("OAL_BWD_SEGMENTS")) want = atoi(env);
-  if (want < 1) want = 1;
-  if (want > NB) want = NB;
-  SL = (NB + want - 1) / want;
-  S = (NB + SL - 1) / SL;
-}
-
 MfmaWork mfma_work_view(void* base, int B, int Hq, int U, int N, int NB) {
   char* p = static_cast<char*>(base);
   size_t off = 0;
@@ -916,7 +675,9 @@ MfmaWork mfma_work_view(void* base, int B, int Hq, int U, int N, int NB) {
   const size_t trows = (size_t)B * Hq * kTRows * NB * kC;
   const size_t chunk = (size_t)kKS * 64 * 16 * sizeof(uint16_t);
   MfmaWork w;
-  bwd_segments(U, NB, w.S, w.SL);
+  const ScanPlan plan = scan_plan(U, NB, (size_t)-1, false);
+  w.S = plan.S;
+  w.SL = plan.SL;
   w.G16 = static_cast<uint16_t*>(take(rows * kD * sizeof(uint16_t)));
   w.Gz = static_cast<float*>(take(rows * sizeof(float)));
   w.GT16 = static_cast<uint16_t*>(take(trows * sizeof(uint16_t)));
@@ -926,10 +687,7 @@ MfmaWork mfma_work_view(void* base, int B, int Hq, int U, int N, int NB) {
   w.dTz = static_cast<float*>(take(sizeof(float) * (size_t)U * NB * kFP));
   w.dwqs = static_cast<float*>(take(sizeof(float) * (size_t)w.S * B * Hq * kS));
   w.dwq = static_cast<float*>(take(sizeof(float) * (size_t)Hq * kS));
-  const size_t seg = w.S > 1 ? sizeof(float) * (size_t)U * w.S * kS * 65 : 0;
-  w.segtot = static_cast<float*>(take(seg));
-  w.carry = static_cast<float*>(take(seg));
-  w.KT16 = static_cast<uint16_t*>(take((size_t)U * kD * NB * kC * sizeof(uint16_t)));
+  w.segtot = static_cast<float*>(take(plan.seg_bytes));
   w.dqf = static_cast<float*>(take(rows * kD * sizeof(float)));
   w.dkl = static_cast<float*>(take((size_t)U * N * kD * sizeof(float)));
   w.dvl = static_cast<float*>(take((size_t)U * N * kD * sizeof(float)));
@@ -956,27 +714,14 @@ int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, cons
     hipLaunchKernelGGL(k2_bwd_prep<T>, dim3(g.B * g.Hq * g.NB), dim3(256), 0, st, qt, static_cast<const T*>(dout),
                        dnum, dden, num, den, g.N, g.NB, floor, w.G16, w.Gz, w.GT16, w.QT16);
   });
-  const dim3 sgrid((unsigned)(((kS / 32 + kSB_TILES - 1) / kSB_TILES) * g.U * w.S));
-  if (w.S == 1) {
-    timed("k2_state_bwd", st, [&] {
-      hipLaunchKernelGGL(k2_state_bwd<2>, sgrid, dim3(256), 0, st, w.QT16, w.GT16, sv.wqs, sv.PR, sv.PZ, nullptr,
-                         g.Hq, g.Hkv, g.N, g.NB, w.SL, w.S, w.dTT, w.dTR, w.dTz, nullptr, w.dwqs);
-    });
-  } else {
-    timed("k2_state_bwd_totals", st, [&] {
-      hipLaunchKernelGGL(k2_state_bwd<0>, sgrid, dim3(256), 0, st, w.QT16, w.GT16, sv.wqs, sv.PR, sv.PZ, nullptr,
-                         g.Hq, g.Hkv, g.N, g.NB, w.SL, w.S, nullptr, nullptr, nullptr, w.segtot, w.dwqs);
-    });
-    timed("k2_seg_carry", st, [&] {
-      hipLaunchKernelGGL(k2_seg_carry, dim3((kS * 65 + 255) / 256, g.U), dim3(256), 0, st, w.segtot, w.S, w.carry);
-    });
-    timed("k2_state_bwd", st, [&] {
-      hipLaunchKernelGGL(k2_state_bwd<1>, sgrid, dim3(256), 0, st, w.QT16, w.GT16, sv.wqs, sv.PR, sv.PZ, w.carry,
-                         g.Hq, g.Hkv, g.N, g.NB, w.SL, w.S, w.dTT, w.dTR, w.dTz, nullptr, nullptr);
-    });
+  {
+    const ScanPlan plan{w.S, w.SL, 0};
+    ScanArgs a{w.QT16, kTRows, w.GT16, kTRows, sv.wqs, sv.PR, sv.PZ, g.U, g.Hq, g.Hkv, g.N, g.NB,
+               w.dTT, w.dTR, w.dTz, nullptr, w.segtot, w.dwqs};
+    launch_scan<false>(plan, a, st, timed);
   }
   {
-    LocalBwdArgs la{w.G16, w.Gz, w.QT16, w.GT16, w.KT16, sv.PZ, sv.PZm, labels, lam, gam, sv.ic, sv.gm, sv.lb,
+    LocalBwdArgs la{w.G16, w.Gz, w.QT16, w.GT16, sv.KT16, sv.PZ, sv.PZm, labels, lam, gam, sv.ic, sv.gm, sv.lb,
                     groups, scale, w.dqf, w.dkl, w.dvl, need_coef ? w.coefl : nullptr};
     launch_local_bwd<T>(g, qt, kt, vt, la, dq != nullptr, dk != nullptr, st, timed);
   }

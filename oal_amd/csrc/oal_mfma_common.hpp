@@ -264,5 +264,17 @@ __device__ __forceinline__ void ring_sync() {
   asm volatile("" ::: "memory");
 }
 
+// Workgroup barrier over LDS only: this wave's LDS reads and writes are done
+// (lgkmcnt(0)), then s_barrier. Unlike __syncthreads() it does not wait for
+// outstanding global loads and stores (vmcnt counts both on gfx950), so
+// register prefetches and state stores stay in flight across it; a use of a
+// loaded register still waits for its own load.
+__device__ __forceinline__ void lds_sync() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt((63 & 15) | ((63 >> 4) << 14) | (7 << 4));
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 }  // namespace oal
 

@@ -1,13 +1,14 @@
 // bf16 matrix-core (MFMA) forward for gfx950.
 //
-// k2_state_fwd  : per (32-slot tile, unit) sequential chunk scan; the running
-//                 state lives in MFMA accumulators; stores the exclusive prefix
-//                 P_c in two k-blocked bf16 layouts plus the fp32 denominator
-//                 column in natural feature order.
-// k2_out_fwd    : per (query head, chunk, unit) one wave: denominator state term
-//                 as a 64x64 quadratic form, intra-chunk kernel from MFMA group
-//                 sums, state readout phi_Q . P_c with query features generated
-//                 in registers, intra term kappa . V, normalize.
+// k2_slot_coefficients : per query head, the feature coefficient of every slot
+//                        and the intra-chunk coefficient packs.
+// (k2_fwd_prep and the chunk-state scan producing P_c are in oal_mfma_scan.hip)
+// k2_intra_fwd         : per (query head, chunk, unit): intra-chunk kernel from
+//                        MFMA group sums, kappa . V, and the denominator's state
+//                        term as a 64x64 quadratic form; writes num, den.
+// k2_out_fwd           : per (query head, chunk, unit): state readout
+//                        phi_Q . P_c with query features generated in
+//                        registers, added to num, then out = num / den.
 //
 // Saved layouts (per unit u and chunk c; "tile" = 32 slots, "k-step" = 16 slots):
 //   PT [u][c][kKS][64 e][16]        bf16  (readout B operand: slots contiguous)
@@ -35,44 +36,51 @@ __global__ __launch_bounds__(256) void k2_slot_coefficients(const int32_t* __res
                                                             const float* __restrict__ gam, int G, float scale,
                                                             float* __restrict__ wqs, float* __restrict__ ic,
                                                             float* __restrict__ gm, float* __restrict__ lb) {
+  // the head's coefficients are read once into LDS; every output then comes
+  // from LDS (no dependent global gathers)
   __shared__ int lab[kD];
+  __shared__ float cg[8 * 8], cl[8], cc;
   const int h = blockIdx.x, t = threadIdx.x;
   if (t < kD) {
     const int g = labels[h * kD + t];
     lab[t] = g < 0 ? 0 : (g >= G ? G - 1 : g);
   }
+  if (t < 64) {
+    const int g = t >> 3, g2 = t & 7;
+    cg[t] = (g < G && g2 < G) ? scale * scale * gam[((size_t)h * G + g) * G + g2] : 0.f;
+  }
+  if (t >= 64 && t < 72) cl[t - 64] = (t - 64) < G ? scale * lam[(size_t)h * G + (t - 64)] : 0.f;
+  if (t == 72) cc = c0[h];
   __syncthreads();
   for (int s = t; s < kS; s += blockDim.x) {
     const int n = kSlot.nat[s];
     const int r = kSlot.ar[s], c = kSlot.ac[s];
     float w = 0.f;
     if (n == 0) {
-      w = c0[h];
+      w = cc;
     } else if (n > 0 && n <= kD) {
-      w = scale * lam[(size_t)h * G + lab[r]];
+      w = cl[lab[r]];
     } else if (n > kD) {
-      w = (r == c ? 1.f : 2.f) * scale * scale * gam[((size_t)h * G + lab[r]) * G + lab[c]];
+      w = (r == c ? 1.f : 2.f) * cg[lab[r] * 8 + lab[c]];
     }
     wqs[(size_t)h * kS + s] = w;
   }
   if (t < kIC) {
     float x = 0.f;
     if (t == 0) {
-      x = c0[h];
+      x = cc;
     } else if (t < kIcGam) {
-      const int g = t - kIcLam;
-      x = g < G ? scale * lam[(size_t)h * G + g] : 0.f;
+      x = cl[t - kIcLam];
     } else if (t < kIcGam + 64) {
-      const int g = (t - kIcGam) >> 3, g2 = (t - kIcGam) & 7;
-      x = (g < G && g2 < G) ? scale * scale * gam[((size_t)h * G + g) * G + g2] : 0.f;
+      x = cg[t - kIcGam];
     }
     ic[(size_t)h * kIC + t] = x;
   }
   for (int e = t; e < kD * kD; e += blockDim.x) {
     const int r = e >> 6, c = e & 63;
-    gm[(size_t)h * kD * kD + e] = scale * scale * gam[((size_t)h * G + lab[r]) * G + lab[c]];
+    gm[(size_t)h * kD * kD + e] = cg[lab[r] * 8 + lab[c]];
   }
-  if (t < kD) lb[(size_t)h * kD + t] = scale * lam[(size_t)h * G + lab[t]];
+  if (t < kD) lb[(size_t)h * kD + t] = cl[lab[t]];
 }
 
 template <typename T>
@@ -100,126 +108,6 @@ __device__ __forceinline__ void load_row(const float* __restrict__ src, size_t r
     float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
     const bf16x8 x = pack8(v);
     r[i] = ok ? x : bf16x8{};
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Forward state scan. grid (kS/32, U), one wave. Lane row = slot (32 per tile),
-// accumulator N-tiles: values 0-31, 32-63, and [den, 0...] (a ones column).
-// ---------------------------------------------------------------------------
-template <typename T>
-__global__ __launch_bounds__(64) void k2_state_fwd(const T* __restrict__ k, const T* __restrict__ v, int N, int NB,
-                                                   uint16_t* __restrict__ PT, uint16_t* __restrict__ PR,
-                                                   float* __restrict__ PZ, float* __restrict__ PZm) {
-  __shared__ float kT[kRow][kC + 4];                               // kT[d][tok]; row 64 = valid, 65 = 0
-  __shared__ __attribute__((aligned(16))) __bf16 vT[96][kC + 8];  // vT[e][tok]; row 64 = valid
-  __shared__ float stage[32][97];
-
-  const int tile = blockIdx.x, u = blockIdx.y;
-  const int l = threadIdx.x, s = l >> 5, row = l & 31;
-  const int slot = tile * 32 + row;
-  const int ar = kSlot.ar[slot], ac = kSlot.ac[slot];
-  const size_t base = (size_t)u * N * kD;
-
-  for (int idx = l; idx < 31 * (kC + 8); idx += 64) vT[65 + idx / (kC + 8)][idx % (kC + 8)] = (__bf16)0.f;
-
-  // lane = token of the chunk being staged
-  auto stage_chunk = [&](const bf16x8 (&kr)[8], const bf16x8 (&vr)[8], bool ok) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        kT[8 * i + j][l] = (float)kr[i][j];
-        vT[8 * i + j][l] = vr[i][j];
-      }
-    kT[64][l] = ok ? 1.f : 0.f;
-    kT[65][l] = 0.f;
-    vT[64][l] = (__bf16)(ok ? 1.f : 0.f);
-  };
-  bf16x8 kr[8], vr[8];
-  {
-    const bool ok = l < N;
-    const size_t off = base + (size_t)(ok ? l : N - 1) * kD;
-    load_row(k, off, ok, kr);
-    load_row(v, off, ok, vr);
-    stage_chunk(kr, vr, ok);
-  }
-
-  f32x16 acc[3];
-#pragma unroll
-  for (int n = 0; n < 3; ++n) acc[n] = f32x16{};
-
-  const size_t chunk_elems = (size_t)kKS * 64 * 16;  // per (u, c) for PT and PR
-  for (int ch = 0; ch < NB; ++ch) {
-    // 1. exclusive prefix P_c = current accumulators
-#pragma unroll
-    for (int n = 0; n < 3; ++n) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) stage[c32_row(i, l)][32 * n + row] = acc[n][i];
-    }
-    __syncthreads();
-    uint16_t* pt = PT + ((size_t)u * NB + ch) * chunk_elems;
-    uint16_t* pr = PR + ((size_t)u * NB + ch) * chunk_elems;
-    {
-      const int t = 2 * tile + s;
-#pragma unroll
-      for (int eh = 0; eh < 2; ++eh) {
-        const int e = row + 32 * eh;
-        uint32_t w[8];
-#pragma unroll
-        for (int q = 0; q < 8; ++q) w[q] = pack_bf16x2(stage[16 * s + 2 * q][e], stage[16 * s + 2 * q + 1][e]);
-        uint4* dst = reinterpret_cast<uint4*>(pt + ((size_t)t * 64 + e) * 16);
-        dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
-        dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
-      }
-#pragma unroll
-      for (int kh = 0; kh < 2; ++kh) {
-        const int kk = 2 * s + kh;
-        uint32_t w[8];
-#pragma unroll
-        for (int q = 0; q < 8; ++q) w[q] = pack_bf16x2(stage[row][16 * kk + 2 * q], stage[row][16 * kk + 2 * q + 1]);
-        uint4* dst = reinterpret_cast<uint4*>(pr + (((size_t)tile * 4 + kk) * 32 + row) * 16);
-        dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
-        dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
-      }
-      if (s == 0) {
-        const int n = kSlot.nat[slot];
-        if (n >= 0) {
-          const float z = stage[row][64];
-          PZ[((size_t)u * NB + ch) * kFP + n] = z;
-          if (n > kD) {
-            float* pm = PZm + ((size_t)u * NB + ch) * kD * kD;
-            pm[ar * kD + ac] = z;
-            pm[ac * kD + ar] = z;
-          }
-        }
-      }
-    }
-    // 2. prefetch chunk c + 1 into registers
-    const int tok_next = (ch + 1) * kC + l;
-    const bool ok_next = tok_next < N;
-    if (ch + 1 < NB) {
-      const size_t off = base + (size_t)(ok_next ? tok_next : N - 1) * kD;
-      load_row(k, off, ok_next, kr);
-      load_row(v, off, ok_next, vr);
-    }
-    // 3. T_c = phi_K^T [V, 1] from the staged chunk c
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      const int j0 = 16 * kk + 8 * s;
-      float f[8];
-#pragma unroll
-      for (int q = 0; q < 8; ++q) f[q] = kT[ar][j0 + q] * kT[ac][j0 + q];
-      const bf16x8 a = pack8(f);
-#pragma unroll
-      for (int n = 0; n < 3; ++n) {
-        const bf16x8 b = *reinterpret_cast<const bf16x8*>(&vT[32 * n + row][j0]);
-        acc[n] = mfma32(a, b, acc[n]);
-      }
-    }
-    __syncthreads();
-    if (ch + 1 < NB) stage_chunk(kr, vr, ok_next);
-    __syncthreads();
   }
 }
 
@@ -652,6 +540,8 @@ MfmaSaved mfma_saved_view(void* base, int Hq, int U, int NB) {
   v.PR = static_cast<uint16_t*>(take(chunk * units));
   v.PZ = static_cast<float*>(take(sizeof(float) * units * kFP));
   v.PZm = static_cast<float*>(take(sizeof(float) * units * kD * kD));
+  v.KT16 = static_cast<uint16_t*>(take(sizeof(uint16_t) * units * kD * kC));
+  v.VT16 = static_cast<uint16_t*>(take(sizeof(uint16_t) * units * (kD + 1) * kC));
   v.bytes = off;
   return v;
 }
@@ -670,10 +560,15 @@ void launch_mfma_forward(const LaunchGeom& g, const void* q, const void* k, cons
     hipLaunchKernelGGL(k2_slot_coefficients, dim3(g.Hq), dim3(256), 0, st, labels, c0, lam, gam, groups, scale,
                        sv.wqs, sv.ic, sv.gm, sv.lb);
   });
-  timed("k2_state_fwd", st, [&] {
-    hipLaunchKernelGGL(k2_state_fwd<T>, dim3(kS / 32, g.U), dim3(64), 0, st, kt, vt, g.N, g.NB, sv.PT, sv.PR, sv.PZ,
-                       sv.PZm);
-  });
+  launch_fwd_prep<T>(g, kt, vt, sv.KT16, sv.VT16, st, timed);
+  {
+    // num is written only later (k2_intra_fwd), so it doubles as the scan's
+    // segment scratch
+    const ScanPlan plan = scan_plan(g.U, g.NB, sizeof(float) * (size_t)g.B * g.Hq * g.N * kD, true);
+    ScanArgs a{sv.KT16, kD, sv.VT16, kD + 1, nullptr, nullptr, nullptr, g.U, g.Hq, g.Hkv, g.N, g.NB,
+               sv.PT, sv.PR, sv.PZ, sv.PZm, num, nullptr};
+    launch_scan<true>(plan, a, st, timed);
+  }
   timed("k2_intra_fwd", st, [&] {
     hipLaunchKernelGGL(k2_intra_fwd<T>, dim3(g.R * g.NB * g.U), dim3(256), 0, st, qt, kt, vt, sv.PZ, sv.PZm, labels,
                        sv.ic, sv.gm, sv.lb, groups, g.Hq, g.Hkv, g.N, g.NB, num, den);

@@ -14,7 +14,6 @@
 // straight back into the MFMA as the K-major operand of the dq / dk / dv
 // products, whose other operand is the transposed bf16 copy of K, q or G.
 //
-// k2_kt_prep     K^T (bf16) per unit, the B operand of the dq products.
 // k2_local_dq    one block per (query head, chunk): dq local part and the state
 //                part of the denominator's dq (gz_i (bz + 2 Mz q_i)).
 // k2_local_dk    one block per (unit, chunk): dk local part summed over the
@@ -86,33 +85,6 @@ __device__ __forceinline__ int tile_jt(int tp) { return tp == 2 ? 1 : 0; }
 __device__ __forceinline__ int tile_it(int tp) { return tp == 0 ? 0 : 1; }
 
 }  // namespace
-
-// ---------------------------------------------------------------------------
-// K^T per unit: KT16 [U][64][NB * 64] bf16 (tokens >= N are zero).
-// ---------------------------------------------------------------------------
-template <typename T>
-__global__ __launch_bounds__(256) void k2_kt_prep(const T* __restrict__ k, int N, int NB,
-                                                  uint16_t* __restrict__ KT16) {
-  __shared__ __attribute__((aligned(16))) __bf16 kT[kD][kC + 8];
-  const int u = blockIdx.x / NB, ch = blockIdx.x % NB;
-  const int tid = threadIdx.x, j = tid >> 2, qq = tid & 3;
-  const int tok = ch * kC + j;
-  const bool ok = tok < N;
-  const T* src = k + ((size_t)u * N + (ok ? tok : N - 1)) * kD + 16 * qq;
-  const bf16x8 a = row8(src, ok), b = row8(src + 8, ok);
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    kT[16 * qq + e][j] = a[e];
-    kT[16 * qq + 8 + e][j] = b[e];
-  }
-  __syncthreads();
-  const size_t np = (size_t)NB * kC;
-  for (int idx = tid; idx < kD * 8; idx += 256) {
-    const int r = idx >> 3, c8 = idx & 7;
-    *reinterpret_cast<bf16x8*>(KT16 + ((size_t)u * kD + r) * np + (size_t)ch * kC + 8 * c8) =
-        *reinterpret_cast<const bf16x8*>(&kT[r][8 * c8]);
-  }
-}
 
 // ---------------------------------------------------------------------------
 // dq local part + denominator-state dq, one block per (query head, chunk),
@@ -550,9 +522,6 @@ template <typename T>
 void launch_local_bwd(const LaunchGeom& g, const T* q, const T* k, const T* v, const LocalBwdArgs& a, bool need_dq,
                       bool need_dkv, hipStream_t st, const Timer& timed) {
   if (need_dq) {
-    timed("k2_kt_prep", st, [&] {
-      hipLaunchKernelGGL(k2_kt_prep<T>, dim3(g.U * g.NB), dim3(256), 0, st, k, g.N, g.NB, a.KT16);
-    });
     timed("k2_local_dq", st, [&] {
       hipLaunchKernelGGL(k2_local_dq<T>, dim3(g.R * g.NB * g.U), dim3(192), 0, st, q, k, v, a.G16, a.Gz, a.KT16, a.PZ,
                          a.PZm, a.labels, a.lam, a.gam, a.gm, a.lb, a.groups, g.Hq, g.Hkv, g.N, g.NB, a.scale, a.dqf);

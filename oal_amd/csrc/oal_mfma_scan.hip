@@ -1,0 +1,571 @@
+// Chunk-state scans on the gfx950 matrix cores, forward and backward.
+//
+// Forward (reference hd_block_gemm_runtime.py:271-320: block totals, exclusive
+// cumsum), per unit u = (batch, kv head):
+//   T_c = raw(K_c)^T [V_c, 1],        P_c = sum_{c' < c} T_c'
+// Backward (reference hd_block_gemm_backward.py:764-908: _query_dcarry and the
+// exclusive right scan), per unit:
+//   dCarry_c = sum_h wq_h o raw(Q_h,c)^T [G_h,c, Gz_h,c],   dT_c = sum_{c' > c} dCarry_c'
+// and the per-slot coefficient partial of each query head
+//   dwq_h[slot] += sum_c <P_c[slot], (raw(Q_h,c)^T [G_h,c, Gz_h,c])[slot]>.
+//
+// k2_scan<FWD, MODE, TPW>: a block of four waves, each owning TPW 32-slot
+// tiles, of one unit and one segment of consecutive chunks; the state of a
+// tile lives in MFMA accumulators laid out value x slot (lane column = slot).
+// The value side of an item is read from LDS once per wave and feeds all of
+// the wave's tiles (TPW = 2 halves those reads per tile; the backward totals
+// keep TPW = 1 for the registers of the per-head products). An item is one
+// (chunk, query head) pair in the backward and one chunk in the forward; its
+// operands (the feature side q^T / k^T and the value side [G^T; Gz] / [V^T; 1],
+// 64 tokens each) are staged once per block into a double-buffered LDS pair,
+// fetched into registers two items ahead. Raw features are products of two
+// fp32 rows of the staged feature side, packed to bf16 as the MFMA B operand.
+//   MODE 0: segment totals (backward: plus coefficient partials); no state out.
+//   MODE 1: replay from the carry of the other segments, emitting every chunk's
+//           state; the backward weights the features by wq_h so that every
+//           head accumulates into the one state.
+//   MODE 2: one segment: MODE 1's output plus MODE 0's partials.
+// Emitted layouts per (unit, chunk), identical in both directions:
+//   R [kS/32][4][32][16 values] bf16, T [kKS][64 values][16 slots] bf16,
+//   Z [kFP] fp32 (denominator column, natural feature order), and in the
+//   forward Zm [64][64] fp32 (the denominator column as a symmetric pair matrix).
+// k2_seg_carry turns segment totals into carries in place: exclusive prefix
+// (forward) or exclusive suffix (backward), fixed order.
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdlib.h>
+
+#include <algorithm>
+#include <cmath>
+
+#include "oal_internal.hpp"
+#include "oal_mfma_common.hpp"
+
+namespace oal {
+
+static __constant__ SlotTable kSlot = make_slot_table();
+
+namespace {
+
+constexpr int kSTiles = 4;                                 // slot tiles (waves) per block
+// tile groups of a scan whose waves own TPW tiles each (18 or 9)
+constexpr int scan_tile_groups(int tpw) { return (kS / 32 + kSTiles * tpw - 1) / (kSTiles * tpw); }
+constexpr int kFRow = kC + 4;                              // fp32 LDS row stride, feature side
+constexpr int kVRow = kC + 8;                              // bf16 LDS row stride, value side
+constexpr int kOpRows = kD + 2;                            // rows 64 (one / den), 65 (zero)
+constexpr size_t kChunkElems = (size_t)kKS * 64 * 16;
+
+}  // namespace
+
+template <bool FWD, int MODE, int TPW>
+__global__ __launch_bounds__(256, 2) void k2_scan(const uint16_t* __restrict__ F, int frows,
+                                               const uint16_t* __restrict__ V, int vrows,
+                                               const float* __restrict__ wqs, const uint16_t* __restrict__ PRin,
+                                               const float* __restrict__ PZin, const float* __restrict__ carry, int Hq,
+                                               int Hkv, int N, int NB, int SL, int Sg, uint16_t* __restrict__ outT,
+                                               uint16_t* __restrict__ outR, float* __restrict__ outZ,
+                                               float* __restrict__ outZm, float* __restrict__ segtot,
+                                               float* __restrict__ dwqs) {
+  constexpr bool EMIT = MODE != 0;
+  constexpr bool PARTIALS = !FWD && MODE != 1;
+  constexpr bool SPLIT = PARTIALS;  // per-head products kept apart (needed for the partials)
+  static_assert(!SPLIT || TPW == 1, "the per-head products fit registers for one tile per wave");
+  constexpr int TG = scan_tile_groups(TPW);
+  __shared__ __attribute__((aligned(16))) float Fs[2][kOpRows * kFRow];
+  __shared__ __attribute__((aligned(16))) __bf16 Vs[2][kOpRows * kVRow];
+  __shared__ float dwl[PARTIALS ? 8 : 1][kSTiles * 32];
+
+  int u, seg, tgi;
+  {
+    const int total = gridDim.x, id = blockIdx.x;
+    const int w = (total & 7) == 0 ? (id & 7) * (total >> 3) + (id >> 3) : id;
+    tgi = w % TG;
+    seg = (w / TG) % Sg;
+    u = w / (TG * Sg);
+  }
+  const int R = Hq / Hkv, b = u / Hkv, kh = u % Hkv;
+  const int RI = FWD ? 1 : R;  // items per chunk
+  const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, s = l >> 5, row = l & 31;
+  // this wave's tiles (TPW consecutive), their slots and slot rows
+  int tile[TPW], slot[TPW], ar[TPW], ac[TPW], nat[TPW];
+  bool live[TPW];
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) {
+    tile[t] = (kSTiles * tgi + wv) * TPW + t;
+    live[t] = tile[t] < kS / 32;
+    slot[t] = live[t] ? tile[t] * 32 + row : 0;
+    ar[t] = kSlot.ar[slot[t]];
+    ac[t] = kSlot.ac[slot[t]];
+    nat[t] = live[t] ? kSlot.nat[slot[t]] : -1;
+  }
+  const bool any_live = live[0];
+  const int c_lo = seg * SL, c_hi = min(NB, c_lo + SL);
+  const int NI = c_hi > c_lo ? (c_hi - c_lo) * RI : 0;
+  const size_t np = (size_t)NB * kC;
+
+  // constant rows: feature side 64 = 1 (the value side is zero for tokens
+  // >= N), 65 = 0; value side 65 = 0
+  for (int i = tid; i < 2 * kC; i += 256) {
+    const int bi = i / kC, j = i % kC;
+    Fs[bi][kD * kFRow + j] = 1.f;
+    Fs[bi][(kD + 1) * kFRow + j] = 0.f;
+    Vs[bi][(kD + 1) * kVRow + j] = (__bf16)0.f;
+  }
+  if constexpr (PARTIALS) {
+    for (int i = tid; i < 8 * kSTiles * 32; i += 256) dwl[i / (kSTiles * 32)][i % (kSTiles * 32)] = 0.f;
+  }
+
+  // acc[t][n]: values 32 n .. 32 n + 31 of tile t; accz: the denominator
+  // column of tile t in accumulator row t (register t of lane group 0)
+  f32x16 acc[TPW][2], accz = f32x16{};
+#pragma unroll
+  for (int t = 0; t < TPW; ++t)
+#pragma unroll
+    for (int n = 0; n < 2; ++n) acc[t][n] = f32x16{};
+  if constexpr (MODE == 1) {
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+      if (live[t]) {
+        const float* cr = carry + (((size_t)u * Sg + seg) * kS + slot[t]) * 65;
+#pragma unroll
+        for (int n = 0; n < 2; ++n)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) acc[t][n][i] = cr[32 * n + c32_row(i, l)];
+        if (s == 0) accz[t] = cr[64];
+      }
+    }
+  }
+
+  auto item_chunk = [&](int it, int& ch, int& hh) {
+    const int ci = it / RI;
+    hh = it - ci * RI;
+    ch = FWD ? c_lo + ci : c_hi - 1 - ci;
+  };
+  struct Stage {
+    uint4 f0, f1, v0, v1, v2;
+    float w[TPW];
+  };
+  const size_t uf0 = (size_t)(tid >> 3) * np + 8 * (tid & 7);
+  const size_t uf1 = (size_t)((tid + 256) >> 3) * np + 8 * (tid & 7);
+  const size_t uv2 = (size_t)kD * np + 8 * (tid & 7);
+  // Every thread issues the same loads on every call (items past the end are
+  // clamped to the last one, the row-64 unit to an in-range column): the
+  // compiler then counts the loads in flight exactly and waits for an item's
+  // loads only where they are stored, keeping the next item's loads in flight.
+  auto load = [&](Stage& st, int it) {
+    int ch, hh;
+    item_chunk(it < NI ? it : NI - 1, ch, hh);
+    const int x = FWD ? u : b * Hq + kh * R + hh;
+    const uint16_t* fb = F + (size_t)x * frows * np + (size_t)ch * kC;
+    const uint16_t* vb = V + (size_t)x * vrows * np + (size_t)ch * kC;
+    st.f0 = *reinterpret_cast<const uint4*>(fb + uf0);
+    st.f1 = *reinterpret_cast<const uint4*>(fb + uf1);
+    st.v0 = *reinterpret_cast<const uint4*>(vb + uf0);
+    st.v1 = *reinterpret_cast<const uint4*>(vb + uf1);
+    st.v2 = *reinterpret_cast<const uint4*>(vb + uv2);
+    if constexpr (!FWD) {
+#pragma unroll
+      for (int t = 0; t < TPW; ++t) {
+        const float wv_ = wqs[(size_t)(kh * R + hh) * kS + slot[t]];
+        st.w[t] = live[t] ? wv_ : 0.f;
+      }
+    }
+  };
+  auto put = [&](int bi, int idx, const uint4& f) {
+    float4* d = reinterpret_cast<float4*>(&Fs[bi][(idx >> 3) * kFRow + 8 * (idx & 7)]);
+    d[0] = make_float4(__uint_as_float(f.x << 16), __uint_as_float(f.x & 0xffff0000u), __uint_as_float(f.y << 16),
+                       __uint_as_float(f.y & 0xffff0000u));
+    d[1] = make_float4(__uint_as_float(f.z << 16), __uint_as_float(f.z & 0xffff0000u), __uint_as_float(f.w << 16),
+                       __uint_as_float(f.w & 0xffff0000u));
+  };
+  auto store = [&](int bi, const Stage& st) {
+    put(bi, tid, st.f0);
+    put(bi, tid + 256, st.f1);
+    *reinterpret_cast<uint4*>(&Vs[bi][(tid >> 3) * kVRow + 8 * (tid & 7)]) = st.v0;
+    *reinterpret_cast<uint4*>(&Vs[bi][((tid + 256) >> 3) * kVRow + 8 * (tid & 7)]) = st.v1;
+    if (tid < 8) *reinterpret_cast<uint4*>(&Vs[bi][kD * kVRow + 8 * tid]) = st.v2;
+  };
+
+  // Permutation matrices of the T-layout transposition (see emit): for value
+  // block kk, K position 8 s' + j of a lane group s' holds the state value
+  // 16 kk + 4 s' + j (j < 4) or 16 kk + 8 + 4 s' + (j - 4) (j >= 4); B routes it
+  // to output column 16 (kk % 2) + that offset of the 32-value half kk / 2.
+  bf16x8 perm[2];
+#pragma unroll
+  for (int p = 0; p < 2; ++p)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int off = j < 4 ? 4 * s + j : 8 + 4 * s + (j - 4);
+      perm[p][j] = (__bf16)(16 * p + off == row ? 1.f : 0.f);
+    }
+
+  // Emission of tile t's state before chunk ch (exclusive prefix / suffix).
+  auto emit = [&](int t, int ch) {
+    const size_t cb = (size_t)u * NB + ch;
+    // R layout straight from the accumulators: lane = slot, 4 values a word pair
+    uint32_t wd[2][4][2];
+#pragma unroll
+    for (int n = 0; n < 2; ++n)
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        wd[n][a][0] = pack_bf16x2(acc[t][n][4 * a], acc[t][n][4 * a + 1]);
+        wd[n][a][1] = pack_bf16x2(acc[t][n][4 * a + 2], acc[t][n][4 * a + 3]);
+      }
+    uint16_t* tr = outR + cb * kChunkElems + (size_t)tile[t] * 4 * 32 * 16;
+#pragma unroll
+    for (int n = 0; n < 2; ++n)
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        const int kk = 2 * n + (a >> 1), pos = 8 * (a & 1) + 4 * s;
+        *reinterpret_cast<uint2*>(tr + ((size_t)kk * 32 + row) * 16 + pos) = make_uint2(wd[n][a][0], wd[n][a][1]);
+      }
+    if (s == 0 && nat[t] >= 0) {
+      const float z = accz[t];
+      outZ[cb * kFP + nat[t]] = z;
+      if constexpr (FWD) {
+        if (nat[t] > kD) {
+          float* pm = outZm + cb * kD * kD;
+          pm[ar[t] * kD + ac[t]] = z;
+          pm[ac[t] * kD + ar[t]] = z;
+        }
+      }
+    }
+    // T layout [kstep][64 values][16 slots]: the matrix cores transpose the
+    // packed tile (D = A P, one nonzero product per output, exact), giving
+    // lane = value and registers = slots 8 (i / 4) + 4 s + i % 4.
+    uint16_t* tt = outT + cb * kChunkElems + (size_t)(2 * tile[t]) * 64 * 16;
+#pragma unroll
+    for (int nh = 0; nh < 2; ++nh) {
+      f32x16 D = f32x16{};
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        const uint4 av = make_uint4(wd[nh][2 * p][0], wd[nh][2 * p][1], wd[nh][2 * p + 1][0], wd[nh][2 * p + 1][1]);
+        D = mfma32(__builtin_bit_cast(bf16x8, av), perm[p], D);
+      }
+      const int e = 32 * nh + row;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int tp = q >> 1, pos = 8 * (q & 1) + 4 * s;
+        *reinterpret_cast<uint2*>(tt + ((size_t)tp * 64 + e) * 16 + pos) =
+            make_uint2(pack_bf16x2(D[4 * q], D[4 * q + 1]), pack_bf16x2(D[4 * q + 2], D[4 * q + 3]));
+      }
+    }
+  };
+
+  float pf[2][16];
+  float pz = 0.f;
+  // One item from LDS buffer bi.
+  auto process = [&](int it, int bi, const float (&w)[TPW]) {
+    int ch, hh;
+    item_chunk(it, ch, hh);
+    if (!any_live) return;
+    if (hh == 0) {
+      if constexpr (PARTIALS) {
+        // P_c rows of this lane's slot, values e = 32 n + 8 a + 4 s + v
+        const size_t cb = (size_t)u * NB + ch;
+        const uint16_t* pr = PRin + cb * kChunkElems + (size_t)tile[0] * 4 * 32 * 16;
+#pragma unroll
+        for (int n = 0; n < 2; ++n)
+#pragma unroll
+          for (int a = 0; a < 4; ++a) {
+            const int kk = 2 * n + (a >> 1), pos = 8 * (a & 1) + 4 * s;
+            const uint2 q = *reinterpret_cast<const uint2*>(pr + ((size_t)kk * 32 + row) * 16 + pos);
+            pf[n][4 * a] = __uint_as_float(q.x << 16);
+            pf[n][4 * a + 1] = __uint_as_float(q.x & 0xffff0000u);
+            pf[n][4 * a + 2] = __uint_as_float(q.y << 16);
+            pf[n][4 * a + 3] = __uint_as_float(q.y & 0xffff0000u);
+          }
+        pz = (s == 0 && nat[0] >= 0) ? PZin[cb * kFP + nat[0]] : 0.f;
+      }
+    }
+    const float* fs = Fs[bi];
+    const __bf16* vs = Vs[bi];
+    f32x16 hT[3];
+    if constexpr (SPLIT) {
+#pragma unroll
+      for (int n = 0; n < 3; ++n) hT[n] = f32x16{};
+    }
+    const int zrow = kD * kVRow;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      // value side (shared by the wave's tiles); the denominator row (row 64)
+      // goes to A row t for tile t, read by the lanes that supply those rows
+      bf16x8 va[2], vz = bf16x8{};
+#pragma unroll
+      for (int n = 0; n < 2; ++n)
+        va[n] = *reinterpret_cast<const bf16x8*>(vs + (32 * n + row) * kVRow + 16 * kk + 8 * s);
+      if (row < TPW) vz = *reinterpret_cast<const bf16x8*>(vs + zrow + 16 * kk + 8 * s);
+#pragma unroll
+      for (int t = 0; t < TPW; ++t) {
+        const float4* pa = reinterpret_cast<const float4*>(fs + ar[t] * kFRow + 16 * kk + 8 * s);
+        const float4* pc = reinterpret_cast<const float4*>(fs + ac[t] * kFRow + 16 * kk + 8 * s);
+        const float4 a0 = pa[0], a1 = pa[1], c0v = pc[0], c1v = pc[1];
+        float f[8] = {a0.x * c0v.x, a0.y * c0v.y, a0.z * c0v.z, a0.w * c0v.w,
+                      a1.x * c1v.x, a1.y * c1v.y, a1.z * c1v.z, a1.w * c1v.w};
+        if constexpr (!FWD && !SPLIT) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) f[j] *= w[t];
+        }
+        const bf16x8 bq = pack8(f);
+        const bf16x8 vzt = row == t ? vz : bf16x8{};
+        if constexpr (SPLIT) {
+          hT[0] = mfma32(va[0], bq, hT[0]);
+          hT[1] = mfma32(va[1], bq, hT[1]);
+          hT[2] = mfma32(vzt, bq, hT[2]);
+        } else {
+          acc[t][0] = mfma32(va[0], bq, acc[t][0]);
+          acc[t][1] = mfma32(va[1], bq, acc[t][1]);
+          accz = mfma32(vzt, bq, accz);
+        }
+      }
+    }
+    if constexpr (SPLIT) {
+      const float wt = w[0];
+#pragma unroll
+      for (int n = 0; n < 2; ++n)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[0][n][i] = fmaf(wt, hT[n][i], acc[0][n][i]);
+      accz[0] = fmaf(wt, hT[2][0], accz[0]);
+      float d = pz * hT[2][0];
+#pragma unroll
+      for (int n = 0; n < 2; ++n)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) d = fmaf(pf[n][i], hT[n][i], d);
+      // both lane groups hold value rows of the same slot
+      const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(d), __float_as_uint(d), false, false);
+      if (s == 0) dwl[hh][wv * 32 + row] += d + __uint_as_float(r[1]);
+    }
+  };
+
+  // State emission before item it when it starts a chunk. It runs at the end
+  // of the previous item, after that item's staging store: the stores then
+  // trail the staging loads in flight (vmcnt retires loads and stores in
+  // order), so the next waits for staging loads do not wait for them.
+  auto emit_before = [&](int it) {
+    if constexpr (EMIT) {
+      if (it < NI && any_live && it % RI == 0) {
+        int ch, hh;
+        item_chunk(it, ch, hh);
+#pragma unroll
+        for (int t = 0; t < TPW; ++t)
+          if (live[t]) emit(t, ch);
+      }
+    }
+  };
+
+  // Pipeline: items it and it + 1 alternate between the register stages sa and
+  // sb; the loads of item it + 2 are issued when item it starts and land in
+  // LDS when item it + 1 ends.
+  Stage sa, sb;
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) sa.w[t] = sb.w[t] = 1.f;
+  if (NI > 0) {
+    load(sa, 0);
+    load(sb, 1);
+    store(0, sa);
+  }
+  emit_before(0);
+  lds_sync();
+  int bi = 0;
+  for (int it = 0; it < NI; it += 2) {
+    {
+      float w[TPW];
+#pragma unroll
+      for (int t = 0; t < TPW; ++t) w[t] = sa.w[t];
+      load(sa, it + 2);
+      process(it, bi, w);
+      if (it + 1 < NI) store(bi ^ 1, sb);
+      emit_before(it + 1);
+      lds_sync();
+      bi ^= 1;
+    }
+    if (it + 1 < NI) {
+      float w[TPW];
+#pragma unroll
+      for (int t = 0; t < TPW; ++t) w[t] = sb.w[t];
+      load(sb, it + 3);
+      process(it + 1, bi, w);
+      if (it + 2 < NI) store(bi ^ 1, sa);
+      emit_before(it + 2);
+      lds_sync();
+      bi ^= 1;
+    }
+  }
+
+  if constexpr (MODE == 0) {
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+      if (live[t]) {
+        float* st = segtot + (((size_t)u * Sg + seg) * kS + slot[t]) * 65;
+#pragma unroll
+        for (int n = 0; n < 2; ++n)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) st[32 * n + c32_row(i, l)] = acc[t][n][i];
+        if (s == 0) st[64] = accz[t];
+      }
+    }
+  }
+  if constexpr (PARTIALS) {
+    const int B = (int)(gridDim.x / (TG * Sg)) / Hkv;
+    if (live[0] && s == 0) {
+      for (int hh = 0; hh < R; ++hh)
+        dwqs[(((size_t)seg * B + b) * Hq + kh * R + hh) * kS + slot[0]] = dwl[hh][wv * 32 + row];
+    }
+  }
+}
+
+// In place: x[u][seg] <- sum over the segments before (forward) or after
+// (backward) seg of x[u][seg'] (fixed order), elementwise.
+template <bool FWD>
+__global__ __launch_bounds__(256) void k2_seg_carry(float* __restrict__ segtot, int S) {
+  const size_t per = (size_t)kS * 65;
+  const size_t e = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (e >= per) return;
+  float* x = segtot + (size_t)blockIdx.y * S * per + e;
+  float run = 0.f;
+  // eight segments' loads in flight before their carries are stored
+  for (int i0 = 0; i0 < S; i0 += 8) {
+    float t[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int i = i0 + k, sg = FWD ? i : S - 1 - i;
+      t[k] = i < S ? x[(size_t)sg * per] : 0.f;
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int i = i0 + k, sg = FWD ? i : S - 1 - i;
+      if (i < S) x[(size_t)sg * per] = run;
+      run += t[k];
+    }
+  }
+}
+
+// Forward operands per (unit, chunk): KT16 [U][64][NB * 64] = k^T and
+// VT16 [U][65][NB * 64] = [v^T; 1 (token < N)], bf16, tokens >= N zero.
+template <typename T>
+__global__ __launch_bounds__(256) void k2_fwd_prep(const T* __restrict__ k, const T* __restrict__ v, int N, int NB,
+                                                   uint16_t* __restrict__ KT16, uint16_t* __restrict__ VT16) {
+  __shared__ __attribute__((aligned(16))) __bf16 kT[kD][kC + 8];
+  __shared__ __attribute__((aligned(16))) __bf16 vT[kD + 1][kC + 8];
+  const int u = blockIdx.x / NB, ch = blockIdx.x % NB;
+  const int tid = threadIdx.x, j = tid >> 2, qq = tid & 3;
+  const int tok = ch * kC + j;
+  const bool ok = tok < N;
+  const size_t off = ((size_t)u * N + (ok ? tok : N - 1)) * kD + 16 * qq;
+  float kv[16], vv[16];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    kv[e] = ok ? to_f(k[off + e]) : 0.f;
+    vv[e] = ok ? to_f(v[off + e]) : 0.f;
+  }
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    kT[16 * qq + e][j] = (__bf16)kv[e];
+    vT[16 * qq + e][j] = (__bf16)vv[e];
+  }
+  if (qq == 0) vT[kD][j] = (__bf16)(ok ? 1.f : 0.f);
+  __syncthreads();
+  const size_t np = (size_t)NB * kC;
+  for (int idx = tid; idx < (2 * kD + 1) * 8; idx += 256) {
+    const int r = idx >> 3, c8 = idx & 7;
+    if (r < kD) {
+      *reinterpret_cast<bf16x8*>(KT16 + ((size_t)u * kD + r) * np + (size_t)ch * kC + 8 * c8) =
+          *reinterpret_cast<const bf16x8*>(&kT[r][8 * c8]);
+    } else {
+      const int rv = r - kD;
+      *reinterpret_cast<bf16x8*>(VT16 + ((size_t)u * (kD + 1) + rv) * np + (size_t)ch * kC + 8 * c8) =
+          *reinterpret_cast<const bf16x8*>(&vT[rv][8 * c8]);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------
+// Tiles per wave of the three scan kernels (totals, replay, single pass):
+// two wherever the per-head products are not kept apart.
+constexpr int scan_tpw(bool fwd, int mode) { return (mode == 1 || fwd) ? 2 : 1; }
+
+ScanPlan scan_plan(int U, int NB, size_t scratch_bytes, bool fwd) {
+  // Segment count from a model of block rounds: each kernel runs two blocks
+  // per CU, a block's time is proportional to its chunks, and a partial last
+  // round costs a full one; each segment adds a little carry traffic.
+  int cus = 256;
+  {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+      cus = n;
+  }
+  const double slots = 2.0 * cus;
+  const size_t seg_bytes = sizeof(float) * (size_t)U * kS * 65;
+  int cap = NB;
+  if (scratch_bytes != (size_t)-1) cap = (int)std::min<size_t>((size_t)NB, scratch_bytes / seg_bytes);
+  if (cap < 1) cap = 1;
+  auto rounds = [&](int mode, int S) {
+    return std::ceil(scan_tile_groups(scan_tpw(fwd, mode)) * (double)U * S / slots);
+  };
+  int best_S = 1;
+  double best = 0.0;
+  for (int want = 1; want <= cap; ++want) {
+    const int SL = (NB + want - 1) / want, S = (NB + SL - 1) / SL;
+    const double est = S == 1 ? rounds(2, 1) * SL : (rounds(0, S) + rounds(1, S)) * SL + 0.1 * S;
+    if (want == 1 || est < best) {
+      best = est;
+      best_S = S;
+    }
+  }
+  if (const char* env = getenv("OAL_SCAN_SEGMENTS")) best_S = std::max(1, std::min(cap, atoi(env)));
+  ScanPlan p;
+  p.SL = (NB + best_S - 1) / best_S;
+  p.S = (NB + p.SL - 1) / p.SL;
+  p.seg_bytes = p.S > 1 ? seg_bytes * p.S : 0;
+  return p;
+}
+
+template <bool FWD>
+void launch_scan(const ScanPlan& p, const ScanArgs& a, hipStream_t st, const Timer& timed) {
+  constexpr int T0 = scan_tpw(FWD, 0), T1 = scan_tpw(FWD, 1), T2 = scan_tpw(FWD, 2);
+  auto grid = [&](int tpw) { return dim3((unsigned)(scan_tile_groups(tpw) * a.U * p.S)); };
+  const dim3 block(256);
+  const char* name = FWD ? "k2_state_fwd" : "k2_state_bwd";
+  if (p.S == 1) {
+    timed(name, st, [&] {
+      hipLaunchKernelGGL((k2_scan<FWD, 2, T2>), grid(T2), block, 0, st, a.F, a.frows, a.V, a.vrows, a.wqs, a.PR,
+                         a.PZ, nullptr, a.Hq, a.Hkv, a.N, a.NB, p.SL, p.S, a.outT, a.outR, a.outZ, a.outZm, nullptr,
+                         a.dwqs);
+    });
+    return;
+  }
+  timed(FWD ? "k2_state_fwd_totals" : "k2_state_bwd_totals", st, [&] {
+    hipLaunchKernelGGL((k2_scan<FWD, 0, T0>), grid(T0), block, 0, st, a.F, a.frows, a.V, a.vrows, a.wqs, a.PR, a.PZ,
+                       nullptr, a.Hq, a.Hkv, a.N, a.NB, p.SL, p.S, nullptr, nullptr, nullptr, nullptr, a.segtot,
+                       a.dwqs);
+  });
+  timed("k2_seg_carry", st, [&] {
+    hipLaunchKernelGGL((k2_seg_carry<FWD>), dim3((kS * 65 + 255) / 256, a.U), dim3(256), 0, st, a.segtot, p.S);
+  });
+  timed(name, st, [&] {
+    hipLaunchKernelGGL((k2_scan<FWD, 1, T1>), grid(T1), block, 0, st, a.F, a.frows, a.V, a.vrows, a.wqs, a.PR,
+                       a.PZ, a.segtot, a.Hq, a.Hkv, a.N, a.NB, p.SL, p.S, a.outT, a.outR, a.outZ, a.outZm, nullptr,
+                       nullptr);
+  });
+}
+
+template void launch_scan<true>(const ScanPlan&, const ScanArgs&, hipStream_t, const Timer&);
+template void launch_scan<false>(const ScanPlan&, const ScanArgs&, hipStream_t, const Timer&);
+
+template <typename T>
+void launch_fwd_prep(const LaunchGeom& g, const T* k, const T* v, uint16_t* KT16, uint16_t* VT16, hipStream_t st,
+                     const Timer& timed) {
+  timed("k2_fwd_prep", st, [&] {
+    hipLaunchKernelGGL(k2_fwd_prep<T>, dim3(g.U * g.NB), dim3(256), 0, st, k, v, g.N, g.NB, KT16, VT16);
+  });
+}
+template void launch_fwd_prep<float>(const LaunchGeom&, const float*, const float*, uint16_t*, uint16_t*,
+                                     hipStream_t, const Timer&);
+template void launch_fwd_prep<uint16_t>(const LaunchGeom&, const uint16_t*, const uint16_t*, uint16_t*, uint16_t*,
+                                        hipStream_t, const Timer&);
+
+}  // namespace oal
