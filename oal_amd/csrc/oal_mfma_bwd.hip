@@ -31,27 +31,6 @@ namespace {
 
 constexpr int LD = kD + 8;  // padded bf16 row stride in LDS
 
-__device__ __forceinline__ void load_row_b(const uint16_t* __restrict__ src, size_t row_base, bool ok,
-                                           bf16x8 (&r)[8]) {
-  const bf16x8* p = reinterpret_cast<const bf16x8*>(src + row_base);
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const bf16x8 x = p[i];
-    r[i] = ok ? x : bf16x8{};
-  }
-}
-__device__ __forceinline__ void load_row_b(const float* __restrict__ src, size_t row_base, bool ok,
-                                           bf16x8 (&r)[8]) {
-  const float4* p = reinterpret_cast<const float4*>(src + row_base);
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const float4 a = p[2 * i], b = p[2 * i + 1];
-    float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-    const bf16x8 x = pack8(v);
-    r[i] = ok ? x : bf16x8{};
-  }
-}
-
 // 32 consecutive elements of a row (16-byte stores).
 __device__ __forceinline__ void store32(float* dst, const float (&v)[32]) {
 #pragma unroll
@@ -69,24 +48,28 @@ __device__ __forceinline__ void store32(uint16_t* dst, const float (&v)[32]) {
   }
 }
 
-__device__ __forceinline__ void store_row(__bf16* dst, const bf16x8 (&r)[8]) {
-#pragma unroll
-  for (int i = 0; i < 8; ++i) *reinterpret_cast<bf16x8*>(dst + 8 * i) = r[i];
+// 8 consecutive elements of a row as one bf16 fragment (zeros when !ok).
+__device__ __forceinline__ bf16x8 frag8(const uint16_t* __restrict__ src, size_t off, bool ok) {
+  const bf16x8 x = *reinterpret_cast<const bf16x8*>(src + off);
+  return ok ? x : bf16x8{};
+}
+__device__ __forceinline__ bf16x8 frag8(const float* __restrict__ src, size_t off, bool ok) {
+  const float4 a = reinterpret_cast<const float4*>(src + off)[0], b = reinterpret_cast<const float4*>(src + off)[1];
+  float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  const bf16x8 x = pack8(v);
+  return ok ? x : bf16x8{};
 }
 
-// Rotated fp32 row x[m] = row[(m + 32 s) % 64] from 8 bf16 fragments.
-__device__ __forceinline__ void rotated_row(const bf16x8 (&r)[8], int s, float (&x)[kD]) {
+// Rotated fp32 row x[m] = row[(m + 32 s) % 64], loaded in rotated order (the
+// rotation is in the per-lane addresses, so every register index is static).
+template <typename T>
+__device__ __forceinline__ void load_rotated(const T* __restrict__ src, size_t row_base, bool ok, int s,
+                                             float (&x)[kD]) {
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int i = 0; i < 8; ++i) {
+    const bf16x8 r = frag8(src, row_base + ((8 * i + 32 * s) & 63), ok);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) x[8 * i + j] = (float)r[i][j];
-  if (s == 1) {
-#pragma unroll
-    for (int m = 0; m < 32; ++m) {
-      const float t = x[m];
-      x[m] = x[m + 32];
-      x[m + 32] = t;
-    }
+    for (int j = 0; j < 8; ++j) x[8 * i + j] = (float)r[j];
   }
 }
 
@@ -383,14 +366,9 @@ __global__ __launch_bounds__(128, 2) void k2_q_fold(const T* __restrict__ q, con
   const size_t rowoff = qbase + (size_t)(ok ? tok : N - 1) * kD;
   float x[kD], dx[kD];
   bf16x8 bfr[4];
-  {
-    bf16x8 qr[8], gr[8];
-    load_row_b(q, rowoff, ok, qr);
-    load_row_b(G16, rowoff, ok, gr);
-    rotated_row(qr, s, x);
+  load_rotated(q, rowoff, ok, s, x);
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) bfr[kk] = gr[2 * kk + s];
-  }
+  for (int kk = 0; kk < 4; ++kk) bfr[kk] = frag8(G16, rowoff + 16 * kk + 8 * s, ok);
 #pragma unroll
   for (int m = 0; m < kD; ++m) dx[m] = 0.f;
   fold_all<6, true>(bfr, x, dx, wl, ring, src, tid, l);
@@ -477,14 +455,18 @@ __global__ __launch_bounds__(128) void k2_kv_fold(const T* __restrict__ k, const
   const size_t rowoff = kbase + (size_t)(ok ? tok : N - 1) * kD;
   float x[kD], dx[kD];
   bf16x8 bfr[4];
-  {
-    bf16x8 kr[8], vr[8];
-    load_row_b(k, rowoff, ok, kr);
-    load_row_b(v, rowoff, ok, vr);
-    if (s == 0) store_row(&ks[32 * wv + row][0], kr);
-    rotated_row(kr, s, x);
+  load_rotated(k, rowoff, ok, s, x);
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) bfr[kk] = vr[2 * kk + s];
+  for (int kk = 0; kk < 4; ++kk) bfr[kk] = frag8(v, rowoff + 16 * kk + 8 * s, ok);
+  // lane group 0 holds the unrotated key row
+  if (s == 0) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float v8[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v8[j] = x[8 * i + j];
+      *reinterpret_cast<bf16x8*>(&ks[32 * wv + row][8 * i]) = pack8(v8);
+    }
   }
 #pragma unroll
   for (int m = 0; m < kD; ++m) dx[m] = 0.f;
