@@ -63,6 +63,18 @@ def credited_flops(kernel: str, b: int, hq: int, hkv: int, n: int) -> float:
     }.get(kernel, 0.0)
 
 
+def measured_traffic(kernel: str, b: int, n: int):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE passes (copy-calibrated), or None when the workload differs or the
+    kernel has no entry."""
+    path = os.path.join(ROOT, "profiles", "config2_traffic.json")
+    if (b, n) != (4, 4096) or not os.path.exists(path):
+        return None
+    with open(path) as fh:
+        entry = json.load(fh).get("kernels", {}).get(kernel)
+    return int(entry["hbm_bytes"]) if entry else None
+
+
 def make_inputs(b: int, n: int, device: torch.device, seed: int = 0):
     from oal_amd.hd_block_gemm_autograd import pad_labels
 
@@ -256,7 +268,8 @@ def main() -> int:
             "peak": BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / BF16_PEAK_TFLOPS, 5),
-            "traffic": None,
+            "traffic": measured_traffic(dominant, b, n),
+            "traffic_unit": "bytes per launch (profiles/config2_traffic.json)",
             "step_credited_tflops": round(total_credited / sec / 1e12, 3),
             "step_frac": round(total_credited / sec / 1e12 / BF16_PEAK_TFLOPS, 5),
         },

@@ -1,6 +1,8 @@
 """Builds liboal_amd.so in-tree with hipcc for gfx950.
 
 Usage: ``python -m oal_amd.build`` (``__graft_entry__.build()`` calls it).
+Each source compiles to an object under oal_amd/_build/ in parallel, then one
+link step writes oal_amd/liboal_amd.so.
 """
 
 from __future__ import annotations
@@ -9,6 +11,7 @@ import os
 import shutil
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 
 PKG = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(PKG)
@@ -17,6 +20,7 @@ SOURCES = [os.path.join(PKG, "csrc", "oal_kernels.hip"), os.path.join(PKG, "csrc
            os.path.join(PKG, "csrc", "oal_mfma_scan.hip")]
 HEADERS = [os.path.join(PKG, "csrc", "oal_common.hpp"), os.path.join(ROOT, "include", "oal_amd.h")]
 OUTPUT = os.path.join(PKG, "liboal_amd.so")
+OBJDIR = os.path.join(PKG, "_build")
 
 
 def hipcc() -> str:
@@ -32,7 +36,6 @@ def compile_flags() -> list[str]:
         "-O3",
         "-std=c++20",
         "-fPIC",
-        "-shared",
         "-I" + os.path.join(ROOT, "include"),
         "-I" + os.path.join(PKG, "csrc"),
         # packed FP32 VALU instructions stay off (numerics)
@@ -40,16 +43,27 @@ def compile_flags() -> list[str]:
     ]
 
 
-def build(verbose: bool = False) -> str:
-    """Compile every HIP source into oal_amd/liboal_amd.so; returns its path."""
-    tmp = OUTPUT + ".tmp"
-    cmd = [hipcc(), *compile_flags(), *SOURCES, "-o", tmp]
+def _run(cmd: list[str], verbose: bool) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         sys.stderr.write(proc.stdout + proc.stderr)
-        raise RuntimeError(f"hipcc failed with exit code {proc.returncode}")
+        raise RuntimeError(f"hipcc failed with exit code {proc.returncode}: {' '.join(cmd[-3:])}")
+
+
+def build(verbose: bool = False) -> str:
+    """Compile every HIP source into oal_amd/liboal_amd.so; returns its path."""
+    os.makedirs(OBJDIR, exist_ok=True)
+    objs = [os.path.join(OBJDIR, os.path.splitext(os.path.basename(s))[0] + ".o") for s in SOURCES]
+    cc = hipcc()
+    jobs = [[cc, *compile_flags(), "-c", src, "-o", obj] for src, obj in zip(SOURCES, objs)]
+    workers = max(1, min(len(jobs), os.cpu_count() or 1))
+    with ThreadPoolExecutor(max_workers=workers) as pool:
+        for fut in [pool.submit(_run, j, verbose) for j in jobs]:
+            fut.result()
+    tmp = OUTPUT + ".tmp"
+    _run([cc, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp], verbose)
     os.replace(tmp, OUTPUT)
     return OUTPUT
 

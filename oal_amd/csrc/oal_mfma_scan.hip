@@ -9,7 +9,7 @@
 // and the per-slot coefficient partial of each query head
 //   dwq_h[slot] += sum_c <P_c[slot], (raw(Q_h,c)^T [G_h,c, Gz_h,c])[slot]>.
 //
-// k2_scan<FWD, MODE, TPW>: a block of four waves, each owning TPW 32-slot
+// k2_scan<FWD, MODE, TPW, NW>: a block of NW waves, each owning TPW 32-slot
 // tiles, of one unit and one segment of consecutive chunks; the state of a
 // tile lives in MFMA accumulators laid out value x slot (lane column = slot).
 // The value side of an item is read from LDS once per wave and feeds all of
@@ -48,9 +48,8 @@ static __constant__ SlotTable kSlot = make_slot_table();
 
 namespace {
 
-constexpr int kSTiles = 4;                                 // slot tiles (waves) per block
-// tile groups of a scan whose waves own TPW tiles each (18 or 9)
-constexpr int scan_tile_groups(int tpw) { return (kS / 32 + kSTiles * tpw - 1) / (kSTiles * tpw); }
+// tile groups of a scan whose NW waves own TPW tiles each
+constexpr int scan_tile_groups(int tpw, int nw) { return (kS / 32 + nw * tpw - 1) / (nw * tpw); }
 constexpr int kFRow = kC + 4;                              // fp32 LDS row stride, feature side
 constexpr int kVRow = kC + 8;                              // bf16 LDS row stride, value side
 constexpr int kOpRows = kD + 2;                            // rows 64 (one / den), 65 (zero)
@@ -58,8 +57,8 @@ constexpr size_t kChunkElems = (size_t)kKS * 64 * 16;
 
 }  // namespace
 
-template <bool FWD, int MODE, int TPW>
-__global__ __launch_bounds__(256, 2) void k2_scan(const uint16_t* __restrict__ F, int frows,
+template <bool FWD, int MODE, int TPW, int NW>
+__global__ __launch_bounds__(64 * NW, NW / 2) void k2_scan(const uint16_t* __restrict__ F, int frows,
                                                const uint16_t* __restrict__ V, int vrows,
                                                const float* __restrict__ wqs, const uint16_t* __restrict__ PRin,
                                                const float* __restrict__ PZin, const float* __restrict__ carry, int Hq,
@@ -71,7 +70,11 @@ __global__ __launch_bounds__(256, 2) void k2_scan(const uint16_t* __restrict__ F
   constexpr bool PARTIALS = !FWD && MODE != 1;
   constexpr bool SPLIT = PARTIALS;  // per-head products kept apart (needed for the partials)
   static_assert(!SPLIT || TPW == 1, "the per-head products fit registers for one tile per wave");
-  constexpr int TG = scan_tile_groups(TPW);
+  constexpr int TG = scan_tile_groups(TPW, NW);
+  constexpr int kSTiles = NW;                // slot tiles (waves) per block
+  constexpr int kNT = 64 * NW;               // threads per block
+  constexpr int kFPT = kD * 8 / kNT;         // 16-byte operand chunks per thread and side
+  static_assert(kFPT * kNT == kD * 8, "a block stages whole operand rows");
   __shared__ __attribute__((aligned(16))) float Fs[2][kOpRows * kFRow];
   __shared__ __attribute__((aligned(16))) __bf16 Vs[2][kOpRows * kVRow];
   __shared__ float dwl[PARTIALS ? 8 : 1][kSTiles * 32];
@@ -106,14 +109,14 @@ __global__ __launch_bounds__(256, 2) void k2_scan(const uint16_t* __restrict__ F
 
   // constant rows: feature side 64 = 1 (the value side is zero for tokens
   // >= N), 65 = 0; value side 65 = 0
-  for (int i = tid; i < 2 * kC; i += 256) {
+  for (int i = tid; i < 2 * kC; i += kNT) {
     const int bi = i / kC, j = i % kC;
     Fs[bi][kD * kFRow + j] = 1.f;
     Fs[bi][(kD + 1) * kFRow + j] = 0.f;
     Vs[bi][(kD + 1) * kVRow + j] = (__bf16)0.f;
   }
   if constexpr (PARTIALS) {
-    for (int i = tid; i < 8 * kSTiles * 32; i += 256) dwl[i / (kSTiles * 32)][i % (kSTiles * 32)] = 0.f;
+    for (int i = tid; i < 8 * kSTiles * 32; i += kNT) dwl[i / (kSTiles * 32)][i % (kSTiles * 32)] = 0.f;
   }
 
   // acc[t][n]: values 32 n .. 32 n + 31 of tile t; accz: the denominator
@@ -143,11 +146,11 @@ __global__ __launch_bounds__(256, 2) void k2_scan(const uint16_t* __restrict__ F
     ch = FWD ? c_lo + ci : c_hi - 1 - ci;
   };
   struct Stage {
-    uint4 f0, f1, v0, v1, v2;
+    uint4 f[kFPT], v[kFPT], v2;
     float w[TPW];
   };
-  const size_t uf0 = (size_t)(tid >> 3) * np + 8 * (tid & 7);
-  const size_t uf1 = (size_t)((tid + 256) >> 3) * np + 8 * (tid & 7);
+  // thread tid stages 16-byte chunks tid + kNT i (row chunk >> 3, column 8 (chunk & 7))
+  auto uoff = [&](int i) { return (size_t)((tid + kNT * i) >> 3) * np + 8 * (tid & 7); };
   const size_t uv2 = (size_t)kD * np + 8 * (tid & 7);
   // Every thread issues the same loads on every call (items past the end are
   // clamped to the last one, the row-64 unit to an in-range column): the
@@ -159,10 +162,11 @@ __global__ __launch_bounds__(256, 2) void k2_scan(const uint16_t* __restrict__ F
     const int x = FWD ? u : b * Hq + kh * R + hh;
     const uint16_t* fb = F + (size_t)x * frows * np + (size_t)ch * kC;
     const uint16_t* vb = V + (size_t)x * vrows * np + (size_t)ch * kC;
-    st.f0 = *reinterpret_cast<const uint4*>(fb + uf0);
-    st.f1 = *reinterpret_cast<const uint4*>(fb + uf1);
-    st.v0 = *reinterpret_cast<const uint4*>(vb + uf0);
-    st.v1 = *reinterpret_cast<const uint4*>(vb + uf1);
+#pragma unroll
+    for (int i = 0; i < kFPT; ++i) {
+      st.f[i] = *reinterpret_cast<const uint4*>(fb + uoff(i));
+      st.v[i] = *reinterpret_cast<const uint4*>(vb + uoff(i));
+    }
     st.v2 = *reinterpret_cast<const uint4*>(vb + uv2);
     if constexpr (!FWD) {
 #pragma unroll
@@ -180,10 +184,12 @@ __global__ __launch_bounds__(256, 2) void k2_scan(const uint16_t* __restrict__ F
                        __uint_as_float(f.w & 0xffff0000u));
   };
   auto store = [&](int bi, const Stage& st) {
-    put(bi, tid, st.f0);
-    put(bi, tid + 256, st.f1);
-    *reinterpret_cast<uint4*>(&Vs[bi][(tid >> 3) * kVRow + 8 * (tid & 7)]) = st.v0;
-    *reinterpret_cast<uint4*>(&Vs[bi][((tid + 256) >> 3) * kVRow + 8 * (tid & 7)]) = st.v1;
+#pragma unroll
+    for (int i = 0; i < kFPT; ++i) {
+      const int idx = tid + kNT * i;
+      put(bi, idx, st.f[i]);
+      *reinterpret_cast<uint4*>(&Vs[bi][(idx >> 3) * kVRow + 8 * (idx & 7)]) = st.v[i];
+    }
     if (tid < 8) *reinterpret_cast<uint4*>(&Vs[bi][kD * kVRow + 8 * tid]) = st.v2;
   };
 
@@ -486,6 +492,8 @@ __global__ __launch_bounds__(256) void k2_fwd_prep(const T* __restrict__ k, cons
 // Tiles per wave of the three scan kernels (totals, replay, single pass):
 // two wherever the per-head products are not kept apart.
 constexpr int scan_tpw(bool fwd, int mode) { return (mode == 1 || fwd) ? 2 : 1; }
+// waves per block of the three scan kernels
+constexpr int scan_nw(bool fwd, int mode) { return 4; }
 
 ScanPlan scan_plan(int U, int NB, size_t scratch_bytes, bool fwd) {
   // Segment count from a model of block rounds: each kernel runs two blocks
@@ -504,7 +512,7 @@ ScanPlan scan_plan(int U, int NB, size_t scratch_bytes, bool fwd) {
   if (scratch_bytes != (size_t)-1) cap = (int)std::min<size_t>((size_t)NB, scratch_bytes / seg_bytes);
   if (cap < 1) cap = 1;
   auto rounds = [&](int mode, int S) {
-    return std::ceil(scan_tile_groups(scan_tpw(fwd, mode)) * (double)U * S / slots);
+    return std::ceil(scan_tile_groups(scan_tpw(fwd, mode), scan_nw(fwd, mode)) * (double)U * S / slots);
   };
   int best_S = 1;
   double best = 0.0;
@@ -527,19 +535,19 @@ ScanPlan scan_plan(int U, int NB, size_t scratch_bytes, bool fwd) {
 template <bool FWD>
 void launch_scan(const ScanPlan& p, const ScanArgs& a, hipStream_t st, const Timer& timed) {
   constexpr int T0 = scan_tpw(FWD, 0), T1 = scan_tpw(FWD, 1), T2 = scan_tpw(FWD, 2);
-  auto grid = [&](int tpw) { return dim3((unsigned)(scan_tile_groups(tpw) * a.U * p.S)); };
-  const dim3 block(256);
+  constexpr int W0 = scan_nw(FWD, 0), W1 = scan_nw(FWD, 1), W2 = scan_nw(FWD, 2);
+  auto grid = [&](int tpw, int nw) { return dim3((unsigned)(scan_tile_groups(tpw, nw) * a.U * p.S)); };
   const char* name = FWD ? "k2_state_fwd" : "k2_state_bwd";
   if (p.S == 1) {
     timed(name, st, [&] {
-      hipLaunchKernelGGL((k2_scan<FWD, 2, T2>), grid(T2), block, 0, st, a.F, a.frows, a.V, a.vrows, a.wqs, a.PR,
+      hipLaunchKernelGGL((k2_scan<FWD, 2, T2, W2>), grid(T2, W2), dim3(64 * W2), 0, st, a.F, a.frows, a.V, a.vrows, a.wqs, a.PR,
                          a.PZ, nullptr, a.Hq, a.Hkv, a.N, a.NB, p.SL, p.S, a.outT, a.outR, a.outZ, a.outZm, nullptr,
                          a.dwqs);
     });
     return;
   }
   timed(FWD ? "k2_state_fwd_totals" : "k2_state_bwd_totals", st, [&] {
-    hipLaunchKernelGGL((k2_scan<FWD, 0, T0>), grid(T0), block, 0, st, a.F, a.frows, a.V, a.vrows, a.wqs, a.PR, a.PZ,
+    hipLaunchKernelGGL((k2_scan<FWD, 0, T0, W0>), grid(T0, W0), dim3(64 * W0), 0, st, a.F, a.frows, a.V, a.vrows, a.wqs, a.PR, a.PZ,
                        nullptr, a.Hq, a.Hkv, a.N, a.NB, p.SL, p.S, nullptr, nullptr, nullptr, nullptr, a.segtot,
                        a.dwqs);
   });
@@ -547,7 +555,7 @@ void launch_scan(const ScanPlan& p, const ScanArgs& a, hipStream_t st, const Tim
     hipLaunchKernelGGL((k2_seg_carry<FWD>), dim3((kS * 65 + 255) / 256, a.U), dim3(256), 0, st, a.segtot, p.S);
   });
   timed(name, st, [&] {
-    hipLaunchKernelGGL((k2_scan<FWD, 1, T1>), grid(T1), block, 0, st, a.F, a.frows, a.V, a.vrows, a.wqs, a.PR,
+    hipLaunchKernelGGL((k2_scan<FWD, 1, T1, W1>), grid(T1, W1), dim3(64 * W1), 0, st, a.F, a.frows, a.V, a.vrows, a.wqs, a.PR,
                        a.PZ, a.segtot, a.Hq, a.Hkv, a.N, a.NB, p.SL, p.S, a.outT, a.outR, a.outZ, a.outZm, nullptr,
                        nullptr);
   });
