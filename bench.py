@@ -167,6 +167,69 @@ def cpu_baseline(seconds: float = 12.0) -> dict:
     }
 
 
+def bench_model(args) -> int:
+    """one bf16 LoRA training step of the 24-layer Qwen-shaped model
+    with OAL in every layer (random init, uniform random token ids, seed 0).
+
+    value = B*N / (seconds per step); the attention share is the summed device time
+    of the OAL kernels (HIP events, recorded during a second pass of the same K
+    steps) over the step time. Under activation checkpointing each layer's OAL
+    forward runs twice per step (forward and recompute) plus one backward.
+    """
+    from oal_amd import _native
+    from oal_amd.qwen_oal import QwenOALConfig, QwenOALModel, train_step
+
+    dev = torch.device("cuda:0")
+    b, n = args.batch, args.seq_len
+    cfg = QwenOALConfig()
+    model = QwenOALModel(cfg, seed=0).to(dev).cast_parameters_(torch.bfloat16)
+    opt = torch.optim.AdamW(model.lora_parameters(), lr=1e-4)
+    tokens = torch.randint(0, cfg.vocab_size, (b, n), generator=torch.Generator().manual_seed(0)).to(dev)
+    for _ in range(args.warmup):
+        train_step(model, tokens, opt)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        loss = train_step(model, tokens, opt)
+    torch.cuda.synchronize()
+    sec = (time.perf_counter() - t0) / args.steps
+    _native.profile_collect()
+    _native.profile_enable(True)
+    for _ in range(args.steps):
+        train_step(model, tokens, opt)
+    torch.cuda.synchronize()
+    _native.profile_enable(False)
+    kernels = _native.profile_collect()
+    oal_ms = sum(total for _, total in kernels.values()) / args.steps
+    result = {
+        "metric": "Qwen2.5-0.5B-shaped OAL LoRA training step tokens/s (BASELINE config 4)",
+        "value": round(b * n / sec, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(sec * 1e3, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (uniform random token ids, seed 0; random-init weights of the Qwen2.5-0.5B shape)",
+        "config": {
+            "workload": "Qwen-shaped OAL model, one LoRA training step, BASELINE config 4",
+            "layers": cfg.num_layers, "hidden": cfg.hidden_size, "q_heads": cfg.num_heads,
+            "kv_heads": cfg.num_kv_heads, "head_dim": cfg.head_dim, "mlp": cfg.intermediate_size,
+            "vocab": cfg.vocab_size, "lora_rank": cfg.lora_rank, "batch": b, "seq_len": n,
+            "checkpointing": cfg.checkpointing,
+        },
+        "loss": round(float(loss), 5),
+        "attention_ms_per_step": round(oal_ms, 3),
+        "attention_share": round(oal_ms / (sec * 1e3), 4),
+        "oal_launches_per_step": sum(c for c, _ in kernels.values()) // args.steps,
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -175,6 +238,11 @@ def main() -> int:
     ap.add_argument("--batch", type=int, default=4)
     ap.add_argument("--seq-len", type=int, default=4096)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument(
+        "--workload", choices=("attention", "model"), default="attention",
+        help="attention: the OAL operator fwd+bwd (BASELINE config 2, the headline metric); "
+             "model: one LoRA training step of the Qwen-shaped OAL model (BASELINE config 4)",
+    )
     ap.add_argument(
         "--copy-calibration-mib", type=int, default=0,
         help="first run one plain device copy of this many MiB (reads and writes that many bytes), "
@@ -188,6 +256,9 @@ def main() -> int:
             file=sys.stderr,
         )
         return 2
+
+    if args.workload == "model":
+        return bench_model(args)
 
     from oal_amd import _native
 
