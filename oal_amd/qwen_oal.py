@@ -139,6 +139,7 @@ class OALAttention(nn.Module):
         self.o_proj = LoRALinear(hq * d, cfg.hidden_size, bias=False, **lora)
         self.register_buffer("dim_groups", seeded_layer_groups(cfg, gen), persistent=True)
         self.register_buffer("factor", seeded_layer_factor(cfg, gen), persistent=True)
+        self.kernel_eps = cfg.kernel_eps
         self._prepared = {}
 
     def head_attention(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
@@ -149,7 +150,7 @@ class OALAttention(nn.Module):
         if prepared is None:
             prepared = prepare_grouped_hd_block_gemm(
                 q, k, v, self.dim_groups, self.factor, scale=self.cfg.head_dim ** -0.5,
-                kernel_eps=self.cfg.kernel_eps, precision=self.cfg.precision,
+                kernel_eps=self.kernel_eps, precision=self.cfg.precision,
             )
             self._prepared[sig] = prepared
         out, _, _ = run_prepared_grouped_hd_block_gemm(prepared, q, k, v, self.factor)
@@ -217,6 +218,17 @@ class QwenOALModel(nn.Module):
         """Casts every parameter (not the buffers: the factors stay fp32, the groups int32)."""
         for p in self.parameters():
             p.data = p.data.to(dtype)
+        return self
+
+    def load_group_asset(self, asset) -> "QwenOALModel":
+        """Sets the dim groups, factors and kernel epsilon of the asset's layers from an
+        :class:`oal_amd.group_assets.OALGroupAsset` (the reference's released grouping)."""
+        for layer_id in asset.layer_ids_zero_based:
+            attn = self.layers[layer_id].attn
+            attn.dim_groups = asset.dim_groups_for_layer(layer_id).to(attn.dim_groups.device)
+            attn.factor = asset.packed_grouped_factor_for_layer(layer_id).to(attn.factor.device)
+            attn.kernel_eps = asset.epsilon
+            attn._prepared.clear()
         return self
 
     def lora_parameters(self):
