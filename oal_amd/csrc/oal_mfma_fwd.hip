@@ -114,7 +114,7 @@ __device__ __forceinline__ void load_row(const float* __restrict__ src, size_t r
 // ---------------------------------------------------------------------------
 // Forward readout: one block of two waves per (query head, chunk, unit); wave w
 // owns tokens 32w..32w+31 (one token per lane row). The per-chunk P^T tiles are
-// streamed through a two-buffer LDS ring of kRG k-steps shared by both waves.
+// streamed through an LDS ring of kNSR stages of kRG k-steps shared by both waves.
 // ---------------------------------------------------------------------------
 constexpr int kRG = 4;                        // k-steps per ring group
 constexpr int kRingGroups = (kKS + kRG - 1) / kRG;
@@ -129,12 +129,15 @@ __device__ __forceinline__ bf16x8 load8(const float* p) {
   return pack8(v);
 }
 
-constexpr int kNSR = 4;  // LDS stages of the readout ring
+// LDS stages of the readout ring: three (24 KB) keep a block of two waves at
+// 33 KB of LDS with the slot weights, so that four blocks (two waves per SIMD,
+// the register limit) fit a CU; one group of four k-steps stays in flight.
+constexpr int kNSR = 3;
 
 // Ring group G (k-steps G * kRG ..) into LDS stage G % kNSR; each k-step tile is
 // 64 values x 16 slots = 128 lanes x 16 bytes.
 template <int G>
-__device__ __forceinline__ void ring_issue(const uint16_t* pt, const LdsRing<4>& ring, int tid) {
+__device__ __forceinline__ void ring_issue(const uint16_t* pt, const LdsRing<kNSR>& ring, int tid) {
   const int wv = tid >> 6;
   __bf16* st = ring.st[G % kNSR];
 #pragma unroll
@@ -145,7 +148,7 @@ __device__ __forceinline__ void ring_issue(const uint16_t* pt, const LdsRing<4>&
 }
 
 template <int T>
-__device__ __forceinline__ void readout_step(const float (&x)[kD], const float* wl, const LdsRing<4>& ring, int lane,
+__device__ __forceinline__ void readout_step(const float (&x)[kD], const float* wl, const LdsRing<kNSR>& ring, int lane,
                                              f32x16 (&acc)[2]) {
   const int s = lane >> 5, row = lane & 31;
   const float4 w0 = *reinterpret_cast<const float4*>(wl + 16 * T + 8 * s);
@@ -159,16 +162,24 @@ __device__ __forceinline__ void readout_step(const float (&x)[kD], const float* 
   acc[1] = mfma32(a, b1, acc[1]);
 }
 
-// Ring pipeline over the k-step groups: groups G + 1, G + 2 may still be in
-// flight while group G is read; group G + 3 is issued after the barrier that
-// retires every read of its stage.
+// Copies one thread issues for ring group G.
 template <int G>
-__device__ __forceinline__ void readout_group(const float (&x)[kD], const float* wl, const LdsRing<4>& ring,
+constexpr int group_copies() {
+  return (G < kRingGroups) ? ((G + 1) * kRG <= kKS ? kRG : kKS - G * kRG) : 0;
+}
+template <int G, int... I>
+constexpr int copies_in_flight(std::integer_sequence<int, I...>) {
+  return (group_copies<G + 1 + I>() + ... + 0);
+}
+
+// Ring pipeline over the k-step groups: groups G + 1 .. G + kNSR - 2 may still
+// be in flight while group G is read; group G + kNSR - 1 is issued after the
+// barrier that retires every read of its stage.
+template <int G>
+__device__ __forceinline__ void readout_group(const float (&x)[kD], const float* wl, const LdsRing<kNSR>& ring,
                                               const uint16_t* pt, int tid, int lane, f32x16 (&acc)[2]) {
-  constexpr int n1 = (G + 1 < kRingGroups) ? ((G + 1) * kRG + kRG <= kKS ? kRG : kKS - (G + 1) * kRG) : 0;
-  constexpr int n2 = (G + 2 < kRingGroups) ? ((G + 2) * kRG + kRG <= kKS ? kRG : kKS - (G + 2) * kRG) : 0;
-  ring_sync<n1 + n2>();
-  if constexpr (G + 3 < kRingGroups) ring_issue<G + 3>(pt, ring, tid);
+  ring_sync<copies_in_flight<G>(std::make_integer_sequence<int, kNSR - 2>{})>();
+  if constexpr (G + kNSR - 1 < kRingGroups) ring_issue<G + kNSR - 1>(pt, ring, tid);
   [&]<int... I>(std::integer_sequence<int, I...>) {
     ((G * kRG + I < kKS ? readout_step<(G * kRG + I < kKS ? G * kRG + I : 0)>(x, wl, ring, lane, acc) : void()), ...);
   }(std::make_integer_sequence<int, kRG>{});
@@ -405,8 +416,13 @@ __global__ __launch_bounds__(128, 2) void k2_out_fwd(const T* __restrict__ q, co
                                                   float floor, T* __restrict__ out, float* __restrict__ num,
                                                   const float* __restrict__ den) {
   __shared__ __attribute__((aligned(16))) __bf16 ring0[kRG * kRingStep], ring1[kRG * kRingStep],
-      ring2[kRG * kRingStep], ring3[kRG * kRingStep];
-  const LdsRing<4> ring{{ring0, ring1, ring2, ring3}};
+      ring2[kRG * kRingStep], ring3[kRG * kRingStep], ring4[kRG * kRingStep], ring5[kRG * kRingStep],
+      ring6[kRG * kRingStep], ring7[kRG * kRingStep];
+  static_assert(kNSR >= 3 && kNSR <= 8, "readout ring depth");
+  __bf16* const stages[8] = {ring0, ring1, ring2, ring3, ring4, ring5, ring6, ring7};
+  LdsRing<kNSR> ring;
+#pragma unroll
+  for (int i = 0; i < kNSR; ++i) ring.st[i] = stages[i];
   __shared__ __attribute__((aligned(16))) float wl[kS];
 
   int hh, ch, u;
@@ -453,9 +469,9 @@ __global__ __launch_bounds__(128, 2) void k2_out_fwd(const T* __restrict__ q, co
       const int tok = tok0 + 32 * wv + c32_row(i, l);
       acc[nt][i] = tok < N ? num[qbase + (size_t)tok * kD + 32 * nt + row] : 0.f;
     }
-  ring_issue<0>(pt, ring, tid);
-  ring_issue<1>(pt, ring, tid);
-  ring_issue<2>(pt, ring, tid);
+  [&]<int... I>(std::integer_sequence<int, I...>) {
+    (ring_issue<I>(pt, ring, tid), ...);
+  }(std::make_integer_sequence<int, kNSR - 1>{});
   readout_group<0>(x, wl, ring, pt, tid, l, acc);
 
   const size_t dbase = (size_t)(b * Hq + h) * N;
