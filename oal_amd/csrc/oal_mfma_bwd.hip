@@ -568,6 +568,7 @@ __global__ __launch_bounds__(256) void k2_coef_grad(const float* __restrict__ dw
   __shared__ float wn[kFeat];
   __shared__ float loc[73];
   __shared__ float xr[kD][9];
+  __shared__ float xq[4][kD][9];
   __shared__ float raw[64];
   __shared__ int lab[kD];
   const int h = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
@@ -605,23 +606,42 @@ __global__ __launch_bounds__(256) void k2_coef_grad(const float* __restrict__ dw
     }
   }
   __syncthreads();
+  // xr[r][g] = sum_{c <= r, g(c) = g} m_rc wn[pair(r, c)]: thread (r, q) sums the
+  // columns c = q mod 4 into eight group bins, then the four quarters are added
+  // in a fixed order
+  {
+    const int r = t >> 2, q = t & 3;
+    float bin[8];
+#pragma unroll
+    for (int g = 0; g < 8; ++g) bin[g] = 0.f;
+    const float* row = wn + 1 + kD + pair_index(r, 0);
+    for (int c = q; c <= r; c += 4) {
+      const float x = (c == r ? 1.f : 2.f) * row[c];
+      const int lc = lab[c];
+#pragma unroll
+      for (int g = 0; g < 8; ++g) bin[g] += lc == g ? x : 0.f;
+    }
+#pragma unroll
+    for (int g = 0; g < 8; ++g) xq[q][r][g] = bin[g];
+  }
+  __syncthreads();
   for (int e = t; e < kD * 8; e += 256) {
     const int r = e >> 3, g = e & 7;
+    xr[r][g] = g < G ? (xq[0][r][g] + xq[1][r][g]) + (xq[2][r][g] + xq[3][r][g]) : 0.f;
+  }
+  __syncthreads();
+  // raw[gr][gc] = scale^2 sum_{r: g(r) = gr} xr[r][gc]: thread (gr, gc, q) sums
+  // the rows r = q mod 4, then the quarters in a fixed order
+  {
+    const int e = t >> 2, q = t & 3, gr = e >> 3, gc = e & 7;
     float acc = 0.f;
-    if (g < G) {
-      const float* row = wn + 1 + kD + pair_index(r, 0);
-      for (int c = 0; c <= r; ++c)
-        if (lab[c] == g) acc += (c == r ? 1.f : 2.f) * row[c];
-    }
-    xr[r][g] = acc;
+    for (int r = q; r < kD; r += 4) acc += lab[r] == gr ? xr[r][gc] : 0.f;
+    xq[q][e][0] = acc;
   }
   __syncthreads();
   if (t < G * G) {
-    const int gr = t / G, gc = t % G;
-    float acc = 0.f;
-    for (int r = 0; r < kD; ++r)
-      if (lab[r] == gr) acc += xr[r][gc];
-    raw[t] = acc * scale * scale;
+    const int gr = t / G, gc = t % G, e = 8 * gr + gc;
+    raw[t] = ((xq[0][e][0] + xq[1][e][0]) + (xq[2][e][0] + xq[3][e][0])) * scale * scale;
   }
   if (t == 64) dc0[h] = wn[0] + loc[0];
   if (t >= 128 && t < 128 + G) {

@@ -40,7 +40,8 @@ __global__ __launch_bounds__(256) void k2_slot_coefficients(const int32_t* __res
   // from LDS (no dependent global gathers)
   __shared__ int lab[kD];
   __shared__ float cg[8 * 8], cl[8], cc;
-  const int h = blockIdx.x, t = threadIdx.x;
+  // block (h, part): slots and gm rows of one eighth; part 0 also writes ic, lb
+  const int h = blockIdx.x, part = blockIdx.y, t = threadIdx.x;
   if (t < kD) {
     const int g = labels[h * kD + t];
     lab[t] = g < 0 ? 0 : (g >= G ? G - 1 : g);
@@ -52,7 +53,9 @@ __global__ __launch_bounds__(256) void k2_slot_coefficients(const int32_t* __res
   if (t >= 64 && t < 72) cl[t - 64] = (t - 64) < G ? scale * lam[(size_t)h * G + (t - 64)] : 0.f;
   if (t == 72) cc = c0[h];
   __syncthreads();
-  for (int s = t; s < kS; s += blockDim.x) {
+  constexpr int kSlotsPerPart = kS / 8;
+  static_assert(kSlotsPerPart * 8 == kS, "slot parts");
+  for (int s = part * kSlotsPerPart + t; s < (part + 1) * kSlotsPerPart; s += blockDim.x) {
     const int n = kSlot.nat[s];
     const int r = kSlot.ar[s], c = kSlot.ac[s];
     float w = 0.f;
@@ -65,7 +68,7 @@ __global__ __launch_bounds__(256) void k2_slot_coefficients(const int32_t* __res
     }
     wqs[(size_t)h * kS + s] = w;
   }
-  if (t < kIC) {
+  if (part == 0 && t < kIC) {
     float x = 0.f;
     if (t == 0) {
       x = cc;
@@ -76,11 +79,11 @@ __global__ __launch_bounds__(256) void k2_slot_coefficients(const int32_t* __res
     }
     ic[(size_t)h * kIC + t] = x;
   }
-  for (int e = t; e < kD * kD; e += blockDim.x) {
+  for (int e = part * (kD * kD / 8) + t; e < (part + 1) * (kD * kD / 8); e += blockDim.x) {
     const int r = e >> 6, c = e & 63;
     gm[(size_t)h * kD * kD + e] = cg[lab[r] * 8 + lab[c]];
   }
-  if (t < kD) lb[(size_t)h * kD + t] = cl[lab[t]];
+  if (part == 0 && t < kD) lb[(size_t)h * kD + t] = cl[lab[t]];
 }
 
 template <typename T>
@@ -573,7 +576,7 @@ void launch_mfma_forward(const LaunchGeom& g, const void* q, const void* k, cons
   const T* kt = static_cast<const T*>(k);
   const T* vt = static_cast<const T*>(v);
   timed("k2_slot_coefficients", st, [&] {
-    hipLaunchKernelGGL(k2_slot_coefficients, dim3(g.Hq), dim3(256), 0, st, labels, c0, lam, gam, groups, scale,
+    hipLaunchKernelGGL(k2_slot_coefficients, dim3(g.Hq, 8), dim3(256), 0, st, labels, c0, lam, gam, groups, scale,
                        sv.wqs, sv.ic, sv.gm, sv.lb);
   });
   launch_fwd_prep<T>(g, kt, vt, sv.KT16, sv.VT16, st, timed);

@@ -21,16 +21,15 @@
 // fetched into registers two items ahead. Raw features are products of two
 // fp32 rows of the staged feature side, packed to bf16 as the MFMA B operand.
 //   MODE 0: segment totals (backward: plus coefficient partials); no state out.
-//   MODE 1: replay from the carry of the other segments, emitting every chunk's
-//           state; the backward weights the features by wq_h so that every
-//           head accumulates into the one state.
+//   MODE 1: replay from the carry of the other segments (the sum of their totals,
+//           nearest segment first, formed by each block for its own tiles),
+//           emitting every chunk's state; the backward weights the features by
+//           wq_h so that every head accumulates into the one state.
 //   MODE 2: one segment: MODE 1's output plus MODE 0's partials.
 // Emitted layouts per (unit, chunk), identical in both directions:
 //   R [kS/32][4][32][16 values] bf16, T [kKS][64 values][16 slots] bf16,
 //   Z [kFP] fp32 (denominator column, natural feature order), and in the
 //   forward Zm [64][64] fp32 (the denominator column as a symmetric pair matrix).
-// k2_seg_carry turns segment totals into carries in place: exclusive prefix
-// (forward) or exclusive suffix (backward), fixed order.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -127,15 +126,27 @@ __global__ __launch_bounds__(64 * NW, NW / 2) void k2_scan(const uint16_t* __res
 #pragma unroll
     for (int n = 0; n < 2; ++n) acc[t][n] = f32x16{};
   if constexpr (MODE == 1) {
+    // carry = sum of the totals of the segments before (forward) or after
+    // (backward) this one, in a fixed order: nearest segment first
+    const int n_other = FWD ? seg : Sg - 1 - seg;
+    for (int o = 0; o < n_other; ++o) {
+      const int so = FWD ? seg - 1 - o : seg + 1 + o;
 #pragma unroll
-    for (int t = 0; t < TPW; ++t) {
-      if (live[t]) {
-        const float* cr = carry + (((size_t)u * Sg + seg) * kS + slot[t]) * 65;
+      for (int t = 0; t < TPW; ++t) {
+        if (live[t]) {
+          const float* cr = carry + (((size_t)u * Sg + so) * kS + slot[t]) * 65;
+          float tv[2][16], tz = 0.f;
 #pragma unroll
-        for (int n = 0; n < 2; ++n)
+          for (int n = 0; n < 2; ++n)
 #pragma unroll
-          for (int i = 0; i < 16; ++i) acc[t][n][i] = cr[32 * n + c32_row(i, l)];
-        if (s == 0) accz[t] = cr[64];
+            for (int i = 0; i < 16; ++i) tv[n][i] = cr[32 * n + c32_row(i, l)];
+          if (s == 0) tz = cr[64];
+#pragma unroll
+          for (int n = 0; n < 2; ++n)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[t][n][i] += tv[n][i];
+          if (s == 0) accz[t] += tz;
+        }
       }
     }
   }
@@ -421,32 +432,6 @@ __global__ __launch_bounds__(64 * NW, NW / 2) void k2_scan(const uint16_t* __res
   }
 }
 
-// In place: x[u][seg] <- sum over the segments before (forward) or after
-// (backward) seg of x[u][seg'] (fixed order), elementwise.
-template <bool FWD>
-__global__ __launch_bounds__(256) void k2_seg_carry(float* __restrict__ segtot, int S) {
-  const size_t per = (size_t)kS * 65;
-  const size_t e = (size_t)blockIdx.x * 256 + threadIdx.x;
-  if (e >= per) return;
-  float* x = segtot + (size_t)blockIdx.y * S * per + e;
-  float run = 0.f;
-  // eight segments' loads in flight before their carries are stored
-  for (int i0 = 0; i0 < S; i0 += 8) {
-    float t[8];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const int i = i0 + k, sg = FWD ? i : S - 1 - i;
-      t[k] = i < S ? x[(size_t)sg * per] : 0.f;
-    }
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const int i = i0 + k, sg = FWD ? i : S - 1 - i;
-      if (i < S) x[(size_t)sg * per] = run;
-      run += t[k];
-    }
-  }
-}
-
 // Forward operands per (unit, chunk): KT16 [U][64][NB * 64] = k^T and
 // VT16 [U][65][NB * 64] = [v^T; 1 (token < N)], bf16, tokens >= N zero.
 template <typename T>
@@ -550,9 +535,6 @@ void launch_scan(const ScanPlan& p, const ScanArgs& a, hipStream_t st, const Tim
     hipLaunchKernelGGL((k2_scan<FWD, 0, T0, W0>), grid(T0, W0), dim3(64 * W0), 0, st, a.F, a.frows, a.V, a.vrows, a.wqs, a.PR, a.PZ,
                        nullptr, a.Hq, a.Hkv, a.N, a.NB, p.SL, p.S, nullptr, nullptr, nullptr, nullptr, a.segtot,
                        a.dwqs);
-  });
-  timed("k2_seg_carry", st, [&] {
-    hipLaunchKernelGGL((k2_seg_carry<FWD>), dim3((kS * 65 + 255) / 256, a.U), dim3(256), 0, st, a.segtot, p.S);
   });
   timed(name, st, [&] {
     hipLaunchKernelGGL((k2_scan<FWD, 1, T1, W1>), grid(T1, W1), dim3(64 * W1), 0, st, a.F, a.frows, a.V, a.vrows, a.wqs, a.PR,

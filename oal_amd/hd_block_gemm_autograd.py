@@ -215,7 +215,7 @@ def _require_positive_denominator(den: torch.Tensor) -> None:
 
     Mirrors ``hd_block_gemm_runtime.py:392-408``.
     """
-    lo, hi = torch.aminmax(den)
+    lo, hi = torch.aminmax(den.detach())
     if not (bool(torch.isfinite(lo)) and bool(torch.isfinite(hi))):
         raise RuntimeError("HD Block-GEMM denominator must be finite")
     if float(lo) <= 0.0:
