@@ -19,7 +19,8 @@
 // k2_local_dk    one block per (unit, chunk): dk local part summed over the
 //                unit's query heads in registers (group sums one at a time).
 // k2_local_dv    one block per (unit, chunk): kappa and the dv local part,
-//                summed over the unit's query heads, and the per-(head, chunk)
+//                summed over the unit's query heads.
+// k2_local_coef  one block per (query head, chunk): the per-(head, chunk)
 //                coefficient partials.
 
 #include <hip/hip_runtime.h>
@@ -381,17 +382,15 @@ __global__ __launch_bounds__(192) void k2_local_dk(const T* __restrict__ q, cons
   local_write(red, acc, t, l, row, tok0, N, kbase, dkl);
 }
 
-// kappa[i][j] (quadratic form in the group sums), dv[j][e] += sum_i kappa g_i[e].
+// kappa[i][j] (quadratic form in the group sums), dv[j][e] += sum_i kappa g_i[e],
+// summed over the unit's query heads in registers.
 template <typename T>
-__global__ __launch_bounds__(192) void k2_local_dv(const T* __restrict__ q, const T* __restrict__ k,
-                                                   const T* __restrict__ v, const uint16_t* __restrict__ G16,
-                                                   const float* __restrict__ Gz, const uint16_t* __restrict__ GT16,
-                                                   const int32_t* __restrict__ labels, const float* __restrict__ ic,
-                                                   int G, int Hq, int Hkv, int N, int NB, float scale,
-                                                   float* __restrict__ dvl, float* __restrict__ coefl) {
+__global__ __launch_bounds__(192, 2) void k2_local_dv(const T* __restrict__ q, const T* __restrict__ k,
+                                                   const uint16_t* __restrict__ GT16, const int32_t* __restrict__ labels,
+                                                   const float* __restrict__ ic, int G, int Hq, int Hkv, int N, int NB,
+                                                   float* __restrict__ dvl) {
   __shared__ __attribute__((aligned(16))) uint32_t mk[2][4][8][2][4];
   __shared__ float red[2][16][64];
-  __shared__ float cp[3 * 64][45];  // per-lane coefficient partials of the 3 tile waves
   int ch;
   const int u = unit_chunk_block(NB, ch);
   const int R = Hq / Hkv, b = u / Hkv, kh = u % Hkv;
@@ -400,14 +399,10 @@ __global__ __launch_bounds__(192) void k2_local_dv(const T* __restrict__ q, cons
   const size_t kbase = (size_t)u * N * kD;
   const size_t np = (size_t)NB * kC;
   const LocalTile t = local_tile(wv, tok0, N, row);
-  bf16x8 kf[4], vf[4];
+  bf16x8 kf[4];
 #pragma unroll
-  for (int kk = 0; kk < 4; ++kk) {
-    kf[kk] = row8(k + kbase + t.jo + 16 * kk + 8 * s, t.jok);
-    vf[kk] = row8(v + kbase + t.jo + 16 * kk + 8 * s, t.jok);
-  }
+  for (int kk = 0; kk < 4; ++kk) kf[kk] = row8(k + kbase + t.jo + 16 * kk + 8 * s, t.jok);
   f32x16 acc[2] = {f32x16{}, f32x16{}};
-  const size_t bn = (size_t)(gridDim.x / NB / Hkv) * NB;
 
   build_masks(mk[0], labels, kh * R, G, tid);
   __syncthreads();
@@ -447,75 +442,102 @@ __global__ __launch_bounds__(192) void k2_local_dv(const T* __restrict__ q, cons
       acc[et] = mfma32(f0, *reinterpret_cast<const bf16x8*>(gt), acc[et]);
       acc[et] = mfma32(f1, *reinterpret_cast<const bf16x8*>(gt + 16), acc[et]);
     }
-    if (coefl) {
-      // ds[i][j] = g_i . v_j + gz_i; partials [0] sum ds, [1 + g] sum ds s_g,
-      // [9 + idx(g <= h)] sum ds s_g s_h (s = scale * group sum)
-      f32x16 ds = f32x16{};
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) ds = mfma32(row8(G16 + qbase + t.io + 16 * kk + 8 * s, t.iok), vf[kk], ds);
-      float ca[45];
-#pragma unroll
-      for (int e = 0; e < 45; ++e) ca[e] = 0.f;
-#pragma unroll
-      for (int a = 0; a < 4; ++a) {
-        const int i0 = 32 * t.it + 8 * a + 4 * s;
-#pragma unroll
-        for (int vv = 0; vv < 4; ++vv) {
-          const int r = 4 * a + vv, i = i0 + vv;
-          const float gzi = tok0 + i < N ? Gz[(size_t)(b * Hq + h) * N + tok0 + i] : 0.f;
-          const float dsv = (t.j <= i && tok0 + i < N) ? ds[r] + gzi : 0.f;
-          float sv[8], tv[8];
-#pragma unroll
-          for (int g = 0; g < 8; ++g) {
-            sv[g] = scale * sg[g][r];
-            tv[g] = dsv * sv[g];
-          }
-          ca[0] += dsv;
-          int e = 9;
-#pragma unroll
-          for (int g = 0; g < 8; ++g) {
-            ca[1 + g] += tv[g];
-#pragma unroll
-            for (int h2 = g; h2 < 8; ++h2) {
-              ca[e] = fmaf(tv[g], sv[h2], ca[e]);
-              ++e;
-            }
-          }
-        }
-      }
-#pragma unroll
-      for (int e = 0; e < 45; ++e) cp[tid][e] = ca[e];
-    }
     __syncthreads();
-    if (coefl) {
-      // column sums over the 192 lanes (fixed order: 4 interleaved partial
-      // sums per column, then their sum), written in the full symmetric
-      // 8 x 8 layout [0] dc0, [1 + g] dlam, [9 + 8 g + h] dGam
-      if (tid < 180) {
-        const int e = tid % 45, part = tid / 45;
-        float x = 0.f;
-        for (int r = part; r < 192; r += 4) x += cp[r][e];
-        (&red[0][0][0])[tid] = x;  // red is free until the final combine
-      }
-      __syncthreads();
-      if (tid < 73) {
-        int e = tid;
-        if (tid >= 9) {
-          int g = (tid - 9) >> 3, h2 = (tid - 9) & 7;
-          if (h2 < g) {
-            const int t2 = g;
-            g = h2;
-            h2 = t2;
-          }
-          e = 9 + g * 8 - g * (g - 1) / 2 + (h2 - g);
-        }
-        const float* rp = &red[0][0][0];
-        coefl[((size_t)h * 73 + tid) * bn + (size_t)b * NB + ch] = (rp[e] + rp[45 + e]) + (rp[90 + e] + rp[135 + e]);
-      }
-      __syncthreads();
-    }
   }
   local_write(red, acc, t, l, row, tok0, N, kbase, dvl);
+}
+
+// Per-(head, chunk) local coefficient partials, one block per (query head,
+// chunk), 3 waves = tile pairs: with ds[i][j] = g_i . v_j + gz_i (j <= i) and
+// s_g the scaled group sums, [0] sum ds, [1 + g] sum ds s_g, [9 + 8 g + h]
+// sum ds s_g s_h (written in the full symmetric 8 x 8 layout), each a fixed-order
+// sum over the block's 192 lanes.
+template <typename T>
+__global__ __launch_bounds__(192, 2) void k2_local_coef(const T* __restrict__ q, const T* __restrict__ k,
+                                                     const T* __restrict__ v, const uint16_t* __restrict__ G16,
+                                                     const float* __restrict__ Gz, const int32_t* __restrict__ labels,
+                                                     int G, int Hq, int Hkv, int N, int NB, float scale,
+                                                     float* __restrict__ coefl) {
+  __shared__ __attribute__((aligned(16))) uint32_t mk[4][8][2][4];
+  __shared__ float cp[3 * 64][45];  // per-lane partials of the 3 tile waves
+  __shared__ float red[4 * 45];
+  int hh, ch, u;
+  head_chunk_unit(Hq / Hkv, NB, (int)(gridDim.x / ((Hq / Hkv) * NB)), hh, ch, u);
+  const int R = Hq / Hkv, b = u / Hkv, kh = u % Hkv, h = kh * R + hh;
+  const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, s = l >> 5, row = l & 31;
+  const int tok0 = ch * kC;
+  const size_t kbase = (size_t)u * N * kD;
+  const size_t qbase = (size_t)(b * Hq + h) * N * kD;
+  const size_t bn = (size_t)(gridDim.x / (R * NB) / Hkv) * NB;
+  const LocalTile t = local_tile(wv, tok0, N, row);
+  build_masks(mk, labels, h, G, tid);
+  __syncthreads();
+  f32x16 sg[8], ds = f32x16{};
+#pragma unroll
+  for (int g = 0; g < 8; ++g) sg[g] = f32x16{};
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) {
+    const bf16x8 qf = row8(q + qbase + t.io + 16 * kk + 8 * s, t.iok);
+    const bf16x8 kf = row8(k + kbase + t.jo + 16 * kk + 8 * s, t.jok);
+#pragma unroll
+    for (int g = 0; g < 8; ++g) sg[g] = mfma32(masked(qf, &mk[kk][g][s][0]), kf, sg[g]);
+    ds = mfma32(row8(G16 + qbase + t.io + 16 * kk + 8 * s, t.iok), row8(v + kbase + t.jo + 16 * kk + 8 * s, t.jok),
+                ds);
+  }
+  float ca[45];
+#pragma unroll
+  for (int e = 0; e < 45; ++e) ca[e] = 0.f;
+#pragma unroll
+  for (int a = 0; a < 4; ++a) {
+    const int i0 = 32 * t.it + 8 * a + 4 * s;
+#pragma unroll
+    for (int vv = 0; vv < 4; ++vv) {
+      const int r = 4 * a + vv, i = i0 + vv;
+      const float gzi = tok0 + i < N ? Gz[(size_t)(b * Hq + h) * N + tok0 + i] : 0.f;
+      const float dsv = (t.j <= i && tok0 + i < N) ? ds[r] + gzi : 0.f;
+      float sv[8], tv[8];
+#pragma unroll
+      for (int g = 0; g < 8; ++g) {
+        sv[g] = scale * sg[g][r];
+        tv[g] = dsv * sv[g];
+      }
+      ca[0] += dsv;
+      int e = 9;
+#pragma unroll
+      for (int g = 0; g < 8; ++g) {
+        ca[1 + g] += tv[g];
+#pragma unroll
+        for (int h2 = g; h2 < 8; ++h2) {
+          ca[e] = fmaf(tv[g], sv[h2], ca[e]);
+          ++e;
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 45; ++e) cp[tid][e] = ca[e];
+  __syncthreads();
+  // column sums over the 192 lanes: 4 interleaved partial sums per column, then their sum
+  if (tid < 180) {
+    const int e = tid % 45, part = tid / 45;
+    float x = 0.f;
+    for (int r = part; r < 192; r += 4) x += cp[r][e];
+    red[tid] = x;
+  }
+  __syncthreads();
+  if (tid < 73) {
+    int e = tid;
+    if (tid >= 9) {
+      int g = (tid - 9) >> 3, h2 = (tid - 9) & 7;
+      if (h2 < g) {
+        const int t2 = g;
+        g = h2;
+        h2 = t2;
+      }
+      e = 9 + g * 8 - g * (g - 1) / 2 + (h2 - g);
+    }
+    coefl[((size_t)h * 73 + tid) * bn + (size_t)b * NB + ch] = (red[e] + red[45 + e]) + (red[90 + e] + red[135 + e]);
+  }
 }
 
 template <typename T>
@@ -533,10 +555,16 @@ void launch_local_bwd(const LaunchGeom& g, const T* q, const T* k, const T* v, c
                          a.labels, a.lam, a.gam, a.groups, g.Hq, g.Hkv, g.N, g.NB, a.scale, a.dkl);
     });
   }
-  if (need_dkv || a.coefl) {
+  if (need_dkv) {
     timed("k2_local_dv", st, [&] {
-      hipLaunchKernelGGL(k2_local_dv<T>, dim3(g.NB * g.U), dim3(192), 0, st, q, k, v, a.G16, a.Gz, a.GT16, a.labels,
-                         a.ic, a.groups, g.Hq, g.Hkv, g.N, g.NB, a.scale, a.dvl, a.coefl);
+      hipLaunchKernelGGL(k2_local_dv<T>, dim3(g.NB * g.U), dim3(192), 0, st, q, k, a.GT16, a.labels, a.ic, a.groups,
+                         g.Hq, g.Hkv, g.N, g.NB, a.dvl);
+    });
+  }
+  if (a.coefl) {
+    timed("k2_local_coef", st, [&] {
+      hipLaunchKernelGGL(k2_local_coef<T>, dim3(g.R * g.NB * g.U), dim3(192), 0, st, q, k, v, a.G16, a.Gz, a.labels,
+                         a.groups, g.Hq, g.Hkv, g.N, g.NB, a.scale, a.coefl);
     });
   }
 }
