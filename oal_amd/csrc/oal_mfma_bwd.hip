@@ -419,117 +419,108 @@ __device__ __forceinline__ void du_group(const float (&x)[kD], const LdsRing<4>&
   if constexpr (G + 1 < NG) du_group<G + 1>(x, ring, src, tid, lane, acc);
 }
 
+// Rows of the Mz operand for the Z^T = Mz K^T products: product md, accumulator
+// row m = 8 a + 4 s + v (lane group s, register 4 a + v) holds dimension
+// 32 s + 16 md + 4 a + v, so that lane group s ends up with dimensions
+// 32 s .. 32 s + 31 of its token (registers 16 md + i), the layout of the fold.
+__device__ __forceinline__ int mz_dim(int md, int m) {
+  const int a = m >> 3, sg = (m >> 2) & 1, v = m & 3;
+  return 32 * sg + 16 * md + 4 * a + v;
+}
+
+// grid (NB, U, 2), 2 waves; wave w owns tokens 32w..32w+31 of the chunk.
+//   part 0: dk = fold of dT V^T through the key features + z1 + Mz k + local dk,
+//           Mz[r][c] = dTz[pair(r, c)] (r != c), 2 dTz[pair(r, r)] on the diagonal;
+//   part 1: dv = raw(K) dT (values 0..63) + local dv.
+// The two parts share nothing, so they run as independent blocks.
 template <typename T>
-__global__ __launch_bounds__(128) void k2_kv_fold(const T* __restrict__ k, const T* __restrict__ v,
-                                                  const uint16_t* __restrict__ dTR, const uint16_t* __restrict__ dTT,
-                                                  const float* __restrict__ dTz, const float* __restrict__ dkl,
-                                                  const float* __restrict__ dvl, int Hq, int Hkv, int N, int NB,
-                                                  T* __restrict__ dk, T* __restrict__ dv) {
+__global__ __launch_bounds__(128, 2) void k2_kv_fold(const T* __restrict__ k, const T* __restrict__ v,
+                                                     const uint16_t* __restrict__ dTR, const uint16_t* __restrict__ dTT,
+                                                     const float* __restrict__ dTz, const float* __restrict__ dkl,
+                                                     const float* __restrict__ dvl, int Hq, int Hkv, int N, int NB,
+                                                     T* __restrict__ dk, T* __restrict__ dv) {
   __shared__ __attribute__((aligned(16))) __bf16 ring0[kFG * 1024], ring1[kFG * 1024], ring2[kFG * 1024],
       ring3[kFG * 1024];
   __shared__ __attribute__((aligned(16))) __bf16 mz[kD][LD];
-  __shared__ __attribute__((aligned(16))) __bf16 ks[kC][LD];
-  __shared__ float dks[kC][kD + 1];
   __shared__ float zl[kD];
 
-  const int ch = blockIdx.x, u = blockIdx.y;
-  const int R = Hq / Hkv, b = u / Hkv, kh = u % Hkv;
+  const int ch = blockIdx.x, u = blockIdx.y, part = blockIdx.z;
   const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, s = l >> 5, row = l & 31;
   const int tok0 = ch * kC;
   const size_t kbase = (size_t)u * N * kD;
   const size_t cbase = ((size_t)u * NB + ch) * ((size_t)kKS * 64 * 16);
-  const float* tz = dTz + ((size_t)u * NB + ch) * kFP;
-
-  // dTz quadratic form: d/dk of sum_p dTz[p] raw(k)[p] = z1 + Mz k with
-  // Mz[r][c] = dTz[pair(r, c)] (r != c), 2 dTz[pair(r, r)] on the diagonal.
-  for (int idx = tid; idx < kD * kD; idx += 128) {
-    const int r = idx >> 6, c = idx & 63;
-    const int hi = r > c ? r : c, lo = r > c ? c : r;
-    const float val = tz[1 + kD + pair_index(hi, lo)];
-    mz[r][c] = (__bf16)(r == c ? 2.f * val : val);
-  }
-  if (tid < kD) zl[tid] = tz[1 + tid];
-
   const int tok = tok0 + 32 * wv + row;
   const bool ok = tok < N;
   const size_t rowoff = kbase + (size_t)(ok ? tok : N - 1) * kD;
-  float x[kD], dx[kD];
-  bf16x8 bfr[4];
+  float x[kD];
   load_rotated(k, rowoff, ok, s, x);
+  const LdsRing<4> ring{{ring0, ring1, ring2, ring3}};
+
+  if (part == 1) {
+    f32x16 acc[2] = {f32x16{}, f32x16{}};
+    ring_issue_u<kKS, 0>(dTT + cbase, ring, tid);
+    ring_issue_u<kKS, 1>(dTT + cbase, ring, tid);
+    ring_issue_u<kKS, 2>(dTT + cbase, ring, tid);
+    du_group<0>(x, ring, dTT + cbase, tid, l, acc);
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int tj = tok0 + 32 * wv + c32_row(i, l);
+        if (tj < N) {
+          const size_t o = kbase + (size_t)tj * kD + 32 * nt + row;
+          dv[o] = from_f<T>(acc[nt][i] + dvl[o]);
+        }
+      }
+    return;
+  }
+
+  const float* tz = dTz + ((size_t)u * NB + ch) * kFP;
+  for (int idx = tid; idx < kD * kD; idx += 128) {
+    const int r = idx >> 6, c = idx & 63;
+    const int d = mz_dim(r >> 5, r & 31);
+    const int hi = d > c ? d : c, lo = d > c ? c : d;
+    const float val = tz[1 + kD + pair_index(hi, lo)];
+    mz[r][c] = (__bf16)(d == c ? 2.f * val : val);
+  }
+  if (tid < kD) zl[tid] = tz[1 + tid];
+  bf16x8 bfr[4];
 #pragma unroll
   for (int kk = 0; kk < 4; ++kk) bfr[kk] = frag8(v, rowoff + 16 * kk + 8 * s, ok);
-  // lane group 0 holds the unrotated key row
-  if (s == 0) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      float v8[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) v8[j] = x[8 * i + j];
-      *reinterpret_cast<bf16x8*>(&ks[32 * wv + row][8 * i]) = pack8(v8);
-    }
-  }
+  float dx[kD];
 #pragma unroll
   for (int m = 0; m < kD; ++m) dx[m] = 0.f;
-
-  // 1. fold of dT V^T through the key features
-  static_assert(kTileElems <= kFG * 1024, "a fold tile fits one dU ring stage");
-  const LdsRing<4> fr{{ring0, ring1, ring2, ring3}};
-  const LdsRing<4> ring{{ring0, ring1, ring2, ring3}};
-  fold_all<4, false>(bfr, x, dx, nullptr, fr, dTR + cbase, tid, l);
-  __syncthreads();
-  // 2. dU = raw(K) dT (values 0..63)
-  f32x16 acc[2] = {f32x16{}, f32x16{}};
-  __syncthreads();  // every read of the fold ring is done before the dU ring reuses it
-  ring_issue_u<kKS, 0>(dTT + cbase, ring, tid);
-  ring_issue_u<kKS, 1>(dTT + cbase, ring, tid);
-  ring_issue_u<kKS, 2>(dTT + cbase, ring, tid);
-  du_group<0>(x, ring, dTT + cbase, tid, l, acc);
-
-  // 3. combine rotation groups, add z1 + Mz k
-  const int tl = 32 * wv + row;
-  if (s == 0) {
+  static_assert(kTileElems <= kFG * 1024, "a fold tile fits one ring stage");
+  fold_all<4, false>(bfr, x, dx, nullptr, ring, dTR + cbase, tid, l);
+  // lane group s: dimensions 32 s .. 32 s + 31 of its token
+  float full[32];
+  combine_rotation_groups(dx, s, full);
+  // Z^T [dimension x token] = Mz K^T for this wave's tokens; B = the lane's own k row
+  bf16x8 kb[4];
 #pragma unroll
-    for (int m = 0; m < kD; ++m) dks[tl][m] = dx[m] + zl[m];
+  for (int kk = 0; kk < 4; ++kk) kb[kk] = frag8(k, rowoff + 16 * kk + 8 * s, ok);
+#pragma unroll
+  for (int md = 0; md < 2; ++md) {
+    f32x16 z = f32x16{};
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+      z = mfma32(*reinterpret_cast<const bf16x8*>(&mz[32 * md + row][16 * kk + 8 * s]), kb[kk], z);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) full[16 * md + i] += z[i];
   }
-  __syncthreads();
-  if (s == 1) {
+  if (ok) {
+    const size_t o = rowoff + 32 * s;
+    const float4* lf = reinterpret_cast<const float4*>(dkl + o);
 #pragma unroll
-    for (int m = 0; m < kD; ++m) dks[tl][(m + 32) & 63] += dx[m];
-  }
-  __syncthreads();
-  {
-    // Z^T [64 d x 32 tok] = Mz K^T for this wave's tokens
-#pragma unroll
-    for (int md = 0; md < 2; ++md) {
-      f32x16 z = f32x16{};
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        const bf16x8 a = *reinterpret_cast<const bf16x8*>(&mz[32 * md + row][16 * kk + 8 * s]);
-        const bf16x8 bb = *reinterpret_cast<const bf16x8*>(&ks[32 * wv + row][16 * kk + 8 * s]);
-        z = mfma32(a, bb, z);
-      }
-#pragma unroll
-      for (int i = 0; i < 16; ++i) dks[32 * wv + row][32 * md + c32_row(i, l)] += z[i];
+    for (int j = 0; j < 8; ++j) {
+      const float4 a = lf[j];
+      full[4 * j] += a.x + zl[32 * s + 4 * j];
+      full[4 * j + 1] += a.y + zl[32 * s + 4 * j + 1];
+      full[4 * j + 2] += a.z + zl[32 * s + 4 * j + 2];
+      full[4 * j + 3] += a.w + zl[32 * s + 4 * j + 3];
     }
+    store32(dk + o, full);
   }
-  __syncthreads();
-  for (int j = 0; j < 32; ++j) {
-    const int tj = tok0 + 32 * wv + j;
-    if (tj >= N) break;
-    const size_t o = kbase + (size_t)tj * kD + l;
-    const float ksum = dks[32 * wv + j][l] + dkl[o], vsum = dvl[o];
-    dk[o] = from_f<T>(ksum);
-    // dv state part lives in the accumulators; add it below
-    dks[32 * wv + j][l] = vsum;
-  }
-  __syncthreads();
-#pragma unroll
-  for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int j = 32 * wv + c32_row(i, l), tj = tok0 + j;
-      if (tj < N) dv[kbase + (size_t)tj * kD + 32 * nt + row] = from_f<T>(acc[nt][i] + dks[j][32 * nt + row]);
-    }
 }
 
 // dwq[h][slot] = sum over (segment, batch) of the state-scan partials, fixed order.
@@ -735,7 +726,7 @@ int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, cons
   }
   if (dk) {
     timed("k2_kv_fold", st, [&] {
-      hipLaunchKernelGGL(k2_kv_fold<T>, dim3(g.NB, g.U), dim3(128), 0, st, kt, vt, w.dTR, w.dTT, w.dTz, w.dkl, w.dvl,
+      hipLaunchKernelGGL(k2_kv_fold<T>, dim3(g.NB, g.U, 2), dim3(128), 0, st, kt, vt, w.dTR, w.dTT, w.dTz, w.dkl, w.dvl,
                          g.Hq, g.Hkv, g.N, g.NB, static_cast<T*>(dk), static_cast<T*>(dv));
     });
   }

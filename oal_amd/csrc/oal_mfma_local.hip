@@ -96,7 +96,7 @@ __device__ __forceinline__ int tile_it(int tp) { return tp == 0 ? 0 : 1; }
 // gz_i (bz_d + 2 (Mz q_i)_d), Mz = gm o PZm, and write dqf.
 // ---------------------------------------------------------------------------
 template <typename T>
-__global__ __launch_bounds__(192) void k2_local_dq(const T* __restrict__ q, const T* __restrict__ k,
+__global__ __launch_bounds__(192, 3) void k2_local_dq(const T* __restrict__ q, const T* __restrict__ k,
                                                    const T* __restrict__ v, const uint16_t* __restrict__ G16,
                                                    const float* __restrict__ Gz, const uint16_t* __restrict__ KT16,
                                                    const float* __restrict__ PZ, const float* __restrict__ PZm,
