@@ -324,7 +324,9 @@ def main() -> int:
         "data": "synthetic (BASELINE config 2 distributions: N(0,1) with 2 outlier dims x8 per head, "
                 "8 uneven groups, c0=1, a~U(0.5,1.5), b~U(0,0.5))",
         "config": {
-            "workload": "OAL causal attention fwd+bwd, BASELINE config 2",
+            "workload": "OAL causal attention fwd+bwd, " + {
+                (4, 4096): "BASELINE config 2", (1, 32768): "BASELINE config 3 (long context)",
+            }.get((b, n), f"config-2 distributions at B={b}, N={n}"),
             "batch": b,
             "q_heads": 14,
             "kv_heads": 2,
