@@ -304,20 +304,33 @@ __global__ __launch_bounds__(64 * NW, NW / 2) void k2_scan(const uint16_t* __res
       for (int n = 0; n < 3; ++n) hT[n] = f32x16{};
     }
     const int zrow = kD * kVRow;
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      // value side (shared by the wave's tiles); the denominator row (row 64)
-      // goes to A row t for tile t, read by the lanes that supply those rows
-      bf16x8 va[2], vz = bf16x8{};
+    // Operands of one k-block (16 tokens): the value side (shared by the wave's
+    // tiles; the denominator row 64 goes to A row t for tile t) and the two fp32
+    // feature rows of each tile's slot. The block kk + 1 is read from LDS before
+    // block kk is computed, so that the read latency overlaps the products.
+    struct KOps {
+      bf16x8 va[2], vz;
+      float4 a0[TPW], a1[TPW], c0[TPW], c1[TPW];
+    };
+    auto read_ops = [&](int kk, KOps& o) {
 #pragma unroll
       for (int n = 0; n < 2; ++n)
-        va[n] = *reinterpret_cast<const bf16x8*>(vs + (32 * n + row) * kVRow + 16 * kk + 8 * s);
-      if (row < TPW) vz = *reinterpret_cast<const bf16x8*>(vs + zrow + 16 * kk + 8 * s);
+        o.va[n] = *reinterpret_cast<const bf16x8*>(vs + (32 * n + row) * kVRow + 16 * kk + 8 * s);
+      o.vz = *reinterpret_cast<const bf16x8*>(vs + zrow + 16 * kk + 8 * s);
 #pragma unroll
       for (int t = 0; t < TPW; ++t) {
         const float4* pa = reinterpret_cast<const float4*>(fs + ar[t] * kFRow + 16 * kk + 8 * s);
         const float4* pc = reinterpret_cast<const float4*>(fs + ac[t] * kFRow + 16 * kk + 8 * s);
-        const float4 a0 = pa[0], a1 = pa[1], c0v = pc[0], c1v = pc[1];
+        o.a0[t] = pa[0];
+        o.a1[t] = pa[1];
+        o.c0[t] = pc[0];
+        o.c1[t] = pc[1];
+      }
+    };
+    auto compute = [&](const KOps& o) {
+#pragma unroll
+      for (int t = 0; t < TPW; ++t) {
+        const float4 a0 = o.a0[t], a1 = o.a1[t], c0v = o.c0[t], c1v = o.c1[t];
         float f[8] = {a0.x * c0v.x, a0.y * c0v.y, a0.z * c0v.z, a0.w * c0v.w,
                       a1.x * c1v.x, a1.y * c1v.y, a1.z * c1v.z, a1.w * c1v.w};
         if constexpr (!FWD && !SPLIT) {
@@ -325,17 +338,24 @@ __global__ __launch_bounds__(64 * NW, NW / 2) void k2_scan(const uint16_t* __res
           for (int j = 0; j < 8; ++j) f[j] *= w[t];
         }
         const bf16x8 bq = pack8(f);
-        const bf16x8 vzt = row == t ? vz : bf16x8{};
+        const bf16x8 vzt = row == t ? o.vz : bf16x8{};
         if constexpr (SPLIT) {
-          hT[0] = mfma32(va[0], bq, hT[0]);
-          hT[1] = mfma32(va[1], bq, hT[1]);
+          hT[0] = mfma32(o.va[0], bq, hT[0]);
+          hT[1] = mfma32(o.va[1], bq, hT[1]);
           hT[2] = mfma32(vzt, bq, hT[2]);
         } else {
-          acc[t][0] = mfma32(va[0], bq, acc[t][0]);
-          acc[t][1] = mfma32(va[1], bq, acc[t][1]);
+          acc[t][0] = mfma32(o.va[0], bq, acc[t][0]);
+          acc[t][1] = mfma32(o.va[1], bq, acc[t][1]);
           accz = mfma32(vzt, bq, accz);
         }
       }
+    };
+    KOps ops[2];
+    read_ops(0, ops[0]);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      if (kk + 1 < 4) read_ops(kk + 1, ops[(kk + 1) & 1]);
+      compute(ops[kk & 1]);
     }
     if constexpr (SPLIT) {
       const float wt = w[0];
