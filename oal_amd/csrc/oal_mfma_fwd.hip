@@ -150,19 +150,27 @@ __device__ __forceinline__ void ring_issue(const uint16_t* pt, const LdsRing<kNS
   }
 }
 
+// Operands of k-step T: this lane group's 8 slot weights and the two P^T
+// fragments (value halves) of the staged tile.
+struct ReadoutOps {
+  float4 w0, w1;
+  bf16x8 b0, b1;
+};
 template <int T>
-__device__ __forceinline__ void readout_step(const float (&x)[kD], const float* wl, const LdsRing<kNSR>& ring, int lane,
-                                             f32x16 (&acc)[2]) {
+__device__ __forceinline__ void readout_read(const float* wl, const LdsRing<kNSR>& ring, int lane, ReadoutOps& o) {
   const int s = lane >> 5, row = lane & 31;
-  const float4 w0 = *reinterpret_cast<const float4*>(wl + 16 * T + 8 * s);
-  const float4 w1 = *reinterpret_cast<const float4*>(wl + 16 * T + 8 * s + 4);
-  const float w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+  o.w0 = *reinterpret_cast<const float4*>(wl + 16 * T + 8 * s);
+  o.w1 = *reinterpret_cast<const float4*>(wl + 16 * T + 8 * s + 4);
   const __bf16* tile = ring.st[(T / kRG) % kNSR] + (T % kRG) * kRingStep;
-  const bf16x8 b0 = *reinterpret_cast<const bf16x8*>(tile + row * 16 + 8 * s);
-  const bf16x8 b1 = *reinterpret_cast<const bf16x8*>(tile + (32 + row) * 16 + 8 * s);
+  o.b0 = *reinterpret_cast<const bf16x8*>(tile + row * 16 + 8 * s);
+  o.b1 = *reinterpret_cast<const bf16x8*>(tile + (32 + row) * 16 + 8 * s);
+}
+template <int T>
+__device__ __forceinline__ void readout_step(const float (&x)[kD], const ReadoutOps& o, f32x16 (&acc)[2]) {
+  const float w[8] = {o.w0.x, o.w0.y, o.w0.z, o.w0.w, o.w1.x, o.w1.y, o.w1.z, o.w1.w};
   const bf16x8 a = feature_fragment<T>(x, w);
-  acc[0] = mfma32(a, b0, acc[0]);
-  acc[1] = mfma32(a, b1, acc[1]);
+  acc[0] = mfma32(a, o.b0, acc[0]);
+  acc[1] = mfma32(a, o.b1, acc[1]);
 }
 
 // Copies one thread issues for ring group G.
@@ -183,9 +191,17 @@ __device__ __forceinline__ void readout_group(const float (&x)[kD], const float*
                                               const uint16_t* pt, int tid, int lane, f32x16 (&acc)[2]) {
   ring_sync<copies_in_flight<G>(std::make_integer_sequence<int, kNSR - 2>{})>();
   if constexpr (G + kNSR - 1 < kRingGroups) ring_issue<G + kNSR - 1>(pt, ring, tid);
+  // the operands of k-step i + 1 are read before k-step i is computed
+  constexpr int n = (G + 1) * kRG <= kKS ? kRG : kKS - G * kRG;
+  ReadoutOps o[2];
+  readout_read<G * kRG>(wl, ring, lane, o[0]);
   [&]<int... I>(std::integer_sequence<int, I...>) {
-    ((G * kRG + I < kKS ? readout_step<(G * kRG + I < kKS ? G * kRG + I : 0)>(x, wl, ring, lane, acc) : void()), ...);
-  }(std::make_integer_sequence<int, kRG>{});
+    (([&] {
+       if constexpr (I + 1 < n) readout_read<G * kRG + I + 1>(wl, ring, lane, o[(I + 1) & 1]);
+       readout_step<G * kRG + I>(x, o[I & 1], acc);
+     }()),
+     ...);
+  }(std::make_integer_sequence<int, n>{});
   if constexpr (G + 1 < kRingGroups) readout_group<G + 1>(x, wl, ring, pt, tid, lane, acc);
 }
 
