@@ -222,12 +222,9 @@ __device__ __forceinline__ const __bf16* ring_unit(const LdsRing<4>& ring) {
   return ring.st[(U / kFG) % kNS] + (U % kFG) * 1024;
 }
 
-// Fold of one 32-slot M-tile (rows permuted so that the rows a lane holds are
-// slots of its rotation group): dx[rb] += d x[cb], dx[cb] += d x[rb].
+// Slot weights of M-tile M for this lane's rows (16 values), from LDS.
 template <int M, bool WEIGHTED>
-__device__ __forceinline__ void fold_tile(const f32x16& D, const float (&x)[kD], float (&dx)[kD], const float* wl,
-                                          int s) {
-  float w16[16];
+__device__ __forceinline__ void fold_weights(const float* wl, int s, float (&w16)[16]) {
 #pragma unroll
   for (int a = 0; a < 4; ++a) {
     if constexpr (WEIGHTED) {
@@ -240,6 +237,13 @@ __device__ __forceinline__ void fold_tile(const f32x16& D, const float (&x)[kD],
       w16[4 * a + 0] = w16[4 * a + 1] = w16[4 * a + 2] = w16[4 * a + 3] = 1.f;
     }
   }
+}
+
+// Fold of one 32-slot M-tile (rows permuted so that the rows a lane holds are
+// slots of its rotation group): dx[rb] += d x[cb], dx[cb] += d x[rb].
+template <int M>
+__device__ __forceinline__ void fold_tile(const f32x16& D, const float (&x)[kD], float (&dx)[kD],
+                                          const float (&w16)[16]) {
   [&]<int... I>(std::integer_sequence<int, I...>) {
     (([&] {
        constexpr int a = I / 4, v = I % 4;
@@ -287,14 +291,15 @@ __device__ __forceinline__ f32x16 fold_mfma(const bf16x8 (&bfr)[4], const __bf16
 }
 
 // Ring pipeline over the 69 M-tiles with NS LDS stages. Group G enters with
-// the product of tile G in flight (Dc); it waits for tile G + 1, refills the
-// stage of tile G (whose reads ended before the barrier) with tile G + NS,
-// issues the product of tile G + 1, then folds tile G, so the fold's VALU work
-// overlaps the next tile's matrix products. Up to NS - 2 tiles stay in flight.
+// the product of tile G in flight (Dc) and its weights read (wc); it waits for
+// tile G + 1, refills the stage of tile G (whose reads ended before the
+// barrier) with tile G + NS, issues the product of tile G + 1 and reads its
+// weights, then folds tile G, so the fold's VALU work overlaps the next tile's
+// matrix products and LDS reads. Up to NS - 2 tiles stay in flight.
 template <int G, int NS, bool WEIGHTED>
 __device__ __forceinline__ void fold_group(const bf16x8 (&bfr)[4], const float (&x)[kD], float (&dx)[kD],
                                            const float* wl, const LdsRing<NS>& ring, const uint16_t* src, int tid,
-                                           int lane, const f32x16& Dc) {
+                                           int lane, const f32x16& Dc, const float (&wc)[16]) {
   constexpr int NT = kS / 32;  // 69 M-tiles
   if constexpr (G + 1 < NT) {
     constexpr int issued = (G + NS - 1 < NT - 1) ? G + NS - 1 : NT - 1;  // last tile issued so far
@@ -302,10 +307,12 @@ __device__ __forceinline__ void fold_group(const bf16x8 (&bfr)[4], const float (
     ring_sync<2 * (issued - (G + 1))>();
     if constexpr (G + NS < NT) fold_issue(src, G + NS, ring.st[(G + NS) % NS], tid);
     const f32x16 Dn = fold_mfma<G + 1>(bfr, ring.st[(G + 1) % NS], lane);
-    fold_tile<G, WEIGHTED>(Dc, x, dx, wl, lane >> 5);
-    fold_group<G + 1, NS, WEIGHTED>(bfr, x, dx, wl, ring, src, tid, lane, Dn);
+    float wn[16];
+    fold_weights<G + 1, WEIGHTED>(wl, lane >> 5, wn);
+    fold_tile<G>(Dc, x, dx, wc);
+    fold_group<G + 1, NS, WEIGHTED>(bfr, x, dx, wl, ring, src, tid, lane, Dn, wn);
   } else {
-    fold_tile<G, WEIGHTED>(Dc, x, dx, wl, lane >> 5);
+    fold_tile<G>(Dc, x, dx, wc);
   }
 }
 
@@ -320,7 +327,9 @@ __device__ __forceinline__ void fold_all(const bf16x8 (&bfr)[4], const float (&x
   }(std::make_integer_sequence<int, NS>{});
   ring_sync<2 * (NS - 1)>();
   const f32x16 D0 = fold_mfma<0>(bfr, ring.st[0], lane);
-  fold_group<0, NS, WEIGHTED>(bfr, x, dx, wl, ring, src, tid, lane, D0);
+  float w0[16];
+  fold_weights<0, WEIGHTED>(wl, lane >> 5, w0);
+  fold_group<0, NS, WEIGHTED>(bfr, x, dx, wl, ring, src, tid, lane, D0, w0);
 }
 
 // The two rotation groups of a token (lanes l and l + 32) hold its gradient
