@@ -151,8 +151,11 @@ __global__ __launch_bounds__(64 * NW, NW / 2) void k2_scan(const uint16_t* __res
     }
   }
 
+  // it / RI as a multiply-high by ceil(2^32 / RI) (exact for RI in 2..8 and
+  // it < 2^20, far above any item count), instead of a runtime division
+  const uint32_t rmagic = RI > 1 ? 0xFFFFFFFFu / (uint32_t)RI + 1u : 0u;
   auto item_chunk = [&](int it, int& ch, int& hh) {
-    const int ci = it / RI;
+    const int ci = RI > 1 ? (int)__umulhi((uint32_t)it, rmagic) : it;
     hh = it - ci * RI;
     ch = FWD ? c_lo + ci : c_hi - 1 - ci;
   };
@@ -381,9 +384,9 @@ __global__ __launch_bounds__(64 * NW, NW / 2) void k2_scan(const uint16_t* __res
   // order), so the next waits for staging loads do not wait for them.
   auto emit_before = [&](int it) {
     if constexpr (EMIT) {
-      if (it < NI && any_live && it % RI == 0) {
-        int ch, hh;
-        item_chunk(it, ch, hh);
+      int ch, hh;
+      item_chunk(it, ch, hh);
+      if (it < NI && any_live && hh == 0) {
 #pragma unroll
         for (int t = 0; t < TPW; ++t)
           if (live[t]) emit(t, ch);
