@@ -252,7 +252,8 @@ def main() -> int:
     if args.gpus != 1:
         print(
             f"bench.py measures one GPU: the operator shards over independent (batch, kv-head) units "
-            f"with no exchange, so --gpus {args.gpus} is not run here (see DESIGN.md)",
+            f"with no exchange (an all-reduce of the coefficient gradients aside), so --gpus {args.gpus} "
+            "is not run here",
             file=sys.stderr,
         )
         return 2
