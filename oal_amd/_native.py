@@ -215,8 +215,9 @@ def backward(q, k, v, labels, c0, lam, gam, num, den, saved, dout, dnum, dden, *
         if work.numel() < wbytes:
             raise ValueError("workspace is smaller than oal_backward_workspace_bytes")
         dq = torch.empty_like(q) if need_q else None
-        dk = torch.empty_like(k) if need_k else None
-        dv = torch.empty_like(v) if need_v else None
+        # the key-side kernels produce dk and dv together
+        dk = torch.empty_like(k) if need_k or need_v else None
+        dv = torch.empty_like(v) if need_k or need_v else None
         if need_coef:
             dc0 = torch.empty_like(c0)
             dlam = torch.empty_like(lam)
@@ -236,4 +237,4 @@ def backward(q, k, v, labels, c0, lam, gam, num, den, saved, dout, dnum, dden, *
             _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dc0), _ptr(dlam), _ptr(dgam), _ptr(work), _stream(dev),
         )
         _check(rc, lib, "oal_backward")
-    return dq, dk, dv, dc0, dlam, dgam
+    return dq, dk if need_k else None, dv if need_v else None, dc0, dlam, dgam

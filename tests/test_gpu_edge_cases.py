@@ -114,3 +114,33 @@ def test_single_group_and_empty_groups():
     args = [t.to(torch.bfloat16).to(dev) for t in (q, k, v)] + [t.to(dev) for t in (lab, c0, lam, gam)]
     _, num, den = grouped_oal(*args, scale=0.125, floor=0.0, precision="bf16")
     assert rel(num, num_r) <= BF16_TOL and rel(den, den_r) <= BF16_TOL
+
+
+@pytest.mark.parametrize("grads", ["q", "k", "v", "kv", "coef"])
+def test_partial_gradient_requests(grads):
+    """Only some inputs require gradients: the others get None, the requested
+    ones match the run where every input requires one."""
+    from oal_amd.hd_block_gemm_autograd import grouped_oal
+
+    dev = _dev()
+    lab = _labels(14, 8)
+    q, k, v, c0, lam, gam = _case(1, 14, 2, 96, lab, 21)
+
+    def run(req):
+        ins = [t.to(torch.bfloat16).to(dev) for t in (q, k, v)] + [t.to(dev) for t in (c0, lam, gam)]
+        for name, t in zip(("q", "k", "v", "c0", "lam", "gam"), ins):
+            t.requires_grad_(name in req)
+        out, num, den = grouped_oal(ins[0], ins[1], ins[2], lab.to(dev), ins[3], ins[4], ins[5], scale=0.125,
+                                    floor=0.0, precision="bf16")
+        g = torch.randn(out.shape, generator=torch.Generator().manual_seed(3)).to(dev)
+        (out.float() * g).sum().backward()
+        return [t.grad for t in ins]
+
+    full = run({"q", "k", "v", "c0", "lam", "gam"})
+    want = {"q": {"q"}, "k": {"k"}, "v": {"v"}, "kv": {"k", "v"}, "coef": {"c0", "lam", "gam"}}[grads]
+    part = run(want)
+    for name, gf, gp in zip(("q", "k", "v", "c0", "lam", "gam"), full, part):
+        if name in want:
+            assert gp is not None and torch.equal(gp, gf), name
+        else:
+            assert gp is None, name
