@@ -662,9 +662,8 @@ __global__ __launch_bounds__(256) void k2_coef_grad(const float* __restrict__ dw
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
-// Segments of the backward state scan: enough (tile group, unit, segment)
-// blocks to give every SIMD about four waves; one segment when that already
-// holds. OAL_BWD_SEGMENTS overrides (for tuning).
+// Workspace carve-up of the backward; the state scan's segment count comes
+// from scan_plan (oal_mfma_scan.hip), which sizes the segment-totals buffer.
 MfmaWork mfma_work_view(void* base, int B, int Hq, int U, int N, int NB) {
   char* p = static_cast<char*>(base);
   size_t off = 0;

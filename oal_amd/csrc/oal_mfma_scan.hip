@@ -506,7 +506,9 @@ constexpr int scan_nw(bool fwd, int mode) { return 4; }
 ScanPlan scan_plan(int U, int NB, size_t scratch_bytes, bool fwd) {
   // Segment count from a model of block rounds: each kernel runs two blocks
   // per CU, a block's time is proportional to its chunks, and a partial last
-  // round costs a full one; each segment adds a little carry traffic.
+  // round costs a full one; each segment adds a little carry traffic (a replay
+  // block reads the totals of the segments on one side of its own).
+  // OAL_SCAN_SEGMENTS overrides the count (for tuning and tests).
   int cus = 256;
   {
     int dev = 0, n = 0;
