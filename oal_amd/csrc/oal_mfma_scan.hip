@@ -77,6 +77,9 @@ __global__ __launch_bounds__(64 * NW, NW / 2) void k2_scan(const uint16_t* __res
   __shared__ __attribute__((aligned(16))) float Fs[2][kOpRows * kFRow];
   __shared__ __attribute__((aligned(16))) __bf16 Vs[2][kOpRows * kVRow];
   __shared__ float dwl[PARTIALS ? 8 : 1][kSTiles * 32];
+  // backward: the slot weight wq_h of every query head of the unit (up to 8)
+  // for the block's slots, [head][wave][tile][slot row]
+  __shared__ float wsl[FWD ? 1 : 8][kSTiles * TPW * 32];
 
   int u, seg, tgi;
   {
@@ -161,7 +164,6 @@ __global__ __launch_bounds__(64 * NW, NW / 2) void k2_scan(const uint16_t* __res
   };
   struct Stage {
     uint4 f[kFPT], v[kFPT], v2;
-    float w[TPW];
   };
   // thread tid stages 16-byte chunks tid + kNT i (row chunk >> 3, column 8 (chunk & 7))
   auto uoff = [&](int i) { return (size_t)((tid + kNT * i) >> 3) * np + 8 * (tid & 7); };
@@ -182,13 +184,6 @@ __global__ __launch_bounds__(64 * NW, NW / 2) void k2_scan(const uint16_t* __res
       st.v[i] = *reinterpret_cast<const uint4*>(vb + uoff(i));
     }
     st.v2 = *reinterpret_cast<const uint4*>(vb + uv2);
-    if constexpr (!FWD) {
-#pragma unroll
-      for (int t = 0; t < TPW; ++t) {
-        const float wv_ = wqs[(size_t)(kh * R + hh) * kS + slot[t]];
-        st.w[t] = live[t] ? wv_ : 0.f;
-      }
-    }
   };
   auto put = [&](int bi, int idx, const uint4& f) {
     float4* d = reinterpret_cast<float4*>(&Fs[bi][(idx >> 3) * kFRow + 8 * (idx & 7)]);
@@ -204,7 +199,9 @@ __global__ __launch_bounds__(64 * NW, NW / 2) void k2_scan(const uint16_t* __res
       put(bi, idx, st.f[i]);
       *reinterpret_cast<uint4*>(&Vs[bi][(idx >> 3) * kVRow + 8 * (idx & 7)]) = st.v[i];
     }
-    if (tid < 8) *reinterpret_cast<uint4*>(&Vs[bi][kD * kVRow + 8 * tid]) = st.v2;
+    // row 64 from every thread (eight locations, each written with one value):
+    // a store skipped by a whole wave would leave its load pending at the loop head
+    *reinterpret_cast<uint4*>(&Vs[bi][kD * kVRow + 8 * (tid & 7)]) = st.v2;
   };
 
   // Permutation matrices of the T-layout transposition (see emit): for value
@@ -273,30 +270,53 @@ __global__ __launch_bounds__(64 * NW, NW / 2) void k2_scan(const uint16_t* __res
     }
   };
 
+  // Coefficient partials: the P_c rows of this lane's slot (values
+  // e = 32 n + 8 a + 4 s + v) and its denominator entry, for the chunk being
+  // processed (pf, pz) and, still packed, for the next chunk (pfn, pzn): the
+  // next chunk's loads are issued a whole chunk of items before their use.
   float pf[2][16];
   float pz = 0.f;
+  uint2 pfn[2][4];
+  float pzn = 0.f;
+  auto fetch_partial_rows = [&](int ch) {
+    const size_t cb = (size_t)u * NB + ch;
+    const uint16_t* pr = PRin + cb * kChunkElems + (size_t)tile[0] * 4 * 32 * 16;
+#pragma unroll
+    for (int n = 0; n < 2; ++n)
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        const int kk = 2 * n + (a >> 1), pos = 8 * (a & 1) + 4 * s;
+        pfn[n][a] = *reinterpret_cast<const uint2*>(pr + ((size_t)kk * 32 + row) * 16 + pos);
+      }
+    pzn = PZin[cb * kFP + (nat[0] >= 0 ? nat[0] : 0)];
+  };
+  if constexpr (PARTIALS) {
+    if (NI > 0 && any_live) fetch_partial_rows(c_hi - 1);
+  }
   // One item from LDS buffer bi.
-  auto process = [&](int it, int bi, const float (&w)[TPW]) {
+  auto process = [&](int it, int bi) {
     int ch, hh;
     item_chunk(it, ch, hh);
     if (!any_live) return;
+    float w[TPW];
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) w[t] = FWD ? 1.f : wsl[FWD ? 0 : hh][(wv * TPW + t) * 32 + row];
     if (hh == 0) {
       if constexpr (PARTIALS) {
-        // P_c rows of this lane's slot, values e = 32 n + 8 a + 4 s + v
-        const size_t cb = (size_t)u * NB + ch;
-        const uint16_t* pr = PRin + cb * kChunkElems + (size_t)tile[0] * 4 * 32 * 16;
 #pragma unroll
         for (int n = 0; n < 2; ++n)
 #pragma unroll
           for (int a = 0; a < 4; ++a) {
-            const int kk = 2 * n + (a >> 1), pos = 8 * (a & 1) + 4 * s;
-            const uint2 q = *reinterpret_cast<const uint2*>(pr + ((size_t)kk * 32 + row) * 16 + pos);
+            const uint2 q = pfn[n][a];
             pf[n][4 * a] = __uint_as_float(q.x << 16);
             pf[n][4 * a + 1] = __uint_as_float(q.x & 0xffff0000u);
             pf[n][4 * a + 2] = __uint_as_float(q.y << 16);
             pf[n][4 * a + 3] = __uint_as_float(q.y & 0xffff0000u);
           }
-        pz = (s == 0 && nat[0] >= 0) ? PZin[cb * kFP + nat[0]] : 0.f;
+        pz = (s == 0 && nat[0] >= 0) ? pzn : 0.f;
+        // the backward runs chunks in descending order; the segment's first
+        // chunk refetches itself (an in-range address, never used)
+        fetch_partial_rows(ch > c_lo ? ch - 1 : ch);
       }
     }
     const float* fs = Fs[bi];
@@ -367,11 +387,13 @@ __global__ __launch_bounds__(64 * NW, NW / 2) void k2_scan(const uint16_t* __res
 #pragma unroll
         for (int i = 0; i < 16; ++i) acc[0][n][i] = fmaf(wt, hT[n][i], acc[0][n][i]);
       accz[0] = fmaf(wt, hT[2][0], accz[0]);
-      float d = pz * hT[2][0];
+      // four independent partial sums (a fixed order), not one 33-long chain
+      float dp[4] = {pz * hT[2][0], 0.f, 0.f, 0.f};
 #pragma unroll
       for (int n = 0; n < 2; ++n)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) d = fmaf(pf[n][i], hT[n][i], d);
+        for (int i = 0; i < 16; ++i) dp[i & 3] = fmaf(pf[n][i], hT[n][i], dp[i & 3]);
+      const float d = (dp[0] + dp[1]) + (dp[2] + dp[3]);
       // both lane groups hold value rows of the same slot
       const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(d), __float_as_uint(d), false, false);
       if (s == 0) dwl[hh][wv * 32 + row] += d + __uint_as_float(r[1]);
@@ -396,10 +418,20 @@ __global__ __launch_bounds__(64 * NW, NW / 2) void k2_scan(const uint16_t* __res
 
   // Pipeline: items it and it + 1 alternate between the register stages sa and
   // sb; the loads of item it + 2 are issued when item it starts and land in
-  // LDS when item it + 1 ends.
+  // LDS when item it + 1 ends. The stores are unconditional (past the last
+  // item they store the clamped last item into the idle buffer): a skipped
+  // store would leave its registers' loads possibly pending at the loop head,
+  // where the compiler would then wait for every load in flight.
   Stage sa, sb;
-#pragma unroll
-  for (int t = 0; t < TPW; ++t) sa.w[t] = sb.w[t] = 1.f;
+  if constexpr (!FWD) {
+    // weights of dead tiles (slot clamped to 0) multiply products that are
+    // never stored
+    for (int i = tid; i < R * kSTiles * TPW * 32; i += kNT) {
+      const int hh = i / (kSTiles * TPW * 32), j = i % (kSTiles * TPW * 32);
+      const int tl = kSTiles * TPW * tgi + j / 32;
+      wsl[hh][j] = wqs[(size_t)(kh * R + hh) * kS + (tl < kS / 32 ? tl * 32 + j % 32 : 0)];
+    }
+  }
   if (NI > 0) {
     load(sa, 0);
     load(sb, 1);
@@ -410,23 +442,17 @@ __global__ __launch_bounds__(64 * NW, NW / 2) void k2_scan(const uint16_t* __res
   int bi = 0;
   for (int it = 0; it < NI; it += 2) {
     {
-      float w[TPW];
-#pragma unroll
-      for (int t = 0; t < TPW; ++t) w[t] = sa.w[t];
       load(sa, it + 2);
-      process(it, bi, w);
-      if (it + 1 < NI) store(bi ^ 1, sb);
+      process(it, bi);
+      store(bi ^ 1, sb);
       emit_before(it + 1);
       lds_sync();
       bi ^= 1;
     }
     if (it + 1 < NI) {
-      float w[TPW];
-#pragma unroll
-      for (int t = 0; t < TPW; ++t) w[t] = sb.w[t];
       load(sb, it + 3);
-      process(it + 1, bi, w);
-      if (it + 2 < NI) store(bi ^ 1, sa);
+      process(it + 1, bi);
+      store(bi ^ 1, sa);
       emit_before(it + 2);
       lds_sync();
       bi ^= 1;
