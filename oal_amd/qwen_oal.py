@@ -140,17 +140,34 @@ class OALAttention(nn.Module):
         self.register_buffer("dim_groups", seeded_layer_groups(cfg, gen), persistent=True)
         self.register_buffer("factor", seeded_layer_factor(cfg, gen), persistent=True)
         self.kernel_eps = cfg.kernel_eps
+        # "triton": the configured fast precision (the matrix-core kernels by
+        # default); "reference": the fp32 kernels, selected for a quality
+        # evaluation by oal_amd.grouped_sessions.grouped_quadratic_reference_session
+        # (the reference adapter's _grouped_execution, attention/grouped.py:182-258)
+        self._grouped_execution = "triton"
         self._prepared = {}
+
+    def execution_precision(self) -> str:
+        """Planner precision of the current execution mode."""
+        if self._grouped_execution == "triton":
+            return self.cfg.precision
+        if self._grouped_execution == "reference":
+            return "fp32_ieee"
+        from .grouped_sessions import GroupedQuadraticAttentionError
+
+        raise GroupedQuadraticAttentionError(
+            f"grouped quadratic operator layer={self.layer_id}: adapter has an invalid grouped execution mode")
 
     def head_attention(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
         """One grouped call with the layer's live factor, cached per call signature."""
+        precision = self.execution_precision()
         sig = (tuple(q.shape), q.dtype, str(q.device), torch.is_grad_enabled(), q.requires_grad,
-               k.requires_grad, v.requires_grad, self.factor.requires_grad)
+               k.requires_grad, v.requires_grad, self.factor.requires_grad, precision)
         prepared = self._prepared.get(sig)
         if prepared is None:
             prepared = prepare_grouped_hd_block_gemm(
                 q, k, v, self.dim_groups, self.factor, scale=self.cfg.head_dim ** -0.5,
-                kernel_eps=self.kernel_eps, precision=self.cfg.precision,
+                kernel_eps=self.kernel_eps, precision=precision,
             )
             self._prepared[sig] = prepared
         out, _, _ = run_prepared_grouped_hd_block_gemm(prepared, q, k, v, self.factor)
