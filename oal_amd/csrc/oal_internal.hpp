@@ -34,11 +34,13 @@ struct MfmaSaved {
   float* PZm;     // [U][NB][64][64] denominator column as a symmetric pair matrix
   uint16_t* KT16; // [U][64][NB * 64] bf16 k^T (tokens >= N zero)
   uint16_t* VT16; // [U][65][NB * 64] bf16 [v^T; 1 (token < N)]
+  uint16_t* KAP;  // [B][Hq][NB][3][64][16] bf16 intra-chunk kappa, k2_local_dv's operand fragments
   size_t bytes;
 };
 
-size_t mfma_saved_bytes(int Hq, int U, int NB);
-MfmaSaved mfma_saved_view(void* base, int Hq, int U, int NB);
+// R = query heads per KV head (B * Hq = U * R)
+size_t mfma_saved_bytes(int Hq, int U, int NB, int R);
+MfmaSaved mfma_saved_view(void* base, int Hq, int U, int NB, int R);
 
 template <typename T>
 void launch_mfma_forward(const LaunchGeom& g, const void* q, const void* k, const void* v, const int32_t* labels,
@@ -78,6 +80,7 @@ struct LocalBwdArgs {
   const uint16_t* QT16;
   const uint16_t* GT16;
   const uint16_t* KT16;
+  const uint16_t* KAP;
   const float* PZ;
   const float* PZm;
   const int32_t* labels;

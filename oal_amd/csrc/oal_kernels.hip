@@ -844,7 +844,7 @@ size_t oal_forward_saved_bytes(int batch, int q_heads, int kv_heads, int seq_len
                                int precision) {
   Geometry g;
   if (check_geometry(batch, q_heads, kv_heads, seq_len, dtype, &g) || check_common(groups, precision)) return 0;
-  if (use_mfma(precision, groups, g)) return oal::mfma_saved_bytes(g.Hq, g.U, g.NB);
+  if (use_mfma(precision, groups, g)) return oal::mfma_saved_bytes(g.Hq, g.U, g.NB, g.R);
   return saved_bytes(g);
 }
 

@@ -706,7 +706,7 @@ int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, cons
   if ((dk != nullptr) != (dv != nullptr)) return 2;
   const bool need_coef = dc0 || dlam || dgam;
   if (need_coef && !(dc0 && dlam && dgam)) return 3;
-  MfmaSaved sv = mfma_saved_view(const_cast<void*>(saved), g.Hq, g.U, g.NB);
+  MfmaSaved sv = mfma_saved_view(const_cast<void*>(saved), g.Hq, g.U, g.NB, g.R);
   MfmaWork w = mfma_work_view(workspace, g.B, g.Hq, g.U, g.N, g.NB);
   const T* qt = static_cast<const T*>(q);
   const T* kt = static_cast<const T*>(k);
@@ -722,7 +722,7 @@ int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, cons
     launch_scan<false>(plan, a, st, timed);
   }
   {
-    LocalBwdArgs la{w.G16, w.Gz, w.QT16, w.GT16, sv.KT16, sv.PZ, sv.PZm, labels, lam, gam, sv.ic, sv.gm, sv.lb,
+    LocalBwdArgs la{w.G16, w.Gz, w.QT16, w.GT16, sv.KT16, sv.KAP, sv.PZ, sv.PZm, labels, lam, gam, sv.ic, sv.gm, sv.lb,
                     groups, scale, w.dqf, w.dkl, w.dvl, need_coef ? w.coefl : nullptr};
     launch_local_bwd<T>(g, qt, kt, vt, la, dq != nullptr, dk != nullptr, st, timed);
   }

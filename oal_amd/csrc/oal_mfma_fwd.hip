@@ -14,6 +14,8 @@
 //   PT [u][c][kKS][64 e][16]        bf16  (readout B operand: slots contiguous)
 //   PR [u][c][kS/32][4][32][16 e]   bf16  (backward A operand: values contiguous)
 //   PZ [u][c][kFP]                  f32   (denominator column, natural order)
+//   KAP [b][h][c][3][64][16]        bf16  (intra-chunk kappa of the 3 lower 32x32 tile
+//                                          pairs as the backward dv product's A fragments)
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -233,7 +235,8 @@ __device__ __forceinline__ void load16(const float* __restrict__ src, size_t off
 // num^T = V^T kappa^T with kappa^T handed to the MFMA straight from the
 // accumulators, and the denominator row sums. Wave 3 evaluates the state part
 // of the denominator as the quadratic form az + q . (bz + Mz q), Mz = gm o PZm.
-// Writes the intra part of num and the full den; k2_out_fwd adds the readout.
+// Writes the intra part of num and the full den (k2_out_fwd adds the readout),
+// and saves the bf16 kappa tiles for the backward (KAP).
 // ---------------------------------------------------------------------------
 template <typename T>
 __global__ __launch_bounds__(256) void k2_intra_fwd(const T* __restrict__ q, const T* __restrict__ k,
@@ -241,7 +244,8 @@ __global__ __launch_bounds__(256) void k2_intra_fwd(const T* __restrict__ q, con
                                                     const float* __restrict__ PZm, const int32_t* __restrict__ labels,
                                                     const float* __restrict__ ic, const float* __restrict__ gm,
                                                     const float* __restrict__ lb, int G, int Hq, int Hkv, int N,
-                                                    int NB, float* __restrict__ num, float* __restrict__ den) {
+                                                    int NB, float* __restrict__ num, float* __restrict__ den,
+                                                    uint16_t* __restrict__ kapf) {
   constexpr int LD = kD + 8;  // bf16 row stride (bank spread)
   __shared__ __attribute__((aligned(16))) __bf16 Qs[kC][LD];
   __shared__ __attribute__((aligned(16))) __bf16 Ks[kC][LD];
@@ -250,6 +254,7 @@ __global__ __launch_bounds__(256) void k2_intra_fwd(const T* __restrict__ q, con
   __shared__ __attribute__((aligned(16))) uint32_t mk[4][8][2][4];
   __shared__ float red[2][16][64];
   __shared__ float bz[kD], dsS[kC], dp2[32];
+  __shared__ __attribute__((aligned(16))) __bf16 kapT[3][32][40];  // kappa^T tiles [j][i], bf16
 
   int hh, ch, u;
   head_chunk_unit(Hq / Hkv, NB, (int)(gridDim.x / ((Hq / Hkv) * NB)), hh, ch, u);
@@ -346,6 +351,7 @@ __global__ __launch_bounds__(256) void k2_intra_fwd(const T* __restrict__ q, con
       }
       kap[r] = (j <= i && irow) ? kv : 0.f;
       dsum += kap[r];
+      kapT[wv][c32_row(r, l)][row] = (__bf16)kap[r];
     }
     dsum += __shfl_xor(dsum, 32, 64);
     // kappa^T as the B operand of num^T = V^T kappa^T: k-step t covers
@@ -402,6 +408,16 @@ __global__ __launch_bounds__(256) void k2_intra_fwd(const T* __restrict__ q, con
     }
   }
   __syncthreads();
+  if (wv < 3) {
+    // kappa for the backward's dv = kappa^T G (k2_local_dv): lane (key row j,
+    // group s) holds kappa[i][j] for query rows i = 16 t + 8 s .. + 7, t = 0, 1
+    // (the K-major A fragments of that product), read back transposed
+    const bf16x8 f0 = *reinterpret_cast<const bf16x8*>(&kapT[wv][row][8 * s]);
+    const bf16x8 f1 = *reinterpret_cast<const bf16x8*>(&kapT[wv][row][16 + 8 * s]);
+    uint16_t* dst = kapf + ((((size_t)(b * Hq + h) * NB + ch) * 3 + wv) * 64 + l) * 16;
+    *reinterpret_cast<bf16x8*>(dst) = f0;
+    *reinterpret_cast<bf16x8*>(dst + 8) = f1;
+  }
   if (wv < 2) {
     const int i = 32 * wv + row, tok = tok0 + i;
     if (wv == 1) {
@@ -556,7 +572,7 @@ __global__ __launch_bounds__(64) void k2_selftest(int* __restrict__ errors) {
 // ---------------------------------------------------------------------------
 // Host launchers
 // ---------------------------------------------------------------------------
-MfmaSaved mfma_saved_view(void* base, int Hq, int U, int NB) {
+MfmaSaved mfma_saved_view(void* base, int Hq, int U, int NB, int R) {
   char* p = static_cast<char*>(base);
   size_t off = 0;
   auto take = [&](size_t bytes) {
@@ -577,17 +593,18 @@ MfmaSaved mfma_saved_view(void* base, int Hq, int U, int NB) {
   v.PZm = static_cast<float*>(take(sizeof(float) * units * kD * kD));
   v.KT16 = static_cast<uint16_t*>(take(sizeof(uint16_t) * units * kD * kC));
   v.VT16 = static_cast<uint16_t*>(take(sizeof(uint16_t) * units * (kD + 1) * kC));
+  v.KAP = static_cast<uint16_t*>(take(sizeof(uint16_t) * units * R * 3 * 64 * 16));
   v.bytes = off;
   return v;
 }
 
-size_t mfma_saved_bytes(int Hq, int U, int NB) { return mfma_saved_view(nullptr, Hq, U, NB).bytes; }
+size_t mfma_saved_bytes(int Hq, int U, int NB, int R) { return mfma_saved_view(nullptr, Hq, U, NB, R).bytes; }
 
 template <typename T>
 void launch_mfma_forward(const LaunchGeom& g, const void* q, const void* k, const void* v, const int32_t* labels,
                          const float* c0, const float* lam, const float* gam, int groups, float scale, float floor,
                          void* out, float* num, float* den, void* saved, hipStream_t st, const Timer& timed) {
-  MfmaSaved sv = mfma_saved_view(saved, g.Hq, g.U, g.NB);
+  MfmaSaved sv = mfma_saved_view(saved, g.Hq, g.U, g.NB, g.R);
   const T* qt = static_cast<const T*>(q);
   const T* kt = static_cast<const T*>(k);
   const T* vt = static_cast<const T*>(v);
@@ -606,7 +623,7 @@ void launch_mfma_forward(const LaunchGeom& g, const void* q, const void* k, cons
   }
   timed("k2_intra_fwd", st, [&] {
     hipLaunchKernelGGL(k2_intra_fwd<T>, dim3(g.R * g.NB * g.U), dim3(256), 0, st, qt, kt, vt, sv.PZ, sv.PZm, labels,
-                       sv.ic, sv.gm, sv.lb, groups, g.Hq, g.Hkv, g.N, g.NB, num, den);
+                       sv.ic, sv.gm, sv.lb, groups, g.Hq, g.Hkv, g.N, g.NB, num, den, sv.KAP);
   });
   timed("k2_out_fwd", st, [&] {
     hipLaunchKernelGGL(k2_out_fwd<T>, dim3(g.R * g.NB * g.U), dim3(128), 0, st, qt, sv.wqs, sv.PT, g.Hq, g.Hkv, g.N,

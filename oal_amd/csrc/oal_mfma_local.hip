@@ -18,8 +18,8 @@
 //                part of the denominator's dq (gz_i (bz + 2 Mz q_i)).
 // k2_local_dk    one block per (unit, chunk): dk local part summed over the
 //                unit's query heads in registers (group sums one at a time).
-// k2_local_dv    one block per (unit, chunk): kappa and the dv local part,
-//                summed over the unit's query heads.
+// k2_local_dv    one block per (unit, chunk): the dv local part from the
+//                forward's saved kappa, summed over the unit's query heads.
 // k2_local_coef  one block per (query head, chunk): the per-(head, chunk)
 //                coefficient partials.
 
@@ -382,14 +382,13 @@ __global__ __launch_bounds__(192) void k2_local_dk(const T* __restrict__ q, cons
   local_write(red, acc, t, l, row, tok0, N, kbase, dkl);
 }
 
-// kappa[i][j] (quadratic form in the group sums), dv[j][e] += sum_i kappa g_i[e],
-// summed over the unit's query heads in registers.
-template <typename T>
-__global__ __launch_bounds__(192, 2) void k2_local_dv(const T* __restrict__ q, const T* __restrict__ k,
-                                                   const uint16_t* __restrict__ GT16, const int32_t* __restrict__ labels,
-                                                   const float* __restrict__ ic, int G, int Hq, int Hkv, int N, int NB,
+// dv[j][e] += sum_i kappa[i][j] g_i[e], summed over the unit's query heads in
+// registers. kappa comes from the forward (k2_intra_fwd saves each tile pair's
+// bf16 kappa as this product's K-major A fragments, 32 bytes per lane), so a
+// head costs two fragment loads, four G^T loads and four matrix products.
+__global__ __launch_bounds__(192, 2) void k2_local_dv(const uint16_t* __restrict__ kapf,
+                                                   const uint16_t* __restrict__ GT16, int Hq, int Hkv, int N, int NB,
                                                    float* __restrict__ dvl) {
-  __shared__ __attribute__((aligned(16))) uint32_t mk[2][4][8][2][4];
   __shared__ float red[2][16][64];
   int ch;
   const int u = unit_chunk_block(NB, ch);
@@ -399,50 +398,18 @@ __global__ __launch_bounds__(192, 2) void k2_local_dv(const T* __restrict__ q, c
   const size_t kbase = (size_t)u * N * kD;
   const size_t np = (size_t)NB * kC;
   const LocalTile t = local_tile(wv, tok0, N, row);
-  bf16x8 kf[4];
-#pragma unroll
-  for (int kk = 0; kk < 4; ++kk) kf[kk] = row8(k + kbase + t.jo + 16 * kk + 8 * s, t.jok);
   f32x16 acc[2] = {f32x16{}, f32x16{}};
-
-  build_masks(mk[0], labels, kh * R, G, tid);
-  __syncthreads();
+#pragma unroll 2
   for (int hh = 0; hh < R; ++hh) {
-    const int h = kh * R + hh, mb = hh & 1;
-    if (hh + 1 < R) build_masks(mk[mb ^ 1], labels, h + 1, G, tid);
-    const size_t qbase = (size_t)(b * Hq + h) * N * kD;
-    f32x16 sg[8];
-#pragma unroll
-    for (int g = 0; g < 8; ++g) sg[g] = f32x16{};
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      const bf16x8 qf = row8(q + qbase + t.io + 16 * kk + 8 * s, t.iok);
-#pragma unroll
-      for (int g = 0; g < 8; ++g) sg[g] = mfma32(masked(qf, &mk[mb][kk][g][s][0]), kf[kk], sg[g]);
-    }
-    const float* cf = ic + (size_t)h * kIC;
-    const float c0h = cf[0];
-    float kap[16];
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int i = 32 * t.it + c32_row(r, l);
-      float kv = c0h;
-#pragma unroll
-      for (int g = 0; g < 8; ++g) {
-        float inner = fmaf(cf[kIcGam + 9 * g], sg[g][r], cf[kIcLam + g]);
-#pragma unroll
-        for (int h2 = g + 1; h2 < 8; ++h2) inner = fmaf(2.f * cf[kIcGam + 8 * g + h2], sg[h2][r], inner);
-        kv = fmaf(sg[g][r], inner, kv);
-      }
-      kap[r] = (t.j <= i && tok0 + i < N) ? kv : 0.f;
-    }
-    const bf16x8 f0 = acc_kfrag(kap, 0, s), f1 = acc_kfrag(kap, 1, s);
+    const int h = kh * R + hh;
+    const uint16_t* kp = kapf + ((((size_t)(b * Hq + h) * NB + ch) * 3 + wv) * 64 + l) * 16;
+    const bf16x8 f0 = *reinterpret_cast<const bf16x8*>(kp), f1 = *reinterpret_cast<const bf16x8*>(kp + 8);
 #pragma unroll
     for (int et = 0; et < 2; ++et) {
       const uint16_t* gt = GT16 + ((size_t)(b * Hq + h) * (kD + 2) + 32 * et + row) * np + tok0 + 32 * t.it + 8 * s;
       acc[et] = mfma32(f0, *reinterpret_cast<const bf16x8*>(gt), acc[et]);
       acc[et] = mfma32(f1, *reinterpret_cast<const bf16x8*>(gt + 16), acc[et]);
     }
-    __syncthreads();
   }
   local_write(red, acc, t, l, row, tok0, N, kbase, dvl);
 }
@@ -557,8 +524,8 @@ void launch_local_bwd(const LaunchGeom& g, const T* q, const T* k, const T* v, c
   }
   if (need_dkv) {
     timed("k2_local_dv", st, [&] {
-      hipLaunchKernelGGL(k2_local_dv<T>, dim3(g.NB * g.U), dim3(192), 0, st, q, k, a.GT16, a.labels, a.ic, a.groups,
-                         g.Hq, g.Hkv, g.N, g.NB, a.dvl);
+      hipLaunchKernelGGL(k2_local_dv, dim3(g.NB * g.U), dim3(192), 0, st, a.KAP, a.GT16, g.Hq, g.Hkv, g.N, g.NB,
+                         a.dvl);
     });
   }
   if (a.coefl) {
