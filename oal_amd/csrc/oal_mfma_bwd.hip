@@ -3,7 +3,7 @@
 // k2_bwd_prep   normalization VJP: G (bf16 token rows and transposed), Gz; transposed q.
 // (the reverse chunk scan dT_c = sum_{c' > c} dCarry_c' and the per-slot
 // coefficient partials are in oal_mfma_scan.hip)
-// (the intra-chunk VJP, k2_local_dq / k2_local_dkv, is in oal_mfma_local.hip)
+// (the intra-chunk VJP, k2_local_dq / k2_local_dk / k2_local_dv, is in oal_mfma_local.hip)
 // k2_q_fold     dq state part: D^T = P G^T on the MFMA, folded through the query
 //               features (rotated rows, static register indices) + local dq.
 // k2_kv_fold    dk state part (D^T = dT V^T folded through the key features),

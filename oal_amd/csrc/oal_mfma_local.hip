@@ -20,8 +20,8 @@
 //                unit's query heads in registers (group sums one at a time).
 // k2_local_dv    one block per (unit, chunk): the dv local part from the
 //                forward's saved kappa, summed over the unit's query heads.
-// k2_local_coef  one block per (query head, chunk): the per-(head, chunk)
-//                coefficient partials.
+//                With the coefficient gradients requested it also writes the
+//                per-(head, chunk) coefficient partials from the same group sums.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -94,21 +94,30 @@ __device__ __forceinline__ int tile_it(int tp) { return tp == 0 ? 0 : 1; }
 //   dq[i][d] = sum_h coef_h(d) sum_j X_h[i][j] K[j][d], X_h = ds o s_h, X_8 = ds
 // with s_h computed one group at a time; waves 0 and 1 (query tiles 0, 1) add
 // gz_i (bz_d + 2 (Mz q_i)_d), Mz = gm o PZm, and write dqf.
+// COEF: the eight group sums are kept (two waves per SIMD instead of three),
+// the block also writes the coefficient partials from them (with ds[i][j] =
+// g_i . v_j + gz_i on live entries: [0] sum ds, [1 + g] sum ds s_g,
+// [9 + 8 g + h] sum ds s_g s_h in the full symmetric 8 x 8 layout, each a
+// fixed-order sum over the block's 192 lanes), and the dq products take s_h
+// from those registers.
 // ---------------------------------------------------------------------------
-template <typename T>
-__global__ __launch_bounds__(192, 3) void k2_local_dq(const T* __restrict__ q, const T* __restrict__ k,
+template <typename T, bool COEF>
+__global__ __launch_bounds__(192, COEF ? 2 : 3) void k2_local_dq(const T* __restrict__ q, const T* __restrict__ k,
                                                    const T* __restrict__ v, const uint16_t* __restrict__ G16,
                                                    const float* __restrict__ Gz, const uint16_t* __restrict__ KT16,
                                                    const float* __restrict__ PZ, const float* __restrict__ PZm,
                                                    const int32_t* __restrict__ labels, const float* __restrict__ lam,
                                                    const float* __restrict__ gam, const float* __restrict__ gm,
                                                    const float* __restrict__ lb, int G, int Hq, int Hkv, int N,
-                                                   int NB, float scale, float* __restrict__ dqf) {
+                                                   int NB, float scale, float* __restrict__ dqf,
+                                                   float* __restrict__ coefl) {
   constexpr int LD = kD + 8;
   __shared__ __attribute__((aligned(16))) uint32_t mk[4][8][2][4];
   __shared__ __attribute__((aligned(16))) __bf16 Mz[kD][LD];
   __shared__ float bz[kD];
   __shared__ float red[2][16][64];  // wave 2's dq (query tile 1)
+  __shared__ float cp[COEF ? 3 * 64 : 1][45];  // per-lane coefficient partials
+  __shared__ float cred[COEF ? 4 * 45 : 1];
 
   int hh, ch, u;
   head_chunk_unit(Hq / Hkv, NB, (int)(gridDim.x / ((Hq / Hkv) * NB)), hh, ch, u);
@@ -160,6 +169,42 @@ __global__ __launch_bounds__(192, 3) void k2_local_dq(const T* __restrict__ q, c
     const int j = 32 * jt + c32_row(r, l);
     dsv[r] = (j <= i && icol) ? ds[r] + gzi : 0.f;
   }
+  f32x16 sgs[COEF ? 8 : 1];
+  if constexpr (COEF) {
+    // all eight group sums, then the partials [0] sum ds, [1 + g] sum ds s_g,
+    // [9 + packed (g <= h)] sum ds s_g s_h over this lane's 16 entries
+#pragma unroll
+    for (int g = 0; g < 8; ++g) sgs[g] = f32x16{};
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+      for (int g = 0; g < 8; ++g) sgs[g] = mfma32(masked(kf[kk], &mk[kk][g][s][0]), qf[kk], sgs[g]);
+    float ca[45];
+#pragma unroll
+    for (int e = 0; e < 45; ++e) ca[e] = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      float sv[8], tv[8];
+#pragma unroll
+      for (int g = 0; g < 8; ++g) {
+        sv[g] = scale * sgs[g][r];
+        tv[g] = dsv[r] * sv[g];
+      }
+      ca[0] += dsv[r];
+      int e = 9;
+#pragma unroll
+      for (int g = 0; g < 8; ++g) {
+        ca[1 + g] += tv[g];
+#pragma unroll
+        for (int h2 = g; h2 < 8; ++h2) {
+          ca[e] = fmaf(tv[g], sv[h2], ca[e]);
+          ++e;
+        }
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 45; ++e) cp[tid][e] = ca[e];
+  }
   bf16x8 kt[2][2];
 #pragma unroll
   for (int dt = 0; dt < 2; ++dt)
@@ -180,9 +225,14 @@ __global__ __launch_bounds__(192, 3) void k2_local_dq(const T* __restrict__ q, c
   for (int h2 = 0; h2 < 9; ++h2) {
     float x[16];
     if (h2 < 8) {
-      f32x16 sh = f32x16{};
+      f32x16 sh;
+      if constexpr (COEF) {
+        sh = sgs[h2];
+      } else {
+        sh = f32x16{};
 #pragma unroll
-      for (int kk = 0; kk < 4; ++kk) sh = mfma32(masked(kf[kk], &mk[kk][h2][s][0]), qf[kk], sh);
+        for (int kk = 0; kk < 4; ++kk) sh = mfma32(masked(kf[kk], &mk[kk][h2][s][0]), qf[kk], sh);
+      }
 #pragma unroll
       for (int r = 0; r < 16; ++r) x[r] = dsv[r] * (scale * sh[r]);
     } else {
@@ -235,6 +285,32 @@ __global__ __launch_bounds__(192, 3) void k2_local_dq(const T* __restrict__ q, c
         const int tok = tok0 + 32 * wv + c32_row(r, l);
         if (tok < N) dqf[qbase + (size_t)tok * kD + 32 * dt + row] = x;
       }
+  }
+  if constexpr (COEF) {
+    // column sums over the 192 lanes (4 interleaved partial sums per column,
+    // then their sum), expanded to the symmetric [1 + 8 + 8 x 8] layout
+    if (tid < 180) {
+      const int e = tid % 45, part = tid / 45;
+      float x = 0.f;
+      for (int r = part; r < 192; r += 4) x += cp[r][e];
+      cred[tid] = x;
+    }
+    __syncthreads();
+    if (tid < 73) {
+      int e = tid;
+      if (tid >= 9) {
+        int g = (tid - 9) >> 3, h2 = (tid - 9) & 7;
+        if (h2 < g) {
+          const int t2 = g;
+          g = h2;
+          h2 = t2;
+        }
+        e = 9 + g * 8 - g * (g - 1) / 2 + (h2 - g);
+      }
+      const size_t bn = (size_t)(gridDim.x / (R * NB) / Hkv) * NB;
+      coefl[((size_t)h * 73 + tid) * bn + (size_t)b * NB + ch] =
+          (cred[e] + cred[45 + e]) + (cred[90 + e] + cred[135 + e]);
+    }
   }
 }
 
@@ -414,106 +490,23 @@ __global__ __launch_bounds__(192, 2) void k2_local_dv(const uint16_t* __restrict
   local_write(red, acc, t, l, row, tok0, N, kbase, dvl);
 }
 
-// Per-(head, chunk) local coefficient partials, one block per (query head,
-// chunk), 3 waves = tile pairs: with ds[i][j] = g_i . v_j + gz_i (j <= i) and
-// s_g the scaled group sums, [0] sum ds, [1 + g] sum ds s_g, [9 + 8 g + h]
-// sum ds s_g s_h (written in the full symmetric 8 x 8 layout), each a fixed-order
-// sum over the block's 192 lanes.
-template <typename T>
-__global__ __launch_bounds__(192, 2) void k2_local_coef(const T* __restrict__ q, const T* __restrict__ k,
-                                                     const T* __restrict__ v, const uint16_t* __restrict__ G16,
-                                                     const float* __restrict__ Gz, const int32_t* __restrict__ labels,
-                                                     int G, int Hq, int Hkv, int N, int NB, float scale,
-                                                     float* __restrict__ coefl) {
-  __shared__ __attribute__((aligned(16))) uint32_t mk[4][8][2][4];
-  __shared__ float cp[3 * 64][45];  // per-lane partials of the 3 tile waves
-  __shared__ float red[4 * 45];
-  int hh, ch, u;
-  head_chunk_unit(Hq / Hkv, NB, (int)(gridDim.x / ((Hq / Hkv) * NB)), hh, ch, u);
-  const int R = Hq / Hkv, b = u / Hkv, kh = u % Hkv, h = kh * R + hh;
-  const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, s = l >> 5, row = l & 31;
-  const int tok0 = ch * kC;
-  const size_t kbase = (size_t)u * N * kD;
-  const size_t qbase = (size_t)(b * Hq + h) * N * kD;
-  const size_t bn = (size_t)(gridDim.x / (R * NB) / Hkv) * NB;
-  const LocalTile t = local_tile(wv, tok0, N, row);
-  build_masks(mk, labels, h, G, tid);
-  __syncthreads();
-  f32x16 sg[8], ds = f32x16{};
-#pragma unroll
-  for (int g = 0; g < 8; ++g) sg[g] = f32x16{};
-#pragma unroll
-  for (int kk = 0; kk < 4; ++kk) {
-    const bf16x8 qf = row8(q + qbase + t.io + 16 * kk + 8 * s, t.iok);
-    const bf16x8 kf = row8(k + kbase + t.jo + 16 * kk + 8 * s, t.jok);
-#pragma unroll
-    for (int g = 0; g < 8; ++g) sg[g] = mfma32(masked(qf, &mk[kk][g][s][0]), kf, sg[g]);
-    ds = mfma32(row8(G16 + qbase + t.io + 16 * kk + 8 * s, t.iok), row8(v + kbase + t.jo + 16 * kk + 8 * s, t.jok),
-                ds);
-  }
-  float ca[45];
-#pragma unroll
-  for (int e = 0; e < 45; ++e) ca[e] = 0.f;
-#pragma unroll
-  for (int a = 0; a < 4; ++a) {
-    const int i0 = 32 * t.it + 8 * a + 4 * s;
-#pragma unroll
-    for (int vv = 0; vv < 4; ++vv) {
-      const int r = 4 * a + vv, i = i0 + vv;
-      const float gzi = tok0 + i < N ? Gz[(size_t)(b * Hq + h) * N + tok0 + i] : 0.f;
-      const float dsv = (t.j <= i && tok0 + i < N) ? ds[r] + gzi : 0.f;
-      float sv[8], tv[8];
-#pragma unroll
-      for (int g = 0; g < 8; ++g) {
-        sv[g] = scale * sg[g][r];
-        tv[g] = dsv * sv[g];
-      }
-      ca[0] += dsv;
-      int e = 9;
-#pragma unroll
-      for (int g = 0; g < 8; ++g) {
-        ca[1 + g] += tv[g];
-#pragma unroll
-        for (int h2 = g; h2 < 8; ++h2) {
-          ca[e] = fmaf(tv[g], sv[h2], ca[e]);
-          ++e;
-        }
-      }
-    }
-  }
-#pragma unroll
-  for (int e = 0; e < 45; ++e) cp[tid][e] = ca[e];
-  __syncthreads();
-  // column sums over the 192 lanes: 4 interleaved partial sums per column, then their sum
-  if (tid < 180) {
-    const int e = tid % 45, part = tid / 45;
-    float x = 0.f;
-    for (int r = part; r < 192; r += 4) x += cp[r][e];
-    red[tid] = x;
-  }
-  __syncthreads();
-  if (tid < 73) {
-    int e = tid;
-    if (tid >= 9) {
-      int g = (tid - 9) >> 3, h2 = (tid - 9) & 7;
-      if (h2 < g) {
-        const int t2 = g;
-        g = h2;
-        h2 = t2;
-      }
-      e = 9 + g * 8 - g * (g - 1) / 2 + (h2 - g);
-    }
-    coefl[((size_t)h * 73 + tid) * bn + (size_t)b * NB + ch] = (red[e] + red[45 + e]) + (red[90 + e] + red[135 + e]);
-  }
-}
-
 template <typename T>
 void launch_local_bwd(const LaunchGeom& g, const T* q, const T* k, const T* v, const LocalBwdArgs& a, bool need_dq,
                       bool need_dkv, hipStream_t st, const Timer& timed) {
-  if (need_dq) {
+  // The coefficient partials come from the dq kernel's group sums, also when
+  // dq itself is not requested (its dq then goes to the workspace unused), so
+  // that every requested gradient is bit-identical whatever else is requested.
+  const bool coef = a.coefl != nullptr;
+  if (need_dq || coef) {
     timed("k2_local_dq", st, [&] {
-      hipLaunchKernelGGL(k2_local_dq<T>, dim3(g.R * g.NB * g.U), dim3(192), 0, st, q, k, v, a.G16, a.Gz, a.KT16, a.PZ,
-                         a.PZm, a.labels, a.lam, a.gam, a.gm, a.lb, a.groups, g.Hq, g.Hkv, g.N, g.NB, a.scale, a.dqf);
+      if (coef)
+        hipLaunchKernelGGL((k2_local_dq<T, true>), dim3(g.R * g.NB * g.U), dim3(192), 0, st, q, k, v, a.G16, a.Gz,
+                           a.KT16, a.PZ, a.PZm, a.labels, a.lam, a.gam, a.gm, a.lb, a.groups, g.Hq, g.Hkv, g.N, g.NB,
+                           a.scale, a.dqf, a.coefl);
+      else
+        hipLaunchKernelGGL((k2_local_dq<T, false>), dim3(g.R * g.NB * g.U), dim3(192), 0, st, q, k, v, a.G16, a.Gz,
+                           a.KT16, a.PZ, a.PZm, a.labels, a.lam, a.gam, a.gm, a.lb, a.groups, g.Hq, g.Hkv, g.N, g.NB,
+                           a.scale, a.dqf, nullptr);
     });
   }
   if (need_dkv) {
@@ -526,12 +519,6 @@ void launch_local_bwd(const LaunchGeom& g, const T* q, const T* k, const T* v, c
     timed("k2_local_dv", st, [&] {
       hipLaunchKernelGGL(k2_local_dv, dim3(g.NB * g.U), dim3(192), 0, st, a.KAP, a.GT16, g.Hq, g.Hkv, g.N, g.NB,
                          a.dvl);
-    });
-  }
-  if (a.coefl) {
-    timed("k2_local_coef", st, [&] {
-      hipLaunchKernelGGL(k2_local_coef<T>, dim3(g.R * g.NB * g.U), dim3(192), 0, st, q, k, v, a.G16, a.Gz, a.labels,
-                         a.groups, g.Hq, g.Hkv, g.N, g.NB, a.scale, a.coefl);
     });
   }
 }
