@@ -62,6 +62,7 @@ struct MfmaWork {
   float* dkl;     // [U][N][64] local dk, summed over the unit's query heads
   float* dvl;     // [U][N][64] local dv, summed over the unit's query heads
   float* coefl;   // [Hq][73][B * NB] local (dc0, dlam[8], dgam[8][8]) per chunk
+  float* coefs;   // [Hq][73] their sums over the chunks
   int S, SL;      // segments of the backward state scan and chunks per segment
   size_t bytes;
 };

@@ -532,10 +532,28 @@ __global__ __launch_bounds__(128, 2) void k2_kv_fold(const T* __restrict__ k, co
   }
 }
 
-// dwq[h][slot] = sum over (segment, batch) of the state-scan partials, fixed order.
+// Grid (slot blocks + 73, Hq). Slot blocks: dwq[h][slot] = sum over (segment,
+// batch) of the state-scan partials. The other 73 blocks of a head: one column
+// of the per-(batch, chunk) local partials each, coefs[h][j] = sum_r
+// coefl[h][j][r]. Every sum in a fixed order.
+constexpr int kDwqSlotBlocks = (kS + 255) / 256;
 __global__ __launch_bounds__(256) void k2_dwq_reduce(const float* __restrict__ dwqs, int rowsets, int Hq,
-                                                     float* __restrict__ dwq) {
-  const int h = blockIdx.y, sl = blockIdx.x * 256 + threadIdx.x;
+                                                     float* __restrict__ dwq, const float* __restrict__ coefl, int bn,
+                                                     float* __restrict__ coefs) {
+  const int h = blockIdx.y;
+  if (blockIdx.x >= kDwqSlotBlocks) {
+    __shared__ float wsum[4];
+    const int j = blockIdx.x - kDwqSlotBlocks;
+    const float* p = coefl + ((size_t)h * 73 + j) * bn;
+    float acc = 0.f;
+    for (int r = threadIdx.x; r < bn; r += 256) acc += p[r];
+    acc = wave_sum(acc);
+    if ((threadIdx.x & 63) == 0) wsum[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) coefs[(size_t)h * 73 + j] = (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
+    return;
+  }
+  const int sl = blockIdx.x * 256 + threadIdx.x;
   if (sl >= kS) return;
   // fixed order; eight loads in flight at a time
   const float* p = dwqs + (size_t)h * kS + sl;
@@ -559,11 +577,12 @@ __global__ __launch_bounds__(256) void k2_dwq_reduce(const float* __restrict__ d
 // natural feature order wn[f]; dc0 = wn[0], dlam[g] = scale sum_{g(d)=g} wn[1+d],
 // and the pair part routes pair (r >= c) to [g(r)][g(c)] through
 // X[r][g] = sum_{c <= r, g(c) = g} m_rc wn[pair(r, c)], raw = E^T X with E the
-// one-hot label matrix. Local part: column sums of the per-chunk partials.
+// one-hot label matrix. Local part: the column sums of the per-chunk partials
+// (coefs, from k2_dwq_reduce).
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k2_coef_grad(const float* __restrict__ dwq, const float* __restrict__ coefl,
-                                                    const int32_t* __restrict__ labels, int Hq, int bn, int G,
-                                                    float scale, float* __restrict__ dc0, float* __restrict__ dlam,
+__global__ __launch_bounds__(256) void k2_coef_grad(const float* __restrict__ dwq, const float* __restrict__ coefs,
+                                                    const int32_t* __restrict__ labels, int Hq, int G, float scale,
+                                                    float* __restrict__ dc0, float* __restrict__ dlam,
                                                     float* __restrict__ dgam) {
   __shared__ float wn[kFeat];
   __shared__ float loc[73];
@@ -571,7 +590,7 @@ __global__ __launch_bounds__(256) void k2_coef_grad(const float* __restrict__ dw
   __shared__ float xq[4][kD][9];
   __shared__ float raw[64];
   __shared__ int lab[kD];
-  const int h = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int h = blockIdx.x, t = threadIdx.x;
   if (t < kD) {
     int g = labels[h * kD + t];
     lab[t] = g < 0 ? 0 : (g >= G ? G - 1 : g);
@@ -580,31 +599,7 @@ __global__ __launch_bounds__(256) void k2_coef_grad(const float* __restrict__ dw
     const int n = kSlot.nat[sl];
     if (n >= 0) wn[n] = dwq[(size_t)h * kS + sl];
   }
-  // column sums of the local partials: each wave owns columns wave, wave + 4, ..;
-  // all of a lane's loads for those columns are issued before the sums
-  {
-    constexpr int kCols = (73 + 3) / 4;
-    float part[kCols];
-#pragma unroll
-    for (int i = 0; i < kCols; ++i) part[i] = 0.f;
-    for (int r0 = 0; r0 < bn; r0 += 64) {
-      const int r = r0 + lane;
-      float v[kCols];
-#pragma unroll
-      for (int i = 0; i < kCols; ++i) {
-        const int j = wave + 4 * i;
-        v[i] = (j < 73 && r < bn) ? coefl[((size_t)h * 73 + j) * bn + r] : 0.f;
-      }
-#pragma unroll
-      for (int i = 0; i < kCols; ++i) part[i] += v[i];
-    }
-#pragma unroll
-    for (int i = 0; i < kCols; ++i) {
-      const int j = wave + 4 * i;
-      const float acc = wave_sum(part[i]);
-      if (lane == 0 && j < 73) loc[j] = acc;
-    }
-  }
+  if (t < 73) loc[t] = coefs[(size_t)h * 73 + t];
   __syncthreads();
   // xr[r][g] = sum_{c <= r, g(c) = g} m_rc wn[pair(r, c)]: thread (r, q) sums the
   // columns c = q mod 4 into eight group bins, then the four quarters are added
@@ -693,6 +688,7 @@ MfmaWork mfma_work_view(void* base, int B, int Hq, int U, int N, int NB) {
   w.dkl = static_cast<float*>(take((size_t)U * N * kD * sizeof(float)));
   w.dvl = static_cast<float*>(take((size_t)U * N * kD * sizeof(float)));
   w.coefl = static_cast<float*>(take(sizeof(float) * (size_t)B * Hq * NB * 73));
+  w.coefs = static_cast<float*>(take(sizeof(float) * (size_t)Hq * 73));
   w.bytes = off;
   return w;
 }
@@ -740,12 +736,12 @@ int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, cons
   }
   if (need_coef) {
     timed("k2_dwq_reduce", st, [&] {
-      hipLaunchKernelGGL(k2_dwq_reduce, dim3((kS + 255) / 256, g.Hq), dim3(256), 0, st, w.dwqs, g.B * w.S, g.Hq,
-                         w.dwq);
+      hipLaunchKernelGGL(k2_dwq_reduce, dim3(kDwqSlotBlocks + 73, g.Hq), dim3(256), 0, st, w.dwqs, g.B * w.S, g.Hq,
+                         w.dwq, w.coefl, g.B * g.NB, w.coefs);
     });
     timed("k2_coef_grad", st, [&] {
-      hipLaunchKernelGGL(k2_coef_grad, dim3(g.Hq), dim3(256), 0, st, w.dwq, w.coefl, labels, g.Hq, g.B * g.NB,
-                         groups, scale, dc0, dlam, dgam);
+      hipLaunchKernelGGL(k2_coef_grad, dim3(g.Hq), dim3(256), 0, st, w.dwq, w.coefs, labels, g.Hq, groups, scale,
+                         dc0, dlam, dgam);
     });
   }
   return 0;
