@@ -91,8 +91,10 @@ __device__ __forceinline__ int tile_it(int tp) { return tp == 0 ? 0 : 1; }
 // dq local part + denominator-state dq, one block per (query head, chunk),
 // grid R * NB * U (XCD-ordered), 3 waves = tile pairs 0..2 (orientation
 // C[j][i] for the group sums; dq accumulators C[i][d], lane = d):
-//   dq[i][d] = sum_h coef_h(d) sum_j X_h[i][j] K[j][d], X_h = ds o s_h, X_8 = ds
-// with s_h computed one group at a time; waves 0 and 1 (query tiles 0, 1) add
+//   dq[i][d] = sum_h coef_h(d) sum_j X_h[i][j] K[j][d], X_h = ds o s'_h, X_8 = ds
+// with s'_h the unscaled group sum (s_h = scale s'_h), computed one group at a
+// time, coef_h(d) = 2 scale^2 Gam[g(d)][h], coef_8(d) = scale lam[g(d)];
+// waves 0 and 1 (query tiles 0, 1) add
 // gz_i (bz_d + 2 (Mz q_i)_d), Mz = gm o PZm, and write dqf.
 // COEF: the eight group sums are kept (two waves per SIMD instead of three),
 // the block also writes the coefficient partials from them (with ds[i][j] =
@@ -187,7 +189,7 @@ __global__ __launch_bounds__(192, COEF ? 2 : 3) void k2_local_dq(const T* __rest
       float sv[8], tv[8];
 #pragma unroll
       for (int g = 0; g < 8; ++g) {
-        sv[g] = scale * sgs[g][r];
+        sv[g] = sgs[g][r];  // unscaled; the sums are scaled once below
         tv[g] = dsv[r] * sv[g];
       }
       ca[0] += dsv[r];
@@ -203,7 +205,7 @@ __global__ __launch_bounds__(192, COEF ? 2 : 3) void k2_local_dq(const T* __rest
       }
     }
 #pragma unroll
-    for (int e = 0; e < 45; ++e) cp[tid][e] = ca[e];
+    for (int e = 0; e < 45; ++e) cp[tid][e] = ca[e] * (e == 0 ? 1.f : e < 9 ? scale : scale * scale);
   }
   bf16x8 kt[2][2];
 #pragma unroll
@@ -217,7 +219,8 @@ __global__ __launch_bounds__(192, COEF ? 2 : 3) void k2_local_dq(const T* __rest
   for (int dt = 0; dt < 2; ++dt) {
     const int gd = clamp_label(labels[h * kD + 32 * dt + row], G);
 #pragma unroll
-    for (int h2 = 0; h2 < 8; ++h2) cf[h2][dt] = h2 < G ? 2.f * scale * gam[((size_t)h * G + gd) * G + h2] : 0.f;
+    for (int h2 = 0; h2 < 8; ++h2)
+      cf[h2][dt] = h2 < G ? 2.f * scale * scale * gam[((size_t)h * G + gd) * G + h2] : 0.f;
     cf[8][dt] = scale * lam[(size_t)h * G + gd];
   }
   f32x16 dq[2] = {f32x16{}, f32x16{}};
@@ -234,7 +237,7 @@ __global__ __launch_bounds__(192, COEF ? 2 : 3) void k2_local_dq(const T* __rest
         for (int kk = 0; kk < 4; ++kk) sh = mfma32(masked(kf[kk], &mk[kk][h2][s][0]), qf[kk], sh);
       }
 #pragma unroll
-      for (int r = 0; r < 16; ++r) x[r] = dsv[r] * (scale * sh[r]);
+      for (int r = 0; r < 16; ++r) x[r] = dsv[r] * sh[r];  // the scale of s_h is in cf
     } else {
 #pragma unroll
       for (int r = 0; r < 16; ++r) x[r] = dsv[r];
@@ -370,8 +373,9 @@ __device__ __forceinline__ void local_write(float (*red)[16][64], const f32x16 (
   }
 }
 
-// dk[j][d] += sum_h coef_h(d) sum_i X_h[i][j] q_i[d], X_h = ds o s_h, X_8 = ds,
-// with s_h computed one group at a time.
+// dk[j][d] += sum_h coef_h(d) sum_i X_h[i][j] q_i[d], X_h = ds o s'_h, X_8 = ds,
+// with s'_h the unscaled group sum computed one group at a time and the
+// coefficients of k2_local_dq (the scale folded into coef_h).
 template <typename T>
 __global__ __launch_bounds__(192) void k2_local_dk(const T* __restrict__ q, const T* __restrict__ k,
                                                    const T* __restrict__ v, const uint16_t* __restrict__ G16,
@@ -426,7 +430,8 @@ __global__ __launch_bounds__(192) void k2_local_dk(const T* __restrict__ q, cons
     for (int dt = 0; dt < 2; ++dt) {
       const int gd = clamp_label(labels[h * kD + 32 * dt + row], G);
 #pragma unroll
-      for (int h2 = 0; h2 < 8; ++h2) cf[h2][dt] = h2 < G ? 2.f * scale * gam[((size_t)h * G + gd) * G + h2] : 0.f;
+      for (int h2 = 0; h2 < 8; ++h2)
+      cf[h2][dt] = h2 < G ? 2.f * scale * scale * gam[((size_t)h * G + gd) * G + h2] : 0.f;
       cf[8][dt] = scale * lam[(size_t)h * G + gd];
     }
 #pragma unroll
@@ -439,7 +444,7 @@ __global__ __launch_bounds__(192) void k2_local_dk(const T* __restrict__ q, cons
           sh = mfma32(masked(row8(q + qbase + t.io + 16 * kk + 8 * s, t.iok), &mk[mb][kk][h2][s][0]),
                       row8(k + kbase + t.jo + 16 * kk + 8 * s, t.jok), sh);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) x[r] = dsv[r] * (scale * sh[r]);
+        for (int r = 0; r < 16; ++r) x[r] = dsv[r] * sh[r];  // the scale of s_h is in cf
       } else {
 #pragma unroll
         for (int r = 0; r < 16; ++r) x[r] = dsv[r];
