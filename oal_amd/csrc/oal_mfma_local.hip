@@ -15,13 +15,13 @@
 // products, whose other operand is the transposed bf16 copy of K, q or G.
 //
 // k2_local_dq    one block per (query head, chunk): dq local part and the state
-//                part of the denominator's dq (gz_i (bz + 2 Mz q_i)).
+//                part of the denominator's dq (gz_i (bz + 2 Mz q_i)). With the
+//                coefficient gradients requested it also writes the per-(head,
+//                chunk) coefficient partials from the same group sums.
 // k2_local_dk    one block per (unit, chunk): dk local part summed over the
 //                unit's query heads in registers (group sums one at a time).
 // k2_local_dv    one block per (unit, chunk): the dv local part from the
 //                forward's saved kappa, summed over the unit's query heads.
-//                With the coefficient gradients requested it also writes the
-//                per-(head, chunk) coefficient partials from the same group sums.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -383,7 +383,10 @@ __global__ __launch_bounds__(192) void k2_local_dk(const T* __restrict__ q, cons
                                                    const int32_t* __restrict__ labels, const float* __restrict__ lam,
                                                    const float* __restrict__ gam, int G, int Hq, int Hkv, int N,
                                                    int NB, float scale, float* __restrict__ dkl) {
-  __shared__ __attribute__((aligned(16))) uint32_t mk[2][4][8][2][4];
+  // group masks and per-dimension coefficients of all the unit's query heads
+  // (up to 8), built once: no dependent label -> coefficient loads per head
+  __shared__ __attribute__((aligned(16))) uint32_t mk[8][4][8][2][4];
+  __shared__ float cfl[8][9][kD];
   __shared__ float red[2][16][64];
   int ch;
   const int u = unit_chunk_block(NB, ch);
@@ -395,11 +398,20 @@ __global__ __launch_bounds__(192) void k2_local_dk(const T* __restrict__ q, cons
   const LocalTile t = local_tile(wv, tok0, N, row);
   f32x16 acc[2] = {f32x16{}, f32x16{}};
 
-  build_masks(mk[0], labels, kh * R, G, tid);
+  for (int hh = 0; hh < R; ++hh) build_masks(mk[hh], labels, kh * R + hh, G, tid);
+  for (int e = tid; e < R * 9 * kD; e += 192) {
+    const int hh = e / (9 * kD), h2 = (e / kD) % 9, d = e % kD, h = kh * R + hh;
+    const int gd = clamp_label(labels[h * kD + d], G);
+    float c = 0.f;
+    if (h2 == 8)
+      c = scale * lam[(size_t)h * G + gd];
+    else if (h2 < G)
+      c = 2.f * scale * scale * gam[((size_t)h * G + gd) * G + h2];
+    cfl[hh][h2][d] = c;
+  }
   __syncthreads();
   for (int hh = 0; hh < R; ++hh) {
-    const int h = kh * R + hh, mb = hh & 1;
-    if (hh + 1 < R) build_masks(mk[mb ^ 1], labels, h + 1, G, tid);
+    const int h = kh * R + hh, mb = hh;
     const size_t qbase = (size_t)(b * Hq + h) * N * kD;
     // ds[i][j] = g_i . v_j + gz_i on live (j <= i, i < N) entries
     f32x16 ds = f32x16{};
@@ -427,13 +439,9 @@ __global__ __launch_bounds__(192) void k2_local_dk(const T* __restrict__ q, cons
                                                        tok0 + 32 * t.it + 16 * tt + 8 * s);
     float cf[9][2];
 #pragma unroll
-    for (int dt = 0; dt < 2; ++dt) {
-      const int gd = clamp_label(labels[h * kD + 32 * dt + row], G);
+    for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
-      for (int h2 = 0; h2 < 8; ++h2)
-      cf[h2][dt] = h2 < G ? 2.f * scale * scale * gam[((size_t)h * G + gd) * G + h2] : 0.f;
-      cf[8][dt] = scale * lam[(size_t)h * G + gd];
-    }
+      for (int h2 = 0; h2 < 9; ++h2) cf[h2][dt] = cfl[hh][h2][32 * dt + row];
 #pragma unroll
     for (int h2 = 0; h2 < 9; ++h2) {
       float x[16];
@@ -458,7 +466,6 @@ __global__ __launch_bounds__(192) void k2_local_dk(const T* __restrict__ q, cons
         for (int r = 0; r < 16; ++r) acc[dt][r] = fmaf(cf[h2][dt], p[r], acc[dt][r]);
       }
     }
-    __syncthreads();
   }
   local_write(red, acc, t, l, row, tok0, N, kbase, dkl);
 }
