@@ -1,6 +1,6 @@
 """Benchmark: OAL grouped quadratic attention fwd+bwd on one MI355X.
 
-Workload: B=4, Hq=14, Hkv=2, N=4096, d=64, bf16, causal,
+Workload (the headline configuration 2): B=4, Hq=14, Hkv=2, N=4096, d=64, bf16, causal,
 8 uneven groups, fwd+bwd through the grouped autograd Function in
 oal_amd.hd_block_gemm_autograd, upstream dO ~ N(0,1) bf16, gradients for q, k, v
 and the coefficients (c0, lam, Gam). Inputs are synthetic and already resident
@@ -168,7 +168,7 @@ def cpu_baseline(seconds: float = 12.0) -> dict:
 
 
 def bench_model(args) -> int:
-    """one bf16 LoRA training step of the 24-layer Qwen-shaped model
+    """Configuration 4: one bf16 LoRA training step of the 24-layer Qwen-shaped model
     with OAL in every layer (random init, uniform random token ids, seed 0).
 
     value = B*N / (seconds per step); the attention share is the summed device time

@@ -1,6 +1,6 @@
 """Qwen2-shaped decoder with OAL grouped quadratic attention in every layer.
 
-The model of BASELINE config 4 (random init, no checkpoint is loaded): hidden
+The benchmark's model-step workload (random init, no checkpoint is loaded): hidden
 896, 24 layers, 14 query / 2 KV heads of dimension 64, SwiGLU MLP 4864, vocab
 151936, RMSNorm (eps 1e-6), rotary embeddings (theta 1e6, rotate-half form),
 tied input/output embeddings; LoRA of rank 16 on the q/k/v/o projections, all

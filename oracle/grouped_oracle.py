@@ -494,7 +494,7 @@ def config_inputs(
     dtype: torch.dtype = torch.float32,
     seed: int = 0,
 ):
-    """Synthetic inputs for the BASELINE configurations (CPU tensors).
+    """Synthetic inputs of the benchmark configurations 0-3 (CPU tensors).
 
     config 0: B=1, H=1, N=256, D=64, q,k,v ~ N(0,1)/sqrt(8), 4 groups of 16.
     configs 1-3: Hq=14, Hkv=2, D=64, q,k,v ~ N(0,1) with 2 seeded outlier dims

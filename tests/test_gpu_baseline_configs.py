@@ -1,4 +1,4 @@
-"""GPU parity at the full BASELINE shapes (configs 1, 2 and 3), bf16 matrix-core path.
+"""GPU parity at the full benchmark shapes (configurations 1, 2 and 3), bf16 matrix-core path.
 
 The fp32 chunked oracle (oracle/grouped_oracle.py) runs these shapes in seconds on
 the host cores, so the comparison is made on every output and gradient, not on
@@ -9,7 +9,7 @@ a sample:
   autograd Function with dO ~ N(0,1) in bf16 (dq, dk, dv, dc0, dlam, dGam);
 * config 3: B=1, N=32768, forward + backward (long-context state carry).
 
-Tolerance: rel-L2 <= 2e-2 in bf16 mode against the fp32
+Tolerance (the bf16-mode bar): rel-L2 <= 2e-2 against the fp32
 oracle evaluated on the same bf16-rounded q, k, v. `out` is compared where the
 oracle's |den| > 1 (elsewhere out = num / den is ill-conditioned); the upstream
 dO is kept on tokens whose denominator is not a near-cancelling sum, the same

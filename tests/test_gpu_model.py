@@ -1,4 +1,4 @@
-"""The Qwen-shaped OAL model (BASELINE config 4 architecture) on the GPU.
+"""The Qwen-shaped OAL model (the model-step benchmark's architecture) on the GPU.
 
 A reduced copy (2 layers, vocab 512, MLP 256; hidden 896 = 14 heads x 64,
 2 KV heads as in the full model) runs one forward + backward on the GPU with

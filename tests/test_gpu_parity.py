@@ -1,6 +1,6 @@
 """GPU parity: the HIP path (through the C ABI) against the CPU oracle.
 
-Tolerances (BASELINE north star): rel-L2 <= 1e-5 in fp32 mode, <= 2e-2 in
+Tolerances: rel-L2 <= 1e-5 in fp32 mode, <= 2e-2 in
 bf16 mode, against the fp64/fp32 oracle on the same seeded inputs.
 """
 
