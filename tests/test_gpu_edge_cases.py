@@ -144,3 +144,12 @@ def test_partial_gradient_requests(grads):
             assert gp is not None and torch.equal(gp, gf), name
         else:
             assert gp is None, name
+
+
+@pytest.mark.parametrize("b,hq,hkv,n", [(3, 6, 3, 1000), (1, 7, 1, 777), (5, 4, 2, 200)])
+def test_irregular_shapes(b, hq, hkv, n):
+    """Unit counts B * Hkv = 9, 1, 10 (the XCD-ordered block mappings fall back to
+    plain order when the block count is not a multiple of 8), N not a multiple of
+    the 64-token chunk, 2 to 7 query heads per KV head, and scan plans whose
+    segments do not divide the chunk count."""
+    _run(b, hq, hkv, n, _labels(hq, 6, seed=n), seed=b + n)
