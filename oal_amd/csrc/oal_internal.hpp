@@ -20,6 +20,9 @@ using Timer = std::function<void(const char*, hipStream_t, const std::function<v
 // Per-head coefficient pack of the intra-chunk kernels: c0, scale * lam[g]
 // (g < 8, zero padded), scale^2 * Gam[g][h] (8 x 8, zero padded).
 constexpr int kIC = 80;
+// Denominator-state entries per (unit, chunk) in pair-matrix form: the 64 x 64
+// pair matrix, the 64 linear entries, the constant, padded.
+constexpr int kZt = 64 * 64 + 64 + 64;
 constexpr int kIcLam = 1;
 constexpr int kIcGam = 9;
 
@@ -35,6 +38,7 @@ struct MfmaSaved {
   uint16_t* KT16; // [U][64][NB * 64] bf16 k^T (tokens >= N zero)
   uint16_t* VT16; // [U][65][NB * 64] bf16 [v^T; 1 (token < N)]
   uint16_t* KAP;  // [B][Hq][NB][3][64][16] bf16 intra-chunk kappa, k2_local_dv's operand fragments
+  float* Zt;      // [U][NB][kZt] per-chunk denominator-state totals (forward scratch)
   size_t bytes;
 };
 
@@ -54,7 +58,10 @@ struct MfmaWork {
   uint16_t* QT16; // [B][Hq][66][NB * 64] bf16: q^T, 1 (token < N), 0
   uint16_t* dTT;  // [U][NB][kKS][64][16] bf16
   uint16_t* dTR;  // [U][NB][kS/32][4][32][16] bf16
-  float* dTz;     // [U][NB][kFP]
+  float* dTz;     // [U][NB][kFP] exclusive suffix of the denominator state (natural order)
+  float* dCt;     // [U][NB][kZt] per-chunk denominator dCarry (pair-matrix form)
+  float* dwz;     // [U][NB][R][kFP] per-(chunk, head) denominator coefficient partials
+  float* dwqz;    // [Hq][kFP] their sums over (batch, chunk)
   float* dwqs;    // [S][B][Hq][kS] slot-coefficient gradients (state part) per segment
   float* dwq;     // [Hq][kS] their sum
   float* segtot;  // [U][S][kS][65] per-segment dCarry totals, then (in place) their carries
@@ -115,24 +122,29 @@ ScanPlan scan_plan(int U, int NB, size_t scratch_bytes, bool fwd);
 struct ScanArgs {
   const uint16_t* F;  // feature side, [X][frows][NB * 64] bf16 (rows 0..63 used)
   int frows;
-  const uint16_t* V;  // value side, [X][vrows][NB * 64] bf16 (rows 0..64 used)
+  const uint16_t* V;  // value side, [X][vrows][NB * 64] bf16 (rows 0..63 used)
   int vrows;
   const float* wqs;   // backward: [Hq][kS] slot coefficients
   const uint16_t* PR; // backward: forward state (R layout), for the coefficient partials
-  const float* PZ;    // backward: forward denominator column
   int U, Hq, Hkv, N, NB;
   uint16_t* outT;     // emitted state, T layout
   uint16_t* outR;     // emitted state, R layout
-  float* outZ;        // emitted denominator column (natural order)
-  float* outZm;       // forward: denominator column as a symmetric pair matrix
-  float* segtot;      // [U][S][kS][65] scratch when S > 1
+  float* segtot;      // [U][S][kS][64] scratch when S > 1
   float* dwqs;        // backward: [S][B][Hq][kS] coefficient partials
 };
 template <bool FWD>
 void launch_scan(const ScanPlan& p, const ScanArgs& a, hipStream_t st, const Timer& timed);
 template <typename T>
-void launch_fwd_prep(const LaunchGeom& g, const T* k, const T* v, uint16_t* KT16, uint16_t* VT16, hipStream_t st,
+void launch_fwd_prep(const LaunchGeom& g, const T* k, const T* v, uint16_t* KT16, uint16_t* VT16, float* Zt,
+                     hipStream_t st, const Timer& timed);
+// Denominator state in pair-matrix form (oal_mfma_scan.hip): the chunk prefix
+// (forward: PZ natural order and PZm) or suffix (backward: dTz) of per-chunk
+// totals, and the backward's per-chunk totals and coefficient partials.
+void launch_den_scan(bool fwd, const LaunchGeom& g, const float* tot, float* outZ, float* outZm, hipStream_t st,
                      const Timer& timed);
+void launch_den_bwd(const LaunchGeom& g, const uint16_t* QT16, const uint16_t* GT16, int trows, const float* gm,
+                    const float* lb, const float* ic, int kic, const float* PZ, const float* PZm, float* dCt,
+                    float* dwz, hipStream_t st, const Timer& timed);
 
 int run_mfma_selftest(int* dev_errors, hipStream_t st);
 

@@ -532,15 +532,64 @@ __global__ __launch_bounds__(128, 2) void k2_kv_fold(const T* __restrict__ k, co
   }
 }
 
-// Grid (slot blocks + 73, Hq). Slot blocks: dwq[h][slot] = sum over (segment,
-// batch) of the state-scan partials. The other 73 blocks of a head: one column
-// of the per-(batch, chunk) local partials each, coefs[h][j] = sum_r
-// coefl[h][j][r]. Every sum in a fixed order.
+// Grid (slot blocks + 73 + den blocks, Hq). Slot blocks: dwq[h][slot] = sum
+// over (segment, batch) of the state-scan partials. The next 73 blocks of a
+// head: one column of the per-(batch, chunk) local partials each, coefs[h][j]
+// = sum_r coefl[h][j][r]. The den blocks (64 entries each): dwqz[h][nat] =
+// sum over (batch, chunk) of the denominator partials dwz [U][NB][R][kFP], the
+// (batch, chunk) rows split over the block's 4 waves (8 loads in flight each),
+// then combined. Every sum in a fixed order.
 constexpr int kDwqSlotBlocks = (kS + 255) / 256;
+constexpr int kDwqDenBlocks = (kFeat + 63) / 64;
 __global__ __launch_bounds__(256) void k2_dwq_reduce(const float* __restrict__ dwqs, int rowsets, int Hq,
                                                      float* __restrict__ dwq, const float* __restrict__ coefl, int bn,
-                                                     float* __restrict__ coefs) {
+                                                     float* __restrict__ coefs, const float* __restrict__ dwz, int B,
+                                                     int Hkv, int NB, float* __restrict__ dwqz) {
   const int h = blockIdx.y;
+  if (blockIdx.x >= kDwqSlotBlocks + 73) {
+    // 64 entries per block; lane l reads entries 4 (l % 16) .. as a float4 of
+    // row-group l / 16 + 4 wave, rows (batch, chunk) i = group + 16 x
+    __shared__ float dpart[16][64];
+    const int l = threadIdx.x & 63, wv = threadIdx.x >> 6, grp = (l >> 4) + 4 * wv, e4 = 4 * (l & 15);
+    const int n0 = (blockIdx.x - kDwqSlotBlocks - 73) * 64;
+    const int R = Hq / Hkv, kh = h / R, hh = h % R;
+    const int rows = B * NB;  // row i = (batch i / NB, chunk i % NB)
+    auto row_ptr = [&](int i) {
+      const int bb = i / NB, c = i % NB;
+      return dwz + (((size_t)(bb * Hkv + kh) * NB + c) * R + hh) * kFP + n0 + e4;
+    };
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    int i = grp;
+    for (; i + 16 * 7 < rows; i += 16 * 8) {
+      float4 v[8];
+#pragma unroll
+      for (int x = 0; x < 8; ++x) v[x] = *reinterpret_cast<const float4*>(row_ptr(i + 16 * x));
+#pragma unroll
+      for (int x = 0; x < 8; ++x) {
+        acc.x += v[x].x;
+        acc.y += v[x].y;
+        acc.z += v[x].z;
+        acc.w += v[x].w;
+      }
+    }
+    for (; i < rows; i += 16) {
+      const float4 v = *reinterpret_cast<const float4*>(row_ptr(i));
+      acc.x += v.x;
+      acc.y += v.y;
+      acc.z += v.z;
+      acc.w += v.w;
+    }
+    *reinterpret_cast<float4*>(&dpart[grp][e4]) = acc;
+    __syncthreads();
+    const int n = n0 + threadIdx.x;
+    if (threadIdx.x < 64 && n < kFeat) {
+      float t = 0.f;
+#pragma unroll
+      for (int g = 0; g < 16; ++g) t += dpart[g][threadIdx.x];
+      dwqz[(size_t)h * kFP + n] = t;
+    }
+    return;
+  }
   if (blockIdx.x >= kDwqSlotBlocks) {
     __shared__ float wsum[4];
     const int j = blockIdx.x - kDwqSlotBlocks;
@@ -580,7 +629,8 @@ __global__ __launch_bounds__(256) void k2_dwq_reduce(const float* __restrict__ d
 // one-hot label matrix. Local part: the column sums of the per-chunk partials
 // (coefs, from k2_dwq_reduce).
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k2_coef_grad(const float* __restrict__ dwq, const float* __restrict__ coefs,
+__global__ __launch_bounds__(256) void k2_coef_grad(const float* __restrict__ dwq, const float* __restrict__ dwqz,
+                                                    const float* __restrict__ coefs,
                                                     const int32_t* __restrict__ labels, int Hq, int G, float scale,
                                                     float* __restrict__ dc0, float* __restrict__ dlam,
                                                     float* __restrict__ dgam) {
@@ -599,6 +649,9 @@ __global__ __launch_bounds__(256) void k2_coef_grad(const float* __restrict__ dw
     const int n = kSlot.nat[sl];
     if (n >= 0) wn[n] = dwq[(size_t)h * kS + sl];
   }
+  __syncthreads();
+  // plus the denominator state's partials (natural order)
+  for (int n = t; n < kFeat; n += 256) wn[n] += dwqz[(size_t)h * kFP + n];
   if (t < 73) loc[t] = coefs[(size_t)h * 73 + t];
   __syncthreads();
   // xr[r][g] = sum_{c <= r, g(c) = g} m_rc wn[pair(r, c)]: thread (r, q) sums the
@@ -681,6 +734,9 @@ MfmaWork mfma_work_view(void* base, int B, int Hq, int U, int N, int NB) {
   w.dTT = static_cast<uint16_t*>(take(chunk * U * NB));
   w.dTR = static_cast<uint16_t*>(take(chunk * U * NB));
   w.dTz = static_cast<float*>(take(sizeof(float) * (size_t)U * NB * kFP));
+  w.dCt = static_cast<float*>(take(sizeof(float) * (size_t)U * NB * kZt));
+  w.dwz = static_cast<float*>(take(sizeof(float) * (size_t)B * Hq * NB * kFP));
+  w.dwqz = static_cast<float*>(take(sizeof(float) * (size_t)Hq * kFP));
   w.dwqs = static_cast<float*>(take(sizeof(float) * (size_t)w.S * B * Hq * kS));
   w.dwq = static_cast<float*>(take(sizeof(float) * (size_t)Hq * kS));
   w.segtot = static_cast<float*>(take(plan.seg_bytes));
@@ -713,9 +769,13 @@ int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, cons
   });
   {
     const ScanPlan plan{w.S, w.SL, 0};
-    ScanArgs a{w.QT16, kTRows, w.GT16, kTRows, sv.wqs, sv.PR, sv.PZ, g.U, g.Hq, g.Hkv, g.N, g.NB,
-               w.dTT, w.dTR, w.dTz, nullptr, w.segtot, w.dwqs};
+    ScanArgs a{w.QT16, kTRows, w.GT16, kTRows, sv.wqs, sv.PR, g.U, g.Hq, g.Hkv, g.N, g.NB,
+               w.dTT, w.dTR, w.segtot, w.dwqs};
     launch_scan<false>(plan, a, st, timed);
+    // denominator state (pair-matrix form): per-chunk dCarry and coefficient
+    // partials, then dTz as the exclusive chunk suffix
+    launch_den_bwd(g, w.QT16, w.GT16, kTRows, sv.gm, sv.lb, sv.ic, kIC, sv.PZ, sv.PZm, w.dCt, w.dwz, st, timed);
+    launch_den_scan(false, g, w.dCt, w.dTz, nullptr, st, timed);
   }
   {
     LocalBwdArgs la{w.G16, w.Gz, w.QT16, w.GT16, sv.KT16, sv.KAP, sv.PZ, sv.PZm, labels, lam, gam, sv.ic, sv.gm, sv.lb,
@@ -736,12 +796,12 @@ int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, cons
   }
   if (need_coef) {
     timed("k2_dwq_reduce", st, [&] {
-      hipLaunchKernelGGL(k2_dwq_reduce, dim3(kDwqSlotBlocks + 73, g.Hq), dim3(256), 0, st, w.dwqs, g.B * w.S, g.Hq,
-                         w.dwq, w.coefl, g.B * g.NB, w.coefs);
+      hipLaunchKernelGGL(k2_dwq_reduce, dim3(kDwqSlotBlocks + 73 + kDwqDenBlocks, g.Hq), dim3(256), 0, st, w.dwqs,
+                         g.B * w.S, g.Hq, w.dwq, w.coefl, g.B * g.NB, w.coefs, w.dwz, g.B, g.Hkv, g.NB, w.dwqz);
     });
     timed("k2_coef_grad", st, [&] {
-      hipLaunchKernelGGL(k2_coef_grad, dim3(g.Hq), dim3(256), 0, st, w.dwq, w.coefs, labels, g.Hq, groups, scale,
-                         dc0, dlam, dgam);
+      hipLaunchKernelGGL(k2_coef_grad, dim3(g.Hq), dim3(256), 0, st, w.dwq, w.dwqz, w.coefs, labels, g.Hq, groups,
+                         scale, dc0, dlam, dgam);
     });
   }
   return 0;

@@ -13,7 +13,10 @@
 // Saved layouts (per unit u and chunk c; "tile" = 32 slots, "k-step" = 16 slots):
 //   PT [u][c][kKS][64 e][16]        bf16  (readout B operand: slots contiguous)
 //   PR [u][c][kS/32][4][32][16 e]   bf16  (backward A operand: values contiguous)
-//   PZ [u][c][kFP]                  f32   (denominator column, natural order)
+//   PZ [u][c][kFP]                  f32   (denominator state, natural feature order)
+//   PZm [u][c][64][64]              f32   (its pair entries as a symmetric matrix; PZ and
+//                                          PZm are k2_den_scan's prefixes of k2_fwd_prep's
+//                                          per-chunk K^T K, sum k and token count)
 //   KAP [b][h][c][3][64][16]        bf16  (intra-chunk kappa of the 3 lower 32x32 tile
 //                                          pairs as the backward dv product's A fragments)
 
@@ -594,6 +597,7 @@ MfmaSaved mfma_saved_view(void* base, int Hq, int U, int NB, int R) {
   v.KT16 = static_cast<uint16_t*>(take(sizeof(uint16_t) * units * kD * kC));
   v.VT16 = static_cast<uint16_t*>(take(sizeof(uint16_t) * units * (kD + 1) * kC));
   v.KAP = static_cast<uint16_t*>(take(sizeof(uint16_t) * units * R * 3 * 64 * 16));
+  v.Zt = static_cast<float*>(take(sizeof(float) * units * kZt));
   v.bytes = off;
   return v;
 }
@@ -612,13 +616,15 @@ void launch_mfma_forward(const LaunchGeom& g, const void* q, const void* k, cons
     hipLaunchKernelGGL(k2_slot_coefficients, dim3(g.Hq, 8), dim3(256), 0, st, labels, c0, lam, gam, groups, scale,
                        sv.wqs, sv.ic, sv.gm, sv.lb);
   });
-  launch_fwd_prep<T>(g, kt, vt, sv.KT16, sv.VT16, st, timed);
+  launch_fwd_prep<T>(g, kt, vt, sv.KT16, sv.VT16, sv.Zt, st, timed);
+  // denominator state (pair-matrix form): PZ, PZm as exclusive chunk prefixes
+  launch_den_scan(true, g, sv.Zt, sv.PZ, sv.PZm, st, timed);
   {
     // num is written only later (k2_intra_fwd), so it doubles as the scan's
     // segment scratch
     const ScanPlan plan = scan_plan(g.U, g.NB, sizeof(float) * (size_t)g.B * g.Hq * g.N * kD, true);
-    ScanArgs a{sv.KT16, kD, sv.VT16, kD + 1, nullptr, nullptr, nullptr, g.U, g.Hq, g.Hkv, g.N, g.NB,
-               sv.PT, sv.PR, sv.PZ, sv.PZm, num, nullptr};
+    ScanArgs a{sv.KT16, kD, sv.VT16, kD + 1, nullptr, nullptr, g.U, g.Hq, g.Hkv, g.N, g.NB,
+               sv.PT, sv.PR, num, nullptr};
     launch_scan<true>(plan, a, st, timed);
   }
   timed("k2_intra_fwd", st, [&] {

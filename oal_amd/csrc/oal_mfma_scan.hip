@@ -2,12 +2,16 @@
 //
 // Forward (reference hd_block_gemm_runtime.py:271-320: block totals, exclusive
 // cumsum), per unit u = (batch, kv head):
-//   T_c = raw(K_c)^T [V_c, 1],        P_c = sum_{c' < c} T_c'
+//   T_c = raw(K_c)^T V_c,        P_c = sum_{c' < c} T_c'
 // Backward (reference hd_block_gemm_backward.py:764-908: _query_dcarry and the
 // exclusive right scan), per unit:
-//   dCarry_c = sum_h wq_h o raw(Q_h,c)^T [G_h,c, Gz_h,c],   dT_c = sum_{c' > c} dCarry_c'
+//   dCarry_c = sum_h wq_h o raw(Q_h,c)^T G_h,c,   dT_c = sum_{c' > c} dCarry_c'
 // and the per-slot coefficient partial of each query head
-//   dwq_h[slot] += sum_c <P_c[slot], (raw(Q_h,c)^T [G_h,c, Gz_h,c])[slot]>.
+//   dwq_h[slot] += sum_c <P_c[slot], (raw(Q_h,c)^T G_h,c)[slot]>.
+// The denominator column (the value-side row of ones / of Gz) is not in these
+// scans: its feature-space state is the 64 x 64 pair matrix of the k2_den_*
+// kernels below, formed with one small product per chunk instead of a
+// 1/32-useful matrix-core column per k-step.
 //
 // k2_scan<FWD, MODE, TPW, NW>: a block of NW waves, each owning TPW 32-slot
 // tiles, of one unit and one segment of consecutive chunks; the state of a
@@ -16,8 +20,8 @@
 // the wave's tiles (TPW = 2 halves those reads per tile; the backward totals
 // keep TPW = 1 for the registers of the per-head products). An item is one
 // (chunk, query head) pair in the backward and one chunk in the forward; its
-// operands (the feature side q^T / k^T and the value side [G^T; Gz] / [V^T; 1],
-// 64 tokens each) are staged once per block into a double-buffered LDS pair,
+// operands (the feature side q^T / k^T and the value side G^T / V^T, 64
+// tokens each) are staged once per block into a double-buffered LDS pair,
 // fetched into registers two items ahead. Raw features are products of two
 // fp32 rows of the staged feature side, packed to bf16 as the MFMA B operand.
 //   MODE 0: segment totals (backward: plus coefficient partials); no state out.
@@ -27,9 +31,7 @@
 //           wq_h so that every head accumulates into the one state.
 //   MODE 2: one segment: MODE 1's output plus MODE 0's partials.
 // Emitted layouts per (unit, chunk), identical in both directions:
-//   R [kS/32][4][32][16 values] bf16, T [kKS][64 values][16 slots] bf16,
-//   Z [kFP] fp32 (denominator column, natural feature order), and in the
-//   forward Zm [64][64] fp32 (the denominator column as a symmetric pair matrix).
+//   R [kS/32][4][32][16 values] bf16, T [kKS][64 values][16 slots] bf16.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -51,7 +53,7 @@ namespace {
 constexpr int scan_tile_groups(int tpw, int nw) { return (kS / 32 + nw * tpw - 1) / (nw * tpw); }
 constexpr int kFRow = kC + 4;                              // fp32 LDS row stride, feature side
 constexpr int kVRow = kC + 8;                              // bf16 LDS row stride, value side
-constexpr int kOpRows = kD + 2;                            // rows 64 (one / den), 65 (zero)
+constexpr int kOpRows = kD + 2;                            // feature side rows 64 (one), 65 (zero)
 constexpr size_t kChunkElems = (size_t)kKS * 64 * 16;
 
 }  // namespace
@@ -60,11 +62,9 @@ template <bool FWD, int MODE, int TPW, int NW>
 __global__ __launch_bounds__(64 * NW, NW / 2) void k2_scan(const uint16_t* __restrict__ F, int frows,
                                                const uint16_t* __restrict__ V, int vrows,
                                                const float* __restrict__ wqs, const uint16_t* __restrict__ PRin,
-                                               const float* __restrict__ PZin, const float* __restrict__ carry, int Hq,
-                                               int Hkv, int N, int NB, int SL, int Sg, uint16_t* __restrict__ outT,
-                                               uint16_t* __restrict__ outR, float* __restrict__ outZ,
-                                               float* __restrict__ outZm, float* __restrict__ segtot,
-                                               float* __restrict__ dwqs) {
+                                               const float* __restrict__ carry, int Hq, int Hkv, int N, int NB, int SL,
+                                               int Sg, uint16_t* __restrict__ outT, uint16_t* __restrict__ outR,
+                                               float* __restrict__ segtot, float* __restrict__ dwqs) {
   constexpr bool EMIT = MODE != 0;
   constexpr bool PARTIALS = !FWD && MODE != 1;
   constexpr bool SPLIT = PARTIALS;  // per-head products kept apart (needed for the partials)
@@ -75,7 +75,7 @@ __global__ __launch_bounds__(64 * NW, NW / 2) void k2_scan(const uint16_t* __res
   constexpr int kFPT = kD * 8 / kNT;         // 16-byte operand chunks per thread and side
   static_assert(kFPT * kNT == kD * 8, "a block stages whole operand rows");
   __shared__ __attribute__((aligned(16))) float Fs[2][kOpRows * kFRow];
-  __shared__ __attribute__((aligned(16))) __bf16 Vs[2][kOpRows * kVRow];
+  __shared__ __attribute__((aligned(16))) __bf16 Vs[2][kD * kVRow];
   __shared__ float dwl[PARTIALS ? 8 : 1][kSTiles * 32];
   // backward: the slot weight wq_h of every query head of the unit (up to 8)
   // for the block's slots, [head][wave][tile][slot row]
@@ -93,7 +93,7 @@ __global__ __launch_bounds__(64 * NW, NW / 2) void k2_scan(const uint16_t* __res
   const int RI = FWD ? 1 : R;  // items per chunk
   const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, s = l >> 5, row = l & 31;
   // this wave's tiles (TPW consecutive), their slots and slot rows
-  int tile[TPW], slot[TPW], ar[TPW], ac[TPW], nat[TPW];
+  int tile[TPW], slot[TPW], ar[TPW], ac[TPW];
   bool live[TPW];
 #pragma unroll
   for (int t = 0; t < TPW; ++t) {
@@ -102,28 +102,25 @@ __global__ __launch_bounds__(64 * NW, NW / 2) void k2_scan(const uint16_t* __res
     slot[t] = live[t] ? tile[t] * 32 + row : 0;
     ar[t] = kSlot.ar[slot[t]];
     ac[t] = kSlot.ac[slot[t]];
-    nat[t] = live[t] ? kSlot.nat[slot[t]] : -1;
   }
   const bool any_live = live[0];
   const int c_lo = seg * SL, c_hi = min(NB, c_lo + SL);
   const int NI = c_hi > c_lo ? (c_hi - c_lo) * RI : 0;
   const size_t np = (size_t)NB * kC;
 
-  // constant rows: feature side 64 = 1 (the value side is zero for tokens
-  // >= N), 65 = 0; value side 65 = 0
+  // constant rows of the feature side: 64 = 1 (the value side is zero for
+  // tokens >= N), 65 = 0
   for (int i = tid; i < 2 * kC; i += kNT) {
     const int bi = i / kC, j = i % kC;
     Fs[bi][kD * kFRow + j] = 1.f;
     Fs[bi][(kD + 1) * kFRow + j] = 0.f;
-    Vs[bi][(kD + 1) * kVRow + j] = (__bf16)0.f;
   }
   if constexpr (PARTIALS) {
     for (int i = tid; i < 8 * kSTiles * 32; i += kNT) dwl[i / (kSTiles * 32)][i % (kSTiles * 32)] = 0.f;
   }
 
-  // acc[t][n]: values 32 n .. 32 n + 31 of tile t; accz: the denominator
-  // column of tile t in accumulator row t (register t of lane group 0)
-  f32x16 acc[TPW][2], accz = f32x16{};
+  // acc[t][n]: values 32 n .. 32 n + 31 of tile t
+  f32x16 acc[TPW][2];
 #pragma unroll
   for (int t = 0; t < TPW; ++t)
 #pragma unroll
@@ -137,18 +134,16 @@ __global__ __launch_bounds__(64 * NW, NW / 2) void k2_scan(const uint16_t* __res
 #pragma unroll
       for (int t = 0; t < TPW; ++t) {
         if (live[t]) {
-          const float* cr = carry + (((size_t)u * Sg + so) * kS + slot[t]) * 65;
-          float tv[2][16], tz = 0.f;
+          const float* cr = carry + (((size_t)u * Sg + so) * kS + slot[t]) * kD;
+          float tv[2][16];
 #pragma unroll
           for (int n = 0; n < 2; ++n)
 #pragma unroll
             for (int i = 0; i < 16; ++i) tv[n][i] = cr[32 * n + c32_row(i, l)];
-          if (s == 0) tz = cr[64];
 #pragma unroll
           for (int n = 0; n < 2; ++n)
 #pragma unroll
             for (int i = 0; i < 16; ++i) acc[t][n][i] += tv[n][i];
-          if (s == 0) accz[t] += tz;
         }
       }
     }
@@ -163,11 +158,10 @@ __global__ __launch_bounds__(64 * NW, NW / 2) void k2_scan(const uint16_t* __res
     ch = FWD ? c_lo + ci : c_hi - 1 - ci;
   };
   struct Stage {
-    uint4 f[kFPT], v[kFPT], v2;
+    uint4 f[kFPT], v[kFPT];
   };
   // thread tid stages 16-byte chunks tid + kNT i (row chunk >> 3, column 8 (chunk & 7))
   auto uoff = [&](int i) { return (size_t)((tid + kNT * i) >> 3) * np + 8 * (tid & 7); };
-  const size_t uv2 = (size_t)kD * np + 8 * (tid & 7);
   // Every thread issues the same loads on every call (items past the end are
   // clamped to the last one, the row-64 unit to an in-range column): the
   // compiler then counts the loads in flight exactly and waits for an item's
@@ -183,7 +177,6 @@ __global__ __launch_bounds__(64 * NW, NW / 2) void k2_scan(const uint16_t* __res
       st.f[i] = *reinterpret_cast<const uint4*>(fb + uoff(i));
       st.v[i] = *reinterpret_cast<const uint4*>(vb + uoff(i));
     }
-    st.v2 = *reinterpret_cast<const uint4*>(vb + uv2);
   };
   auto put = [&](int bi, int idx, const uint4& f) {
     float4* d = reinterpret_cast<float4*>(&Fs[bi][(idx >> 3) * kFRow + 8 * (idx & 7)]);
@@ -199,9 +192,6 @@ __global__ __launch_bounds__(64 * NW, NW / 2) void k2_scan(const uint16_t* __res
       put(bi, idx, st.f[i]);
       *reinterpret_cast<uint4*>(&Vs[bi][(idx >> 3) * kVRow + 8 * (idx & 7)]) = st.v[i];
     }
-    // row 64 from every thread (eight locations, each written with one value):
-    // a store skipped by a whole wave would leave its load pending at the loop head
-    *reinterpret_cast<uint4*>(&Vs[bi][kD * kVRow + 8 * (tid & 7)]) = st.v2;
   };
 
   // Permutation matrices of the T-layout transposition (see emit): for value
@@ -237,17 +227,6 @@ __global__ __launch_bounds__(64 * NW, NW / 2) void k2_scan(const uint16_t* __res
         const int kk = 2 * n + (a >> 1), pos = 8 * (a & 1) + 4 * s;
         *reinterpret_cast<uint2*>(tr + ((size_t)kk * 32 + row) * 16 + pos) = make_uint2(wd[n][a][0], wd[n][a][1]);
       }
-    if (s == 0 && nat[t] >= 0) {
-      const float z = accz[t];
-      outZ[cb * kFP + nat[t]] = z;
-      if constexpr (FWD) {
-        if (nat[t] > kD) {
-          float* pm = outZm + cb * kD * kD;
-          pm[ar[t] * kD + ac[t]] = z;
-          pm[ac[t] * kD + ar[t]] = z;
-        }
-      }
-    }
     // T layout [kstep][64 values][16 slots]: the matrix cores transpose the
     // packed tile (D = A P, one nonzero product per output, exact), giving
     // lane = value and registers = slots 8 (i / 4) + 4 s + i % 4.
@@ -271,13 +250,11 @@ __global__ __launch_bounds__(64 * NW, NW / 2) void k2_scan(const uint16_t* __res
   };
 
   // Coefficient partials: the P_c rows of this lane's slot (values
-  // e = 32 n + 8 a + 4 s + v) and its denominator entry, for the chunk being
-  // processed (pf, pz) and, still packed, for the next chunk (pfn, pzn): the
-  // next chunk's loads are issued a whole chunk of items before their use.
+  // e = 32 n + 8 a + 4 s + v) for the chunk being processed (pf) and, still
+  // packed, for the next chunk (pfn): the next chunk's loads are issued a whole
+  // chunk of items before their use.
   float pf[2][16];
-  float pz = 0.f;
   uint2 pfn[2][4];
-  float pzn = 0.f;
   auto fetch_partial_rows = [&](int ch) {
     const size_t cb = (size_t)u * NB + ch;
     const uint16_t* pr = PRin + cb * kChunkElems + (size_t)tile[0] * 4 * 32 * 16;
@@ -288,7 +265,6 @@ __global__ __launch_bounds__(64 * NW, NW / 2) void k2_scan(const uint16_t* __res
         const int kk = 2 * n + (a >> 1), pos = 8 * (a & 1) + 4 * s;
         pfn[n][a] = *reinterpret_cast<const uint2*>(pr + ((size_t)kk * 32 + row) * 16 + pos);
       }
-    pzn = PZin[cb * kFP + (nat[0] >= 0 ? nat[0] : 0)];
   };
   if constexpr (PARTIALS) {
     if (NI > 0 && any_live) fetch_partial_rows(c_hi - 1);
@@ -313,7 +289,6 @@ __global__ __launch_bounds__(64 * NW, NW / 2) void k2_scan(const uint16_t* __res
             pf[n][4 * a + 2] = __uint_as_float(q.y << 16);
             pf[n][4 * a + 3] = __uint_as_float(q.y & 0xffff0000u);
           }
-        pz = (s == 0 && nat[0] >= 0) ? pzn : 0.f;
         // the backward runs chunks in descending order; the segment's first
         // chunk refetches itself (an in-range address, never used)
         fetch_partial_rows(ch > c_lo ? ch - 1 : ch);
@@ -321,25 +296,22 @@ __global__ __launch_bounds__(64 * NW, NW / 2) void k2_scan(const uint16_t* __res
     }
     const float* fs = Fs[bi];
     const __bf16* vs = Vs[bi];
-    f32x16 hT[3];
+    f32x16 hT[2];
     if constexpr (SPLIT) {
 #pragma unroll
-      for (int n = 0; n < 3; ++n) hT[n] = f32x16{};
+      for (int n = 0; n < 2; ++n) hT[n] = f32x16{};
     }
-    const int zrow = kD * kVRow;
     // Operands of one k-block (16 tokens): the value side (shared by the wave's
-    // tiles; the denominator row 64 goes to A row t for tile t) and the two fp32
-    // feature rows of each tile's slot. The block kk + 1 is read from LDS before
+    // tiles) and the two fp32 feature rows of each tile's slot. The block kk + 1 is read from LDS before
     // block kk is computed, so that the read latency overlaps the products.
     struct KOps {
-      bf16x8 va[2], vz;
+      bf16x8 va[2];
       float4 a0[TPW], a1[TPW], c0[TPW], c1[TPW];
     };
     auto read_ops = [&](int kk, KOps& o) {
 #pragma unroll
       for (int n = 0; n < 2; ++n)
         o.va[n] = *reinterpret_cast<const bf16x8*>(vs + (32 * n + row) * kVRow + 16 * kk + 8 * s);
-      o.vz = *reinterpret_cast<const bf16x8*>(vs + zrow + 16 * kk + 8 * s);
 #pragma unroll
       for (int t = 0; t < TPW; ++t) {
         const float4* pa = reinterpret_cast<const float4*>(fs + ar[t] * kFRow + 16 * kk + 8 * s);
@@ -361,15 +333,12 @@ __global__ __launch_bounds__(64 * NW, NW / 2) void k2_scan(const uint16_t* __res
           for (int j = 0; j < 8; ++j) f[j] *= w[t];
         }
         const bf16x8 bq = pack8(f);
-        const bf16x8 vzt = row == t ? o.vz : bf16x8{};
         if constexpr (SPLIT) {
           hT[0] = mfma32(o.va[0], bq, hT[0]);
           hT[1] = mfma32(o.va[1], bq, hT[1]);
-          hT[2] = mfma32(vzt, bq, hT[2]);
         } else {
           acc[t][0] = mfma32(o.va[0], bq, acc[t][0]);
           acc[t][1] = mfma32(o.va[1], bq, acc[t][1]);
-          accz = mfma32(vzt, bq, accz);
         }
       }
     };
@@ -386,9 +355,8 @@ __global__ __launch_bounds__(64 * NW, NW / 2) void k2_scan(const uint16_t* __res
       for (int n = 0; n < 2; ++n)
 #pragma unroll
         for (int i = 0; i < 16; ++i) acc[0][n][i] = fmaf(wt, hT[n][i], acc[0][n][i]);
-      accz[0] = fmaf(wt, hT[2][0], accz[0]);
-      // four independent partial sums (a fixed order), not one 33-long chain
-      float dp[4] = {pz * hT[2][0], 0.f, 0.f, 0.f};
+      // four independent partial sums (a fixed order), not one 32-long chain
+      float dp[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int n = 0; n < 2; ++n)
 #pragma unroll
@@ -463,12 +431,11 @@ __global__ __launch_bounds__(64 * NW, NW / 2) void k2_scan(const uint16_t* __res
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {
       if (live[t]) {
-        float* st = segtot + (((size_t)u * Sg + seg) * kS + slot[t]) * 65;
+        float* st = segtot + (((size_t)u * Sg + seg) * kS + slot[t]) * kD;
 #pragma unroll
         for (int n = 0; n < 2; ++n)
 #pragma unroll
           for (int i = 0; i < 16; ++i) st[32 * n + c32_row(i, l)] = acc[t][n][i];
-        if (s == 0) st[64] = accz[t];
       }
     }
   }
@@ -482,10 +449,14 @@ __global__ __launch_bounds__(64 * NW, NW / 2) void k2_scan(const uint16_t* __res
 }
 
 // Forward operands per (unit, chunk): KT16 [U][64][NB * 64] = k^T and
-// VT16 [U][65][NB * 64] = [v^T; 1 (token < N)], bf16, tokens >= N zero.
+// VT16 [U][65][NB * 64] = [v^T; 1 (token < N)], bf16, tokens >= N zero; and
+// the chunk's denominator-state totals Zt [U][NB][kZt]: [r * 64 + c] =
+// sum_j k_jr k_jc (matrix cores, wave w owns the 32 x 32 block (w / 2, w % 2)),
+// [4096 + d] = sum_j k_jd.
 template <typename T>
 __global__ __launch_bounds__(256) void k2_fwd_prep(const T* __restrict__ k, const T* __restrict__ v, int N, int NB,
-                                                   uint16_t* __restrict__ KT16, uint16_t* __restrict__ VT16) {
+                                                   uint16_t* __restrict__ KT16, uint16_t* __restrict__ VT16,
+                                                   float* __restrict__ Zt) {
   __shared__ __attribute__((aligned(16))) __bf16 kT[kD][kC + 8];
   __shared__ __attribute__((aligned(16))) __bf16 vT[kD + 1][kC + 8];
   const int u = blockIdx.x / NB, ch = blockIdx.x % NB;
@@ -518,6 +489,22 @@ __global__ __launch_bounds__(256) void k2_fwd_prep(const T* __restrict__ k, cons
           *reinterpret_cast<const bf16x8*>(&vT[rv][8 * c8]);
     }
   }
+  {
+    const int w = tid >> 6, l = tid & 63, s = l >> 5, row = l & 31, mr = w >> 1, mc = w & 1;
+    f32x16 acc = f32x16{};
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+      acc = mfma32(*reinterpret_cast<const bf16x8*>(&kT[32 * mr + row][16 * kk + 8 * s]),
+                   *reinterpret_cast<const bf16x8*>(&kT[32 * mc + row][16 * kk + 8 * s]), acc);
+    float* z = Zt + ((size_t)u * NB + ch) * kZt;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) z[(32 * mr + c32_row(i, l)) * kD + 32 * mc + row] = acc[i];
+    if (tid < kD) {
+      float sum = 0.f;
+      for (int j = 0; j < kC; ++j) sum += (float)kT[tid][j];
+      z[kD * kD + tid] = sum;
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -543,7 +530,7 @@ ScanPlan scan_plan(int U, int NB, size_t scratch_bytes, bool fwd) {
       cus = n;
   }
   const double slots = 2.0 * cus;
-  const size_t seg_bytes = sizeof(float) * (size_t)U * kS * 65;
+  const size_t seg_bytes = sizeof(float) * (size_t)U * kS * kD;
   int cap = NB;
   if (scratch_bytes != (size_t)-1) cap = (int)std::min<size_t>((size_t)NB, scratch_bytes / seg_bytes);
   if (cap < 1) cap = 1;
@@ -577,20 +564,17 @@ void launch_scan(const ScanPlan& p, const ScanArgs& a, hipStream_t st, const Tim
   if (p.S == 1) {
     timed(name, st, [&] {
       hipLaunchKernelGGL((k2_scan<FWD, 2, T2, W2>), grid(T2, W2), dim3(64 * W2), 0, st, a.F, a.frows, a.V, a.vrows, a.wqs, a.PR,
-                         a.PZ, nullptr, a.Hq, a.Hkv, a.N, a.NB, p.SL, p.S, a.outT, a.outR, a.outZ, a.outZm, nullptr,
-                         a.dwqs);
+                         nullptr, a.Hq, a.Hkv, a.N, a.NB, p.SL, p.S, a.outT, a.outR, nullptr, a.dwqs);
     });
     return;
   }
   timed(FWD ? "k2_state_fwd_totals" : "k2_state_bwd_totals", st, [&] {
-    hipLaunchKernelGGL((k2_scan<FWD, 0, T0, W0>), grid(T0, W0), dim3(64 * W0), 0, st, a.F, a.frows, a.V, a.vrows, a.wqs, a.PR, a.PZ,
-                       nullptr, a.Hq, a.Hkv, a.N, a.NB, p.SL, p.S, nullptr, nullptr, nullptr, nullptr, a.segtot,
-                       a.dwqs);
+    hipLaunchKernelGGL((k2_scan<FWD, 0, T0, W0>), grid(T0, W0), dim3(64 * W0), 0, st, a.F, a.frows, a.V, a.vrows, a.wqs, a.PR,
+                       nullptr, a.Hq, a.Hkv, a.N, a.NB, p.SL, p.S, nullptr, nullptr, a.segtot, a.dwqs);
   });
   timed(name, st, [&] {
     hipLaunchKernelGGL((k2_scan<FWD, 1, T1, W1>), grid(T1, W1), dim3(64 * W1), 0, st, a.F, a.frows, a.V, a.vrows, a.wqs, a.PR,
-                       a.PZ, a.segtot, a.Hq, a.Hkv, a.N, a.NB, p.SL, p.S, a.outT, a.outR, a.outZ, a.outZm, nullptr,
-                       nullptr);
+                       a.segtot, a.Hq, a.Hkv, a.N, a.NB, p.SL, p.S, a.outT, a.outR, nullptr, nullptr);
   });
 }
 
@@ -598,15 +582,15 @@ template void launch_scan<true>(const ScanPlan&, const ScanArgs&, hipStream_t, c
 template void launch_scan<false>(const ScanPlan&, const ScanArgs&, hipStream_t, const Timer&);
 
 template <typename T>
-void launch_fwd_prep(const LaunchGeom& g, const T* k, const T* v, uint16_t* KT16, uint16_t* VT16, hipStream_t st,
-                     const Timer& timed) {
+void launch_fwd_prep(const LaunchGeom& g, const T* k, const T* v, uint16_t* KT16, uint16_t* VT16, float* Zt,
+                     hipStream_t st, const Timer& timed) {
   timed("k2_fwd_prep", st, [&] {
-    hipLaunchKernelGGL(k2_fwd_prep<T>, dim3(g.U * g.NB), dim3(256), 0, st, k, v, g.N, g.NB, KT16, VT16);
+    hipLaunchKernelGGL(k2_fwd_prep<T>, dim3(g.U * g.NB), dim3(256), 0, st, k, v, g.N, g.NB, KT16, VT16, Zt);
   });
 }
-template void launch_fwd_prep<float>(const LaunchGeom&, const float*, const float*, uint16_t*, uint16_t*,
+template void launch_fwd_prep<float>(const LaunchGeom&, const float*, const float*, uint16_t*, uint16_t*, float*,
                                      hipStream_t, const Timer&);
 template void launch_fwd_prep<uint16_t>(const LaunchGeom&, const uint16_t*, const uint16_t*, uint16_t*, uint16_t*,
-                                        hipStream_t, const Timer&);
+                                        float*, hipStream_t, const Timer&);
 
 }  // namespace oal
