@@ -645,14 +645,29 @@ __global__ __launch_bounds__(256) void k2_coef_grad(const float* __restrict__ dw
     int g = labels[h * kD + t];
     lab[t] = g < 0 ? 0 : (g >= G ? G - 1 : g);
   }
-  for (int sl = t; sl < kS; sl += 256) {
-    const int n = kSlot.nat[sl];
-    if (n >= 0) wn[n] = dwq[(size_t)h * kS + sl];
+  // every global load of the thread in flight together (clamped indices, the
+  // clamped copies unused)
+  constexpr int kJS = (kS + 255) / 256, kJF = (kFeat + 255) / 256;
+  float a[kJS], z[kJF];
+#pragma unroll
+  for (int j = 0; j < kJS; ++j) a[j] = dwq[(size_t)h * kS + min(t + 256 * j, kS - 1)];
+#pragma unroll
+  for (int j = 0; j < kJF; ++j) z[j] = dwqz[(size_t)h * kFP + min(t + 256 * j, kFeat - 1)];
+  const float lc = coefs[(size_t)h * 73 + min(t, 72)];
+#pragma unroll
+  for (int j = 0; j < kJS; ++j) {
+    const int sl = t + 256 * j;
+    if (sl < kS) {
+      const int n = kSlot.nat[sl];
+      if (n >= 0) wn[n] = a[j];
+    }
   }
+  if (t < 73) loc[t] = lc;
   __syncthreads();
   // plus the denominator state's partials (natural order)
-  for (int n = t; n < kFeat; n += 256) wn[n] += dwqz[(size_t)h * kFP + n];
-  if (t < 73) loc[t] = coefs[(size_t)h * 73 + t];
+#pragma unroll
+  for (int j = 0; j < kJF; ++j)
+    if (t + 256 * j < kFeat) wn[t + 256 * j] += z[j];
   __syncthreads();
   // xr[r][g] = sum_{c <= r, g(c) = g} m_rc wn[pair(r, c)]: thread (r, q) sums the
   // columns c = q mod 4 into eight group bins, then the four quarters are added

@@ -19,10 +19,11 @@ namespace oal {
 // [r * 64 + c] the pair entry (r, c) of a symmetric 64 x 64 matrix, [4096 + d]
 // the linear entry d, [4160] the constant entry (backward only; the forward's
 // constant total of a chunk before the last is its 64 tokens).
-// k2_den_scan<FWD>: thread per entry, chunks in order; the forward writes the
-// exclusive prefix PZ [U][NB][kFP] (natural feature order) and PZm
-// [U][NB][64][64] (the pair matrix), the backward the exclusive suffix dTz
-// [U][NB][kFP]. Fixed order (chunk by chunk).
+// k2_den_scan<FWD>: the forward writes the exclusive prefix PZ [U][NB][kFP]
+// (natural feature order) and PZm [U][NB][64][64] (the pair matrix), the
+// backward the exclusive suffix dTz [U][NB][kFP]. The summation order is fixed
+// (per 64-chunk tile: four 16-chunk row sums, then the walk), so results do
+// not depend on the launch.
 // ---------------------------------------------------------------------------
 // Entry e of a chunk total: its natural feature index (-1 for a pair entry
 // above the diagonal, which the natural order does not hold).
@@ -35,38 +36,58 @@ __device__ __forceinline__ int den_entry_nat(int e) {
 }
 
 // Block (64 entries, unit), 256 threads: tiles of 64 chunks x 64 entries are
-// loaded into LDS with coalesced row loads, then 64 threads (one per entry)
-// walk the tile's chunks in order, each chunk's stores coalesced across them.
+// loaded into LDS with coalesced row loads; each wave then walks 16 of the
+// tile's chunks in order from the running sum plus the earlier waves' row
+// sums, one thread per entry, each chunk's stores coalesced across the wave.
 template <bool FWD>
 __global__ __launch_bounds__(256) void k2_den_scan(const float* __restrict__ tot, int NB, float* __restrict__ outZ,
                                                    float* __restrict__ outZm) {
   constexpr int kEntries = kD * kD + kD + 1;
   __shared__ float tile[64][65];
+  __shared__ float psum[4][64];
   const int u = blockIdx.y, e0 = blockIdx.x * 64, tid = threadIdx.x;
-  const int e = e0 + (tid & 63);
+  const int e = e0 + (tid & 63);  // every wave: the same 64 entries
   const int nat = den_entry_nat(e);
   float run = 0.f;
   for (int t0 = 0; t0 < NB; t0 += 64) {
     const int nt = min(64, NB - t0);
     __syncthreads();
-    // row i of the tile = the i-th chunk in scan order
-    for (int i = tid >> 6; i < nt; i += 4) {
+    // row i of the tile = the i-th chunk in scan order; all 16 loads of a
+    // thread in flight together (rows past the tile reload its last row, unread;
+    // entries past kEntries read the padding of the row, unread)
+    float x[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int i = min((tid >> 6) + 4 * j, nt - 1);
       const int ch = FWD ? t0 + i : NB - 1 - (t0 + i);
-      tile[i][tid & 63] = (e < kEntries) ? tot[((size_t)u * NB + ch) * kZt + e] : 0.f;
+      x[j] = tot[((size_t)u * NB + ch) * kZt + min(e, kZt - 1)];
     }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) tile[(tid >> 6) + 4 * j][tid & 63] = x[j];
     __syncthreads();
-    if (tid < 64 && e < kEntries) {
-      for (int i = 0; i < nt; ++i) {
+    // two-level prefix over the tile: wave q walks tile rows 16 q .. 16 q + 15
+    // from run plus the row sums of the waves before it
+    const int q = tid >> 6, lane = tid & 63;
+    const bool cnst = FWD && nat == 0;  // the forward's constant: 64 tokens per chunk
+    float wsum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) wsum += (16 * q + i < nt) ? (cnst ? (float)kC : tile[16 * q + i][lane]) : 0.f;
+    psum[q][lane] = wsum;
+    __syncthreads();
+    float start = run;
+    for (int p2 = 0; p2 < q; ++p2) start += psum[p2][lane];
+    if (e < kEntries) {
+      for (int i = 16 * q; i < min(16 * q + 16, nt); ++i) {
         const int ch = FWD ? t0 + i : NB - 1 - (t0 + i);
         const size_t cb = (size_t)u * NB + ch;
-        if (nat >= 0) outZ[cb * kFP + nat] = run;
+        if (nat >= 0) outZ[cb * kFP + nat] = start;
         if constexpr (FWD) {
-          if (e < kD * kD) outZm[cb * kD * kD + e] = run;
+          if (e < kD * kD) outZm[cb * kD * kD + e] = start;
         }
-        // the forward's constant total of every chunk before the last is its 64 tokens
-        run += (FWD && nat == 0) ? (float)kC : tile[i][tid];
+        start += cnst ? (float)kC : tile[i][lane];
       }
     }
+    run += (psum[0][lane] + psum[1][lane]) + (psum[2][lane] + psum[3][lane]);
   }
 }
 
@@ -115,27 +136,26 @@ __global__ __launch_bounds__(256, 2) void k2_den_bwd(const uint16_t* __restrict_
 #pragma unroll
     for (int n = 0; n < 3; ++n) pz[n] = n < 2 ? PZ[cb * kFP + 1 + 32 * n + row] : PZ[cb * kFP];
   }
-  // weights of the wave's entries for query head h: pair gm, linear lb, constant c0
-  auto load_w = [&](int h, float (&wv)[16]) {
-    if (w < 3) {
+  // weights of query head h: pair gm of the wave's block (wave 3: of block
+  // (1, 0), unused), linear lb of d = row, 32 + row and the constant c0, loaded
+  // by every wave without branches (a branch would put the arrays on the stack)
+  auto load_w = [&](int h, float (&wv)[16], float (&wl)[3]) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int r = 32 * mr + c32_row(i, l), c = 32 * mc + row;
-        wv[i] = gm[((size_t)h * kD + r) * kD + c];
-      }
-    } else {
-      wv[0] = lb[(size_t)h * kD + row];
-      wv[1] = lb[(size_t)h * kD + 32 + row];
-      wv[2] = ic[(size_t)h * kic];
+    for (int i = 0; i < 16; ++i) {
+      const int r = 32 * mr + c32_row(i, l), c = 32 * mc + row;
+      wv[i] = gm[((size_t)h * kD + r) * kD + c];
     }
+    wl[0] = lb[(size_t)h * kD + row];
+    wl[1] = lb[(size_t)h * kD + 32 + row];
+    wl[2] = ic[(size_t)h * kic];
   };
   // LDS byte offset of q^T row r, tokens 16 kk + 8 s .. of staged head hl
   auto qoff = [&](int hl, int r, int kk) { return ((hl * kD + r) * 8 + ((2 * kk + s) ^ (r & 7))) * 16; };
   const char* qsb = reinterpret_cast<const char*>(&qs[0][0][0]);
   for (int h0 = 0; h0 < R; h0 += kDenHeads) {
     const int nb = min(kDenHeads, R - h0);
-    float wcur[16];
-    load_w(kh * R + h0, wcur);
+    float wcur[16], lcur[3];
+    load_w(kh * R + h0, wcur, lcur);
     __syncthreads();
     // each wave copies 8 rows (1 KiB) per call: lane l -> row 8 j + l / 8, slot
     // l % 8 = k8 ^ (l / 8); heads past the batch reload its last head (never read)
@@ -156,8 +176,8 @@ __global__ __launch_bounds__(256, 2) void k2_den_bwd(const uint16_t* __restrict_
 #pragma unroll 1
     for (int hl = 0; hl < nb; ++hl) {
       const int hh = h0 + hl, h = kh * R + hh;
-      float wnext[16];
-      load_w(kh * R + h0 + min(hl + 1, nb - 1), wnext);
+      float wnext[16], lnext[3];
+      load_w(kh * R + h0 + min(hl + 1, nb - 1), wnext, lnext);
       float* part = dwz + (cb * R + hh) * kFP;  // offsets below are unsigned 32-bit
       if (w < 3) {
         f32x16 H = f32x16{};
@@ -198,16 +218,18 @@ __global__ __launch_bounds__(256, 2) void k2_den_bwd(const uint16_t* __restrict_
         if (s == 0) {
 #pragma unroll
           for (int n = 0; n < 2; ++n) part[1 + 32 * n + row] = pz[n] * L[n][0];
-          dc[0] = fmaf(wcur[0], L[0][0], dc[0]);
-          dl1 = fmaf(wcur[1], L[1][0], dl1);
+          dc[0] = fmaf(lcur[0], L[0][0], dc[0]);
+          dl1 = fmaf(lcur[1], L[1][0], dl1);
           if (row == 0) {
-            dl2 = fmaf(wcur[2], L[2][0], dl2);
+            dl2 = fmaf(lcur[2], L[2][0], dl2);
             part[0] = pz[2] * L[2][0];
           }
         }
       }
 #pragma unroll
       for (int i = 0; i < 16; ++i) wcur[i] = wnext[i];
+#pragma unroll
+      for (int i = 0; i < 3; ++i) lcur[i] = lnext[i];
       (void)h;
     }
   }
