@@ -32,6 +32,8 @@ import torch  # noqa: E402
 
 F_LOGICAL = 2145  # 1 + 64 + 2080 features
 DA = 65  # value columns + the denominator column
+DA_MC = 64  # columns the matrix-core state kernels contract (the denominator column runs
+# apart, as a 64 x 64 pair matrix per chunk, in k2_fwd_prep / k2_den_bwd / k2_den_scan)
 BF16_PEAK_TFLOPS = 2516.6  # MI355X dense bf16 MFMA (256 CU x 2.4 GHz x 4096 FLOP/clk)
 METRIC = "OAL attn fwd+bwd tokens/s at N=4096 d=64 bf16; % bf16 MFMA peak"
 
@@ -42,8 +44,11 @@ def credited_flops(kernel: str, b: int, hq: int, hkv: int, n: int) -> float:
     fwd:  T_c update 2*F*DA per kv token; readout 2*F*DA per query token
     bwd:  dCarry and dphi_Q 2*F*DA each per query token; dphi_K and dU
           2*F*DA each per kv token.   Sum = 6*F*DA*B*N*(Hq+Hkv).
+    The matrix-core kernels (k2_*) are credited with the DA_MC = 64 value
+    columns they contract; the denominator column's work is done elsewhere.
     """
     unit = 2.0 * F_LOGICAL * DA
+    mc = 2.0 * F_LOGICAL * DA_MC
     q_tok = b * hq * n
     kv_tok = b * hkv * n
     return {
@@ -53,13 +58,13 @@ def credited_flops(kernel: str, b: int, hq: int, hkv: int, n: int) -> float:
         "k_q_bwd": unit * q_tok,
         "k_kv_bwd": 2 * unit * kv_tok,
         # matrix-core kernels
-        "k2_state_fwd": unit * kv_tok,
-        "k2_state_fwd_totals": unit * kv_tok,
-        "k2_out_fwd": unit * q_tok,
-        "k2_state_bwd": unit * q_tok,
-        "k2_state_bwd_totals": unit * q_tok,
-        "k2_q_fold": unit * q_tok,
-        "k2_kv_fold": 2 * unit * kv_tok,
+        "k2_state_fwd": mc * kv_tok,
+        "k2_state_fwd_totals": mc * kv_tok,
+        "k2_out_fwd": mc * q_tok,
+        "k2_state_bwd": mc * q_tok,
+        "k2_state_bwd_totals": mc * q_tok,
+        "k2_q_fold": mc * q_tok,
+        "k2_kv_fold": 2 * mc * kv_tok,
     }.get(kernel, 0.0)
 
 
