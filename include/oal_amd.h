@@ -22,6 +22,9 @@
  *   out [B][Hq][N][64] (dtype);  num [B][Hq][N][64] f32;  den [B][Hq][N] f32
  *   labels [Hq][64] int32 in [0, groups);  c0 [Hq];  lam [Hq][groups];
  *   gam [Hq][groups][groups]  (all f32);  1 <= groups <= 64
+ * The q, k, v, out, num, den, saved, workspace, dout, dnum, dden, dq, dk and dv
+ * pointers must be 16-byte aligned (the kernels move rows with 16-byte accesses);
+ * a misaligned one is rejected with an error, before anything is enqueued.
  *
  * Return value: 0 on success, nonzero on invalid arguments or a launch error;
  * oal_last_error() then describes the failure (thread-local string).

@@ -107,6 +107,15 @@ def _ptr(t: torch.Tensor | None):
     return None if t is None else ctypes.c_void_p(t.data_ptr())
 
 
+def _aligned(t: torch.Tensor | None) -> torch.Tensor | None:
+    """t, or a fresh copy when its data pointer is not 16-byte aligned (the
+    kernels move rows with 16-byte accesses; a view with an odd storage offset
+    would otherwise be rejected by the library)."""
+    if t is None or t.data_ptr() % 16 == 0:
+        return t
+    return t.clone(memory_format=torch.contiguous_format)
+
+
 def _dtype_code(dtype: torch.dtype) -> int:
     if dtype == torch.float32:
         return DTYPE_F32
@@ -171,6 +180,7 @@ def forward(q, k, v, labels, c0, lam, gam, *, scale: float, floor: float, precis
     """
     lib = load_library()
     _require_device(q, k, v, labels, c0, lam, gam)
+    q, k, v = (_aligned(t) for t in (q, k, v))
     b, hq, n, d = q.shape
     hkv = k.shape[1]
     assert d == HEAD_DIM and v.shape[-1] == HEAD_DIM
@@ -230,6 +240,8 @@ def backward(q, k, v, labels, c0, lam, gam, num, den, saved, dout, dnum, dden, *
             dnum = dnum.to(torch.float32).contiguous()
         if dden is not None:
             dden = dden.to(torch.float32).contiguous()
+        q, k, v, num, den, saved, dout, dnum, dden = (
+            _aligned(t) for t in (q, k, v, num, den, saved, dout, dnum, dden))
         rc = lib.oal_backward(
             _ptr(q), _ptr(k), _ptr(v), _ptr(labels), _ptr(c0), _ptr(lam), _ptr(gam), groups,
             b, hq, hkv, n, code, pcode, float(scale), float(floor),

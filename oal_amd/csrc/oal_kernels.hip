@@ -833,6 +833,9 @@ int oal_feature_stride(void) { return oal::kFP; }
 
 int oal_chunk_size(void) { return oal::kC; }
 
+// The kernels move token rows and state tiles with 16-byte loads and stores.
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
 static int check_common(int groups, int precision) {
   if (groups < 1 || groups > 64) return fail("groups must be in [1, 64]");
   if (precision != OAL_PRECISION_FP32 && precision != OAL_PRECISION_BF16)
@@ -864,6 +867,9 @@ int oal_forward(const void* q, const void* k, const void* v, const int32_t* labe
   if (check_geometry(batch, q_heads, kv_heads, seq_len, dtype, &g)) return 1;
   if (!q || !k || !v || !labels || !c0 || !lam || !gam || !out || !num || !den || !saved)
     return fail("oal_forward: null pointer argument");
+  const void* ptrs[] = {q, k, v, num, den, out, saved};
+  for (const void* p : ptrs)
+    if (!aligned16(p)) return fail("oal_forward: tensor pointers must be 16-byte aligned");
   if (check_common(groups, precision)) return 1;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (use_mfma(precision, groups, g)) {
@@ -895,6 +901,9 @@ int oal_backward(const void* q, const void* k, const void* v, const int32_t* lab
   if (check_geometry(batch, q_heads, kv_heads, seq_len, dtype, &g)) return 1;
   if (!q || !k || !v || !labels || !c0 || !lam || !gam || !num || !den || !saved || !workspace)
     return fail("oal_backward: null pointer argument");
+  const void* ptrs[] = {q, k, v, num, den, saved, workspace, dout, dnum, dden, dq, dk, dv};
+  for (const void* p : ptrs)
+    if (p && !aligned16(p)) return fail("oal_backward: tensor pointers must be 16-byte aligned");
   if (check_common(groups, precision)) return 1;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (use_mfma(precision, groups, g)) {

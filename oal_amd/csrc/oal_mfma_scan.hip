@@ -464,11 +464,43 @@ __global__ __launch_bounds__(256) void k2_fwd_prep(const T* __restrict__ k, cons
   const int tok = ch * kC + j;
   const bool ok = tok < N;
   const size_t off = ((size_t)u * N + (ok ? tok : N - 1)) * kD + 16 * qq;
+  // 16 consecutive elements per thread as 16-byte vector loads, issued before
+  // any use (the row index is clamped, so every load is in bounds)
   float kv[16], vv[16];
+  if constexpr (sizeof(T) == 2) {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    u32x4 kw[2], vw[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      kw[i] = reinterpret_cast<const u32x4*>(k + off)[i];
+      vw[i] = reinterpret_cast<const u32x4*>(v + off)[i];
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        kv[8 * i + 2 * e] = __uint_as_float(kw[i][e] << 16);
+        kv[8 * i + 2 * e + 1] = __uint_as_float(kw[i][e] & 0xffff0000u);
+        vv[8 * i + 2 * e] = __uint_as_float(vw[i][e] << 16);
+        vv[8 * i + 2 * e + 1] = __uint_as_float(vw[i][e] & 0xffff0000u);
+      }
+  } else {
+    float4 kf[4], vf[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      kf[i] = reinterpret_cast<const float4*>(k + off)[i];
+      vf[i] = reinterpret_cast<const float4*>(v + off)[i];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      kv[4 * i] = kf[i].x, kv[4 * i + 1] = kf[i].y, kv[4 * i + 2] = kf[i].z, kv[4 * i + 3] = kf[i].w;
+      vv[4 * i] = vf[i].x, vv[4 * i + 1] = vf[i].y, vv[4 * i + 2] = vf[i].z, vv[4 * i + 3] = vf[i].w;
+    }
+  }
 #pragma unroll
   for (int e = 0; e < 16; ++e) {
-    kv[e] = ok ? to_f(k[off + e]) : 0.f;
-    vv[e] = ok ? to_f(v[off + e]) : 0.f;
+    kv[e] = ok ? kv[e] : 0.f;
+    vv[e] = ok ? vv[e] : 0.f;
   }
 #pragma unroll
   for (int e = 0; e < 16; ++e) {
@@ -499,11 +531,17 @@ __global__ __launch_bounds__(256) void k2_fwd_prep(const T* __restrict__ k, cons
     float* z = Zt + ((size_t)u * NB + ch) * kZt;
 #pragma unroll
     for (int i = 0; i < 16; ++i) z[(32 * mr + c32_row(i, l)) * kD + 32 * mc + row] = acc[i];
-    if (tid < kD) {
+    // sum_j k_jd: thread (d, quarter) sums 16 tokens, then the quarters in a fixed order
+    __shared__ float ksum[4][kD];
+    {
+      const int d = tid & 63, qt = tid >> 6;
       float sum = 0.f;
-      for (int j = 0; j < kC; ++j) sum += (float)kT[tid][j];
-      z[kD * kD + tid] = sum;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) sum += (float)kT[d][16 * qt + i];
+      ksum[qt][d] = sum;
     }
+    __syncthreads();
+    if (tid < kD) z[kD * kD + tid] = (ksum[0][tid] + ksum[1][tid]) + (ksum[2][tid] + ksum[3][tid]);
   }
 }
 

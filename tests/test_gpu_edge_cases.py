@@ -153,3 +153,34 @@ def test_irregular_shapes(b, hq, hkv, n):
     the 64-token chunk, 2 to 7 query heads per KV head, and scan plans whose
     segments do not divide the chunk count."""
     _run(b, hq, hkv, n, _labels(hq, 6, seed=n), seed=b + n)
+
+
+def test_misaligned_views_match_aligned_tensors():
+    """q, k, v whose data pointers are 2 bytes past a 16-byte boundary (views
+    into a larger buffer) give bit-identical outputs and gradients: the binding
+    copies them to aligned memory before the library's 16-byte row accesses."""
+    from oal_amd.hd_block_gemm_autograd import grouped_oal
+
+    dev = _dev()
+    labels = torch.arange(64).remainder(4).repeat(2, 1).to(torch.int32)
+    q, k, v, c0, lam, gam = _case(1, 2, 1, 130, labels, seed=5)
+
+    def run(shift):
+        outs = []
+        leaves = []
+        for t in (q, k, v):
+            buf = torch.zeros(t.numel() + shift, dtype=torch.bfloat16, device=dev)
+            x = buf[shift:].view(t.shape)
+            x.copy_(t.to(torch.bfloat16))
+            leaves.append(x.requires_grad_())
+        out, num, den = grouped_oal(*leaves, labels.to(dev), c0.to(dev), lam.to(dev), gam.to(dev), scale=0.125,
+                                    floor=0.0, precision="bf16")
+        (num.float().sum() + den.float().sum()).backward()
+        torch.cuda.synchronize()
+        return [out, num, den] + [x.grad for x in leaves], leaves
+
+    base, leaves0 = run(0)
+    mis, leaves1 = run(1)
+    assert leaves0[0].data_ptr() % 16 == 0 and leaves1[0].data_ptr() % 16 == 2
+    for a, b in zip(base, mis):
+        assert torch.equal(a, b)

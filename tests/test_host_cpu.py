@@ -57,6 +57,13 @@ def test_size_queries_and_argument_errors_without_a_gpu():
     rc = lib.oal_forward(None, None, None, None, None, None, None, 8, 1, 1, 1, 64, 7, 0, 0.1, 0.0,
                          None, None, None, None, None)
     assert rc != 0 and b"dtype" in lib.oal_last_error()
+    # misaligned tensor pointers are rejected before anything is enqueued (the
+    # pointers are never dereferenced on this path)
+    ok, odd = ctypes.c_void_p(1 << 20), ctypes.c_void_p((1 << 20) + 8)
+    small = (ctypes.c_float * 64)()
+    rc = lib.oal_forward(odd, ok, ok, small, small, small, small, 8, 1, 1, 1, 64, 0, 0, ctypes.c_float(0.1),
+                         ctypes.c_float(0.0), ok, ok, ok, ok, None)
+    assert rc != 0 and b"16-byte" in lib.oal_last_error()
 
 
 def _case(dtype=torch.float32):
