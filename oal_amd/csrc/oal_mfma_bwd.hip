@@ -450,8 +450,10 @@ __global__ __launch_bounds__(128, 2) void k2_kv_fold(const T* __restrict__ k, co
                                                      T* __restrict__ dk, T* __restrict__ dv) {
   __shared__ __attribute__((aligned(16))) __bf16 ring0[kFG * 1024], ring1[kFG * 1024], ring2[kFG * 1024],
       ring3[kFG * 1024];
-  __shared__ __attribute__((aligned(16))) __bf16 mz[kD][LD];
-  __shared__ float zl[kD];
+  // mz rows unpadded, 16-byte chunk c of row r stored at chunk c ^ (r & 7) (the
+  // fragment reads stay conflict-free); with the ring that is exactly 40 KiB, so
+  // four blocks (the register limit) fit a CU
+  __shared__ __attribute__((aligned(16))) __bf16 mz[kD][kD];
 
   const int ch = blockIdx.x, u = blockIdx.y, part = blockIdx.z;
   const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, s = l >> 5, row = l & 31;
@@ -490,9 +492,10 @@ __global__ __launch_bounds__(128, 2) void k2_kv_fold(const T* __restrict__ k, co
     const int d = mz_dim(r >> 5, r & 31);
     const int hi = d > c ? d : c, lo = d > c ? c : d;
     const float val = tz[1 + kD + pair_index(hi, lo)];
-    mz[r][c] = (__bf16)(d == c ? 2.f * val : val);
+    mz[r][(((c >> 3) ^ (r & 7)) << 3) | (c & 7)] = (__bf16)(d == c ? 2.f * val : val);
   }
-  if (tid < kD) zl[tid] = tz[1 + tid];
+  // z1 goes to LDS after the fold, into the then idle ring
+  const float zv = tz[1 + (tid & 63)];
   bf16x8 bfr[4];
 #pragma unroll
   for (int kk = 0; kk < 4; ++kk) bfr[kk] = frag8(v, rowoff + 16 * kk + 8 * s, ok);
@@ -501,6 +504,10 @@ __global__ __launch_bounds__(128, 2) void k2_kv_fold(const T* __restrict__ k, co
   for (int m = 0; m < kD; ++m) dx[m] = 0.f;
   static_assert(kTileElems <= kFG * 1024, "a fold tile fits one ring stage");
   fold_all<4, false>(bfr, x, dx, nullptr, ring, dTR + cbase, tid, l);
+  float* zl = reinterpret_cast<float*>(ring0);
+  __syncthreads();
+  if (tid < kD) zl[tid] = zv;
+  __syncthreads();
   // lane group s: dimensions 32 s .. 32 s + 31 of its token
   float full[32];
   combine_rotation_groups(dx, s, full);
@@ -513,7 +520,7 @@ __global__ __launch_bounds__(128, 2) void k2_kv_fold(const T* __restrict__ k, co
     f32x16 z = f32x16{};
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk)
-      z = mfma32(*reinterpret_cast<const bf16x8*>(&mz[32 * md + row][16 * kk + 8 * s]), kb[kk], z);
+      z = mfma32(*reinterpret_cast<const bf16x8*>(&mz[32 * md + row][((2 * kk + s) ^ (row & 7)) << 3]), kb[kk], z);
 #pragma unroll
     for (int i = 0; i < 16; ++i) full[16 * md + i] += z[i];
   }
