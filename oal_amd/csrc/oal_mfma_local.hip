@@ -214,14 +214,23 @@ __global__ __launch_bounds__(192, COEF ? 2 : 3) void k2_local_dq(const T* __rest
     for (int t = 0; t < 2; ++t)
       kt[dt][t] = *reinterpret_cast<const bf16x8*>(KT16 + ((size_t)u * kD + 32 * dt + row) * np + tok0 + 32 * jt +
                                                     16 * t + 8 * s);
+  // coefficient loads issued together: both labels, then every gam / lam entry
+  // unconditionally (group index clamped, so in bounds) and masked afterwards
   float cf[9][2];
+  int gd[2];
+#pragma unroll
+  for (int dt = 0; dt < 2; ++dt) gd[dt] = clamp_label(labels[h * kD + 32 * dt + row], G);
 #pragma unroll
   for (int dt = 0; dt < 2; ++dt) {
-    const int gd = clamp_label(labels[h * kD + 32 * dt + row], G);
 #pragma unroll
-    for (int h2 = 0; h2 < 8; ++h2)
-      cf[h2][dt] = h2 < G ? 2.f * scale * scale * gam[((size_t)h * G + gd) * G + h2] : 0.f;
-    cf[8][dt] = scale * lam[(size_t)h * G + gd];
+    for (int h2 = 0; h2 < 8; ++h2) cf[h2][dt] = gam[((size_t)h * G + gd[dt]) * G + min(h2, G - 1)];
+    cf[8][dt] = lam[(size_t)h * G + gd[dt]];
+  }
+#pragma unroll
+  for (int dt = 0; dt < 2; ++dt) {
+#pragma unroll
+    for (int h2 = 0; h2 < 8; ++h2) cf[h2][dt] = h2 < G ? 2.f * scale * scale * cf[h2][dt] : 0.f;
+    cf[8][dt] *= scale;
   }
   f32x16 dq[2] = {f32x16{}, f32x16{}};
 #pragma unroll
@@ -399,15 +408,34 @@ __global__ __launch_bounds__(192) void k2_local_dk(const T* __restrict__ q, cons
   f32x16 acc[2] = {f32x16{}, f32x16{}};
 
   for (int hh = 0; hh < R; ++hh) build_masks(mk[hh], labels, kh * R + hh, G, tid);
-  for (int e = tid; e < R * 9 * kD; e += 192) {
-    const int hh = e / (9 * kD), h2 = (e / kD) % 9, d = e % kD, h = kh * R + hh;
-    const int gd = clamp_label(labels[h * kD + d], G);
-    float c = 0.f;
-    if (h2 == 8)
-      c = scale * lam[(size_t)h * G + gd];
-    else if (h2 < G)
-      c = 2.f * scale * scale * gam[((size_t)h * G + gd) * G + h2];
-    cfl[hh][h2][d] = c;
+  {
+    // the coefficient table with every load of a thread in flight together:
+    // entries past R * 9 * 64 clamped (in bounds, unstored), the group index of
+    // gam clamped and masked afterwards
+    constexpr int kIt = (8 * 9 * kD + 191) / 192;
+    const int ne = R * 9 * kD;
+    int gd[kIt];
+#pragma unroll
+    for (int j = 0; j < kIt; ++j) {
+      const int e = min(tid + 192 * j, ne - 1);
+      const int hh = e / (9 * kD), d = e % kD;
+      gd[j] = clamp_label(labels[(kh * R + hh) * kD + d], G);
+    }
+    float cv[kIt];
+#pragma unroll
+    for (int j = 0; j < kIt; ++j) {
+      const int e = min(tid + 192 * j, ne - 1);
+      const int hh = e / (9 * kD), h2 = (e / kD) % 9, h = kh * R + hh;
+      cv[j] = h2 == 8 ? lam[(size_t)h * G + gd[j]] : gam[((size_t)h * G + gd[j]) * G + min(h2, G - 1)];
+    }
+#pragma unroll
+    for (int j = 0; j < kIt; ++j) {
+      const int e = tid + 192 * j;
+      if (e < ne) {
+        const int hh = e / (9 * kD), h2 = (e / kD) % 9, d = e % kD;
+        cfl[hh][h2][d] = h2 == 8 ? scale * cv[j] : (h2 < G ? 2.f * scale * scale * cv[j] : 0.f);
+      }
+    }
   }
   __syncthreads();
   for (int hh = 0; hh < R; ++hh) {
