@@ -661,14 +661,12 @@ __global__ __launch_bounds__(256) void k2_coef_grad(const float* __restrict__ dw
 #pragma unroll
   for (int j = 0; j < kJF; ++j) z[j] = dwqz[(size_t)h * kFP + min(t + 256 * j, kFeat - 1)];
   const float lc = coefs[(size_t)h * 73 + min(t, 72)];
+  int nat[kJS];
 #pragma unroll
-  for (int j = 0; j < kJS; ++j) {
-    const int sl = t + 256 * j;
-    if (sl < kS) {
-      const int n = kSlot.nat[sl];
-      if (n >= 0) wn[n] = a[j];
-    }
-  }
+  for (int j = 0; j < kJS; ++j) nat[j] = kSlot.nat[min(t + 256 * j, kS - 1)];
+#pragma unroll
+  for (int j = 0; j < kJS; ++j)
+    if (t + 256 * j < kS && nat[j] >= 0) wn[nat[j]] = a[j];
   if (t < 73) loc[t] = lc;
   __syncthreads();
   // plus the denominator state's partials (natural order)
