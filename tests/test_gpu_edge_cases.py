@@ -146,12 +146,13 @@ def test_partial_gradient_requests(grads):
             assert gp is None, name
 
 
-@pytest.mark.parametrize("b,hq,hkv,n", [(3, 6, 3, 1000), (1, 7, 1, 777), (5, 4, 2, 200)])
+@pytest.mark.parametrize("b,hq,hkv,n", [(3, 6, 3, 1000), (1, 7, 1, 777), (5, 4, 2, 200), (1, 2, 1, 4165)])
 def test_irregular_shapes(b, hq, hkv, n):
     """Unit counts B * Hkv = 9, 1, 10 (the XCD-ordered block mappings fall back to
     plain order when the block count is not a multiple of 8), N not a multiple of
     the 64-token chunk, 2 to 7 query heads per KV head, and scan plans whose
-    segments do not divide the chunk count."""
+    segments do not divide the chunk count. N = 4165 is 66 chunks: the
+    denominator prefix scans take a full 64-chunk tile, then a tile of two."""
     _run(b, hq, hkv, n, _labels(hq, 6, seed=n), seed=b + n)
 
 
