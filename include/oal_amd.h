@@ -103,8 +103,14 @@ int oal_forward(const void* q, const void* k, const void* v,
  * dout (dtype), dnum [B][Hq][N][64] f32 and dden [B][Hq][N] f32 may each be NULL
  * (no upstream gradient). dq, dk, dv (dtype) and the coefficient gradients
  * dc0 [Hq], dlam [Hq][groups], dgam [Hq][groups][groups] (f32, overwritten) may be
- * NULL when not requested. dgam[h][g(r)][g(c)] accumulates pair (r, c) with r >= c
- * only, the reference's gather routing (grouped_reference.py:89-93).
+ * NULL when not requested; dc0, dlam and dgam are requested together (all or
+ * none), and on the bf16 path dk and dv are too. dgam is the gradient of
+ * sum_{g,g'} gam[g][g'] s_g s_g' with gam a symmetric matrix: an off-diagonal
+ * entry carries the mean of the two routings of its pairs. (The reference's
+ * gather, grouped_reference.py:89-93, routes pair (r, c), r >= c, to
+ * [g(r)][g(c)] only; gradients reaching a factor L with gam = L L^T, or a
+ * per-pair coefficient, are the same under both.) Invalid combinations are
+ * refused before anything is enqueued.
  */
 int oal_backward(const void* q, const void* k, const void* v,
                  const int32_t* labels, const float* c0, const float* lam, const float* gam,

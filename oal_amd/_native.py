@@ -121,7 +121,106 @@ def _dtype_code(dtype: torch.dtype) -> int:
         return DTYPE_F32
     if dtype == torch.bfloat16:
         return DTYPE_BF16
-    raise TypeError("the HIP kernels take float32 or bfloat16 q, k, v")
+    raise RuntimeError("q, k and v must be float32 or bfloat16 for the HIP kernels")
+
+
+# ---------------------------------------------------------------------------
+# Argument checks. Every tensor is checked for type, dtype, shape, layout and
+# device before any pointer crosses the C ABI, as the reference's native op
+# checks its operands (oal_attention/csrc/hd_cublas_compat.cpp:47-61, 104-148):
+# the kernels trust the sizes they are given, so a short or mis-shaped buffer
+# would otherwise be read or written out of bounds on the device. Failures are
+# RuntimeError (the reference's TORCH_CHECK) and leave nothing enqueued.
+# ---------------------------------------------------------------------------
+def _check_tensor(t, name: str, *, dtype: torch.dtype, shape: tuple, device: torch.device | None = None) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise RuntimeError(f"{name} must be a torch.Tensor")
+    if t.layout != torch.strided:
+        raise RuntimeError(f"{name} must be strided")
+    if t.dtype != dtype:
+        raise RuntimeError(f"{name} must be {str(dtype).replace('torch.', '')}, got {str(t.dtype).replace('torch.', '')}")
+    if tuple(t.shape) != tuple(shape):
+        raise RuntimeError(f"{name} must have shape {list(shape)}, got {list(t.shape)}")
+    if not t.is_contiguous():
+        raise RuntimeError(f"{name} must be contiguous")
+    if device is not None and t.device != device:
+        raise RuntimeError(f"{name} must be on the same device as q ({device}), got {t.device}")
+
+
+def _check_bytes(t, name: str, nbytes: int, device: torch.device) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise RuntimeError(f"{name} must be a torch.Tensor")
+    if t.dtype != torch.uint8 or t.ndim != 1 or not t.is_contiguous():
+        raise RuntimeError(f"{name} must be a contiguous 1-D uint8 tensor")
+    if t.numel() < nbytes:
+        raise RuntimeError(f"{name} holds {t.numel()} bytes; {nbytes} are needed")
+    if t.device != device:
+        raise RuntimeError(f"{name} must be on the same device as q ({device}), got {t.device}")
+
+
+def _span(t: torch.Tensor) -> tuple[int, int]:
+    start = t.data_ptr()
+    return start, start + t.numel() * t.element_size()
+
+
+def _check_no_overlap(out: torch.Tensor, name: str, others: dict) -> None:
+    lo, hi = _span(out)
+    for other_name, t in others.items():
+        if t is None or t.device != out.device:
+            continue
+        a, b = _span(t)
+        if a < hi and lo < b:
+            raise RuntimeError(f"{name} must not overlap {other_name}")
+
+
+def check_forward_args(q, k, v, labels, c0, lam, gam) -> tuple[int, int, int, int, int]:
+    """Validate the forward operands; returns (B, Hq, Hkv, N, groups)."""
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        if not isinstance(t, torch.Tensor):
+            raise RuntimeError(f"{name} must be a torch.Tensor")
+        if t.ndim != 4:
+            raise RuntimeError(f"{name} must be rank 4 [B, H, N, {HEAD_DIM}]")
+    b, hq, n, d = q.shape
+    hkv = k.shape[1]
+    if min(b, hq, hkv, n) <= 0:
+        raise RuntimeError("batch, head counts and sequence length must be positive")
+    if hq % hkv != 0:
+        raise RuntimeError("query head count must be divisible by KV head count")
+    if d != HEAD_DIM:
+        raise RuntimeError(f"q, k and v must be padded to {HEAD_DIM} features")
+    _dtype_code(q.dtype)
+    dev = q.device
+    _check_tensor(q, "q", dtype=q.dtype, shape=(b, hq, n, HEAD_DIM))
+    _check_tensor(k, "k", dtype=q.dtype, shape=(b, hkv, n, HEAD_DIM), device=dev)
+    _check_tensor(v, "v", dtype=q.dtype, shape=(b, hkv, n, HEAD_DIM), device=dev)
+    if not isinstance(lam, torch.Tensor) or lam.ndim != 2:
+        raise RuntimeError("lam must be a [Hq, G] tensor")
+    groups = lam.shape[1]
+    if not 1 <= groups <= 64:
+        raise RuntimeError("the group count must be in [1, 64]")
+    _check_tensor(labels, "labels", dtype=torch.int32, shape=(hq, HEAD_DIM), device=dev)
+    _check_tensor(c0, "c0", dtype=torch.float32, shape=(hq,), device=dev)
+    _check_tensor(lam, "lam", dtype=torch.float32, shape=(hq, groups), device=dev)
+    _check_tensor(gam, "gam", dtype=torch.float32, shape=(hq, groups, groups), device=dev)
+    return b, hq, hkv, n, groups
+
+
+def check_backward_args(q, k, v, labels, c0, lam, gam, num, den, saved, dout, dnum, dden):
+    """Validate the VJP operands (dout, dnum and dden in the kernels' dtypes);
+    returns (B, Hq, Hkv, N, groups)."""
+    b, hq, hkv, n, groups = check_forward_args(q, k, v, labels, c0, lam, gam)
+    dev = q.device
+    _check_tensor(num, "num", dtype=torch.float32, shape=(b, hq, n, HEAD_DIM), device=dev)
+    _check_tensor(den, "den", dtype=torch.float32, shape=(b, hq, n, 1), device=dev)
+    if not isinstance(saved, torch.Tensor) or saved.dtype != torch.uint8 or saved.ndim != 1:
+        raise RuntimeError("saved must be the 1-D uint8 tensor the forward returned")
+    if dout is not None:
+        _check_tensor(dout, "dout", dtype=q.dtype, shape=(b, hq, n, HEAD_DIM), device=dev)
+    if dnum is not None:
+        _check_tensor(dnum, "dnum", dtype=torch.float32, shape=(b, hq, n, HEAD_DIM), device=dev)
+    if dden is not None:
+        _check_tensor(dden, "dden", dtype=torch.float32, shape=(b, hq, n, 1), device=dev)
+    return b, hq, hkv, n, groups
 
 
 def _require_device(*tensors: torch.Tensor) -> None:
@@ -174,26 +273,24 @@ def selftest() -> int:
 
 
 def forward(q, k, v, labels, c0, lam, gam, *, scale: float, floor: float, precision: str = "fp32"):
-    """Run the HIP forward. q [B,Hq,N,64], k/v [B,Hkv,N,64] contiguous, same dtype.
+    """Run the HIP forward. q [B,Hq,N,64], k/v [B,Hkv,N,64] contiguous, same dtype;
+    labels int32 [Hq,64]; c0 [Hq], lam [Hq,G], gam [Hq,G,G] float32.
 
     Returns (out [dtype], num f32, den f32 [B,Hq,N,1], saved uint8).
     """
     lib = load_library()
-    _require_device(q, k, v, labels, c0, lam, gam)
+    b, hq, hkv, n, groups = check_forward_args(q, k, v, labels, c0, lam, gam)
+    pcode = _precision_code(precision)
+    _require_device(q)
     q, k, v = (_aligned(t) for t in (q, k, v))
-    b, hq, n, d = q.shape
-    hkv = k.shape[1]
-    assert d == HEAD_DIM and v.shape[-1] == HEAD_DIM
     code = _dtype_code(q.dtype)
-    groups = lam.shape[1]
     dev = q.device
     with torch.cuda.device(dev):
-        pcode = _precision_code(precision)
         nbytes = lib.oal_forward_saved_bytes(b, hq, hkv, n, groups, code, pcode)
         if nbytes == 0:
             _check(1, lib, "oal_forward_saved_bytes")
-        out = torch.empty((b, hq, n, d), dtype=q.dtype, device=dev)
-        num = torch.empty((b, hq, n, d), dtype=torch.float32, device=dev)
+        out = torch.empty((b, hq, n, HEAD_DIM), dtype=q.dtype, device=dev)
+        num = torch.empty((b, hq, n, HEAD_DIM), dtype=torch.float32, device=dev)
         den = torch.empty((b, hq, n, 1), dtype=torch.float32, device=dev)
         saved = torch.empty((nbytes,), dtype=torch.uint8, device=dev)
         rc = lib.oal_forward(
@@ -208,22 +305,36 @@ def forward(q, k, v, labels, c0, lam, gam, *, scale: float, floor: float, precis
 def backward(q, k, v, labels, c0, lam, gam, num, den, saved, dout, dnum, dden, *, scale: float, floor: float,
              need_q: bool, need_k: bool, need_v: bool, need_coef: bool, precision: str = "fp32",
              workspace: torch.Tensor | None = None):
-    """Run the HIP VJP; returns (dq, dk, dv, dc0, dlam, dgam) with None where not requested."""
+    """Run the HIP VJP; returns (dq, dk, dv, dc0, dlam, dgam) with None where not requested.
+
+    dout is cast to q's dtype and dnum, dden to float32 (the kernels' operand
+    types) before the checks; every operand is then validated.
+    """
     lib = load_library()
-    _require_device(q, k, v, num, den, saved, dout, dnum, dden)
-    b, hq, n, d = q.shape
-    hkv = k.shape[1]
+    if isinstance(q, torch.Tensor):
+        if dout is not None:
+            dout = dout.to(q.dtype).contiguous()
+        if dnum is not None:
+            dnum = dnum.to(torch.float32).contiguous()
+        if dden is not None:
+            dden = dden.to(torch.float32)
+            dden = (dden.unsqueeze(-1) if dden.ndim == 3 else dden).contiguous()
+    b, hq, hkv, n, groups = check_backward_args(q, k, v, labels, c0, lam, gam, num, den, saved, dout, dnum, dden)
+    pcode = _precision_code(precision)
+    _require_device(q)
     code = _dtype_code(q.dtype)
-    groups = lam.shape[1]
     dev = q.device
     with torch.cuda.device(dev):
-        pcode = _precision_code(precision)
+        sbytes = lib.oal_forward_saved_bytes(b, hq, hkv, n, groups, code, pcode)
         wbytes = lib.oal_backward_workspace_bytes(b, hq, hkv, n, groups, code, pcode)
-        if wbytes == 0:
+        if sbytes == 0 or wbytes == 0:
             _check(1, lib, "oal_backward_workspace_bytes")
+        _check_bytes(saved, "saved", sbytes, dev)
+        if workspace is not None:
+            _check_bytes(workspace, "workspace", wbytes, dev)
+            _check_no_overlap(workspace, "workspace", {"q": q, "k": k, "v": v, "num": num, "den": den,
+                                                       "saved": saved, "dout": dout, "dnum": dnum, "dden": dden})
         work = workspace if workspace is not None else torch.empty((wbytes,), dtype=torch.uint8, device=dev)
-        if work.numel() < wbytes:
-            raise ValueError("workspace is smaller than oal_backward_workspace_bytes")
         dq = torch.empty_like(q) if need_q else None
         # the key-side kernels produce dk and dv together
         dk = torch.empty_like(k) if need_k or need_v else None
@@ -234,12 +345,6 @@ def backward(q, k, v, labels, c0, lam, gam, num, den, saved, dout, dnum, dden, *
             dgam = torch.empty_like(gam)
         else:
             dc0 = dlam = dgam = None
-        if dout is not None:
-            dout = dout.to(q.dtype).contiguous()
-        if dnum is not None:
-            dnum = dnum.to(torch.float32).contiguous()
-        if dden is not None:
-            dden = dden.to(torch.float32).contiguous()
         q, k, v, num, den, saved, dout, dnum, dden = (
             _aligned(t) for t in (q, k, v, num, den, saved, dout, dnum, dden))
         rc = lib.oal_backward(

@@ -767,7 +767,6 @@ int backward_impl(const Geometry& g, const void* q, const void* k, const void* v
                        sv.carry_z, w.G, w.Gz, g.Hq, g.Hkv, g.N, g.NB, static_cast<T*>(dq), w.dwq_part); });
   }
   if (need_coef) {
-    if (!(dc0 && dlam && dgam)) return fail("dc0, dlam and dgam must be given together");
     timed("k_dwq_reduce", st, [&] { hipLaunchKernelGGL(k_dwq_reduce, dim3((kFP + 255) / 256, g.Hq), dim3(256), 0, st, w.dwq_part, g.B, g.Hq, g.NB,
                        w.dwq); });
     timed("k_coef_grad", st, [&] { hipLaunchKernelGGL(k_coef_grad, dim3(g.Hq), dim3(256), 0, st, w.dwq, labels, groups, scale, dc0, dlam, dgam); });
@@ -905,8 +904,12 @@ int oal_backward(const void* q, const void* k, const void* v, const int32_t* lab
   for (const void* p : ptrs)
     if (p && !aligned16(p)) return fail("oal_backward: tensor pointers must be 16-byte aligned");
   if (check_common(groups, precision)) return 1;
+  // argument combinations the kernels cannot serve are refused before anything is enqueued
+  if ((dc0 || dlam || dgam) && !(dc0 && dlam && dgam)) return fail("dc0, dlam and dgam must be given together");
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (use_mfma(precision, groups, g)) {
+    if ((dk != nullptr) != (dv != nullptr))
+      return fail("oal_backward: dk and dv must be requested together on the matrix-core path");
     const oal::LaunchGeom lg = launch_geom(g);
     int rc;
     if (dtype == OAL_DTYPE_F32)

@@ -789,12 +789,14 @@ int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, cons
   });
   {
     const ScanPlan plan{w.S, w.SL, 0};
+    // without a coefficient gradient the scan forms no coefficient partials
     ScanArgs a{w.QT16, kTRows, w.GT16, kTRows, sv.wqs, sv.PR, g.U, g.Hq, g.Hkv, g.N, g.NB,
-               w.dTT, w.dTR, w.segtot, w.dwqs};
+               w.dTT, w.dTR, w.segtot, need_coef ? w.dwqs : nullptr};
     launch_scan<false>(plan, a, st, timed);
     // denominator state (pair-matrix form): per-chunk dCarry and coefficient
     // partials, then dTz as the exclusive chunk suffix
-    launch_den_bwd(g, w.QT16, w.GT16, kTRows, sv.gm, sv.lb, sv.ic, kIC, sv.PZ, sv.PZm, w.dCt, w.dwz, st, timed);
+    launch_den_bwd(g, w.QT16, w.GT16, kTRows, sv.gm, sv.lb, sv.ic, kIC, sv.PZ, sv.PZm, w.dCt,
+                   need_coef ? w.dwz : nullptr, st, timed);
     launch_den_scan(false, g, w.dCt, w.dTz, nullptr, st, timed);
   }
   {

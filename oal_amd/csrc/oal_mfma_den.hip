@@ -102,7 +102,7 @@ __global__ __launch_bounds__(256) void k2_den_scan(const float* __restrict__ tot
 // constant c0) feeds k2_den_scan<false>; the per-head coefficient partial
 //   dwz[u][c][h][nat] = PZ_c[nat] H_h[nat]
 // (natural order, every nat < kFeat) is summed over (batch, chunk) by
-// k2_dwq_reduce. QT16 / GT16 are the transposed bf16 operands of the backward
+// k2_dwq_reduce (dwz == nullptr: not formed). QT16 / GT16 are the transposed bf16 operands of the backward
 // scan ([q^T; 1; 0] and [G^T; Gz; 0], tokens >= N zero).
 // ---------------------------------------------------------------------------
 constexpr int kDenHeads = 8;  // query heads staged in LDS per batch
@@ -195,7 +195,7 @@ __global__ __launch_bounds__(256, 2) void k2_den_bwd(const uint16_t* __restrict_
         for (int i = 0; i < 16; ++i) {
           const int r = 32 * mr + c32_row(i, l), c = 32 * mc + row;
           dc[i] = fmaf((r == c ? 1.f : 2.f) * wcur[i], H[i], dc[i]);
-          if (r >= c) part[(unsigned)(1 + kD + pair_index(r, c))] = pz[i] * H[i];
+          if (dwz && r >= c) part[(unsigned)(1 + kD + pair_index(r, c))] = pz[i] * H[i];
         }
       } else {
         // A row 0 = gz (other rows zero); B = q^T rows 32 n + row (n < 2) or,
@@ -216,13 +216,15 @@ __global__ __launch_bounds__(256, 2) void k2_den_bwd(const uint16_t* __restrict_
           L[2] = mfma32(a, ones, L[2]);
         }
         if (s == 0) {
+          if (dwz) {
 #pragma unroll
-          for (int n = 0; n < 2; ++n) part[1 + 32 * n + row] = pz[n] * L[n][0];
+            for (int n = 0; n < 2; ++n) part[1 + 32 * n + row] = pz[n] * L[n][0];
+          }
           dc[0] = fmaf(lcur[0], L[0][0], dc[0]);
           dl1 = fmaf(lcur[1], L[1][0], dl1);
           if (row == 0) {
             dl2 = fmaf(lcur[2], L[2][0], dl2);
-            part[0] = pz[2] * L[2][0];
+            if (dwz) part[0] = pz[2] * L[2][0];
           }
         }
       }

@@ -30,12 +30,15 @@
 //           emitting every chunk's state; the backward weights the features by
 //           wq_h so that every head accumulates into the one state.
 //   MODE 2: one segment: MODE 1's output plus MODE 0's partials.
+// PART (backward, MODE 0 and 2): form the coefficient partials; without them
+// (no coefficient gradient requested) the forward state is not read. The
+// per-head products stay apart either way, so that the state -- and every
+// gradient -- is bit-identical whichever gradients are requested.
 // Emitted layouts per (unit, chunk), identical in both directions:
 //   R [kS/32][4][32][16 values] bf16, T [kKS][64 values][16 slots] bf16.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
-#include <stdlib.h>
 
 #include <algorithm>
 #include <cmath>
@@ -58,7 +61,7 @@ constexpr size_t kChunkElems = (size_t)kKS * 64 * 16;
 
 }  // namespace
 
-template <bool FWD, int MODE, int TPW, int NW>
+template <bool FWD, int MODE, int TPW, int NW, bool PART>
 __global__ __launch_bounds__(64 * NW, NW / 2) void k2_scan(const uint16_t* __restrict__ F, int frows,
                                                const uint16_t* __restrict__ V, int vrows,
                                                const float* __restrict__ wqs, const uint16_t* __restrict__ PRin,
@@ -66,8 +69,8 @@ __global__ __launch_bounds__(64 * NW, NW / 2) void k2_scan(const uint16_t* __res
                                                int Sg, uint16_t* __restrict__ outT, uint16_t* __restrict__ outR,
                                                float* __restrict__ segtot, float* __restrict__ dwqs) {
   constexpr bool EMIT = MODE != 0;
-  constexpr bool PARTIALS = !FWD && MODE != 1;
-  constexpr bool SPLIT = PARTIALS;  // per-head products kept apart (needed for the partials)
+  constexpr bool SPLIT = !FWD && MODE != 1;  // per-head products kept apart (needed for the partials)
+  constexpr bool PARTIALS = SPLIT && PART;
   static_assert(!SPLIT || TPW == 1, "the per-head products fit registers for one tile per wave");
   constexpr int TG = scan_tile_groups(TPW, NW);
   constexpr int kSTiles = NW;                // slot tiles (waves) per block
@@ -355,6 +358,8 @@ __global__ __launch_bounds__(64 * NW, NW / 2) void k2_scan(const uint16_t* __res
       for (int n = 0; n < 2; ++n)
 #pragma unroll
         for (int i = 0; i < 16; ++i) acc[0][n][i] = fmaf(wt, hT[n][i], acc[0][n][i]);
+    }
+    if constexpr (PARTIALS) {
       // four independent partial sums (a fixed order), not one 32-long chain
       float dp[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -555,25 +560,19 @@ constexpr int scan_tpw(bool fwd, int mode) { return (mode == 1 || fwd) ? 2 : 1; 
 constexpr int scan_nw(bool fwd, int mode) { return 4; }
 
 ScanPlan scan_plan(int U, int NB, size_t scratch_bytes, bool fwd) {
-  // Segment count from a model of block rounds: each kernel runs two blocks
-  // per CU, a block's time is proportional to its chunks, and a partial last
-  // round costs a full one; each segment adds a little carry traffic (a replay
-  // block reads the totals of the segments on one side of its own).
-  // OAL_SCAN_SEGMENTS overrides the count (for tuning and tests).
-  int cus = 256;
-  {
-    int dev = 0, n = 0;
-    if (hipGetDevice(&dev) == hipSuccess &&
-        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
-      cus = n;
-  }
-  const double slots = 2.0 * cus;
+  // Segment count from a model of block rounds on MI355X's 256 CUs: each
+  // kernel runs two blocks per CU, a block's time is proportional to its
+  // chunks, and a partial last round costs a full one; each segment adds a
+  // little carry traffic (a replay block reads the totals of the segments on
+  // one side of its own). A function of the geometry alone, so that a size
+  // query and the launch it sizes always agree.
+  constexpr double kSlots = 2.0 * 256;
   const size_t seg_bytes = sizeof(float) * (size_t)U * kS * kD;
   int cap = NB;
   if (scratch_bytes != (size_t)-1) cap = (int)std::min<size_t>((size_t)NB, scratch_bytes / seg_bytes);
   if (cap < 1) cap = 1;
   auto rounds = [&](int mode, int S) {
-    return std::ceil(scan_tile_groups(scan_tpw(fwd, mode), scan_nw(fwd, mode)) * (double)U * S / slots);
+    return std::ceil(scan_tile_groups(scan_tpw(fwd, mode), scan_nw(fwd, mode)) * (double)U * S / kSlots);
   };
   int best_S = 1;
   double best = 0.0;
@@ -585,7 +584,6 @@ ScanPlan scan_plan(int U, int NB, size_t scratch_bytes, bool fwd) {
       best_S = S;
     }
   }
-  if (const char* env = getenv("OAL_SCAN_SEGMENTS")) best_S = std::max(1, std::min(cap, atoi(env)));
   ScanPlan p;
   p.SL = (NB + best_S - 1) / best_S;
   p.S = (NB + p.SL - 1) / p.SL;
@@ -593,27 +591,39 @@ ScanPlan scan_plan(int U, int NB, size_t scratch_bytes, bool fwd) {
   return p;
 }
 
-template <bool FWD>
-void launch_scan(const ScanPlan& p, const ScanArgs& a, hipStream_t st, const Timer& timed) {
+template <bool FWD, bool PART>
+static void launch_scan_impl(const ScanPlan& p, const ScanArgs& a, hipStream_t st, const Timer& timed) {
   constexpr int T0 = scan_tpw(FWD, 0), T1 = scan_tpw(FWD, 1), T2 = scan_tpw(FWD, 2);
   constexpr int W0 = scan_nw(FWD, 0), W1 = scan_nw(FWD, 1), W2 = scan_nw(FWD, 2);
   auto grid = [&](int tpw, int nw) { return dim3((unsigned)(scan_tile_groups(tpw, nw) * a.U * p.S)); };
   const char* name = FWD ? "k2_state_fwd" : "k2_state_bwd";
   if (p.S == 1) {
     timed(name, st, [&] {
-      hipLaunchKernelGGL((k2_scan<FWD, 2, T2, W2>), grid(T2, W2), dim3(64 * W2), 0, st, a.F, a.frows, a.V, a.vrows, a.wqs, a.PR,
-                         nullptr, a.Hq, a.Hkv, a.N, a.NB, p.SL, p.S, a.outT, a.outR, nullptr, a.dwqs);
+      hipLaunchKernelGGL((k2_scan<FWD, 2, T2, W2, PART>), grid(T2, W2), dim3(64 * W2), 0, st, a.F, a.frows, a.V,
+                         a.vrows, a.wqs, a.PR, nullptr, a.Hq, a.Hkv, a.N, a.NB, p.SL, p.S, a.outT, a.outR, nullptr,
+                         a.dwqs);
     });
     return;
   }
   timed(FWD ? "k2_state_fwd_totals" : "k2_state_bwd_totals", st, [&] {
-    hipLaunchKernelGGL((k2_scan<FWD, 0, T0, W0>), grid(T0, W0), dim3(64 * W0), 0, st, a.F, a.frows, a.V, a.vrows, a.wqs, a.PR,
-                       nullptr, a.Hq, a.Hkv, a.N, a.NB, p.SL, p.S, nullptr, nullptr, a.segtot, a.dwqs);
+    hipLaunchKernelGGL((k2_scan<FWD, 0, T0, W0, PART>), grid(T0, W0), dim3(64 * W0), 0, st, a.F, a.frows, a.V,
+                       a.vrows, a.wqs, a.PR, nullptr, a.Hq, a.Hkv, a.N, a.NB, p.SL, p.S, nullptr, nullptr, a.segtot,
+                       a.dwqs);
   });
   timed(name, st, [&] {
-    hipLaunchKernelGGL((k2_scan<FWD, 1, T1, W1>), grid(T1, W1), dim3(64 * W1), 0, st, a.F, a.frows, a.V, a.vrows, a.wqs, a.PR,
-                       a.segtot, a.Hq, a.Hkv, a.N, a.NB, p.SL, p.S, a.outT, a.outR, nullptr, nullptr);
+    hipLaunchKernelGGL((k2_scan<FWD, 1, T1, W1, PART>), grid(T1, W1), dim3(64 * W1), 0, st, a.F, a.frows, a.V,
+                       a.vrows, a.wqs, a.PR, a.segtot, a.Hq, a.Hkv, a.N, a.NB, p.SL, p.S, a.outT, a.outR, nullptr,
+                       nullptr);
   });
+}
+
+template <bool FWD>
+void launch_scan(const ScanPlan& p, const ScanArgs& a, hipStream_t st, const Timer& timed) {
+  // the backward forms the coefficient partials only when dwqs is given
+  if (!FWD && a.dwqs != nullptr)
+    launch_scan_impl<FWD, true>(p, a, st, timed);
+  else
+    launch_scan_impl<FWD, false>(p, a, st, timed);
 }
 
 template void launch_scan<true>(const ScanPlan&, const ScanArgs&, hipStream_t, const Timer&);

@@ -4,10 +4,12 @@ Mirrors the reference surface ``oal_attention/grouped_quadratic.py:277-397``:
 the same arguments, validation rules and error types, the same factor ->
 (c0, lam, Gam) expansion (kept in torch so autograd reaches the factor), the
 same return conventions. ``execution="triton"`` and ``"auto"`` run the
-hand-written gfx950 HIP kernels (there is no Triton here). The pure-torch
-``"reference"`` execution of the original is a CPU implementation; this
-package ships no CPU compute path, so ``"reference"`` raises and points to the
-test oracle instead.
+hand-written gfx950 HIP kernels (there is no Triton here). ``"reference"`` -- in
+the original a pure-torch evaluation in the working dtype on any device
+(grouped_quadratic.py:332-355), which the caller's quality sessions use on GPU
+tensors (qwen_lora_experiment/attention/grouped.py:125-152, 244-247) -- runs the
+fp32 HIP kernels on q, k, v cast to float32 (the 1e-5 fp32 parity route). This
+package ships no CPU compute path: CPU tensors raise under every execution.
 """
 
 from __future__ import annotations
@@ -227,25 +229,41 @@ def oal_attention(
         if not math.isfinite(resolved_scale):
             raise ValueError("scale must be finite")
 
-    if execution == "reference":
-        raise RuntimeError(
-            "execution='reference' is the reference's pure-torch CPU path; oal_amd ships only the "
-            "gfx950 HIP kernels (use execution='auto' on a ROCm device)"
-        )
     if q.device.type != "cuda" or torch.version.hip is None:
+        if execution == "reference":
+            raise RuntimeError(
+                "execution='reference' runs the fp32 HIP kernels and requires ROCm device input; oal_amd "
+                "ships no CPU compute path (the pure-torch formula is test infrastructure only)"
+            )
         raise RuntimeError("grouped quadratic HIP execution requires ROCm device input")
-    if q.dtype not in _HIP_INPUT_DTYPES:
-        raise TypeError("grouped quadratic HIP execution supports float16, bfloat16 and float32")
-    if factor.dtype != torch.float32:
-        raise TypeError("grouped quadratic HIP factor must use FP32")
-    if q.shape[-1] > 64 or v.shape[-1] > 64:
-        raise ValueError("grouped quadratic HIP execution supports D<=64")
-    constant, linear, quadratic = _expand_factor_coefficients(
-        factor, query_heads=q.shape[1], gmax=gmax, kernel_eps=resolved_eps, working_dtype=torch.float32
-    )
-    output, numerator, denominator = grouped_oal(
-        q, k, v, dim_groups, constant, linear, quadratic, scale=resolved_scale, floor=0.0
-    )
+    if execution == "reference":
+        # the reference evaluates in the working dtype (:332-355); the HIP reference
+        # route is the fp32 kernels, so an FP64 working dtype cannot be honoured
+        if working_dtype != torch.float32:
+            raise TypeError("grouped quadratic HIP reference execution computes in FP32; FP64 inputs are unsupported")
+        if q.shape[-1] > 64 or v.shape[-1] > 64:
+            raise ValueError("grouped quadratic HIP execution supports D<=64")
+        q_work, k_work, v_work = (t.to(dtype=working_dtype) for t in (q, k, v))
+        constant, linear, quadratic = _expand_factor_coefficients(
+            factor, query_heads=q.shape[1], gmax=gmax, kernel_eps=resolved_eps, working_dtype=working_dtype
+        )
+        output, numerator, denominator = grouped_oal(
+            q_work, k_work, v_work, dim_groups, constant, linear, quadratic, scale=resolved_scale, floor=0.0,
+            precision="fp32",
+        )
+    else:
+        if q.dtype not in _HIP_INPUT_DTYPES:
+            raise TypeError("grouped quadratic HIP execution supports float16, bfloat16 and float32")
+        if factor.dtype != torch.float32:
+            raise TypeError("grouped quadratic HIP factor must use FP32")
+        if q.shape[-1] > 64 or v.shape[-1] > 64:
+            raise ValueError("grouped quadratic HIP execution supports D<=64")
+        constant, linear, quadratic = _expand_factor_coefficients(
+            factor, query_heads=q.shape[1], gmax=gmax, kernel_eps=resolved_eps, working_dtype=torch.float32
+        )
+        output, numerator, denominator = grouped_oal(
+            q, k, v, dim_groups, constant, linear, quadratic, scale=resolved_scale, floor=0.0
+        )
 
     if not (bool(torch.isfinite(numerator).all()) and bool(torch.isfinite(denominator).all())):
         raise RuntimeError("Grouped Quadratic result must be finite")

@@ -3,9 +3,13 @@
 The benchmark's model-step workload (random init, no checkpoint is loaded): hidden
 896, 24 layers, 14 query / 2 KV heads of dimension 64, SwiGLU MLP 4864, vocab
 151936, RMSNorm (eps 1e-6), rotary embeddings (theta 1e6, rotate-half form),
-tied input/output embeddings; LoRA of rank 16 on the q/k/v/o projections, all
-other weights frozen; each decoder layer runs under non-reentrant activation
-checkpointing, so the backward recomputes the attention forward.
+tied input/output embeddings; LoRA of rank 16 on the q/k/v/o projections and a
+trainable fp32 OAL factor per layer ([14, 45], one packed lower-triangular factor
+per query head, as the reference's kernel parameter bank holds one nn.Parameter
+per head, qwen_lora_experiment/kernel_parameters.py:115-128), all other weights
+frozen; each decoder layer runs under non-reentrant activation checkpointing, so
+the backward recomputes the attention forward. The training step therefore runs
+the operator's coefficient-gradient kernels, as the reference's does.
 
 It mirrors the reference adapter chain around the operator:
 * the Qwen projection / RoPE shell (qwen_lora_experiment/attention/common.py:375-415,
@@ -138,7 +142,8 @@ class OALAttention(nn.Module):
         self.v_proj = LoRALinear(cfg.hidden_size, hkv * d, bias=True, **lora)
         self.o_proj = LoRALinear(hq * d, cfg.hidden_size, bias=False, **lora)
         self.register_buffer("dim_groups", seeded_layer_groups(cfg, gen), persistent=True)
-        self.register_buffer("factor", seeded_layer_factor(cfg, gen), persistent=True)
+        # trainable, kept in fp32 whatever the model's compute dtype
+        self.factor = nn.Parameter(seeded_layer_factor(cfg, gen))
         self.kernel_eps = cfg.kernel_eps
         # "triton": the configured fast precision (the matrix-core kernels by
         # default); "reference": the fp32 kernels, selected for a quality
@@ -232,9 +237,11 @@ class QwenOALModel(nn.Module):
                 nn.init.zeros_(p)
 
     def cast_parameters_(self, dtype: torch.dtype) -> "QwenOALModel":
-        """Casts every parameter (not the buffers: the factors stay fp32, the groups int32)."""
-        for p in self.parameters():
-            p.data = p.data.to(dtype)
+        """Casts every parameter except the OAL factors (they stay fp32, as the
+        reference's kernel bank keeps them; the dim-group buffers stay int32)."""
+        for name, p in self.named_parameters():
+            if not name.endswith("attn.factor"):
+                p.data = p.data.to(dtype)
         return self
 
     def load_group_asset(self, asset) -> "QwenOALModel":
@@ -243,13 +250,26 @@ class QwenOALModel(nn.Module):
         for layer_id in asset.layer_ids_zero_based:
             attn = self.layers[layer_id].attn
             attn.dim_groups = asset.dim_groups_for_layer(layer_id).to(attn.dim_groups.device)
-            attn.factor = asset.packed_grouped_factor_for_layer(layer_id).to(attn.factor.device)
+            with torch.no_grad():
+                attn.factor.copy_(asset.packed_grouped_factor_for_layer(layer_id))
             attn.kernel_eps = asset.epsilon
             attn._prepared.clear()
         return self
 
     def lora_parameters(self):
         return [p for n, p in self.named_parameters() if n.endswith("lora_a") or n.endswith("lora_b")]
+
+    def oal_parameters(self):
+        """The per-layer OAL factors (trainable, fp32)."""
+        return [layer.attn.factor for layer in self.layers]
+
+    def optimizer(self, lora_lr: float = 1e-4, kernel_lr: float = 1e-3) -> torch.optim.Optimizer:
+        """AdamW with separate LoRA and OAL-factor groups (the reference's pilot optimizer
+        keeps the two learning rates apart, qwen_lora_experiment/model_setup.py:462-560)."""
+        return torch.optim.AdamW([
+            {"params": self.lora_parameters(), "lr": lora_lr},
+            {"params": self.oal_parameters(), "lr": kernel_lr},
+        ])
 
     def forward(self, tokens: torch.Tensor) -> torch.Tensor:
         """tokens [B, N] -> logits [B, N, vocab] (output head tied to the embedding)."""

@@ -10,10 +10,19 @@ a sample:
 * config 3: B=1, N=32768, forward + backward (long-context state carry).
 
 Tolerance (the bf16-mode bar): rel-L2 <= 2e-2 against the fp32
-oracle evaluated on the same bf16-rounded q, k, v. `out` is compared where the
-oracle's |den| > 1 (elsewhere out = num / den is ill-conditioned); the upstream
-dO is kept on tokens whose denominator is not a near-cancelling sum, the same
-conditioning mask as tests/test_gpu_parity.py.
+oracle evaluated on the same bf16-rounded q, k, v.
+
+The config coefficients (c0 = 1, lam ~ U(0.5, 1.5), Gam_gh ~ U(0, 0.5) for g <= h,
+mirrored) are not PSD: every head's Gam has a negative eigenvalue, and the oracle
+finds 1, 19 and 7 tokens with den <= 0 at configs 1, 2 and 3 (min den -2.08,
+-3.50, -0.94). The reference's HD runtime raises on such an output
+(hd_block_gemm_runtime.py:392-408); its public entry points take a PSD factor
+and cannot receive these coefficients at all. The tests time and compare the
+operator on them anyway, with two masks whose excluded-token counts are printed
+and bounded by 0.1%: `out` is compared where the oracle's |den| > 1 (4, 36 and
+16 tokens excluded; elsewhere out = num / den is ill-conditioned), and the
+upstream dO is kept on tokens whose denominator is not a near-cancelling sum
+(26 and 107 tokens excluded at configs 1 and 2, 41 at config 3).
 """
 
 import os
@@ -42,9 +51,18 @@ def rel(a, b):
     return float((a - b).norm() / b.norm())
 
 
+def _assert_few_excluded(keep, what, bound=1e-3):
+    dropped = int((~keep).sum())
+    print(f"{what}: {dropped} of {keep.numel()} tokens excluded", flush=True)
+    assert dropped <= bound * keep.numel(), (what, dropped, keep.numel())
+    return dropped
+
+
 def _well_conditioned(q32, k32, v32, wq, den_r, max_cond=20.0):
     _, _, den_abs = go.chunked_forward(q32.abs(), k32.abs(), v32, wq.abs(), chunk=64)
-    return (den_r.abs() > 1.0) & (den_abs <= max_cond * den_r.abs())
+    keep = (den_r.abs() > 1.0) & (den_abs <= max_cond * den_r.abs())
+    _assert_few_excluded(keep, "dO conditioning")
+    return keep
 
 
 def _inputs(config, dev):
@@ -55,7 +73,11 @@ def _inputs(config, dev):
 
 
 def _forward_errors(out, num, den, out_r, num_r, den_r):
-    ok = (den_r.abs() > 1.0).expand_as(out_r)
+    nonpos = int((den_r <= 0).sum())
+    print(f"oracle den <= 0 on {nonpos} tokens (the reference would raise on this input)", flush=True)
+    ok = den_r.abs() > 1.0
+    _assert_few_excluded(ok, "out comparison")
+    ok = ok.expand_as(out_r)
     return {"num": rel(num, num_r), "den": rel(den, den_r), "out": rel(out.float().cpu()[ok], out_r[ok])}
 
 

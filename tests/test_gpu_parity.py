@@ -172,9 +172,30 @@ def test_oal_attention_factor_gradient_matches_dense_oracle():
 
 
 def _well_conditioned(q32, k32, v32, wq, den_r, max_cond=20.0):
-    """Tokens whose denominator is not a near-cancelling sum of feature terms."""
+    """Tokens whose denominator is not a near-cancelling sum of feature terms.
+
+    The config coefficients are not PSD (every head's Gam has a negative
+    eigenvalue), so some denominators cancel or even cross zero; the mask keeps
+    every other token and asserts that it drops at most 1% of them (the short
+    sequences here; the first tokens' denominators are sums of few terms --
+    at the full config shapes the bound is 0.1%)."""
     _, _, den_abs = go.chunked_forward(q32.abs(), k32.abs(), v32, wq.abs(), chunk=64)
-    return (den_r.abs() > 1.0) & (den_abs <= max_cond * den_r.abs())
+    keep = (den_r.abs() > 1.0) & (den_abs <= max_cond * den_r.abs())
+    _assert_few_excluded(keep, "dO conditioning")
+    return keep
+
+
+def _assert_few_excluded(keep, what, bound=1e-2):
+    dropped = int((~keep).sum())
+    print(f"{what}: {dropped} of {keep.numel()} tokens excluded", flush=True)
+    assert dropped <= bound * keep.numel(), (what, dropped, keep.numel())
+
+
+def _out_mask(den_r):
+    """out = num / den is ill-conditioned where den crosses zero: compare it where |den| > 1."""
+    ok = den_r.abs() > 1.0
+    _assert_few_excluded(ok, "out comparison")
+    return ok
 
 
 def _bf16_case(batch, seq_len, seed=0):
@@ -194,7 +215,7 @@ def test_bf16_config1_forward_matches_fp32_oracle():
     out_r, num_r, den_r = go.chunked_forward(inp["q"], inp["k"], inp["v"], wq, chunk=64)
     assert rel(num, num_r) <= BF16_TOL
     assert rel(den, den_r) <= BF16_TOL
-    ok = den_r.abs() > 1.0  # out is ill-conditioned where den crosses zero
+    ok = _out_mask(den_r)
     assert rel(out.float().cpu()[ok.expand_as(out_r)], out_r[ok.expand_as(out_r)]) <= BF16_TOL
 
 
@@ -242,7 +263,7 @@ def test_bf16_matrix_core_forward_matches_fp32_oracle(n):
     wq = go.feature_coefficients(inp["groups"], inp["c0"], inp["lam"], inp["gam"], scale=inp["scale"], head_dim=64)
     out_r, num_r, den_r = go.chunked_forward(q32, k32, v32, wq, chunk=64)
     e_num, e_den = rel(num, num_r), rel(den, den_r)
-    ok = den_r.abs() > 1.0
+    ok = _out_mask(den_r)
     e_out = rel(out.float().cpu()[ok.expand_as(out_r)], out_r[ok.expand_as(out_r)])
     print(f"bf16 mfma forward N={n}: num {e_num:.2e} den {e_den:.2e} out {e_out:.2e}")
     assert e_num <= BF16_TOL and e_den <= BF16_TOL and e_out <= BF16_TOL
@@ -286,17 +307,19 @@ def test_bf16_matrix_core_backward_matches_fp32_oracle(batch, n, upstream):
     assert all(e <= BF16_TOL for e in errs.values()), errs
 
 
-@pytest.mark.parametrize("segments", ["1", "3"])
-def test_bf16_state_scan_segmentation_is_invisible(segments, monkeypatch):
-    """Both chunk-state scans run in S segments (totals, carry, replay) or in
-    one pass; either way the forward outputs and the gradients must match the
-    oracle (N = 1088: 17 chunks, so 3 segments are uneven; the forward's
-    segment scratch holds 3 segments at this size)."""
+@pytest.mark.parametrize("batch,n", [(1, 64), (4, 1088)])
+def test_bf16_state_scan_segmentation_is_invisible(batch, n):
+    """Both chunk-state scans run in one pass (one segment: N = 64, a single
+    chunk) or in S segments (totals, carry, replay): at B = 4, N = 1088 (17
+    chunks) the forward's segment scratch (its num buffer) holds 3 segments, so
+    it runs 3 of 6, 6 and 5 chunks, and the backward runs 6 segments of 3, 3, 3,
+    3, 3 and 2 chunks. Either way the forward outputs and the gradients must
+    match the oracle. The segmentation is a function of the geometry alone."""
     from oal_amd.hd_block_gemm_autograd import grouped_oal
 
     dev = _dev()
-    monkeypatch.setenv("OAL_SCAN_SEGMENTS", segments)
-    inp = _bf16_case(1, 1088, seed=9)
+    segments = f"B={batch} N={n}"
+    inp = _bf16_case(batch, n, seed=9)
     qb, kb, vb = (inp[nm].to(torch.bfloat16).to(dev).requires_grad_() for nm in ("q", "k", "v"))
     c0, lam, gam = (inp[nm].to(dev).requires_grad_() for nm in ("c0", "lam", "gam"))
     out, num, den = grouped_oal(qb, kb, vb, inp["groups"].to(dev), c0, lam, gam, scale=inp["scale"], floor=0.0,

@@ -112,8 +112,11 @@ def test_cpu_tensors_fail_loudly_instead_of_falling_back():
         gq.oal_attention(q, k, v, groups, factor)
     with pytest.raises(RuntimeError, match="reference"):
         gq.oal_attention(q, k, v, groups, factor, execution="reference")
+    qp, kp, vp = (torch.nn.functional.pad(t, (0, 64 - t.shape[-1])).contiguous() for t in (q, k, v))
+    labels = torch.nn.functional.pad(groups, (0, 60)).expand(2, 64).contiguous()
     with pytest.raises(RuntimeError, match="ROCm|HIP"):
-        _native.forward(q, k, v, groups, factor[:1], factor[None, :2], factor[None, None, :1], scale=0.5, floor=0.0)
+        _native.forward(qp, kp, vp, labels, torch.ones(2), torch.ones(2, 2), torch.ones(2, 2, 2), scale=0.5,
+                        floor=0.0)
 
 
 def test_factor_expansion_is_exactly_symmetric_and_matches_known_answer():
