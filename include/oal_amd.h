@@ -122,6 +122,29 @@ int oal_backward(const void* q, const void* k, const void* v,
                  void* workspace, void* stream);
 
 /*
+ * Allocation-free variant of oal_backward. No counterpart in the reference: it
+ * is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). Same
+ * arguments and results as oal_backward, without the workspace: the workspace
+ * is a file-scope device array of OAL_NOALLOC_SCRATCH_BYTES (256 MiB) that each
+ * GPU the library runs on holds until the process ends. A geometry whose
+ * oal_backward_workspace_bytes exceeds it is refused with an error (B = 1,
+ * N = 4096, 14/2 heads needs 146 MiB on the bf16 path). Nothing is allocated or
+ * freed. The stream must belong to the current device. Every call on a GPU
+ * shares that GPU's array: calls that overlap on one GPU (two streams, two host
+ * threads) race and must be serialized by the caller.
+ */
+#define OAL_NOALLOC_SCRATCH_BYTES (256u << 20)
+int oal_backward_noalloc(const void* q, const void* k, const void* v,
+                         const int32_t* labels, const float* c0, const float* lam, const float* gam,
+                         int groups, int batch, int q_heads, int kv_heads, int seq_len, int dtype,
+                         int precision, float scale, float floor,
+                         const float* num, const float* den, const void* saved,
+                         const void* dout, const float* dnum, const float* dden,
+                         void* dq, void* dk, void* dv, float* dc0, float* dlam, float* dgam,
+                         void* stream);
+
+/*
  * Matrix-core self-test: one wave checks the MFMA accumulator layouts the bf16
  * kernels assume and adds the number of mismatching elements to
  * *device_errors (a device int the caller zeroed). No counterpart in the

@@ -49,6 +49,11 @@ _SIGNATURES = {
          _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
         _i,
     ),
+    "oal_backward_noalloc": (
+        [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _f, _f, _vp, _vp, _vp, _vp, _vp, _vp,
+         _vp, _vp, _vp, _vp, _vp, _vp, _vp],
+        _i,
+    ),
     "oal_selftest": ([_vp, _vp], _i),
 }
 

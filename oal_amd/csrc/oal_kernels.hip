@@ -774,6 +774,43 @@ int backward_impl(const Geometry& g, const void* q, const void* k, const void* v
   return launch_status("oal_backward launch");
 }
 
+// ---------------------------------------------------------------------------
+// Scratch of the allocation-free backward (oal_backward_noalloc): a file-scope
+// device array, one copy per GPU, held until the process ends. Host code never
+// passes its name to a kernel (in host code the name is a stand-in, not a
+// device address): the address each device holds it at is looked up once per
+// device, with that device current, and kept in g_scratch.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) unsigned char scratch[OAL_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch[kMaxDevices] = {};
+
+// The current device's scratch address, or nullptr (with the error set).
+void* scratch_address() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) {
+    fail("oal_backward_noalloc: no current HIP device");
+    return nullptr;
+  }
+  if (dev >= kMaxDevices) {
+    fail("oal_backward_noalloc: device index beyond the supported 64");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void* ptr = nullptr;
+    const hipError_t err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || !ptr) {
+      fail(std::string("oal_backward_noalloc: hipGetSymbolAddress(scratch) failed: ") + hipGetErrorString(err));
+      return nullptr;
+    }
+    g_scratch[dev] = ptr;
+  }
+  return g_scratch[dev];
+}
+
 }  // namespace
 
 extern "C" {
@@ -934,6 +971,36 @@ int oal_backward(const void* q, const void* k, const void* v, const int32_t* lab
   if (groups <= 8) return backward_impl<uint16_t, 8>(OAL_BWD_ARGS);
   return backward_impl<uint16_t, 64>(OAL_BWD_ARGS);
 #undef OAL_BWD_ARGS
+}
+
+int oal_backward_noalloc(const void* q, const void* k, const void* v, const int32_t* labels, const float* c0,
+                         const float* lam, const float* gam, int groups, int batch, int q_heads, int kv_heads,
+                         int seq_len, int dtype, int precision, float scale, float floor, const float* num,
+                         const float* den, const void* saved, const void* dout, const float* dnum, const float* dden,
+                         void* dq, void* dk, void* dv, float* dc0, float* dlam, float* dgam, void* stream) {
+  const size_t need = oal_backward_workspace_bytes(batch, q_heads, kv_heads, seq_len, groups, dtype, precision);
+  if (need == 0) return 1;  // invalid geometry; the size query set the error
+  if (need > (size_t)OAL_NOALLOC_SCRATCH_BYTES) {
+    char msg[256];
+    snprintf(msg, sizeof(msg),
+             "oal_backward_noalloc: this geometry needs %zu bytes of workspace; the static scratch holds %zu "
+             "(use oal_backward with a caller-allocated workspace)",
+             need, (size_t)OAL_NOALLOC_SCRATCH_BYTES);
+    return fail(msg);
+  }
+  // the stream must run on the current device, whose scratch copy is used
+  if (stream) {
+    int sdev = -1, cur = -1;
+    if (hipStreamGetDevice(static_cast<hipStream_t>(stream), &sdev) != hipSuccess || hipGetDevice(&cur) != hipSuccess)
+      return fail("oal_backward_noalloc: cannot resolve the stream's device");
+    if (sdev != cur) return fail("oal_backward_noalloc: the stream must belong to the current device");
+  }
+  void* ws = scratch_address();
+  if (!ws) return 1;
+  // every workspace byte the backward reads it has written first in the same
+  // call, so the scratch needs no clearing between calls
+  return oal_backward(q, k, v, labels, c0, lam, gam, groups, batch, q_heads, kv_heads, seq_len, dtype, precision,
+                      scale, floor, num, den, saved, dout, dnum, dden, dq, dk, dv, dc0, dlam, dgam, ws, stream);
 }
 
 int oal_selftest(int* device_errors, void* stream) {
