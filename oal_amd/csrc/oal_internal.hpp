@@ -70,6 +70,8 @@ struct MfmaWork {
   float* dvl;     // [U][N][64] local dv, summed over the unit's query heads
   float* coefl;   // [Hq][73][B * NB] local (dc0, dlam[8], dgam[8][8]) per chunk
   float* coefs;   // [Hq][73] their sums over the chunks
+  uint16_t* dCT;  // [U][S][kKS][64][16] bf16 segment carries of dT (S > 1), T layout
+  uint16_t* dCR;  // [U][S][kS/32][4][32][16] bf16, R layout
   int S, SL;      // segments of the backward state scan and chunks per segment
   size_t bytes;
 };
@@ -109,14 +111,17 @@ template <typename T>
 void launch_local_bwd(const LaunchGeom& g, const T* q, const T* k, const T* v, const LocalBwdArgs& a, bool need_dq,
                       bool need_dkv, hipStream_t st, const Timer& timed);
 
-// Segmentation of a chunk-state scan: S segments of SL chunks. More than one
-// segment runs as totals, carry, replay and needs seg_bytes of scratch;
-// scratch_bytes caps S ((size_t)-1: no cap). OAL_SCAN_SEGMENTS overrides.
+// Segmentation of a chunk-state scan: S segments of SL chunks, a function of
+// the geometry alone. The forward runs more than one segment as totals, carry,
+// replay; the backward as one local pass per segment plus the segments'
+// carries. Either needs seg_bytes of segment totals; scratch_bytes caps S
+// ((size_t)-1: no cap).
 struct ScanPlan {
   int S, SL;
   size_t seg_bytes;
 };
 ScanPlan scan_plan(int U, int NB, size_t scratch_bytes, bool fwd);
+ScanPlan bwd_scan_plan(int U, int NB, int R);
 
 // Operands and outputs of one chunk-state scan (oal_mfma_scan.hip).
 struct ScanArgs {
@@ -131,6 +136,8 @@ struct ScanArgs {
   uint16_t* outR;     // emitted state, R layout
   float* segtot;      // [U][S][kS][64] scratch when S > 1
   float* dwqs;        // backward: [S][B][Hq][kS] coefficient partials
+  uint16_t* carryT;   // backward with S > 1: [U][S] segment carries, T layout
+  uint16_t* carryR;   // backward with S > 1: [U][S] segment carries, R layout
 };
 template <bool FWD>
 void launch_scan(const ScanPlan& p, const ScanArgs& a, hipStream_t st, const Timer& timed);

@@ -204,24 +204,6 @@ __global__ __launch_bounds__(256) void k2_bwd_prep(const T* __restrict__ q, cons
 constexpr int kFG = 4;  // units per ring group
 constexpr int kNS = 4;  // LDS stages of a ring
 
-// Group G (units G * kFG ..) of a k-blocked state into LDS stage G % kNS;
-// 128 threads, each unit is 64 rows x 16 bf16 = 128 lanes x 16 bytes.
-// Stage G % kNS holds units G * kFG .. of group G.
-template <int NU, int G>
-__device__ __forceinline__ void ring_issue_u(const uint16_t* src, const LdsRing<4>& ring, int tid) {
-  const int wv = tid >> 6;
-  __bf16* st = ring.st[G % kNS];
-#pragma unroll
-  for (int i = 0; i < kFG; ++i) {
-    const int u = G * kFG + i;
-    if (u < NU) copy16_to_lds(src + (size_t)u * 1024 + tid * 8, st + i * 1024 + 64 * wv * 8);
-  }
-}
-template <int U>
-__device__ __forceinline__ const __bf16* ring_unit(const LdsRing<4>& ring) {
-  return ring.st[(U / kFG) % kNS] + (U % kFG) * 1024;
-}
-
 // Slot weights of M-tile M for this lane's rows (16 values), from LDS.
 template <int M, bool WEIGHTED>
 __device__ __forceinline__ void fold_weights(const float* wl, int s, float (&w16)[16]) {
@@ -272,21 +254,39 @@ __device__ __forceinline__ int fold_row(int r) {
 // 16 values = 2048 bf16) per stage, kNS stages; 128 threads move 32 B each.
 constexpr int kTileElems = 4 * 32 * 16;
 
-__device__ __forceinline__ void fold_issue(const uint16_t* src, int m, __bf16* st, int tid) {
+// With CARRY, the stage also holds the same M-tile of a second state (the
+// segment carry of k2_kv_fold) right after the first, and the products of both
+// accumulate into one D: D = (A + A') B.
+template <bool CARRY>
+__device__ __forceinline__ void fold_issue(const uint16_t* src, const uint16_t* csrc, int m, __bf16* st, int tid) {
   const int wv = tid >> 6;
   const uint16_t* g = src + (size_t)m * kTileElems;
   copy16_to_lds(g + tid * 8, st + 64 * wv * 8);
   copy16_to_lds(g + (tid + 128) * 8, st + (128 + 64 * wv) * 8);
+  if constexpr (CARRY) {
+    const uint16_t* c = csrc + (size_t)m * kTileElems;
+    copy16_to_lds(c + tid * 8, st + kTileElems + 64 * wv * 8);
+    copy16_to_lds(c + (tid + 128) * 8, st + kTileElems + (128 + 64 * wv) * 8);
+  }
+}
+template <bool CARRY>
+constexpr int fold_copies() {
+  return CARRY ? 4 : 2;
 }
 
 // D^T of M-tile M: 32 slots (rows, fold_row order) x 32 tokens (lane column).
-template <int M>
+template <int M, bool CARRY>
 __device__ __forceinline__ f32x16 fold_mfma(const bf16x8 (&bfr)[4], const __bf16* tile, int lane) {
   const int s = lane >> 5, arow = fold_row(lane & 31);
   f32x16 D = f32x16{};
 #pragma unroll
   for (int kk = 0; kk < 4; ++kk)
     D = mfma32(*reinterpret_cast<const bf16x8*>(tile + kk * 512 + arow * 16 + 8 * s), bfr[kk], D);
+  if constexpr (CARRY) {
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+      D = mfma32(*reinterpret_cast<const bf16x8*>(tile + kTileElems + kk * 512 + arow * 16 + 8 * s), bfr[kk], D);
+  }
   return D;
 }
 
@@ -296,40 +296,41 @@ __device__ __forceinline__ f32x16 fold_mfma(const bf16x8 (&bfr)[4], const __bf16
 // barrier) with tile G + NS, issues the product of tile G + 1 and reads its
 // weights, then folds tile G, so the fold's VALU work overlaps the next tile's
 // matrix products and LDS reads. Up to NS - 2 tiles stay in flight.
-template <int G, int NS, bool WEIGHTED>
+template <int G, int NS, bool WEIGHTED, bool CARRY>
 __device__ __forceinline__ void fold_group(const bf16x8 (&bfr)[4], const float (&x)[kD], float (&dx)[kD],
-                                           const float* wl, const LdsRing<NS>& ring, const uint16_t* src, int tid,
-                                           int lane, const f32x16& Dc, const float (&wc)[16]) {
+                                           const float* wl, const LdsRing<NS>& ring, const uint16_t* src,
+                                           const uint16_t* csrc, int tid, int lane, const f32x16& Dc,
+                                           const float (&wc)[16]) {
   constexpr int NT = kS / 32;  // 69 M-tiles
   if constexpr (G + 1 < NT) {
     constexpr int issued = (G + NS - 1 < NT - 1) ? G + NS - 1 : NT - 1;  // last tile issued so far
     pin64(dx);  // the fold of tile G - 1 stays in group G - 1
-    ring_sync<2 * (issued - (G + 1))>();
-    if constexpr (G + NS < NT) fold_issue(src, G + NS, ring.st[(G + NS) % NS], tid);
-    const f32x16 Dn = fold_mfma<G + 1>(bfr, ring.st[(G + 1) % NS], lane);
+    ring_sync<fold_copies<CARRY>() * (issued - (G + 1))>();
+    if constexpr (G + NS < NT) fold_issue<CARRY>(src, csrc, G + NS, ring.st[(G + NS) % NS], tid);
+    const f32x16 Dn = fold_mfma<G + 1, CARRY>(bfr, ring.st[(G + 1) % NS], lane);
     float wn[16];
     fold_weights<G + 1, WEIGHTED>(wl, lane >> 5, wn);
     fold_tile<G>(Dc, x, dx, wc);
-    fold_group<G + 1, NS, WEIGHTED>(bfr, x, dx, wl, ring, src, tid, lane, Dn, wn);
+    fold_group<G + 1, NS, WEIGHTED, CARRY>(bfr, x, dx, wl, ring, src, csrc, tid, lane, Dn, wn);
   } else {
     fold_tile<G>(Dc, x, dx, wc);
   }
 }
 
 // Whole fold: tiles 0 .. NS - 1 in flight, product of tile 0, then the groups.
-template <int NS, bool WEIGHTED>
+template <int NS, bool WEIGHTED, bool CARRY>
 __device__ __forceinline__ void fold_all(const bf16x8 (&bfr)[4], const float (&x)[kD], float (&dx)[kD],
-                                         const float* wl, const LdsRing<NS>& ring, const uint16_t* src, int tid,
-                                         int lane) {
+                                         const float* wl, const LdsRing<NS>& ring, const uint16_t* src,
+                                         const uint16_t* csrc, int tid, int lane) {
   static_assert(NS >= 3 && NS <= kS / 32, "ring depth");
   [&]<int... I>(std::integer_sequence<int, I...>) {
-    (fold_issue(src, I, ring.st[I], tid), ...);
+    (fold_issue<CARRY>(src, csrc, I, ring.st[I], tid), ...);
   }(std::make_integer_sequence<int, NS>{});
-  ring_sync<2 * (NS - 1)>();
-  const f32x16 D0 = fold_mfma<0>(bfr, ring.st[0], lane);
+  ring_sync<fold_copies<CARRY>() * (NS - 1)>();
+  const f32x16 D0 = fold_mfma<0, CARRY>(bfr, ring.st[0], lane);
   float w0[16];
   fold_weights<0, WEIGHTED>(wl, lane >> 5, w0);
-  fold_group<0, NS, WEIGHTED>(bfr, x, dx, wl, ring, src, tid, lane, D0, w0);
+  fold_group<0, NS, WEIGHTED, CARRY>(bfr, x, dx, wl, ring, src, csrc, tid, lane, D0, w0);
 }
 
 // The two rotation groups of a token (lanes l and l + 32) hold its gradient
@@ -380,7 +381,7 @@ __global__ __launch_bounds__(128, 2) void k2_q_fold(const T* __restrict__ q, con
   for (int kk = 0; kk < 4; ++kk) bfr[kk] = frag8(G16, rowoff + 16 * kk + 8 * s, ok);
 #pragma unroll
   for (int m = 0; m < kD; ++m) dx[m] = 0.f;
-  fold_all<6, true>(bfr, x, dx, wl, ring, src, tid, l);
+  fold_all<6, true, false>(bfr, x, dx, wl, ring, src, nullptr, tid, l);
 
   // lane group s writes dimensions 32 s .. 32 s + 31 of its token
   float full[32];
@@ -404,28 +405,61 @@ __global__ __launch_bounds__(128, 2) void k2_q_fold(const T* __restrict__ q, con
 // dk, dv: state parts (fold of dT V^T, dU = raw(K) dT, dTz quadratic form) plus
 // the per-head local parts. grid (NB, U), 2 waves; wave w owns tokens 32w..+31.
 // ---------------------------------------------------------------------------
-template <int T>
+// dU = raw(K) dT: k-step T of the T-layout state in LDS; with CARRY the same
+// k-step of the segment carry follows the UPG state units of each ring stage,
+// and its products accumulate into the same accumulators.
+template <int T, int UPG, bool CARRY>
 __device__ __forceinline__ void du_step(const float (&x)[kD], const LdsRing<4>& ring, int lane, f32x16 (&acc)[2]) {
   const int s = lane >> 5, row = lane & 31;
-  const __bf16* tile = ring_unit<T>(ring);
+  const __bf16* tile = ring.st[(T / UPG) % kNS] + (T % UPG) * 1024;
   const bf16x8 b0 = *reinterpret_cast<const bf16x8*>(tile + row * 16 + 8 * s);
   const bf16x8 b1 = *reinterpret_cast<const bf16x8*>(tile + (32 + row) * 16 + 8 * s);
   const bf16x8 a = raw_fragment<T>(x);
   acc[0] = mfma32(a, b0, acc[0]);
   acc[1] = mfma32(a, b1, acc[1]);
+  if constexpr (CARRY) {
+    const bf16x8 c0 = *reinterpret_cast<const bf16x8*>(tile + UPG * 1024 + row * 16 + 8 * s);
+    const bf16x8 c1 = *reinterpret_cast<const bf16x8*>(tile + UPG * 1024 + (32 + row) * 16 + 8 * s);
+    acc[0] = mfma32(a, c0, acc[0]);
+    acc[1] = mfma32(a, c1, acc[1]);
+  }
 }
-template <int G>
-__device__ __forceinline__ void du_group(const float (&x)[kD], const LdsRing<4>& ring, const uint16_t* src, int tid, int lane,
-                                         f32x16 (&acc)[2]) {
-  constexpr int NG = (kKS + kFG - 1) / kFG;
-  constexpr int n1 = (G + 1 < NG) ? ((G + 1) * kFG + kFG <= kKS ? kFG : kKS - (G + 1) * kFG) : 0;
-  constexpr int n2 = (G + 2 < NG) ? ((G + 2) * kFG + kFG <= kKS ? kFG : kKS - (G + 2) * kFG) : 0;
-  ring_sync<n1 + n2>();
-  if constexpr (G + 3 < NG) ring_issue_u<kKS, G + 3>(src, ring, tid);
+// Units (1024 bf16 each) of ring group G in flight per thread.
+template <int UPG, bool CARRY, int G>
+constexpr int du_copies() {
+  constexpr int NG = (kKS + UPG - 1) / UPG;
+  if constexpr (G >= NG) {
+    return 0;
+  } else {
+    constexpr int n = (G + 1) * UPG <= kKS ? UPG : kKS - G * UPG;
+    return CARRY ? 2 * n : n;
+  }
+}
+template <int UPG, bool CARRY, int G>
+__device__ __forceinline__ void du_issue(const uint16_t* src, const uint16_t* csrc, const LdsRing<4>& ring,
+                                         int tid) {
+  const int wv = tid >> 6;
+  __bf16* st = ring.st[G % kNS];
+#pragma unroll
+  for (int i = 0; i < UPG; ++i) {
+    const int u = G * UPG + i;
+    if (u < kKS) {
+      copy16_to_lds(src + (size_t)u * 1024 + tid * 8, st + i * 1024 + 64 * wv * 8);
+      if constexpr (CARRY) copy16_to_lds(csrc + (size_t)u * 1024 + tid * 8, st + (UPG + i) * 1024 + 64 * wv * 8);
+    }
+  }
+}
+template <int G, int UPG, bool CARRY>
+__device__ __forceinline__ void du_group(const float (&x)[kD], const LdsRing<4>& ring, const uint16_t* src,
+                                         const uint16_t* csrc, int tid, int lane, f32x16 (&acc)[2]) {
+  constexpr int NG = (kKS + UPG - 1) / UPG;
+  ring_sync<du_copies<UPG, CARRY, G + 1>() + du_copies<UPG, CARRY, G + 2>()>();
+  if constexpr (G + 3 < NG) du_issue<UPG, CARRY, G + 3>(src, csrc, ring, tid);
   [&]<int... I>(std::integer_sequence<int, I...>) {
-    ((G * kFG + I < kKS ? du_step<(G * kFG + I < kKS ? G * kFG + I : 0)>(x, ring, lane, acc) : void()), ...);
-  }(std::make_integer_sequence<int, kFG>{});
-  if constexpr (G + 1 < NG) du_group<G + 1>(x, ring, src, tid, lane, acc);
+    ((G * UPG + I < kKS ? du_step<(G * UPG + I < kKS ? G * UPG + I : 0), UPG, CARRY>(x, ring, lane, acc) : void()),
+     ...);
+  }(std::make_integer_sequence<int, UPG>{});
+  if constexpr (G + 1 < NG) du_group<G + 1, UPG, CARRY>(x, ring, src, csrc, tid, lane, acc);
 }
 
 // Rows of the Mz operand for the Z^T = Mz K^T products: product md, accumulator
@@ -442,12 +476,18 @@ __device__ __forceinline__ int mz_dim(int md, int m) {
 //           Mz[r][c] = dTz[pair(r, c)] (r != c), 2 dTz[pair(r, r)] on the diagonal;
 //   part 1: dv = raw(K) dT (values 0..63) + local dv.
 // The two parts share nothing, so they run as independent blocks.
-template <typename T>
+// CARRY: dT of chunk ch is the backward scan's segment-local state plus the
+// carry of the chunk's segment (ch / SL, cR / cT [U][S]); both products of each
+// step accumulate into the same registers, so the carry costs matrix products
+// and staging only (the feature and fold arithmetic is shared).
+template <typename T, bool CARRY>
 __global__ __launch_bounds__(128, 2) void k2_kv_fold(const T* __restrict__ k, const T* __restrict__ v,
                                                      const uint16_t* __restrict__ dTR, const uint16_t* __restrict__ dTT,
-                                                     const float* __restrict__ dTz, const float* __restrict__ dkl,
-                                                     const float* __restrict__ dvl, int Hq, int Hkv, int N, int NB,
-                                                     T* __restrict__ dk, T* __restrict__ dv) {
+                                                     const uint16_t* __restrict__ cR, const uint16_t* __restrict__ cT,
+                                                     int SL, int S, const float* __restrict__ dTz,
+                                                     const float* __restrict__ dkl, const float* __restrict__ dvl,
+                                                     int Hq, int Hkv, int N, int NB, T* __restrict__ dk,
+                                                     T* __restrict__ dv) {
   __shared__ __attribute__((aligned(16))) __bf16 ring0[kFG * 1024], ring1[kFG * 1024], ring2[kFG * 1024],
       ring3[kFG * 1024];
   // mz rows unpadded, 16-byte chunk c of row r stored at chunk c ^ (r & 7) (the
@@ -460,6 +500,8 @@ __global__ __launch_bounds__(128, 2) void k2_kv_fold(const T* __restrict__ k, co
   const int tok0 = ch * kC;
   const size_t kbase = (size_t)u * N * kD;
   const size_t cbase = ((size_t)u * NB + ch) * ((size_t)kKS * 64 * 16);
+  // the carry of the chunk's segment (unused without CARRY)
+  const size_t sbase = ((size_t)u * S + (CARRY ? ch / SL : 0)) * ((size_t)kKS * 64 * 16);
   const int tok = tok0 + 32 * wv + row;
   const bool ok = tok < N;
   const size_t rowoff = kbase + (size_t)(ok ? tok : N - 1) * kD;
@@ -469,10 +511,13 @@ __global__ __launch_bounds__(128, 2) void k2_kv_fold(const T* __restrict__ k, co
 
   if (part == 1) {
     f32x16 acc[2] = {f32x16{}, f32x16{}};
-    ring_issue_u<kKS, 0>(dTT + cbase, ring, tid);
-    ring_issue_u<kKS, 1>(dTT + cbase, ring, tid);
-    ring_issue_u<kKS, 2>(dTT + cbase, ring, tid);
-    du_group<0>(x, ring, dTT + cbase, tid, l, acc);
+    // four k-steps of dT per ring stage, or two of dT and two of the carry
+    constexpr int UPG = CARRY ? 2 : 4;
+    const uint16_t* csrc = CARRY ? cT + sbase : nullptr;
+    du_issue<UPG, CARRY, 0>(dTT + cbase, csrc, ring, tid);
+    du_issue<UPG, CARRY, 1>(dTT + cbase, csrc, ring, tid);
+    du_issue<UPG, CARRY, 2>(dTT + cbase, csrc, ring, tid);
+    du_group<0, UPG, CARRY>(x, ring, dTT + cbase, csrc, tid, l, acc);
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
@@ -502,8 +547,8 @@ __global__ __launch_bounds__(128, 2) void k2_kv_fold(const T* __restrict__ k, co
   float dx[kD];
 #pragma unroll
   for (int m = 0; m < kD; ++m) dx[m] = 0.f;
-  static_assert(kTileElems <= kFG * 1024, "a fold tile fits one ring stage");
-  fold_all<4, false>(bfr, x, dx, nullptr, ring, dTR + cbase, tid, l);
+  static_assert(2 * kTileElems <= kFG * 1024, "a fold tile and its carry tile fit one ring stage");
+  fold_all<4, false, CARRY>(bfr, x, dx, nullptr, ring, dTR + cbase, CARRY ? cR + sbase : nullptr, tid, l);
   float* zl = reinterpret_cast<float*>(ring0);
   __syncthreads();
   if (tid < kD) zl[tid] = zv;
@@ -744,7 +789,7 @@ MfmaWork mfma_work_view(void* base, int B, int Hq, int U, int N, int NB) {
   const size_t trows = (size_t)B * Hq * kTRows * NB * kC;
   const size_t chunk = (size_t)kKS * 64 * 16 * sizeof(uint16_t);
   MfmaWork w;
-  const ScanPlan plan = scan_plan(U, NB, (size_t)-1, false);
+  const ScanPlan plan = bwd_scan_plan(U, NB, B * Hq / U);
   w.S = plan.S;
   w.SL = plan.SL;
   w.G16 = static_cast<uint16_t*>(take(rows * kD * sizeof(uint16_t)));
@@ -765,6 +810,8 @@ MfmaWork mfma_work_view(void* base, int B, int Hq, int U, int N, int NB) {
   w.dvl = static_cast<float*>(take((size_t)U * N * kD * sizeof(float)));
   w.coefl = static_cast<float*>(take(sizeof(float) * (size_t)B * Hq * NB * 73));
   w.coefs = static_cast<float*>(take(sizeof(float) * (size_t)Hq * 73));
+  w.dCT = plan.S > 1 ? static_cast<uint16_t*>(take(chunk * U * plan.S)) : nullptr;
+  w.dCR = plan.S > 1 ? static_cast<uint16_t*>(take(chunk * U * plan.S)) : nullptr;
   w.bytes = off;
   return w;
 }
@@ -791,7 +838,7 @@ int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, cons
     const ScanPlan plan{w.S, w.SL, 0};
     // without a coefficient gradient the scan forms no coefficient partials
     ScanArgs a{w.QT16, kTRows, w.GT16, kTRows, sv.wqs, sv.PR, g.U, g.Hq, g.Hkv, g.N, g.NB,
-               w.dTT, w.dTR, w.segtot, need_coef ? w.dwqs : nullptr};
+               w.dTT, w.dTR, w.segtot, need_coef ? w.dwqs : nullptr, w.dCT, w.dCR};
     launch_scan<false>(plan, a, st, timed);
     // denominator state (pair-matrix form): per-chunk dCarry and coefficient
     // partials, then dTz as the exclusive chunk suffix
@@ -812,8 +859,14 @@ int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, cons
   }
   if (dk) {
     timed("k2_kv_fold", st, [&] {
-      hipLaunchKernelGGL(k2_kv_fold<T>, dim3(g.NB, g.U, 2), dim3(128), 0, st, kt, vt, w.dTR, w.dTT, w.dTz, w.dkl, w.dvl,
-                         g.Hq, g.Hkv, g.N, g.NB, static_cast<T*>(dk), static_cast<T*>(dv));
+      if (w.S > 1)
+        hipLaunchKernelGGL((k2_kv_fold<T, true>), dim3(g.NB, g.U, 2), dim3(128), 0, st, kt, vt, w.dTR, w.dTT, w.dCR,
+                           w.dCT, w.SL, w.S, w.dTz, w.dkl, w.dvl, g.Hq, g.Hkv, g.N, g.NB, static_cast<T*>(dk),
+                           static_cast<T*>(dv));
+      else
+        hipLaunchKernelGGL((k2_kv_fold<T, false>), dim3(g.NB, g.U, 2), dim3(128), 0, st, kt, vt, w.dTR, w.dTT,
+                           nullptr, nullptr, 1, 1, w.dTz, w.dkl, w.dvl, g.Hq, g.Hkv, g.N, g.NB,
+                           static_cast<T*>(dk), static_cast<T*>(dv));
     });
   }
   if (need_coef) {

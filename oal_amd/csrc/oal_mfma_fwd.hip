@@ -624,7 +624,7 @@ void launch_mfma_forward(const LaunchGeom& g, const void* q, const void* k, cons
     // segment scratch
     const ScanPlan plan = scan_plan(g.U, g.NB, sizeof(float) * (size_t)g.B * g.Hq * g.N * kD, true);
     ScanArgs a{sv.KT16, kD, sv.VT16, kD + 1, nullptr, nullptr, g.U, g.Hq, g.Hkv, g.N, g.NB,
-               sv.PT, sv.PR, num, nullptr};
+               sv.PT, sv.PR, num, nullptr, nullptr, nullptr};
     launch_scan<true>(plan, a, st, timed);
   }
   timed("k2_intra_fwd", st, [&] {

@@ -30,6 +30,16 @@
 //           emitting every chunk's state; the backward weights the features by
 //           wq_h so that every head accumulates into the one state.
 //   MODE 2: one segment: MODE 1's output plus MODE 0's partials.
+//   MODE 3 (backward): one pass per segment from a zero carry: emits each
+//           chunk's segment-local suffix state, forms MODE 0's partials and
+//           writes the segment total. The state a consumer needs is that local
+//           state plus the segment's carry (MODE 4); the only consumer of the
+//           backward state, k2_kv_fold, adds the carry with matrix products of
+//           its own, so the backward contracts every item once.
+//   MODE 4 (backward): the carry of each segment, the sum of the totals of the
+//           segments after it, emitted once per (unit, segment) in the R and T
+//           layouts; no items. A block walks its tiles' segments from the last
+//           one backwards with a running sum, so each total is read once.
 // PART (backward, MODE 0 and 2): form the coefficient partials; without them
 // (no coefficient gradient requested) the forward state is not read. The
 // per-head products stay apart either way, so that the state -- and every
@@ -62,14 +72,15 @@ constexpr size_t kChunkElems = (size_t)kKS * 64 * 16;
 }  // namespace
 
 template <bool FWD, int MODE, int TPW, int NW, bool PART>
-__global__ __launch_bounds__(64 * NW, NW / 2) void k2_scan(const uint16_t* __restrict__ F, int frows,
+__global__ __launch_bounds__(64 * NW, (NW + 1) / 2) void k2_scan(const uint16_t* __restrict__ F, int frows,
                                                const uint16_t* __restrict__ V, int vrows,
                                                const float* __restrict__ wqs, const uint16_t* __restrict__ PRin,
                                                const float* __restrict__ carry, int Hq, int Hkv, int N, int NB, int SL,
                                                int Sg, uint16_t* __restrict__ outT, uint16_t* __restrict__ outR,
                                                float* __restrict__ segtot, float* __restrict__ dwqs) {
-  constexpr bool EMIT = MODE != 0;
-  constexpr bool SPLIT = !FWD && MODE != 1;  // per-head products kept apart (needed for the partials)
+  constexpr bool EMIT = MODE == 1 || MODE == 2 || MODE == 3;
+  // per-head products kept apart (needed for the partials)
+  constexpr bool SPLIT = !FWD && (MODE == 0 || MODE == 2 || MODE == 3);
   constexpr bool PARTIALS = SPLIT && PART;
   static_assert(!SPLIT || TPW == 1, "the per-head products fit registers for one tile per wave");
   constexpr int TG = scan_tile_groups(TPW, NW);
@@ -77,8 +88,9 @@ __global__ __launch_bounds__(64 * NW, NW / 2) void k2_scan(const uint16_t* __res
   constexpr int kNT = 64 * NW;               // threads per block
   constexpr int kFPT = kD * 8 / kNT;         // 16-byte operand chunks per thread and side
   static_assert(kFPT * kNT == kD * 8, "a block stages whole operand rows");
-  __shared__ __attribute__((aligned(16))) float Fs[2][kOpRows * kFRow];
-  __shared__ __attribute__((aligned(16))) __bf16 Vs[2][kD * kVRow];
+  // (MODE 4 stages no operands)
+  __shared__ __attribute__((aligned(16))) float Fs[MODE == 4 ? 1 : 2][MODE == 4 ? 1 : kOpRows * kFRow];
+  __shared__ __attribute__((aligned(16))) __bf16 Vs[MODE == 4 ? 1 : 2][MODE == 4 ? 1 : kD * kVRow];
   __shared__ float dwl[PARTIALS ? 8 : 1][kSTiles * 32];
   // backward: the slot weight wq_h of every query head of the unit (up to 8)
   // for the block's slots, [head][wave][tile][slot row]
@@ -88,9 +100,10 @@ __global__ __launch_bounds__(64 * NW, NW / 2) void k2_scan(const uint16_t* __res
   {
     const int total = gridDim.x, id = blockIdx.x;
     const int w = (total & 7) == 0 ? (id & 7) * (total >> 3) + (id >> 3) : id;
+    const int sg = MODE == 4 ? 1 : Sg;  // MODE 4: one block walks every segment
     tgi = w % TG;
-    seg = (w / TG) % Sg;
-    u = w / (TG * Sg);
+    seg = (w / TG) % sg;
+    u = w / (TG * sg);
   }
   const int R = Hq / Hkv, b = u / Hkv, kh = u % Hkv;
   const int RI = FWD ? 1 : R;  // items per chunk
@@ -113,10 +126,12 @@ __global__ __launch_bounds__(64 * NW, NW / 2) void k2_scan(const uint16_t* __res
 
   // constant rows of the feature side: 64 = 1 (the value side is zero for
   // tokens >= N), 65 = 0
-  for (int i = tid; i < 2 * kC; i += kNT) {
-    const int bi = i / kC, j = i % kC;
-    Fs[bi][kD * kFRow + j] = 1.f;
-    Fs[bi][(kD + 1) * kFRow + j] = 0.f;
+  if constexpr (MODE != 4) {
+    for (int i = tid; i < 2 * kC; i += kNT) {
+      const int bi = i / kC, j = i % kC;
+      Fs[bi][kD * kFRow + j] = 1.f;
+      Fs[bi][(kD + 1) * kFRow + j] = 0.f;
+    }
   }
   if constexpr (PARTIALS) {
     for (int i = tid; i < 8 * kSTiles * 32; i += kNT) dwl[i / (kSTiles * 32)][i % (kSTiles * 32)] = 0.f;
@@ -131,22 +146,34 @@ __global__ __launch_bounds__(64 * NW, NW / 2) void k2_scan(const uint16_t* __res
   if constexpr (MODE == 1) {
     // carry = sum of the totals of the segments before (forward) or after
     // (backward) this one, in a fixed order: nearest segment first
+    // (the accumulator registers 4 a .. 4 a + 3 of a lane hold four consecutive
+    // values of its slot, read as one 16-byte load; all loads of a segment are
+    // issued before they are added)
     const int n_other = FWD ? seg : Sg - 1 - seg;
     for (int o = 0; o < n_other; ++o) {
       const int so = FWD ? seg - 1 - o : seg + 1 + o;
+      float4 tv[TPW][2][4];
+#pragma unroll
+      for (int t = 0; t < TPW; ++t) {
+        const float* cr = carry + (((size_t)u * Sg + so) * kS + slot[t]) * kD;
+#pragma unroll
+        for (int n = 0; n < 2; ++n)
+#pragma unroll
+          for (int a = 0; a < 4; ++a)
+            tv[t][n][a] = *reinterpret_cast<const float4*>(cr + 32 * n + c32_row(4 * a, l));
+      }
 #pragma unroll
       for (int t = 0; t < TPW; ++t) {
         if (live[t]) {
-          const float* cr = carry + (((size_t)u * Sg + so) * kS + slot[t]) * kD;
-          float tv[2][16];
 #pragma unroll
           for (int n = 0; n < 2; ++n)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) tv[n][i] = cr[32 * n + c32_row(i, l)];
-#pragma unroll
-          for (int n = 0; n < 2; ++n)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) acc[t][n][i] += tv[n][i];
+            for (int a = 0; a < 4; ++a) {
+              acc[t][n][4 * a] += tv[t][n][a].x;
+              acc[t][n][4 * a + 1] += tv[t][n][a].y;
+              acc[t][n][4 * a + 2] += tv[t][n][a].z;
+              acc[t][n][4 * a + 3] += tv[t][n][a].w;
+            }
         }
       }
     }
@@ -210,9 +237,10 @@ __global__ __launch_bounds__(64 * NW, NW / 2) void k2_scan(const uint16_t* __res
       perm[p][j] = (__bf16)(16 * p + off == row ? 1.f : 0.f);
     }
 
-  // Emission of tile t's state before chunk ch (exclusive prefix / suffix).
-  auto emit = [&](int t, int ch) {
-    const size_t cb = (size_t)u * NB + ch;
+  // Emission of tile t's state into state block cb (unit u and chunk ch: the
+  // exclusive prefix / suffix before ch, cb = u * NB + ch; MODE 4: the carry of
+  // segment seg, cb = u * Sg + seg).
+  auto emit = [&](int t, size_t cb) {
     // R layout straight from the accumulators: lane = slot, 4 values a word pair
     uint32_t wd[2][4][2];
 #pragma unroll
@@ -251,6 +279,44 @@ __global__ __launch_bounds__(64 * NW, NW / 2) void k2_scan(const uint16_t* __res
       }
     }
   };
+
+  if constexpr (MODE == 4) {
+    // carry of segment so = running sum of the totals of segments > so (added
+    // from the last segment backwards); the next total's loads are issued
+    // before the current carry is emitted
+    float4 tv[TPW][2][4];
+    auto load_total = [&](int so) {
+#pragma unroll
+      for (int t = 0; t < TPW; ++t) {
+        const float* cr = carry + (((size_t)u * Sg + so) * kS + slot[t]) * kD;
+#pragma unroll
+        for (int n = 0; n < 2; ++n)
+#pragma unroll
+          for (int a = 0; a < 4; ++a)
+            tv[t][n][a] = *reinterpret_cast<const float4*>(cr + 32 * n + c32_row(4 * a, l));
+      }
+    };
+    load_total(Sg - 1);
+    for (int so = Sg - 1; so >= 0; --so) {
+#pragma unroll
+      for (int t = 0; t < TPW; ++t)
+        if (live[t]) emit(t, (size_t)u * Sg + so);
+      if (so == 0) break;
+#pragma unroll
+      for (int t = 0; t < TPW; ++t)
+#pragma unroll
+        for (int n = 0; n < 2; ++n)
+#pragma unroll
+          for (int a = 0; a < 4; ++a) {
+            acc[t][n][4 * a] += tv[t][n][a].x;
+            acc[t][n][4 * a + 1] += tv[t][n][a].y;
+            acc[t][n][4 * a + 2] += tv[t][n][a].z;
+            acc[t][n][4 * a + 3] += tv[t][n][a].w;
+          }
+      load_total(so - 1);
+    }
+    return;
+  }
 
   // Coefficient partials: the P_c rows of this lane's slot (values
   // e = 32 n + 8 a + 4 s + v) for the chunk being processed (pf) and, still
@@ -384,7 +450,7 @@ __global__ __launch_bounds__(64 * NW, NW / 2) void k2_scan(const uint16_t* __res
       if (it < NI && any_live && hh == 0) {
 #pragma unroll
         for (int t = 0; t < TPW; ++t)
-          if (live[t]) emit(t, ch);
+          if (live[t]) emit(t, (size_t)u * NB + ch);
       }
     }
   };
@@ -432,7 +498,7 @@ __global__ __launch_bounds__(64 * NW, NW / 2) void k2_scan(const uint16_t* __res
     }
   }
 
-  if constexpr (MODE == 0) {
+  if constexpr (MODE == 0 || MODE == 3) {
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {
       if (live[t]) {
@@ -440,7 +506,9 @@ __global__ __launch_bounds__(64 * NW, NW / 2) void k2_scan(const uint16_t* __res
 #pragma unroll
         for (int n = 0; n < 2; ++n)
 #pragma unroll
-          for (int i = 0; i < 16; ++i) st[32 * n + c32_row(i, l)] = acc[t][n][i];
+          for (int a = 0; a < 4; ++a)
+            *reinterpret_cast<float4*>(st + 32 * n + c32_row(4 * a, l)) =
+                make_float4(acc[t][n][4 * a], acc[t][n][4 * a + 1], acc[t][n][4 * a + 2], acc[t][n][4 * a + 3]);
       }
     }
   }
@@ -553,11 +621,11 @@ __global__ __launch_bounds__(256) void k2_fwd_prep(const T* __restrict__ k, cons
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
-// Tiles per wave of the three scan kernels (totals, replay, single pass):
-// two wherever the per-head products are not kept apart.
-constexpr int scan_tpw(bool fwd, int mode) { return (mode == 1 || fwd) ? 2 : 1; }
-// waves per block of the three scan kernels
-constexpr int scan_nw(bool fwd, int mode) { return 4; }
+// Tiles per wave of the scan kernels (modes 0-4): two wherever the per-head
+// products are not kept apart (MODE 4: one, for one wave per tile).
+constexpr int scan_tpw(bool fwd, int mode) { return mode == 4 ? 1 : (fwd || mode == 1) ? 2 : 1; }
+// waves per block of the scan kernels
+constexpr int scan_nw(bool fwd, int mode) { return mode == 4 ? 1 : 4; }
 
 ScanPlan scan_plan(int U, int NB, size_t scratch_bytes, bool fwd) {
   // Segment count from a model of block rounds on MI355X's 256 CUs: each
@@ -591,6 +659,30 @@ ScanPlan scan_plan(int U, int NB, size_t scratch_bytes, bool fwd) {
   return p;
 }
 
+ScanPlan bwd_scan_plan(int U, int NB, int R) {
+  // One local pass per segment (MODE 3, two blocks per CU), so the time is
+  // about rounds x (items per segment + a pipeline start of two items); each
+  // segment adds its totals and carry traffic. A function of the geometry
+  // alone.
+  constexpr double kSlots = 2.0 * 256;
+  const int tg = scan_tile_groups(scan_tpw(false, 3), scan_nw(false, 3));
+  int best_S = 1;
+  double best = 0.0;
+  for (int want = 1; want <= NB; ++want) {
+    const int SL = (NB + want - 1) / want, S = (NB + SL - 1) / SL;
+    const double est = std::ceil(tg * (double)U * S / kSlots) * (SL * R + 2.0) + (S > 1 ? 0.25 * S : 0.0);
+    if (want == 1 || est < best) {
+      best = est;
+      best_S = S;
+    }
+  }
+  ScanPlan p;
+  p.SL = (NB + best_S - 1) / best_S;
+  p.S = (NB + p.SL - 1) / p.SL;
+  p.seg_bytes = p.S > 1 ? sizeof(float) * (size_t)U * kS * kD * p.S : 0;
+  return p;
+}
+
 template <bool FWD, bool PART>
 static void launch_scan_impl(const ScanPlan& p, const ScanArgs& a, hipStream_t st, const Timer& timed) {
   constexpr int T0 = scan_tpw(FWD, 0), T1 = scan_tpw(FWD, 1), T2 = scan_tpw(FWD, 2);
@@ -605,16 +697,36 @@ static void launch_scan_impl(const ScanPlan& p, const ScanArgs& a, hipStream_t s
     });
     return;
   }
-  timed(FWD ? "k2_state_fwd_totals" : "k2_state_bwd_totals", st, [&] {
-    hipLaunchKernelGGL((k2_scan<FWD, 0, T0, W0, PART>), grid(T0, W0), dim3(64 * W0), 0, st, a.F, a.frows, a.V,
-                       a.vrows, a.wqs, a.PR, nullptr, a.Hq, a.Hkv, a.N, a.NB, p.SL, p.S, nullptr, nullptr, a.segtot,
-                       a.dwqs);
-  });
-  timed(name, st, [&] {
-    hipLaunchKernelGGL((k2_scan<FWD, 1, T1, W1, PART>), grid(T1, W1), dim3(64 * W1), 0, st, a.F, a.frows, a.V,
-                       a.vrows, a.wqs, a.PR, a.segtot, a.Hq, a.Hkv, a.N, a.NB, p.SL, p.S, a.outT, a.outR, nullptr,
-                       nullptr);
-  });
+  if constexpr (!FWD) {
+    // one local pass per segment, then the segments' carries
+    constexpr int T3 = scan_tpw(false, 3), W3 = scan_nw(false, 3);
+    constexpr int T4 = scan_tpw(false, 4), W4 = scan_nw(false, 4);
+    timed(name, st, [&] {
+      hipLaunchKernelGGL((k2_scan<false, 3, T3, W3, PART>), grid(T3, W3), dim3(64 * W3), 0, st, a.F, a.frows, a.V,
+                         a.vrows, a.wqs, a.PR, nullptr, a.Hq, a.Hkv, a.N, a.NB, p.SL, p.S, a.outT, a.outR, a.segtot,
+                         a.dwqs);
+    });
+    timed("k2_state_bwd_carry", st, [&] {
+      const dim3 g4((unsigned)(scan_tile_groups(T4, W4) * a.U));  // one block per (unit, tile group)
+      hipLaunchKernelGGL((k2_scan<false, 4, T4, W4, false>), g4, dim3(64 * W4), 0, st, a.F, a.frows,
+                         a.V, a.vrows, a.wqs, a.PR, a.segtot, a.Hq, a.Hkv, a.N, a.NB, p.SL, p.S, a.carryT,
+                         a.carryR, nullptr, nullptr);
+    });
+    return;
+  }
+  if constexpr (FWD) {
+    // segment totals, then each segment's replay from the totals before it
+    timed("k2_state_fwd_totals", st, [&] {
+      hipLaunchKernelGGL((k2_scan<true, 0, T0, W0, false>), grid(T0, W0), dim3(64 * W0), 0, st, a.F, a.frows, a.V,
+                         a.vrows, a.wqs, a.PR, nullptr, a.Hq, a.Hkv, a.N, a.NB, p.SL, p.S, nullptr, nullptr,
+                         a.segtot, nullptr);
+    });
+    timed(name, st, [&] {
+      hipLaunchKernelGGL((k2_scan<true, 1, T1, W1, false>), grid(T1, W1), dim3(64 * W1), 0, st, a.F, a.frows, a.V,
+                         a.vrows, a.wqs, a.PR, a.segtot, a.Hq, a.Hkv, a.N, a.NB, p.SL, p.S, a.outT, a.outR, nullptr,
+                         nullptr);
+    });
+  }
 }
 
 template <bool FWD>

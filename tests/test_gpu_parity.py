@@ -310,11 +310,13 @@ def test_bf16_matrix_core_backward_matches_fp32_oracle(batch, n, upstream):
 @pytest.mark.parametrize("batch,n", [(1, 64), (4, 1088)])
 def test_bf16_state_scan_segmentation_is_invisible(batch, n):
     """Both chunk-state scans run in one pass (one segment: N = 64, a single
-    chunk) or in S segments (totals, carry, replay): at B = 4, N = 1088 (17
-    chunks) the forward's segment scratch (its num buffer) holds 3 segments, so
-    it runs 3 of 6, 6 and 5 chunks, and the backward runs 6 segments of 3, 3, 3,
-    3, 3 and 2 chunks. Either way the forward outputs and the gradients must
-    match the oracle. The segmentation is a function of the geometry alone."""
+    chunk) or in S segments: at B = 4, N = 1088 (17 chunks) the forward's
+    segment scratch (its num buffer) holds 3 segments, so it runs totals, carry
+    and replay over 3 segments of 6, 6 and 5 chunks, and the backward runs one
+    local pass over each of 3 segments of 6, 6 and 5 chunks, their carries, and
+    k2_kv_fold's carry products. Either way the forward outputs and the
+    gradients must match the oracle. The segmentation is a function of the
+    geometry alone."""
     from oal_amd.hd_block_gemm_autograd import grouped_oal
 
     dev = _dev()
