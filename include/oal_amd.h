@@ -45,8 +45,12 @@ extern "C" {
 /* Arithmetic precision (reference HD planner "precision", hd_block_gemm.py:132-153):
  * OAL_PRECISION_FP32  fp32 arithmetic throughout (VALU kernels), any group count.
  * OAL_PRECISION_BF16  bf16 operands, fp32 accumulation on the gfx950 matrix cores
- *                     (MFMA) when groups <= 8; larger group counts use the fp32
- *                     kernels. */
+ *                     (MFMA) for any group count up to 64 and up to 8 query heads
+ *                     per KV head (more run the fp32 kernels). Up to 8 groups the
+ *                     intra-chunk term is formed from group sums; more groups --
+ *                     per-pair coefficients, labels d -> d with 64 groups -- form
+ *                     the intra-chunk local score in feature form,
+ *                     phi_Q . phi_K^T on the matrix cores. */
 #define OAL_PRECISION_FP32 0
 #define OAL_PRECISION_BF16 1
 

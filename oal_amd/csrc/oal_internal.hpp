@@ -70,12 +70,15 @@ struct MfmaWork {
   float* dvl;     // [U][N][64] local dv, summed over the unit's query heads
   float* coefl;   // [Hq][73][B * NB] local (dc0, dlam[8], dgam[8][8]) per chunk
   float* coefs;   // [Hq][73] their sums over the chunks
+  float* dkp;     // per-pair path: [B][Hq][N][64] local dk per query head
+  float* dwql;    // per-pair path: [Hq][B * NB * 2][kS] local slot-coefficient partials
   uint16_t* dCT;  // [U][S][kKS][64][16] bf16 segment carries of dT (S > 1), T layout
   uint16_t* dCR;  // [U][S][kS/32][4][32][16] bf16, R layout
   int S, SL;      // segments of the backward state scan and chunks per segment
   size_t bytes;
 };
-MfmaWork mfma_work_view(void* base, int B, int Hq, int U, int N, int NB);
+// pairwise: more than 8 groups (the per-pair path's local buffers)
+MfmaWork mfma_work_view(void* base, int B, int Hq, int U, int N, int NB, bool pairwise);
 
 template <typename T>
 int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, const void* v, const int32_t* labels,
@@ -105,7 +108,19 @@ struct LocalBwdArgs {
   float* dkl;
   float* dvl;
   float* coefl;  // nullptr when the coefficient gradients are not requested
+  // per-pair coefficients (more than 8 groups): feature-form local VJP
+  bool pairwise;
+  const float* wqs;  // [Hq][kS] slot coefficients
+  float* dkp;        // [B][Hq][N][64] local dk per query head, summed over the heads into dkl
+  float* dwql;       // [Hq][B * NB * 2][kS] local slot-coefficient partials (nullptr: not requested)
 };
+
+// Feature-form local VJP of the per-pair path (oal_mfma_pair.hip).
+template <typename T>
+void launch_pair_local_bwd(const LaunchGeom& g, const T* q, const T* k, const T* v, const LocalBwdArgs& a,
+                           bool need_dq, bool need_dkv, hipStream_t st, const Timer& timed);
+void launch_pair_coef_grad(const LaunchGeom& g, const float* dwq, const float* dwqz, const int32_t* labels, int G,
+                           float scale, float* dc0, float* dlam, float* dgam, hipStream_t st, const Timer& timed);
 
 template <typename T>
 void launch_local_bwd(const LaunchGeom& g, const T* q, const T* k, const T* v, const LocalBwdArgs& a, bool need_dq,

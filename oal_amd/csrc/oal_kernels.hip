@@ -708,10 +708,11 @@ void timed(const char* name, hipStream_t st, F&& launch) {
   if (a && b) g_prof_records.push_back({name, a, b});
 }
 
-// The matrix-core kernels keep up to 8 groups and up to 8 query heads per KV head
-// in registers; other shapes run the fp32 kernels.
+// The matrix-core kernels keep up to 8 query heads per KV head in registers;
+// more run the fp32 kernels. Up to 8 groups take the group-sum intra-chunk
+// kernels, more (per-pair coefficients) the feature-form ones.
 bool use_mfma(int precision, int groups, const Geometry& g) {
-  return precision == OAL_PRECISION_BF16 && groups <= 8 && g.R <= 8;
+  return precision == OAL_PRECISION_BF16 && groups <= 64 && g.R <= 8;
 }
 
 oal::LaunchGeom launch_geom(const Geometry& g) { return oal::LaunchGeom{g.B, g.Hq, g.Hkv, g.N, g.NB, g.U, g.R}; }
@@ -891,7 +892,8 @@ size_t oal_backward_workspace_bytes(int batch, int q_heads, int kv_heads, int se
                                     int precision) {
   Geometry g;
   if (check_geometry(batch, q_heads, kv_heads, seq_len, dtype, &g) || check_common(groups, precision)) return 0;
-  if (use_mfma(precision, groups, g)) return oal::mfma_work_view(nullptr, g.B, g.Hq, g.U, g.N, g.NB).bytes;
+  if (use_mfma(precision, groups, g))
+    return oal::mfma_work_view(nullptr, g.B, g.Hq, g.U, g.N, g.NB, groups > 8).bytes;
   return work_view(g, nullptr).bytes;
 }
 

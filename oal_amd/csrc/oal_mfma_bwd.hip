@@ -22,58 +22,13 @@
 
 #include "oal_internal.hpp"
 #include "oal_mfma_common.hpp"
+#include "oal_mfma_fold.hpp"
 
 namespace oal {
 
 static __constant__ SlotTable kSlot = make_slot_table();
+using namespace fold;
 
-namespace {
-
-constexpr int LD = kD + 8;  // padded bf16 row stride in LDS
-
-// 32 consecutive elements of a row (16-byte stores).
-__device__ __forceinline__ void store32(float* dst, const float (&v)[32]) {
-#pragma unroll
-  for (int j = 0; j < 8; ++j)
-    reinterpret_cast<float4*>(dst)[j] = make_float4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
-}
-__device__ __forceinline__ void store32(uint16_t* dst, const float (&v)[32]) {
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    uint32_t w[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      w[i] = uint32_t(from_f<uint16_t>(v[8 * j + 2 * i])) | (uint32_t(from_f<uint16_t>(v[8 * j + 2 * i + 1])) << 16);
-    reinterpret_cast<uint4*>(dst)[j] = make_uint4(w[0], w[1], w[2], w[3]);
-  }
-}
-
-// 8 consecutive elements of a row as one bf16 fragment (zeros when !ok).
-__device__ __forceinline__ bf16x8 frag8(const uint16_t* __restrict__ src, size_t off, bool ok) {
-  const bf16x8 x = *reinterpret_cast<const bf16x8*>(src + off);
-  return ok ? x : bf16x8{};
-}
-__device__ __forceinline__ bf16x8 frag8(const float* __restrict__ src, size_t off, bool ok) {
-  const float4 a = reinterpret_cast<const float4*>(src + off)[0], b = reinterpret_cast<const float4*>(src + off)[1];
-  float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-  const bf16x8 x = pack8(v);
-  return ok ? x : bf16x8{};
-}
-
-// Rotated fp32 row x[m] = row[(m + 32 s) % 64], loaded in rotated order (the
-// rotation is in the per-lane addresses, so every register index is static).
-template <typename T>
-__device__ __forceinline__ void load_rotated(const T* __restrict__ src, size_t row_base, bool ok, int s,
-                                             float (&x)[kD]) {
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const bf16x8 r = frag8(src, row_base + ((8 * i + 32 * s) & 63), ok);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) x[8 * i + j] = (float)r[j];
-  }
-}
-
-}  // namespace
 
 // 16 consecutive elements of a row as fp32 (zeros when !ok).
 __device__ __forceinline__ void load16f(const uint16_t* __restrict__ src, size_t off, bool ok, float (&x)[16]) {
@@ -204,52 +159,6 @@ __global__ __launch_bounds__(256) void k2_bwd_prep(const T* __restrict__ q, cons
 constexpr int kFG = 4;  // units per ring group
 constexpr int kNS = 4;  // LDS stages of a ring
 
-// Slot weights of M-tile M for this lane's rows (16 values), from LDS.
-template <int M, bool WEIGHTED>
-__device__ __forceinline__ void fold_weights(const float* wl, int s, float (&w16)[16]) {
-#pragma unroll
-  for (int a = 0; a < 4; ++a) {
-    if constexpr (WEIGHTED) {
-      const float4 ww = *reinterpret_cast<const float4*>(wl + 16 * (2 * M + a / 2) + 8 * s + 4 * (a % 2));
-      w16[4 * a + 0] = ww.x;
-      w16[4 * a + 1] = ww.y;
-      w16[4 * a + 2] = ww.z;
-      w16[4 * a + 3] = ww.w;
-    } else {
-      w16[4 * a + 0] = w16[4 * a + 1] = w16[4 * a + 2] = w16[4 * a + 3] = 1.f;
-    }
-  }
-}
-
-// Fold of one 32-slot M-tile (rows permuted so that the rows a lane holds are
-// slots of its rotation group): dx[rb] += d x[cb], dx[cb] += d x[rb].
-template <int M>
-__device__ __forceinline__ void fold_tile(const f32x16& D, const float (&x)[kD], float (&dx)[kD],
-                                          const float (&w16)[16]) {
-  [&]<int... I>(std::integer_sequence<int, I...>) {
-    (([&] {
-       constexpr int a = I / 4, v = I % 4;
-       constexpr int base = 8 * (2 * M + a / 2) + 4 * (a % 2) + v;
-       constexpr int rb = kSlotHost.rb[base], cb = kSlotHost.cb[base];
-       const float d = D[I] * w16[I];
-       if constexpr (rb < 64 && cb < 64) {
-         dx[rb] += d * x[cb];
-         dx[cb] += d * x[rb];
-       } else if constexpr (rb < 64 && cb == 64) {
-         dx[rb] += d;
-       }
-     }()),
-     ...);
-  }(std::make_integer_sequence<int, 16>{});
-}
-
-// A-operand rows of M-tile: lane row r = 8a + 4s' + v reads within-tile slot
-// 16(a/2) + 8s' + 4(a%2) + v of the PR tile (32 slots x 16 values per unit).
-__device__ __forceinline__ int fold_row(int r) {
-  const int a = r >> 3, sp = (r >> 2) & 1, v = r & 3;
-  return 16 * (a >> 1) + 8 * sp + 4 * (a & 1) + v;
-}
-
 // Fold ring: one 32-slot M-tile of a PR-layout state (4 k-slices x 32 rows x
 // 16 values = 2048 bf16) per stage, kNS stages; 128 threads move 32 B each.
 constexpr int kTileElems = 4 * 32 * 16;
@@ -331,20 +240,6 @@ __device__ __forceinline__ void fold_all(const bf16x8 (&bfr)[4], const float (&x
   float w0[16];
   fold_weights<0, WEIGHTED>(wl, lane >> 5, w0);
   fold_group<0, NS, WEIGHTED, CARRY>(bfr, x, dx, wl, ring, src, csrc, tid, lane, D0, w0);
-}
-
-// The two rotation groups of a token (lanes l and l + 32) hold its gradient
-// in rotated order: lane group s has dimension (m + 32 s) % 64 at index m.
-// Returns, in lane group s, the full gradient of dimensions 32 s + m (m < 32).
-__device__ __forceinline__ void combine_rotation_groups(const float (&dx)[kD], int s, float (&out)[32]) {
-#pragma unroll
-  for (int m = 0; m < 32; ++m) {
-    // partner's dx[m + 32]: lanes < 32 receive it in the second result,
-    // lanes >= 32 in the first
-    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(dx[m + 32]), __float_as_uint(dx[m + 32]),
-                                                    false, false);
-    out[m] = dx[m] + __uint_as_float(s ? r[0] : r[1]);
-  }
 }
 
 // ---------------------------------------------------------------------------
@@ -462,15 +357,6 @@ __device__ __forceinline__ void du_group(const float (&x)[kD], const LdsRing<4>&
   if constexpr (G + 1 < NG) du_group<G + 1, UPG, CARRY>(x, ring, src, csrc, tid, lane, acc);
 }
 
-// Rows of the Mz operand for the Z^T = Mz K^T products: product md, accumulator
-// row m = 8 a + 4 s + v (lane group s, register 4 a + v) holds dimension
-// 32 s + 16 md + 4 a + v, so that lane group s ends up with dimensions
-// 32 s .. 32 s + 31 of its token (registers 16 md + i), the layout of the fold.
-__device__ __forceinline__ int mz_dim(int md, int m) {
-  const int a = m >> 3, sg = (m >> 2) & 1, v = m & 3;
-  return 32 * sg + 16 * md + 4 * a + v;
-}
-
 // grid (NB, U, 2), 2 waves; wave w owns tokens 32w..32w+31 of the chunk.
 //   part 0: dk = fold of dT V^T through the key features + z1 + Mz k + local dk,
 //           Mz[r][c] = dTz[pair(r, c)] (r != c), 2 dTz[pair(r, r)] on the diagonal;
@@ -584,8 +470,9 @@ __global__ __launch_bounds__(128, 2) void k2_kv_fold(const T* __restrict__ k, co
   }
 }
 
-// Grid (slot blocks + 73 + den blocks, Hq). Slot blocks: dwq[h][slot] = sum
-// over (segment, batch) of the state-scan partials. The next 73 blocks of a
+// Grid (slot blocks + ncol + den blocks, Hq). Slot blocks: dwq[h][slot] = sum
+// over (segment, batch) of the state-scan partials (per-pair path: plus the
+// sum over (batch, chunk, query tile) of the local slot partials dwql). The next 73 blocks of a
 // head: one column of the per-(batch, chunk) local partials each, coefs[h][j]
 // = sum_r coefl[h][j][r]. The den blocks (64 entries each): dwqz[h][nat] =
 // sum over (batch, chunk) of the denominator partials dwz [U][NB][R][kFP], the
@@ -596,14 +483,15 @@ constexpr int kDwqDenBlocks = (kFeat + 63) / 64;
 __global__ __launch_bounds__(256) void k2_dwq_reduce(const float* __restrict__ dwqs, int rowsets, int Hq,
                                                      float* __restrict__ dwq, const float* __restrict__ coefl, int bn,
                                                      float* __restrict__ coefs, const float* __restrict__ dwz, int B,
-                                                     int Hkv, int NB, float* __restrict__ dwqz) {
+                                                     int Hkv, int NB, float* __restrict__ dwqz,
+                                                     const float* __restrict__ dwql, int lrows, int ncol) {
   const int h = blockIdx.y;
-  if (blockIdx.x >= kDwqSlotBlocks + 73) {
+  if (blockIdx.x >= kDwqSlotBlocks + ncol) {
     // 64 entries per block; lane l reads entries 4 (l % 16) .. as a float4 of
     // row-group l / 16 + 4 wave, rows (batch, chunk) i = group + 16 x
     __shared__ float dpart[16][64];
     const int l = threadIdx.x & 63, wv = threadIdx.x >> 6, grp = (l >> 4) + 4 * wv, e4 = 4 * (l & 15);
-    const int n0 = (blockIdx.x - kDwqSlotBlocks - 73) * 64;
+    const int n0 = (blockIdx.x - kDwqSlotBlocks - ncol) * 64;
     const int R = Hq / Hkv, kh = h / R, hh = h % R;
     const int rows = B * NB;  // row i = (batch i / NB, chunk i % NB)
     auto row_ptr = [&](int i) {
@@ -669,6 +557,21 @@ __global__ __launch_bounds__(256) void k2_dwq_reduce(const float* __restrict__ d
     for (int i = 0; i < 8; ++i) acc += v[i];
   }
   for (; r < rowsets; ++r) acc += p[(size_t)r * st];
+  if (dwql) {
+    // per-pair path: the local partials of every (batch, chunk, query tile) row
+    const float* lp = dwql + (size_t)h * lrows * kS + sl;
+    float lacc = 0.f;
+    int i = 0;
+    for (; i + 8 <= lrows; i += 8) {
+      float v[8];
+#pragma unroll
+      for (int x = 0; x < 8; ++x) v[x] = lp[(size_t)(i + x) * kS];
+#pragma unroll
+      for (int x = 0; x < 8; ++x) lacc += v[x];
+    }
+    for (; i < lrows; ++i) lacc += lp[(size_t)i * kS];
+    acc += lacc;
+  }
   dwq[(size_t)h * kS + sl] = acc;
 }
 
@@ -777,7 +680,7 @@ __global__ __launch_bounds__(256) void k2_coef_grad(const float* __restrict__ dw
 // ---------------------------------------------------------------------------
 // Workspace carve-up of the backward; the state scan's segment count comes
 // from scan_plan (oal_mfma_scan.hip), which sizes the segment-totals buffer.
-MfmaWork mfma_work_view(void* base, int B, int Hq, int U, int N, int NB) {
+MfmaWork mfma_work_view(void* base, int B, int Hq, int U, int N, int NB, bool pairwise) {
   char* p = static_cast<char*>(base);
   size_t off = 0;
   auto take = [&](size_t bytes) {
@@ -810,6 +713,8 @@ MfmaWork mfma_work_view(void* base, int B, int Hq, int U, int N, int NB) {
   w.dvl = static_cast<float*>(take((size_t)U * N * kD * sizeof(float)));
   w.coefl = static_cast<float*>(take(sizeof(float) * (size_t)B * Hq * NB * 73));
   w.coefs = static_cast<float*>(take(sizeof(float) * (size_t)Hq * 73));
+  w.dkp = pairwise ? static_cast<float*>(take(rows * kD * sizeof(float))) : nullptr;
+  w.dwql = pairwise ? static_cast<float*>(take(sizeof(float) * (size_t)Hq * B * NB * 2 * kS)) : nullptr;
   w.dCT = plan.S > 1 ? static_cast<uint16_t*>(take(chunk * U * plan.S)) : nullptr;
   w.dCR = plan.S > 1 ? static_cast<uint16_t*>(take(chunk * U * plan.S)) : nullptr;
   w.bytes = off;
@@ -826,7 +731,8 @@ int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, cons
   const bool need_coef = dc0 || dlam || dgam;
   if (need_coef && !(dc0 && dlam && dgam)) return 3;
   MfmaSaved sv = mfma_saved_view(const_cast<void*>(saved), g.Hq, g.U, g.NB, g.R);
-  MfmaWork w = mfma_work_view(workspace, g.B, g.Hq, g.U, g.N, g.NB);
+  const bool pairwise = groups > 8;
+  MfmaWork w = mfma_work_view(workspace, g.B, g.Hq, g.U, g.N, g.NB, pairwise);
   const T* qt = static_cast<const T*>(q);
   const T* kt = static_cast<const T*>(k);
   const T* vt = static_cast<const T*>(v);
@@ -848,7 +754,8 @@ int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, cons
   }
   {
     LocalBwdArgs la{w.G16, w.Gz, w.QT16, w.GT16, sv.KT16, sv.KAP, sv.PZ, sv.PZm, labels, lam, gam, sv.ic, sv.gm, sv.lb,
-                    groups, scale, w.dqf, w.dkl, w.dvl, need_coef ? w.coefl : nullptr};
+                    groups, scale, w.dqf, w.dkl, w.dvl, (need_coef && !pairwise) ? w.coefl : nullptr,
+                    pairwise, sv.wqs, w.dkp, (need_coef && pairwise) ? w.dwql : nullptr};
     launch_local_bwd<T>(g, qt, kt, vt, la, dq != nullptr, dk != nullptr, st, timed);
   }
   if (dq) {
@@ -870,14 +777,22 @@ int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, cons
     });
   }
   if (need_coef) {
+    // group-sum path: the 73 local coefficient columns; per-pair path: the
+    // local slot partials added to the state's
+    const int ncol = pairwise ? 0 : 73;
     timed("k2_dwq_reduce", st, [&] {
-      hipLaunchKernelGGL(k2_dwq_reduce, dim3(kDwqSlotBlocks + 73 + kDwqDenBlocks, g.Hq), dim3(256), 0, st, w.dwqs,
-                         g.B * w.S, g.Hq, w.dwq, w.coefl, g.B * g.NB, w.coefs, w.dwz, g.B, g.Hkv, g.NB, w.dwqz);
+      hipLaunchKernelGGL(k2_dwq_reduce, dim3(kDwqSlotBlocks + ncol + kDwqDenBlocks, g.Hq), dim3(256), 0, st, w.dwqs,
+                         g.B * w.S, g.Hq, w.dwq, w.coefl, g.B * g.NB, w.coefs, w.dwz, g.B, g.Hkv, g.NB, w.dwqz,
+                         pairwise ? w.dwql : nullptr, g.B * g.NB * 2, ncol);
     });
-    timed("k2_coef_grad", st, [&] {
-      hipLaunchKernelGGL(k2_coef_grad, dim3(g.Hq), dim3(256), 0, st, w.dwq, w.dwqz, w.coefs, labels, g.Hq, groups,
-                         scale, dc0, dlam, dgam);
-    });
+    if (pairwise) {
+      launch_pair_coef_grad(g, w.dwq, w.dwqz, labels, groups, scale, dc0, dlam, dgam, st, timed);
+    } else {
+      timed("k2_coef_grad", st, [&] {
+        hipLaunchKernelGGL(k2_coef_grad, dim3(g.Hq), dim3(256), 0, st, w.dwq, w.dwqz, w.coefs, labels, g.Hq, groups,
+                           scale, dc0, dlam, dgam);
+      });
+    }
   }
   return 0;
 }

@@ -30,11 +30,13 @@ namespace oal {
 
 static __constant__ SlotTable kSlot = make_slot_table();
 
-// Per-head coefficients, one block per query head:
+// Per-head coefficients, grid (query head, 8 parts):
 //   wqs[h][slot]  wq of natural feature nat(slot) (0 for invalid slots);
-//   ic[h]         c0, scale*lam[g], scale^2*Gam[g][g'] padded to 8 groups;
+//   ic[h]         c0, scale*lam[g], scale^2*Gam[g][g'] padded to 8 groups (the
+//                 group-sum intra-chunk kernels; G > 8 keeps only c0);
 //   gm[h][r][c]   scale^2 * Gam[g(r)][g(c)]  (denominator quadratic form);
 //   lb[h][d]      scale * lam[g(d)].
+// Any group count up to 64: labels d -> d with G = 64 gives per-pair coefficients.
 __global__ __launch_bounds__(256) void k2_slot_coefficients(const int32_t* __restrict__ labels,
                                                             const float* __restrict__ c0,
                                                             const float* __restrict__ lam,
@@ -44,19 +46,16 @@ __global__ __launch_bounds__(256) void k2_slot_coefficients(const int32_t* __res
   // the head's coefficients are read once into LDS; every output then comes
   // from LDS (no dependent global gathers)
   __shared__ int lab[kD];
-  __shared__ float cg[8 * 8], cl[8], cc;
+  __shared__ float cg[kD * kD], cl[kD], cc;
   // block (h, part): slots and gm rows of one eighth; part 0 also writes ic, lb
   const int h = blockIdx.x, part = blockIdx.y, t = threadIdx.x;
   if (t < kD) {
     const int g = labels[h * kD + t];
     lab[t] = g < 0 ? 0 : (g >= G ? G - 1 : g);
   }
-  if (t < 64) {
-    const int g = t >> 3, g2 = t & 7;
-    cg[t] = (g < G && g2 < G) ? scale * scale * gam[((size_t)h * G + g) * G + g2] : 0.f;
-  }
-  if (t >= 64 && t < 72) cl[t - 64] = (t - 64) < G ? scale * lam[(size_t)h * G + (t - 64)] : 0.f;
-  if (t == 72) cc = c0[h];
+  for (int e = t; e < G * G; e += blockDim.x) cg[e] = scale * scale * gam[(size_t)h * G * G + e];
+  if (t < G) cl[t] = scale * lam[(size_t)h * G + t];
+  if (t == 0) cc = c0[h];
   __syncthreads();
   constexpr int kSlotsPerPart = kS / 8;
   static_assert(kSlotsPerPart * 8 == kS, "slot parts");
@@ -69,7 +68,7 @@ __global__ __launch_bounds__(256) void k2_slot_coefficients(const int32_t* __res
     } else if (n > 0 && n <= kD) {
       w = cl[lab[r]];
     } else if (n > kD) {
-      w = (r == c ? 1.f : 2.f) * cg[lab[r] * 8 + lab[c]];
+      w = (r == c ? 1.f : 2.f) * cg[lab[r] * G + lab[c]];
     }
     wqs[(size_t)h * kS + s] = w;
   }
@@ -77,16 +76,17 @@ __global__ __launch_bounds__(256) void k2_slot_coefficients(const int32_t* __res
     float x = 0.f;
     if (t == 0) {
       x = cc;
-    } else if (t < kIcGam) {
-      x = cl[t - kIcLam];
-    } else if (t < kIcGam + 64) {
-      x = cg[t - kIcGam];
+    } else if (G <= 8 && t < kIcGam) {
+      x = t - kIcLam < G ? cl[t - kIcLam] : 0.f;
+    } else if (G <= 8 && t < kIcGam + 64) {
+      const int g = (t - kIcGam) >> 3, g2 = (t - kIcGam) & 7;
+      x = (g < G && g2 < G) ? cg[g * G + g2] : 0.f;
     }
     ic[(size_t)h * kIC + t] = x;
   }
   for (int e = part * (kD * kD / 8) + t; e < (part + 1) * (kD * kD / 8); e += blockDim.x) {
     const int r = e >> 6, c = e & 63;
-    gm[(size_t)h * kD * kD + e] = cg[lab[r] * 8 + lab[c]];
+    gm[(size_t)h * kD * kD + e] = cg[lab[r] * G + lab[c]];
   }
   if (part == 0 && t < kD) lb[(size_t)h * kD + t] = cl[lab[t]];
 }
@@ -229,6 +229,44 @@ __device__ __forceinline__ void load16(const float* __restrict__ src, size_t off
 }
 
 // ---------------------------------------------------------------------------
+// Feature-form local score of a 32 x 32 tile (per-pair coefficients):
+//   kappa^T[j][i] = sum_slot raw(k_j)[slot] wq[slot] raw(q_i)[slot]
+// on v_mfma_f32_32x32x16_bf16 over the 138 k-steps of 16 slots: the A operand
+// is the key row's raw features (lane row = key token j), the B operand the
+// query row's weighted features (lane column = query token i), both generated
+// from rotated rows held in registers (static indices) with the weights of the
+// lane group's eight slots read from LDS. Reference: the local score
+// phi_Q . phi_K^T of hd_block_gemm_runtime.py:530-540.
+// ---------------------------------------------------------------------------
+// Rotated fp32 row x[m] = row[(m + 32 s) % 64] of a bf16 row in LDS.
+__device__ __forceinline__ void lds_rotated_row(const __bf16* rowp, int s, float (&x)[kD]) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const bf16x8 r = *reinterpret_cast<const bf16x8*>(rowp + ((8 * i + 32 * s) & 63));
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[8 * i + j] = (float)r[j];
+  }
+}
+template <int T>
+__device__ __forceinline__ f32x16 pair_step(const float (&xk)[kD], const float (&xq)[kD], const float* wl, int s,
+                                            f32x16 S) {
+  const float4 w0 = *reinterpret_cast<const float4*>(wl + 16 * T + 8 * s);
+  const float4 w1 = *reinterpret_cast<const float4*>(wl + 16 * T + 8 * s + 4);
+  const float w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+  return mfma32(raw_fragment<T>(xk), feature_fragment<T>(xq, w), S);
+}
+template <int... T>
+__device__ __forceinline__ f32x16 pair_score_impl(const float (&xk)[kD], const float (&xq)[kD], const float* wl, int s,
+                                                  std::integer_sequence<int, T...>) {
+  f32x16 S = f32x16{};
+  ((S = pair_step<T>(xk, xq, wl, s, S)), ...);
+  return S;
+}
+__device__ __forceinline__ f32x16 pair_score(const float (&xk)[kD], const float (&xq)[kD], const float* wl, int s) {
+  return pair_score_impl(xk, xq, wl, s, std::make_integer_sequence<int, kKS>{});
+}
+
+// ---------------------------------------------------------------------------
 // Intra-chunk forward, one block of 4 waves per (query head, chunk, unit).
 // Waves 0-2 each own one lower 32x32 tile of kappa^T (rows j = key token,
 // columns i = query token), (j-tile, i-tile) = (0,0), (0,1), (1,1):
@@ -240,15 +278,18 @@ __device__ __forceinline__ void load16(const float* __restrict__ src, size_t off
 // of the denominator as the quadratic form az + q . (bz + Mz q), Mz = gm o PZm.
 // Writes the intra part of num and the full den (k2_out_fwd adds the readout),
 // and saves the bf16 kappa tiles for the backward (KAP).
+// PAIRWISE (more than 8 groups, per-pair coefficients): waves 0-2 form their
+// kappa^T tile in feature form (pair_score) from the slot weights wqs instead
+// of the group sums; everything else is shared.
 // ---------------------------------------------------------------------------
-template <typename T>
+template <typename T, bool PAIRWISE>
 __global__ __launch_bounds__(256) void k2_intra_fwd(const T* __restrict__ q, const T* __restrict__ k,
                                                     const T* __restrict__ v, const float* __restrict__ PZ,
                                                     const float* __restrict__ PZm, const int32_t* __restrict__ labels,
                                                     const float* __restrict__ ic, const float* __restrict__ gm,
-                                                    const float* __restrict__ lb, int G, int Hq, int Hkv, int N,
-                                                    int NB, float* __restrict__ num, float* __restrict__ den,
-                                                    uint16_t* __restrict__ kapf) {
+                                                    const float* __restrict__ lb, const float* __restrict__ wqs,
+                                                    int G, int Hq, int Hkv, int N, int NB, float* __restrict__ num,
+                                                    float* __restrict__ den, uint16_t* __restrict__ kapf) {
   constexpr int LD = kD + 8;  // bf16 row stride (bank spread)
   __shared__ __attribute__((aligned(16))) __bf16 Qs[kC][LD];
   __shared__ __attribute__((aligned(16))) __bf16 Ks[kC][LD];
@@ -258,6 +299,7 @@ __global__ __launch_bounds__(256) void k2_intra_fwd(const T* __restrict__ q, con
   __shared__ float red[2][16][64];
   __shared__ float bz[kD], dsS[kC], dp2[32];
   __shared__ __attribute__((aligned(16))) __bf16 kapT[3][32][40];  // kappa^T tiles [j][i], bf16
+  __shared__ __attribute__((aligned(16))) float wl[PAIRWISE ? kS : 4];  // the head's slot weights
 
   int hh, ch, u;
   head_chunk_unit(Hq / Hkv, NB, (int)(gridDim.x / ((Hq / Hkv) * NB)), hh, ch, u);
@@ -298,8 +340,12 @@ __global__ __launch_bounds__(256) void k2_intra_fwd(const T* __restrict__ q, con
                     g1.x * z1.x, g1.y * z1.y, g1.z * z1.z, g1.w * z1.w};
       *reinterpret_cast<bf16x8*>(&Mz[r][16 * qq + 8 * i]) = pack8(y);
     }
+    if constexpr (PAIRWISE) {
+      for (int i = tid; i < kS / 4; i += 256)
+        reinterpret_cast<float4*>(wl)[i] = reinterpret_cast<const float4*>(wqs + (size_t)h * kS)[i];
+    }
     // group masks: entry (kk, g, ss, w) covers dims d, d + 1 with d = 16 kk + 8 ss + 2 w
-    {
+    if constexpr (!PAIRWISE) {
       const int kk = tid >> 6, g = (tid >> 3) & 7, ss = (tid >> 2) & 1, w = tid & 3;
       const int d = 16 * kk + 8 * ss + 2 * w;
       int g0 = labels[h * kD + d], g1 = labels[h * kD + d + 1];
@@ -316,43 +362,57 @@ __global__ __launch_bounds__(256) void k2_intra_fwd(const T* __restrict__ q, con
   if (wv < 3) {
     const int tj = wv == 2 ? 1 : 0, ti = wv == 0 ? 0 : 1;
     typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-    f32x16 sg[8];
-#pragma unroll
-    for (int g = 0; g < 8; ++g) sg[g] = f32x16{};
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      const u32x4 kf = *reinterpret_cast<const u32x4*>(&Ks[32 * tj + row][16 * kk + 8 * s]);
-      const bf16x8 qf = *reinterpret_cast<const bf16x8*>(&Qs[32 * ti + row][16 * kk + 8 * s]);
-#pragma unroll
-      for (int g = 0; g < 8; ++g) {
-        const u32x4 m = *reinterpret_cast<const u32x4*>(&mk[kk][g][s][0]);
-        sg[g] = mfma32(__builtin_bit_cast(bf16x8, kf & m), qf, sg[g]);
-      }
-    }
-    float lamc[8], gd[8], g2[8][8];
-    const float c0h = cf[0];
-#pragma unroll
-    for (int g = 0; g < 8; ++g) {
-      lamc[g] = cf[kIcLam + g];
-      gd[g] = cf[kIcGam + 9 * g];
-#pragma unroll
-      for (int h2 = 0; h2 < 8; ++h2) g2[g][h2] = 2.f * cf[kIcGam + 8 * g + h2];
-    }
     const int i = 32 * ti + row;
     const bool irow = tok0 + i < N;
+    float kv[16];  // kappa^T[j][i], j = 32 tj + c32_row(r)
+    if constexpr (PAIRWISE) {
+      float xk[kD], xq[kD];
+      lds_rotated_row(&Ks[32 * tj + row][0], s, xk);
+      lds_rotated_row(&Qs[32 * ti + row][0], s, xq);
+      const f32x16 S = pair_score(xk, xq, wl, s);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) kv[r] = S[r];
+    } else {
+      f32x16 sg[8];
+#pragma unroll
+      for (int g = 0; g < 8; ++g) sg[g] = f32x16{};
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const u32x4 kf = *reinterpret_cast<const u32x4*>(&Ks[32 * tj + row][16 * kk + 8 * s]);
+        const bf16x8 qf = *reinterpret_cast<const bf16x8*>(&Qs[32 * ti + row][16 * kk + 8 * s]);
+#pragma unroll
+        for (int g = 0; g < 8; ++g) {
+          const u32x4 m = *reinterpret_cast<const u32x4*>(&mk[kk][g][s][0]);
+          sg[g] = mfma32(__builtin_bit_cast(bf16x8, kf & m), qf, sg[g]);
+        }
+      }
+      float lamc[8], gd[8], g2[8][8];
+      const float c0h = cf[0];
+#pragma unroll
+      for (int g = 0; g < 8; ++g) {
+        lamc[g] = cf[kIcLam + g];
+        gd[g] = cf[kIcGam + 9 * g];
+#pragma unroll
+        for (int h2 = 0; h2 < 8; ++h2) g2[g][h2] = 2.f * cf[kIcGam + 8 * g + h2];
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float x = c0h;
+#pragma unroll
+        for (int g = 0; g < 8; ++g) {
+          float inner = fmaf(gd[g], sg[g][r], lamc[g]);
+#pragma unroll
+          for (int h2 = g + 1; h2 < 8; ++h2) inner = fmaf(g2[g][h2], sg[h2][r], inner);
+          x = fmaf(sg[g][r], inner, x);
+        }
+        kv[r] = x;
+      }
+    }
     float kap[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int j = 32 * tj + c32_row(r, l);
-      float kv = c0h;
-#pragma unroll
-      for (int g = 0; g < 8; ++g) {
-        float inner = fmaf(gd[g], sg[g][r], lamc[g]);
-#pragma unroll
-        for (int h2 = g + 1; h2 < 8; ++h2) inner = fmaf(g2[g][h2], sg[h2][r], inner);
-        kv = fmaf(sg[g][r], inner, kv);
-      }
-      kap[r] = (j <= i && irow) ? kv : 0.f;
+      kap[r] = (j <= i && irow) ? kv[r] : 0.f;
       dsum += kap[r];
       kapT[wv][c32_row(r, l)][row] = (__bf16)kap[r];
     }
@@ -628,8 +688,15 @@ void launch_mfma_forward(const LaunchGeom& g, const void* q, const void* k, cons
     launch_scan<true>(plan, a, st, timed);
   }
   timed("k2_intra_fwd", st, [&] {
-    hipLaunchKernelGGL(k2_intra_fwd<T>, dim3(g.R * g.NB * g.U), dim3(256), 0, st, qt, kt, vt, sv.PZ, sv.PZm, labels,
-                       sv.ic, sv.gm, sv.lb, groups, g.Hq, g.Hkv, g.N, g.NB, num, den, sv.KAP);
+    // more than 8 groups: per-pair coefficients, the feature-form local score
+    if (groups > 8)
+      hipLaunchKernelGGL((k2_intra_fwd<T, true>), dim3(g.R * g.NB * g.U), dim3(256), 0, st, qt, kt, vt, sv.PZ,
+                         sv.PZm, labels, sv.ic, sv.gm, sv.lb, sv.wqs, groups, g.Hq, g.Hkv, g.N, g.NB, num, den,
+                         sv.KAP);
+    else
+      hipLaunchKernelGGL((k2_intra_fwd<T, false>), dim3(g.R * g.NB * g.U), dim3(256), 0, st, qt, kt, vt, sv.PZ,
+                         sv.PZm, labels, sv.ic, sv.gm, sv.lb, sv.wqs, groups, g.Hq, g.Hkv, g.N, g.NB, num, den,
+                         sv.KAP);
   });
   timed("k2_out_fwd", st, [&] {
     hipLaunchKernelGGL(k2_out_fwd<T>, dim3(g.R * g.NB * g.U), dim3(128), 0, st, qt, sv.wqs, sv.PT, g.Hq, g.Hkv, g.N,

@@ -536,8 +536,11 @@ void launch_local_bwd(const LaunchGeom& g, const T* q, const T* k, const T* v, c
   // The coefficient partials come from the dq kernel's group sums, also when
   // dq itself is not requested (its dq then goes to the workspace unused), so
   // that every requested gradient is bit-identical whatever else is requested.
+  if (a.pairwise) {
+    launch_pair_local_bwd<T>(g, q, k, v, a, need_dq, need_dkv, st, timed);
+  }
   const bool coef = a.coefl != nullptr;
-  if (need_dq || coef) {
+  if (!a.pairwise && (need_dq || coef)) {
     timed("k2_local_dq", st, [&] {
       if (coef)
         hipLaunchKernelGGL((k2_local_dq<T, true>), dim3(g.R * g.NB * g.U), dim3(192), 0, st, q, k, v, a.G16, a.Gz,
@@ -549,7 +552,7 @@ void launch_local_bwd(const LaunchGeom& g, const T* q, const T* k, const T* v, c
                            a.scale, a.dqf, nullptr);
     });
   }
-  if (need_dkv) {
+  if (!a.pairwise && need_dkv) {
     timed("k2_local_dk", st, [&] {
       hipLaunchKernelGGL(k2_local_dk<T>, dim3(g.NB * g.U), dim3(192), 0, st, q, k, v, a.G16, a.Gz, a.QT16,
                          a.labels, a.lam, a.gam, a.groups, g.Hq, g.Hkv, g.N, g.NB, a.scale, a.dkl);

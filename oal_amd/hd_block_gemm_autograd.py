@@ -15,8 +15,12 @@ Two ``torch.autograd.Function`` classes share the same HIP forward/VJP:
   forward(q, k, v, a, b, c, scale, eps, layout, plan) -> (out, num, den) with
   logical per-dimension b [Hq, D] and per-pair c [Hq, D(D+1)/2]; backward
   returns 6 gradients + 4 ``None``, no double backward, gradients cast to the
-  input dtypes (:333-347). It runs the same kernels with one group per
-  dimension (labels = d, lam = b, Gam = symmetric fill of c).
+  input dtypes (:333-347). It runs the same library with one group per
+  dimension (labels = d, lam = b, Gam = symmetric fill of c, G = 64) in the
+  plan's precision: ``bf16_tensorcore`` takes the matrix-core path, whose
+  intra-chunk local score is then formed in feature form (phi_Q . phi_K^T on
+  the matrix cores, as ``hd_block_gemm_runtime.py:530-540``); ``fp32_ieee``
+  (or no plan) the fp32 kernels.
 
 Both pad D and DV up to 64 with zeros (padding contributes nothing) and slice
 the results back.
@@ -168,11 +172,13 @@ class _HDParallelBlockGemmFunction(torch.autograd.Function):
         kd = _kernel_dtype(q.dtype)
         qp, kp, vp = (_pad_last(t.detach().to(kd)) for t in (q, k, v))
         c0g, lam, gam, labels = logical_to_grouped(a.detach(), b.detach(), c.detach(), d)
-        out, num, den, saved = _native.forward(qp, kp, vp, labels, c0g, lam, gam, scale=scale, floor=eps)
+        precision = _plan_kernel_precision(plan)
+        out, num, den, saved = _native.forward(qp, kp, vp, labels, c0g, lam, gam, scale=scale, floor=eps,
+                                               precision=precision)
         if plan is not None and getattr(plan, "require_positive_denominator", True):
             _require_positive_denominator(den)
         ctx.save_for_backward(qp, kp, vp, c0g, lam, gam, labels, num, den, saved)
-        ctx.meta = (float(scale), float(eps), d, dv, gradient_mask)
+        ctx.meta = (float(scale), float(eps), d, dv, gradient_mask, precision)
         ctx.input_dtypes = tuple(t.dtype for t in (q, k, v, a, b, c))
         out = out[..., :dv].to(q.dtype)
         return out, num[..., :dv], den
@@ -182,7 +188,7 @@ class _HDParallelBlockGemmFunction(torch.autograd.Function):
         if torch.is_grad_enabled():
             raise RuntimeError("HD Block-GEMM does not support double backward")
         qp, kp, vp, c0g, lam, gam, labels, num, den, saved = ctx.saved_tensors
-        scale, eps, d, dv, mask = ctx.meta
+        scale, eps, d, dv, mask, precision = ctx.meta
         if dout is None and dnum is None and dden is None:
             return (None,) * 10
         if dout is not None:
@@ -193,7 +199,7 @@ class _HDParallelBlockGemmFunction(torch.autograd.Function):
         dq, dk, dvv, dc0, dlam, dgam = _native.backward(
             qp, kp, vp, labels, c0g, lam, gam, num, den, saved, dout, dnum, dden,
             scale=scale, floor=eps, need_q=need_q, need_k=need_k, need_v=need_v,
-            need_coef=need_a or need_b or need_c,
+            need_coef=need_a or need_b or need_c, precision=precision,
         )
         rows, cols = _pair_rows_cols(d, qp.device)
         grads = [
@@ -208,6 +214,14 @@ class _HDParallelBlockGemmFunction(torch.autograd.Function):
         ]
         out = [g.to(dt) if g is not None else None for g, dt in zip(grads, ctx.input_dtypes)]
         return (*out, None, None, None, None)
+
+
+def _plan_kernel_precision(plan) -> str:
+    """Planner precision -> kernel arithmetic ("bf16" on the matrix cores for
+    ``bf16_tensorcore``, else "fp32"; no plan: "fp32")."""
+    if plan is not None and getattr(plan, "precision", "fp32_ieee") == "bf16_tensorcore":
+        return "bf16"
+    return "fp32"
 
 
 def _require_positive_denominator(den: torch.Tensor) -> None:

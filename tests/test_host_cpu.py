@@ -44,8 +44,13 @@ def test_size_queries_and_argument_errors_without_a_gpu():
     fp32 = lib.oal_forward_saved_bytes(1, 14, 2, 4096, 8, 1, 0)
     mfma = lib.oal_forward_saved_bytes(1, 14, 2, 4096, 8, 1, 1)
     assert fp32 > 0 and mfma > 0 and mfma != fp32
-    # more than 8 groups keeps the fp32 kernels (and their saved layout)
-    assert lib.oal_forward_saved_bytes(1, 14, 2, 4096, 64, 1, 1) == fp32
+    # more than 8 groups stays on the matrix cores (feature-form local score,
+    # same saved layout); more than 8 query heads per KV head runs the fp32 kernels
+    assert lib.oal_forward_saved_bytes(1, 14, 2, 4096, 64, 1, 1) == mfma
+    assert lib.oal_forward_saved_bytes(1, 18, 2, 4096, 8, 1, 1) == lib.oal_forward_saved_bytes(1, 18, 2, 4096, 8, 1, 0)
+    # the per-pair path's workspace holds its local buffers too
+    assert lib.oal_backward_workspace_bytes(1, 14, 2, 4096, 64, 1, 1) > lib.oal_backward_workspace_bytes(
+        1, 14, 2, 4096, 8, 1, 1)
     assert lib.oal_backward_workspace_bytes(4, 14, 2, 4096, 8, 1, 1) > 0
     assert lib.oal_forward_saved_bytes(1, 14, 3, 4096, 8, 1, 0) == 0  # Hq % Hkv != 0
     assert b"divisible" in lib.oal_last_error()
