@@ -267,6 +267,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--batch", type=int, default=4)
     ap.add_argument("--seq-len", type=int, default=4096)
+    ap.add_argument("--precision", choices=("bf16", "fp32"), default="bf16",
+                    help="bf16: the matrix-core kernels (the headline metric); fp32: the fp32 route that "
+                         "oal_attention's default execution takes (bf16 inputs, fp32 arithmetic)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-materialized", action="store_true",
                     help="also time the materializing reference algorithm at B=1, N=512 and 1024 (about a minute)")
@@ -305,6 +308,7 @@ def main() -> int:
         torch.cuda.synchronize()
         del src, dst
     inp = make_inputs(b, n, dev)
+    inp["precision"] = args.precision
     for _ in range(args.warmup):
         step(inp)
     torch.cuda.synchronize()
@@ -353,7 +357,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": "bf16" if args.precision == "bf16" else "f32 (bf16 inputs)",
         "data": "synthetic (BASELINE config 2 distributions: N(0,1) with 2 outlier dims x8 per head, "
                 "8 uneven groups, c0=1, a~U(0.5,1.5), b~U(0,0.5)); these coefficients are not PSD and the "
                 "fp32 oracle finds den <= 0 on 19 of the 229376 tokens at config 2, an output the reference's "

@@ -387,8 +387,18 @@ __global__ __launch_bounds__(256) void k_q_bwd(const T* __restrict__ q, const T*
       for (int j = 0; j <= i; ++j) dphi += dsm[i][j] * kx[j][r] * kx[j][c];
       const float qr = qx[i][r], qc = qx[i][c];
       const float wd = wqh[f] * dphi;
-      atomicAdd(&dqa[i][r], wd * qc);
-      atomicAdd(&dqa[i][c], wd * qr);
+      // the four lanes of token i (one wave) add their features' terms to its
+      // row in turn, feature order f0 + 4 m + 0 .. 3: a fixed summation order
+      // (lanes of the other tokens write other rows in the same turn)
+      const float ar = wd * qc, ac = wd * qr;
+#pragma unroll
+      for (int turn = 0; turn < 4; ++turn) {
+        if (fq == turn) {
+          dqa[i][r] += ar;
+          dqa[i][c] += ac;
+        }
+        __builtin_amdgcn_wave_barrier();
+      }
       // sum over the 64 tokens: lanes sharing t % 4 within the wave, then waves
       float part = qr * qc * dphi;
       part += __shfl_xor(part, 4, 64);
@@ -467,8 +477,16 @@ __global__ __launch_bounds__(256) void k_kv_bwd(const T* __restrict__ q, const T
       const int r = kTab.r[f], c = kTab.c[f];
       float dphi = pt[fl][kD] * kx[j][kD];
       for (int e = 0; e < kD; ++e) dphi += pt[fl][e] * vx[j][e];
-      atomicAdd(&dka[j][r], dphi * kx[j][c]);
-      atomicAdd(&dka[j][c], dphi * kx[j][r]);
+      // the four lanes of token j (one wave) add in turn: a fixed order
+      const float ar = dphi * kx[j][c], ac = dphi * kx[j][r];
+#pragma unroll
+      for (int turn = 0; turn < 4; ++turn) {
+        if (xq == turn) {
+          dka[j][r] += ar;
+          dka[j][c] += ac;
+        }
+        __builtin_amdgcn_wave_barrier();
+      }
     }
   }
 
