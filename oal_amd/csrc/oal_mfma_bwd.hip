@@ -357,11 +357,15 @@ __device__ __forceinline__ void du_group(const float (&x)[kD], const LdsRing<4>&
   if constexpr (G + 1 < NG) du_group<G + 1, UPG, CARRY>(x, ring, src, csrc, tid, lane, acc);
 }
 
-// grid (NB, U, 2), 2 waves; wave w owns tokens 32w..32w+31 of the chunk.
+// grid NB * U * 2 blocks of 2 waves; wave w owns tokens 32w..32w+31 of the chunk.
 //   part 0: dk = fold of dT V^T through the key features + z1 + Mz k + local dk,
 //           Mz[r][c] = dTz[pair(r, c)] (r != c), 2 dTz[pair(r, r)] on the diagonal;
 //   part 1: dv = raw(K) dT (values 0..63) + local dv.
-// The two parts share nothing, so they run as independent blocks.
+// The two parts share nothing, so they run as independent blocks. Block ids
+// are dealt to the 8 XCDs round-robin; item w = (id % 8) * (total / 8) + id / 8
+// (chunk fastest, then part, then unit) gives each XCD consecutive chunks of
+// both parts of a unit, so that the chunks of a segment read its carry through
+// one L2.
 // CARRY: dT of chunk ch is the backward scan's segment-local state plus the
 // carry of the chunk's segment (ch / SL, cR / cT [U][S]); both products of each
 // step accumulate into the same registers, so the carry costs matrix products
@@ -381,7 +385,14 @@ __global__ __launch_bounds__(128, 2) void k2_kv_fold(const T* __restrict__ k, co
   // four blocks (the register limit) fit a CU
   __shared__ __attribute__((aligned(16))) __bf16 mz[kD][kD];
 
-  const int ch = blockIdx.x, u = blockIdx.y, part = blockIdx.z;
+  int ch, u, part;
+  {
+    const int total = gridDim.x, id = blockIdx.x;
+    const int w = (total & 7) == 0 ? (id & 7) * (total >> 3) + (id >> 3) : id;
+    ch = w % NB;
+    part = (w / NB) & 1;
+    u = w / (2 * NB);
+  }
   const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, s = l >> 5, row = l & 31;
   const int tok0 = ch * kC;
   const size_t kbase = (size_t)u * N * kD;
@@ -767,11 +778,11 @@ int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, cons
   if (dk) {
     timed("k2_kv_fold", st, [&] {
       if (w.S > 1)
-        hipLaunchKernelGGL((k2_kv_fold<T, true>), dim3(g.NB, g.U, 2), dim3(128), 0, st, kt, vt, w.dTR, w.dTT, w.dCR,
+        hipLaunchKernelGGL((k2_kv_fold<T, true>), dim3(g.NB * g.U * 2), dim3(128), 0, st, kt, vt, w.dTR, w.dTT, w.dCR,
                            w.dCT, w.SL, w.S, w.dTz, w.dkl, w.dvl, g.Hq, g.Hkv, g.N, g.NB, static_cast<T*>(dk),
                            static_cast<T*>(dv));
       else
-        hipLaunchKernelGGL((k2_kv_fold<T, false>), dim3(g.NB, g.U, 2), dim3(128), 0, st, kt, vt, w.dTR, w.dTT,
+        hipLaunchKernelGGL((k2_kv_fold<T, false>), dim3(g.NB * g.U * 2), dim3(128), 0, st, kt, vt, w.dTR, w.dTT,
                            nullptr, nullptr, 1, 1, w.dTz, w.dkl, w.dvl, g.Hq, g.Hkv, g.N, g.NB,
                            static_cast<T*>(dk), static_cast<T*>(dv));
     });
