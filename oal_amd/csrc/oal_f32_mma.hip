@@ -1,0 +1,780 @@
+// fp32 route on the gfx950 matrix cores (v_mfma_f32_32x32x2f32), for up to 8
+// groups: the same chunked feature form as the scalar fp32 kernels of
+// oal_kernels.hip (and the same natural-order fp32 state buffers, so the
+// saved state is interchangeable), with the 2145-wide state contractions on
+// the matrix cores and the intra-chunk terms in group-sum form.
+//
+//   k3_state_fwd   P_c = sum_{c' < c} raw(K_c')^T [V_c', 1]          (exclusive prefix)
+//   k3_state_bwd   dT_c = sum_{c' > c} sum_h wq_h o raw(Q_h,c')^T [G, Gz]_h,c'
+//                  and the state part of the feature-coefficient gradient
+//                  dwq_part[b][h][c][f] = <P_c[f], raw(Q_h,c)^T [G, Gz]_h,c[f]>
+//   k3_readout     num += phi(x) . S (out: num / den), or dv = raw(K) dT + local
+//   k3_fold        dq = fold of (P [G, Gz]^T) through wq o raw(q) + local,
+//                  dk = fold of (dT [V, 1]^T) through raw(k) + local
+//   k3_q_local     local dq and the local coefficient partials (group sums)
+//   k3_coef_reduce per-head sums of those partials
+//
+// Matrix layout of v_mfma_f32_32x32x2f32: lane l supplies A[l % 32][l / 32]
+// and B[l / 32][l % 32]; accumulator register i of lane l holds
+// C[8 (i / 4) + 4 (l / 32) + i % 4][l % 32] (the 32 x 32 layout of the bf16
+// kernels). The K index pairs (k, lane group s) are mapped to the contracted
+// dimension in whatever order keeps the operand loads contiguous; both
+// operands use the same map.
+//
+// Reference: the feature-form state terms follow hd_block_gemm_runtime.py
+// :271-320 (block totals, exclusive prefix), :411-614 (query readout) and
+// hd_block_gemm_backward.py :473-761 (query-side VJP), :764-908 (dCarry and
+// its right scan), :1031-1452 (key/value-side VJP); the local terms follow
+// the closed-form VJP of grouped_reference.py:214-318 in group-sum form.
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <utility>
+
+#include "oal_common.hpp"
+#include "oal_internal.hpp"
+#include "oal_mfma_common.hpp"
+#include "oal_mfma_fold.hpp"
+
+namespace oal {
+
+namespace {
+
+__constant__ FeatureTable kTab3 = make_feature_table();
+__constant__ SlotTable kSlot3 = make_slot_table();
+
+__device__ __forceinline__ f32x16 mfma_f32(float a, float b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+// The other lane group's value of x (lanes l and l ^ 32).
+__device__ __forceinline__ float partner(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
+}
+
+// 16 consecutive elements of a token row as fp32 (zeros when !ok).
+__device__ __forceinline__ void load16(const float* __restrict__ src, size_t off, bool ok, float (&v)[16]) {
+  const float4* p = reinterpret_cast<const float4*>(src + off);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float4 a = p[i];
+    v[4 * i] = ok ? a.x : 0.f;
+    v[4 * i + 1] = ok ? a.y : 0.f;
+    v[4 * i + 2] = ok ? a.z : 0.f;
+    v[4 * i + 3] = ok ? a.w : 0.f;
+  }
+}
+__device__ __forceinline__ void load16(const uint16_t* __restrict__ src, size_t off, bool ok, float (&v)[16]) {
+  const uint4* p = reinterpret_cast<const uint4*>(src + off);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const uint4 a = p[i];
+    const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[8 * i + 2 * e] = ok ? __uint_as_float(w[e] << 16) : 0.f;
+      v[8 * i + 2 * e + 1] = ok ? __uint_as_float(w[e] & 0xffff0000u) : 0.f;
+    }
+  }
+}
+
+// Rotated fp32 row x[m] = row[(m + 32 s) % 64], exact (the bf16 route's
+// load_rotated rounds its input to bf16).
+template <typename T>
+__device__ __forceinline__ void load_rotated_f32(const T* __restrict__ src, size_t row_base, bool ok, int s,
+                                                 float (&x)[kD]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float v[16];
+    load16(src, row_base + ((16 * i + 32 * s) & 63), ok, v);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) x[16 * i + j] = v[j];
+  }
+}
+
+// Thread t of a 256-thread block holds dims 16 (t % 4) .. + 15 of token t / 4
+// of a chunk; rows past N are zero.
+template <typename T>
+__device__ __forceinline__ void load_chunk_rows(const T* __restrict__ src, size_t base, int tok0, int N,
+                                                float (&v)[16]) {
+  const int j = threadIdx.x >> 2, q4 = threadIdx.x & 3, tok = tok0 + j;
+  const bool ok = tok < N;
+  load16(src, base + (size_t)(ok ? tok : N - 1) * kD + 16 * q4, ok, v);
+}
+template <int LDW>
+__device__ __forceinline__ void store_chunk_rows(float (*dst)[LDW], const float (&v)[16]) {
+  const int j = threadIdx.x >> 2, q4 = threadIdx.x & 3;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) dst[j][16 * q4 + i] = v[i];
+}
+
+// Stores this lane's accumulator values (rows 32 m + 8 a + 4 s + 0..3 of
+// the value dimension) into row f of a [.][64] state.
+__device__ __forceinline__ void store_state_row(float* __restrict__ row, int m, int s, const f32x16& acc) {
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+    *reinterpret_cast<float4*>(row + 32 * m + 8 * a + 4 * s) =
+        make_float4(acc[4 * a], acc[4 * a + 1], acc[4 * a + 2], acc[4 * a + 3]);
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// Forward state scan: block (64-feature slice, unit), 4 waves; wave w owns
+// features 64 x + 32 (w / 2) + lane % 32 (lane column) and values
+// 32 (w % 2) .. + 31 (accumulator rows). Per chunk: emit the prefix, then add
+// raw(K_c)^T [V_c, 1] as D^T[e][f] = sum_t V[t][e] raw_f(k_t) (K = tokens,
+// token 32 s + k at step k), the ones column as a per-lane sum.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void k3_state_fwd(const T* __restrict__ k, const T* __restrict__ v, int N, int NB,
+                                                    float* __restrict__ carry, float* __restrict__ carry_z) {
+  __shared__ float kx[kC][kRow];   // [k, 1 (token < N), 0]
+  __shared__ float vx[kC][kD + 1];
+  const int u = blockIdx.y, tid = threadIdx.x, wv = tid >> 6, l = tid & 63, s = l >> 5, row = l & 31;
+  const int m = wv & 1, f = blockIdx.x * 64 + 32 * (wv >> 1) + row;
+  const int r = kTab3.r[f], c = kTab3.c[f];
+  const size_t base = (size_t)u * N * kD;
+  float kr[16], vr[16];
+  load_chunk_rows(k, base, 0, N, kr);
+  load_chunk_rows(v, base, 0, N, vr);
+  f32x16 acc = f32x16{};
+  float accz = 0.f;
+  for (int ch = 0; ch < NB; ++ch) {
+    const size_t cb = (size_t)u * NB + ch;
+    store_state_row(carry + (cb * kFP + f) * kD, m, s, acc);
+    const float zt = accz + partner(accz);
+    if (m == 0 && s == 0) carry_z[cb * kFP + f] = zt;
+    __syncthreads();
+    store_chunk_rows(kx, kr);
+    store_chunk_rows(vx, vr);
+    if ((tid & 3) == 0) {
+      kx[tid >> 2][kD] = ch * kC + (tid >> 2) < N ? 1.f : 0.f;
+      kx[tid >> 2][kD + 1] = 0.f;
+    }
+    __syncthreads();
+    if (ch + 1 < NB) {
+      load_chunk_rows(k, base, (ch + 1) * kC, N, kr);
+      load_chunk_rows(v, base, (ch + 1) * kC, N, vr);
+    }
+#pragma unroll 8
+    for (int kk = 0; kk < 32; ++kk) {
+      const int t = 32 * s + kk;
+      const float phi = kx[t][r] * kx[t][c];
+      acc = mfma_f32(vx[t][32 * m + row], phi, acc);
+      accz += phi;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Backward state scan: block (64-feature slice, unit), waves as above; walks
+// the chunks downwards, the unit's query heads within a chunk. Per item
+// (chunk, head): H = raw(Q)^T [G, Gz] (kept apart), dT += wq_h o H; before a
+// chunk's first item the suffix of the later chunks is emitted. With dwq_part
+// the item also writes <P_c[f], H[f]> (values of both waves and the ones
+// column, in a fixed order).
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void k3_state_bwd(const T* __restrict__ q, const float* __restrict__ G,
+                                                    const float* __restrict__ Gz, const float* __restrict__ wq,
+                                                    const float* __restrict__ P, const float* __restrict__ Pz, int Hq,
+                                                    int Hkv, int N, int NB, float* __restrict__ dT,
+                                                    float* __restrict__ dTz, float* __restrict__ dwq_part) {
+  __shared__ float qx[kC][kRow];
+  __shared__ float gs[kC][kD + 1];  // [G, Gz]
+  __shared__ float xch[2][32];
+  const int u = blockIdx.y, R = Hq / Hkv, b = u / Hkv, kh = u % Hkv;
+  const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, s = l >> 5, row = l & 31;
+  const int m = wv & 1, ft = wv >> 1, f = blockIdx.x * 64 + 32 * ft + row;
+  const int r = kTab3.r[f], c = kTab3.c[f];
+  const int NI = NB * R;
+  float qr[16], gr[16], gzr = 0.f;
+  auto load_item = [&](int it) {
+    const int ch = NB - 1 - it / R, h = kh * R + it % R;
+    const size_t hb = (size_t)(b * Hq + h) * N;
+    load_chunk_rows(q, hb * kD, ch * kC, N, qr);
+    load_chunk_rows(G, hb * kD, ch * kC, N, gr);
+    const int tok = ch * kC + (tid >> 2);
+    gzr = (tid & 3) == 0 && tok < N ? Gz[hb + tok] : 0.f;
+  };
+  load_item(0);
+  f32x16 acc = f32x16{};
+  float accz = 0.f;
+  float pr[16];
+  float pz = 0.f;
+  for (int it = 0; it < NI; ++it) {
+    const int ch = NB - 1 - it / R, hh = it % R, h = kh * R + hh;
+    const size_t cb = (size_t)u * NB + ch;
+    if (hh == 0) {
+      store_state_row(dT + (cb * kFP + f) * kD, m, s, acc);
+      const float zt = accz + partner(accz);
+      if (m == 0 && s == 0) dTz[cb * kFP + f] = zt;
+      if (dwq_part) {
+        const float* prow = P + (cb * kFP + f) * kD + 32 * m + 4 * s;
+#pragma unroll
+        for (int a = 0; a < 4; ++a) {
+          const float4 x = *reinterpret_cast<const float4*>(prow + 8 * a);
+          pr[4 * a] = x.x;
+          pr[4 * a + 1] = x.y;
+          pr[4 * a + 2] = x.z;
+          pr[4 * a + 3] = x.w;
+        }
+        pz = Pz[cb * kFP + f];
+      }
+    }
+    const float w = wq[(size_t)h * kFP + f];
+    __syncthreads();
+    store_chunk_rows(qx, qr);
+    store_chunk_rows(gs, gr);
+    if ((tid & 3) == 0) {
+      qx[tid >> 2][kD] = ch * kC + (tid >> 2) < N ? 1.f : 0.f;
+      qx[tid >> 2][kD + 1] = 0.f;
+      gs[tid >> 2][kD] = gzr;
+    }
+    __syncthreads();
+    if (it + 1 < NI) load_item(it + 1);
+    f32x16 hT = f32x16{};
+    float hz = 0.f;
+#pragma unroll 8
+    for (int kk = 0; kk < 32; ++kk) {
+      const int t = 32 * s + kk;
+      const float phi = qx[t][r] * qx[t][c];
+      hT = mfma_f32(gs[t][32 * m + row], phi, hT);
+      hz += phi * gs[t][kD];
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[i] = fmaf(w, hT[i], acc[i]);
+    accz = fmaf(w, hz, accz);
+    if (dwq_part) {
+      float dp[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < 16; ++i) dp[i & 3] = fmaf(pr[i], hT[i], dp[i & 3]);
+      float p = (dp[0] + dp[1]) + (dp[2] + dp[3]);
+      p += partner(p);
+      const float hzt = hz + partner(hz);
+      if (m == 1 && s == 0) xch[ft][row] = p;
+      __syncthreads();
+      if (m == 0 && s == 0) dwq_part[((size_t)(b * Hq + h) * NB + ch) * kFP + f] = p + xch[ft][row] + pz * hzt;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Slot-ordered state tiles. M-tile M holds the 32 slots 32 M .. 32 M + 31
+// (bases 16 M .. 16 M + 15): row j = the natural-order state row of slot
+// 32 M + j (64 values, then the ones column; zero for an invalid slot),
+// gathered into LDS rows of kStRow floats.
+// ---------------------------------------------------------------------------
+constexpr int kStRow = kD + 4;
+constexpr int kMT = kS / 32;  // 69
+
+// NT threads stage one tile: thread t moves 2048 / NT values (float4s) and,
+// for t < 32, the ones column of row t. With wqh (a query head's feature
+// coefficients) each row is scaled by its slot's coefficient: the products
+// that read the tile are linear in it, so the weighted tile gives the
+// weighted readout or fold directly.
+template <int NT>
+struct TileRegs {
+  float4 v[512 / NT];
+  float z;
+};
+template <int NT>
+__device__ __forceinline__ void load_tile(const float* __restrict__ S, const float* __restrict__ Sz, size_t cb, int M,
+                                          const float* __restrict__ wqh, TileRegs<NT>& tr) {
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < 512 / NT; ++i) {
+    const int idx = t + NT * i, j = idx >> 4, c4 = idx & 15;
+    const int nat = kSlot3.nat[32 * M + j];
+    float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (nat >= 0) {
+      a = *reinterpret_cast<const float4*>(S + (cb * kFP + nat) * kD + 4 * c4);
+      if (wqh) {
+        const float w = wqh[nat];
+        a = make_float4(a.x * w, a.y * w, a.z * w, a.w * w);
+      }
+    }
+    tr.v[i] = a;
+  }
+  if (t < 32) {
+    const int nat = kSlot3.nat[32 * M + t];
+    tr.z = nat >= 0 ? Sz[cb * kFP + nat] * (wqh ? wqh[nat] : 1.f) : 0.f;
+  }
+}
+template <int NT>
+__device__ __forceinline__ void store_tile(float* __restrict__ st, const TileRegs<NT>& tr) {
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < 512 / NT; ++i) {
+    const int idx = t + NT * i, j = idx >> 4, c4 = idx & 15;
+    *reinterpret_cast<float4*>(st + j * kStRow + 4 * c4) = tr.v[i];
+  }
+  if (t < 32) st[t * kStRow + kD] = tr.z;
+}
+
+
+// ---------------------------------------------------------------------------
+// Readout: block of 4 waves per (query head, chunk, unit) (MODE 0) or (chunk,
+// unit) (MODE 1); wave w owns values 32 (w % 2) .. + 31 (accumulator rows)
+// and tokens 32 (w / 2) + lane % 32 (lane column):
+//   D^T[e][t] = sum_slots S[slot][e] phi_slot(x_t),
+// one base per step: lane group s evaluates slot (base, s) on its rotated row
+// (static registers); the tile rows carry the slot weights (MODE 0). MODE 0
+// adds D to the local numerator in num, the ones column to den, and writes
+// out = num / den'; MODE 1 writes dv = D + dvl.
+// ---------------------------------------------------------------------------
+template <int B, int MODE>
+__device__ __forceinline__ void readout_base(const float (&x)[kD], const float* st, int m, int s, int row,
+                                             f32x16& acc, float& zacc) {
+  constexpr int lb = B % 16;
+  const int sr = 16 * (lb / 8) + 8 * s + lb % 8;  // row of slot (B, s) in the tile
+  const float phi = base_value<B>(x);
+  acc = mfma_f32(st[sr * kStRow + 32 * m + row], phi, acc);
+  if constexpr (MODE == 0) {
+    zacc = fmaf(st[sr * kStRow + kD], phi, zacc);
+    // keep the chain in step with the products (deferring it holds every
+    // product live and spills)
+    asm volatile("" : "+v"(zacc));
+  }
+}
+
+template <int M, int MODE>
+__device__ __forceinline__ void readout_tiles(const float (&x)[kD], float* st0, float* st1,
+                                              const float* __restrict__ S, const float* __restrict__ Sz, size_t cb,
+                                              const float* wqh, int m, int s, int row, TileRegs<256>& tr,
+                                              f32x16& acc, float& zacc) {
+  const float* st = (M & 1) ? st1 : st0;
+  [&]<int... J>(std::integer_sequence<int, J...>) {
+    (readout_base<16 * M + J, MODE>(x, st, m, s, row, acc, zacc), ...);
+  }(std::make_integer_sequence<int, 16>{});
+  if constexpr (M + 1 < kMT) {
+    store_tile<256>((M & 1) ? st0 : st1, tr);
+    if constexpr (M + 2 < kMT) load_tile<256>(S, Sz, cb, M + 2, wqh, tr);
+    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
+    readout_tiles<M + 1, MODE>(x, st0, st1, S, Sz, cb, wqh, m, s, row, tr, acc, zacc);
+  }
+}
+
+template <typename T, int MODE>
+__global__ __launch_bounds__(256, 2) void k3_readout(const T* __restrict__ x_in, const float* __restrict__ wq,
+                                                     const float* __restrict__ S, const float* __restrict__ Sz, int Hq,
+                                                     int Hkv, int N, int NB, float floor, float* __restrict__ num,
+                                                     float* __restrict__ den, T* __restrict__ out,
+                                                     const float* __restrict__ dvl, T* __restrict__ dv) {
+  __shared__ __attribute__((aligned(16))) float st0[32 * kStRow], st1[32 * kStRow];
+  __shared__ float zd[kC];
+  int hh = 0, ch, u;
+  if constexpr (MODE == 0) {
+    head_chunk_unit(Hq / Hkv, NB, (int)(gridDim.x / ((Hq / Hkv) * NB)), hh, ch, u);
+  } else {
+    const int total = gridDim.x, id = blockIdx.x;
+    const int w = (total & 7) == 0 ? (id & 7) * (total >> 3) + (id >> 3) : id;
+    ch = w % NB;
+    u = w / NB;
+  }
+  const int R = Hq / Hkv, b = u / Hkv, kh = u % Hkv, h = kh * R + hh;
+  const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, s = l >> 5, row = l & 31;
+  const int m = wv & 1, n = wv >> 1;
+  const int tok0 = ch * kC;
+  const size_t xbase = MODE == 0 ? (size_t)(b * Hq + h) * N * kD : (size_t)u * N * kD;
+  const size_t cb = (size_t)u * NB + ch;
+  const float* wqh = MODE == 0 ? wq + (size_t)h * kFP : nullptr;
+  const int tok = tok0 + 32 * n + row;
+  const bool ok = tok < N;
+  float x[kD];
+  load_rotated_f32(x_in, xbase + (size_t)(ok ? tok : N - 1) * kD, ok, s, x);
+  TileRegs<256> tr;
+  load_tile<256>(S, Sz, cb, 0, wqh, tr);
+  store_tile<256>(st0, tr);
+  load_tile<256>(S, Sz, cb, 1, wqh, tr);
+  __syncthreads();
+  f32x16 acc = f32x16{};
+  float zacc = 0.f;
+  readout_tiles<0, MODE>(x, st0, st1, S, Sz, cb, wqh, m, s, row, tr, acc, zacc);
+
+  if constexpr (MODE == 0) {
+    const size_t dbase = (size_t)(b * Hq + h) * N;
+    if (m == 0) {
+      const float z = zacc + partner(zacc);
+      if (s == 0) zd[32 * n + row] = (ok ? den[dbase + tok] : 0.f) + z;
+    }
+    __syncthreads();
+    if (ok) {
+      const float dd = zd[32 * n + row];
+      if (m == 0 && s == 0) den[dbase + tok] = dd;
+      const float inv = 1.f / (floor > 0.f ? fmaxf(dd, floor) : dd);
+      float* nrow = num + xbase + (size_t)tok * kD + 32 * m + 4 * s;
+      T* orow = out + xbase + (size_t)tok * kD + 32 * m + 4 * s;
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        const float4 loc = *reinterpret_cast<const float4*>(nrow + 8 * a);
+        const float y[4] = {acc[4 * a] + loc.x, acc[4 * a + 1] + loc.y, acc[4 * a + 2] + loc.z,
+                            acc[4 * a + 3] + loc.w};
+        *reinterpret_cast<float4*>(nrow + 8 * a) = make_float4(y[0], y[1], y[2], y[3]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) orow[8 * a + e] = from_f<T>(y[e] * inv);
+      }
+    }
+  } else {
+    if (ok) {
+      const float* lrow = dvl + xbase + (size_t)tok * kD + 32 * m + 4 * s;
+      T* drow = dv + xbase + (size_t)tok * kD + 32 * m + 4 * s;
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        const float4 loc = *reinterpret_cast<const float4*>(lrow + 8 * a);
+        drow[8 * a] = from_f<T>(acc[4 * a] + loc.x);
+        drow[8 * a + 1] = from_f<T>(acc[4 * a + 1] + loc.y);
+        drow[8 * a + 2] = from_f<T>(acc[4 * a + 2] + loc.z);
+        drow[8 * a + 3] = from_f<T>(acc[4 * a + 3] + loc.w);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Fold: block of 2 waves per (query head, chunk, unit) (MODE 0, dq) or
+// (chunk, unit) (MODE 1, dk); wave w owns tokens 32 w + lane % 32. Per
+// M-tile: D^T[slot][t] = sum_e S[slot][e] y_t[e] + Sz[slot] y_t[64] (A rows
+// in the fold row order, K index = value 32 s + k at step k, the ones column
+// as a 33rd step in lane group 0), y = [G, Gz] (MODE 0) or [v, 1] (MODE 1),
+// then folded through the rotated row (static registers); the tile rows carry
+// the slot weights (MODE 0). The result plus the local part is written as
+// dq / dk.
+// ---------------------------------------------------------------------------
+template <int M>
+__device__ __forceinline__ void fold_tile_f32(const float (&x)[kD], float (&dx)[kD], const float (&yv)[32], float yz,
+                                              const float* st, int s, int row) {
+  const float* ar = st + fold::fold_row(row) * kStRow + 32 * s;
+  f32x16 D = f32x16{};
+#pragma unroll
+  for (int k4 = 0; k4 < 8; ++k4) {
+    const float4 a = *reinterpret_cast<const float4*>(ar + 4 * k4);
+    D = mfma_f32(a.x, yv[4 * k4], D);
+    D = mfma_f32(a.y, yv[4 * k4 + 1], D);
+    D = mfma_f32(a.z, yv[4 * k4 + 2], D);
+    D = mfma_f32(a.w, yv[4 * k4 + 3], D);
+  }
+  const float az = s == 0 ? st[fold::fold_row(row) * kStRow + kD] : 0.f;
+  D = mfma_f32(az, s == 0 ? yz : 0.f, D);
+  float w16[16];
+  fold::fold_weights<M, false>(nullptr, s, w16);
+  fold::fold_tile<M>(D, x, dx, w16);
+}
+
+template <int M>
+__device__ __forceinline__ void fold_tiles(const float (&x)[kD], float (&dx)[kD], const float (&yv)[32], float yz,
+                                           float* st0, float* st1, const float* __restrict__ S,
+                                           const float* __restrict__ Sz, size_t cb, const float* wqh, int s, int row,
+                                           TileRegs<128>& tr) {
+  pin64(dx);
+  fold_tile_f32<M>(x, dx, yv, yz, (M & 1) ? st1 : st0, s, row);
+  if constexpr (M + 1 < kMT) {
+    store_tile<128>((M & 1) ? st0 : st1, tr);
+    if constexpr (M + 2 < kMT) load_tile<128>(S, Sz, cb, M + 2, wqh, tr);
+    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
+    fold_tiles<M + 1>(x, dx, yv, yz, st0, st1, S, Sz, cb, wqh, s, row, tr);
+  }
+}
+
+template <typename T, int MODE>
+__global__ __launch_bounds__(128, 2) void k3_fold(const T* __restrict__ x_in, const float* __restrict__ y_in,
+                                                  const T* __restrict__ v_in, const float* __restrict__ yz_in,
+                                                  const float* __restrict__ wq, const float* __restrict__ S,
+                                                  const float* __restrict__ Sz, const float* __restrict__ local,
+                                                  int Hq, int Hkv, int N, int NB, T* __restrict__ dx_out) {
+  __shared__ __attribute__((aligned(16))) float st0[32 * kStRow], st1[32 * kStRow];
+  int hh = 0, ch, u;
+  if constexpr (MODE == 0) {
+    head_chunk_unit(Hq / Hkv, NB, (int)(gridDim.x / ((Hq / Hkv) * NB)), hh, ch, u);
+  } else {
+    const int total = gridDim.x, id = blockIdx.x;
+    const int w = (total & 7) == 0 ? (id & 7) * (total >> 3) + (id >> 3) : id;
+    ch = w % NB;
+    u = w / NB;
+  }
+  const int R = Hq / Hkv, b = u / Hkv, kh = u % Hkv, h = kh * R + hh;
+  const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, s = l >> 5, row = l & 31;
+  const int tok0 = ch * kC;
+  const size_t xbase = MODE == 0 ? (size_t)(b * Hq + h) * N * kD : (size_t)u * N * kD;
+  const size_t cb = (size_t)u * NB + ch;
+  const float* wqh = MODE == 0 ? wq + (size_t)h * kFP : nullptr;
+  const int tok = tok0 + 32 * wv + row;
+  const bool ok = tok < N;
+  const size_t rowoff = xbase + (size_t)(ok ? tok : N - 1) * kD;
+  float x[kD], dx[kD];
+  load_rotated_f32(x_in, rowoff, ok, s, x);
+  // the lane group's half of y (values 32 s .. 32 s + 31) and the ones column
+  float yv[32];
+  float yz;
+  if constexpr (MODE == 0) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float4 a = reinterpret_cast<const float4*>(y_in + rowoff + 32 * s)[i];
+      yv[4 * i] = ok ? a.x : 0.f;
+      yv[4 * i + 1] = ok ? a.y : 0.f;
+      yv[4 * i + 2] = ok ? a.z : 0.f;
+      yv[4 * i + 3] = ok ? a.w : 0.f;
+    }
+    yz = ok ? yz_in[(size_t)(b * Hq + h) * N + tok] : 0.f;
+  } else {
+    float t16[16];
+    load16(v_in, rowoff + 32 * s, ok, t16);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) yv[i] = t16[i];
+    load16(v_in, rowoff + 32 * s + 16, ok, t16);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) yv[16 + i] = t16[i];
+    yz = ok ? 1.f : 0.f;
+  }
+#pragma unroll
+  for (int i = 0; i < kD; ++i) dx[i] = 0.f;
+  TileRegs<128> tr;
+  load_tile<128>(S, Sz, cb, 0, wqh, tr);
+  store_tile<128>(st0, tr);
+  load_tile<128>(S, Sz, cb, 1, wqh, tr);
+  __syncthreads();
+  fold_tiles<0>(x, dx, yv, yz, st0, st1, S, Sz, cb, wqh, s, row, tr);
+  float full[32];
+  fold::combine_rotation_groups(dx, s, full);
+  if (ok) {
+    const size_t o = rowoff + 32 * s;
+    const float4* lf = reinterpret_cast<const float4*>(local + o);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float4 a = lf[j];
+      full[4 * j] += a.x;
+      full[4 * j + 1] += a.y;
+      full[4 * j + 2] += a.z;
+      full[4 * j + 3] += a.w;
+    }
+    fold::store32(dx_out + o, full);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Local dq and coefficient partials, one block per (query head, chunk, unit),
+// 256 threads: thread (i = t / 4, quarter xq = t % 4) owns dims 16 xq .. + 15
+// of token i. With s_g = scale sum_{d in g} q_i[d] k_j[d] and
+// ds_ij = g_i . v_j + gz_i (j <= i):
+//   dq_i[d] = sum_j ds_ij scale (lam_g(d) + 2 sum_h Gam_g(d)h s_h) k_j[d]
+// (the fp32 kernels' symmetric-Gam convention), written to dql; the
+// coefficient partials [0] sum ds, [1 + g] sum ds s_g, [9 + 8 g + h] sum ds
+// s_g s_h (full symmetric 8 x 8), each a fixed-order sum over the block.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void k3_q_local(const T* __restrict__ q, const T* __restrict__ k,
+                                                  const T* __restrict__ v, const float* __restrict__ G,
+                                                  const float* __restrict__ Gz, const int32_t* __restrict__ labels,
+                                                  const float* __restrict__ c0, const float* __restrict__ lam,
+                                                  const float* __restrict__ gam, int Gn, int Hq, int Hkv, int N,
+                                                  int NB, float scale, float* __restrict__ dql,
+                                                  float* __restrict__ coefl) {
+  __shared__ float qx[kC][kRow];
+  __shared__ float kx[kC][kRow];
+  __shared__ float vx[kC][kD + 1];
+  __shared__ float gs[kC][kD + 1];
+  __shared__ float dsm[kC][kC + 1];
+  __shared__ float cp[kC][46];
+  __shared__ HeadGroups<8> hg;
+  int hh, ch, u;
+  head_chunk_unit(Hq / Hkv, NB, (int)(gridDim.x / ((Hq / Hkv) * NB)), hh, ch, u);
+  const int R = Hq / Hkv, b = u / Hkv, kh = u % Hkv, h = kh * R + hh;
+  const int t = threadIdx.x, i = t >> 2, xq = t & 3;
+  const int tok0 = ch * kC;
+  const size_t qbase = (size_t)(b * Hq + h) * N * kD;
+  const size_t kbase = (size_t)u * N * kD;
+  {
+    float a[16];
+    load_chunk_rows(q, qbase, tok0, N, a);
+    store_chunk_rows(qx, a);
+    load_chunk_rows(k, kbase, tok0, N, a);
+    store_chunk_rows(kx, a);
+    load_chunk_rows(v, kbase, tok0, N, a);
+    store_chunk_rows(vx, a);
+    load_chunk_rows(G, qbase, tok0, N, a);
+    store_chunk_rows(gs, a);
+    if (xq == 0) {
+      const int tok = tok0 + i;
+      gs[i][kD] = tok < N ? Gz[(size_t)(b * Hq + h) * N + tok] : 0.f;
+    }
+  }
+  load_head_groups(hg, labels, c0, lam, gam, Gn, h);  // synchronizes the block
+  for (int mm = 0; mm < kC / 4; ++mm) {
+    const int j = xq + 4 * mm;
+    float ds = 0.f;
+    if (j <= i && tok0 + i < N) {
+      ds = gs[i][kD];
+      for (int e = 0; e < kD; ++e) ds += gs[i][e] * vx[j][e];
+    }
+    dsm[i][j] = ds;
+  }
+  __syncthreads();
+  float dq[16];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) dq[e] = 0.f;
+  // coefficient entries e of the 45 (c0, 8 lam, 36 gam g <= h) with e % 4 == xq
+  float cacc[12];
+#pragma unroll
+  for (int e = 0; e < 12; ++e) cacc[e] = 0.f;
+  int lab16[16];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) lab16[e] = hg.lab[16 * xq + e];
+  for (int j = 0; j <= i; ++j) {
+    const float ds = dsm[i][j];
+    float sg[8];
+    group_sums(hg, Gn, qx[i], kx[j], scale, sg);
+    float kg[8];
+#pragma unroll
+    for (int g = 0; g < 8; ++g) kg[g] = g < Gn ? kappa_grad(hg, Gn, g, sg) : 0.f;
+    const float dss = ds * scale;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      float kgd = 0.f;
+#pragma unroll
+      for (int g = 0; g < 8; ++g) kgd = lab16[e] == g ? kg[g] : kgd;
+      dq[e] += dss * kgd * kx[j][16 * xq + e];
+    }
+    // entry index e: 0 -> ds, 1 + g -> ds s_g, 9 + idx(g <= h) -> ds s_g s_h
+#pragma unroll
+    for (int c = 0; c < 12; ++c) {
+      const int e = xq + 4 * c;
+      if (e >= 45) break;
+      float val;
+      if (e == 0) {
+        val = ds;
+      } else if (e <= 8) {
+        val = ds * sg[e - 1];
+      } else {
+        int rem = e - 9, g = 0;
+        while (rem >= 8 - g) {
+          rem -= 8 - g;
+          ++g;
+        }
+        val = ds * sg[g] * sg[g + rem];
+      }
+      cacc[c] += val;
+    }
+  }
+  const int tok = tok0 + i;
+  if (tok < N) {
+    float* dst = dql + qbase + (size_t)tok * kD + 16 * xq;
+#pragma unroll
+    for (int e = 0; e < 16; e += 4) *reinterpret_cast<float4*>(dst + e) = make_float4(dq[e], dq[e + 1], dq[e + 2], dq[e + 3]);
+  }
+  if (coefl) {
+#pragma unroll
+    for (int c = 0; c < 12; ++c) {
+      const int e = xq + 4 * c;
+      if (e < 45) cp[i][e] = cacc[c];
+    }
+    __syncthreads();
+    float* out = coefl + ((size_t)(b * Hq + h) * NB + ch) * 73;
+    for (int e = t; e < 45; e += 256) {
+      float acc = 0.f;
+      for (int r = 0; r < kC; ++r) acc += cp[r][e];
+      if (e == 0) {
+        out[0] = acc;
+      } else if (e <= 8) {
+        out[e] = acc;
+      } else {
+        int rem = e - 9, g = 0;
+        while (rem >= 8 - g) {
+          rem -= 8 - g;
+          ++g;
+        }
+        const int hgi = g + rem;
+        out[9 + 8 * g + hgi] = acc;
+        out[9 + 8 * hgi + g] = acc;
+      }
+    }
+  }
+}
+
+// Per-head sums of the local coefficient partials over (batch, chunk), in a
+// fixed order: coefs[h][e].
+__global__ __launch_bounds__(128) void k3_coef_reduce(const float* __restrict__ coefl, int B, int Hq, int NB,
+                                                      float* __restrict__ coefs) {
+  const int h = blockIdx.x, e = threadIdx.x;
+  if (e >= 73) return;
+  float acc = 0.f;
+  for (int b = 0; b < B; ++b)
+    for (int ch = 0; ch < NB; ++ch) acc += coefl[((size_t)(b * Hq + h) * NB + ch) * 73 + e];
+  coefs[(size_t)h * 73 + e] = acc;
+}
+
+// ---------------------------------------------------------------------------
+// Host launchers
+// ---------------------------------------------------------------------------
+template <typename T>
+void launch_f32_state_fwd(const LaunchGeom& g, const T* k, const T* v, float* carry, float* carry_z, hipStream_t st,
+                          const Timer& timed) {
+  timed("k3_state_fwd", st, [&] {
+    hipLaunchKernelGGL(k3_state_fwd<T>, dim3(kFP / 64, g.U), dim3(256), 0, st, k, v, g.N, g.NB, carry, carry_z);
+  });
+}
+
+template <typename T>
+void launch_f32_readout_fwd(const LaunchGeom& g, const T* q, const float* wq, const float* carry, const float* carry_z,
+                            float floor, float* num, float* den, T* out, hipStream_t st, const Timer& timed) {
+  timed("k3_readout", st, [&] {
+    hipLaunchKernelGGL((k3_readout<T, 0>), dim3(g.R * g.NB * g.U), dim3(256), 0, st, q, wq, carry, carry_z, g.Hq,
+                       g.Hkv, g.N, g.NB, floor, num, den, out, nullptr, nullptr);
+  });
+}
+
+template <typename T>
+void launch_f32_backward(const LaunchGeom& g, const F32BwdArgs<T>& a, hipStream_t st, const Timer& timed) {
+  // the scan also forms the state coefficient partials (its per-item products)
+  if (a.dk || a.dv || a.dwq_part) {
+    timed("k3_state_bwd", st, [&] {
+      hipLaunchKernelGGL(k3_state_bwd<T>, dim3(kFP / 64, g.U), dim3(256), 0, st, a.q, a.G, a.Gz, a.wq, a.P, a.Pz,
+                         g.Hq, g.Hkv, g.N, g.NB, a.dT, a.dTz, a.dwq_part);
+    });
+  }
+  if (a.dq || a.coefl) {
+    timed("k3_q_local", st, [&] {
+      hipLaunchKernelGGL(k3_q_local<T>, dim3(g.R * g.NB * g.U), dim3(256), 0, st, a.q, a.k, a.v, a.G, a.Gz, a.labels,
+                         a.c0, a.lam, a.gam, a.groups, g.Hq, g.Hkv, g.N, g.NB, a.scale, a.dql, a.coefl);
+    });
+  }
+  if (a.dq) {
+    timed("k3_fold_q", st, [&] {
+      hipLaunchKernelGGL((k3_fold<T, 0>), dim3(g.R * g.NB * g.U), dim3(128), 0, st, a.q, a.G, nullptr, a.Gz, a.wq,
+                         a.P, a.Pz, a.dql, g.Hq, g.Hkv, g.N, g.NB, a.dq);
+    });
+  }
+  if (a.dk) {
+    timed("k3_fold_k", st, [&] {
+      hipLaunchKernelGGL((k3_fold<T, 1>), dim3(g.NB * g.U), dim3(128), 0, st, a.k, nullptr, a.v, nullptr, nullptr,
+                         a.dT, a.dTz, a.dkl, g.Hq, g.Hkv, g.N, g.NB, a.dk);
+    });
+  }
+  if (a.dv) {
+    timed("k3_readout_v", st, [&] {
+      hipLaunchKernelGGL((k3_readout<T, 1>), dim3(g.NB * g.U), dim3(256), 0, st, a.k, nullptr, a.dT, a.dTz, g.Hq,
+                         g.Hkv, g.N, g.NB, 0.f, nullptr, nullptr, nullptr, a.dvl, a.dv);
+    });
+  }
+  if (a.coefl) {
+    timed("k3_coef_reduce", st, [&] {
+      hipLaunchKernelGGL(k3_coef_reduce, dim3(g.Hq), dim3(128), 0, st, a.coefl, g.B, g.Hq, g.NB, a.coefs);
+    });
+  }
+}
+
+#define OAL_F32MMA_INST(T)                                                                                        \
+  template void launch_f32_state_fwd<T>(const LaunchGeom&, const T*, const T*, float*, float*, hipStream_t,        \
+                                        const Timer&);                                                            \
+  template void launch_f32_readout_fwd<T>(const LaunchGeom&, const T*, const float*, const float*, const float*, \
+                                          float, float*, float*, T*, hipStream_t, const Timer&);                  \
+  template void launch_f32_backward<T>(const LaunchGeom&, const F32BwdArgs<T>&, hipStream_t, const Timer&);
+OAL_F32MMA_INST(float)
+OAL_F32MMA_INST(uint16_t)
+#undef OAL_F32MMA_INST
+
+}  // namespace oal

@@ -139,6 +139,32 @@ ScanPlan scan_plan(int U, int NB, size_t scratch_bytes, bool fwd);
 ScanPlan bwd_scan_plan(int U, int NB, int R);
 
 // Operands and outputs of one chunk-state scan (oal_mfma_scan.hip).
+// Matrix-core fp32 route (oal_f32_mma.hip, up to 8 groups): natural-order
+// fp32 states as the scalar fp32 kernels keep them.
+template <typename T>
+void launch_f32_state_fwd(const LaunchGeom& g, const T* k, const T* v, float* carry, float* carry_z, hipStream_t st,
+                          const Timer& timed);
+template <typename T>
+void launch_f32_readout_fwd(const LaunchGeom& g, const T* q, const float* wq, const float* carry, const float* carry_z,
+                            float floor, float* num, float* den, T* out, hipStream_t st, const Timer& timed);
+template <typename T>
+struct F32BwdArgs {
+  const T *q, *k, *v;
+  const float *G, *Gz, *wq, *P, *Pz;
+  const int32_t* labels;
+  const float *c0, *lam, *gam;
+  int groups;
+  float scale;
+  float *dT, *dTz;    // [U][NB][kFP][64], [U][NB][kFP]
+  float* dwq_part;    // state coefficient partials [B][Hq][NB][kFP] (nullptr: not requested)
+  float *dql, *dkl, *dvl;  // local parts (dkl, dvl written by the scalar local kernel)
+  float* coefl;       // local coefficient partials [B][Hq][NB][73] (nullptr: not requested)
+  float* coefs;       // their per-head sums [Hq][73]
+  T *dq, *dk, *dv;
+};
+template <typename T>
+void launch_f32_backward(const LaunchGeom& g, const F32BwdArgs<T>& a, hipStream_t st, const Timer& timed);
+
 struct ScanArgs {
   const uint16_t* F;  // feature side, [X][frows][NB * 64] bf16 (rows 0..63 used)
   int frows;

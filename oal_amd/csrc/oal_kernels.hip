@@ -151,7 +151,9 @@ __global__ __launch_bounds__(256) void k_state_fwd(const T* __restrict__ k, cons
 // (reference _contract_query_wave :411-614 and _write_and_normalize_query_wave
 // :351-385). Thread t owns token i = t/4 and value columns 16*(t%4) .. +15.
 // ---------------------------------------------------------------------------
-template <typename T, int GMAX>
+// STATE = false (the matrix-core fp32 route): the intra-chunk part only, num and
+// den written unnormalized; k3_readout adds the state part and writes out.
+template <typename T, int GMAX, bool STATE = true>
 __global__ __launch_bounds__(256) void k_out_fwd(const T* __restrict__ q, const T* __restrict__ k,
                                                  const T* __restrict__ v, const float* __restrict__ wq,
                                                  const float* __restrict__ carry,
@@ -199,17 +201,21 @@ __global__ __launch_bounds__(256) void k_out_fwd(const T* __restrict__ q, const 
   float accz = 0.f;
   const size_t crow0 = ((size_t)u * NB + ch) * kFP;
   const float* wqh = wq + (size_t)h * kFP;
-  for (int f0 = 0; f0 < kFP; f0 += kTile) {
-    __syncthreads();
-    stage_state_tile(pt, carry, carry_z, crow0 + f0);
-    __syncthreads();
-    for (int fl = 0; fl < kTile; ++fl) {
-      const int f = f0 + fl;
-      const float phi = wqh[f] * qx[i][kTab.r[f]] * qx[i][kTab.c[f]];
+  if constexpr (STATE) {
+    for (int f0 = 0; f0 < kFP; f0 += kTile) {
+      __syncthreads();
+      stage_state_tile(pt, carry, carry_z, crow0 + f0);
+      __syncthreads();
+      for (int fl = 0; fl < kTile; ++fl) {
+        const int f = f0 + fl;
+        const float phi = wqh[f] * qx[i][kTab.r[f]] * qx[i][kTab.c[f]];
 #pragma unroll
-      for (int e = 0; e < 16; ++e) acc[e] += phi * pt[fl][cq * 16 + e];
-      accz += phi * pt[fl][kD];
+        for (int e = 0; e < 16; ++e) acc[e] += phi * pt[fl][cq * 16 + e];
+        accz += phi * pt[fl][kD];
+      }
     }
+  } else {
+    __syncthreads();
   }
   for (int j = 0; j <= i; ++j) {
     const float kv = kap[i][j];
@@ -225,7 +231,7 @@ __global__ __launch_bounds__(256) void k_out_fwd(const T* __restrict__ q, const 
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
       num[o + e] = acc[e];
-      out[o + e] = from_f<T>(acc[e] * inv);
+      if constexpr (STATE) out[o + e] = from_f<T>(acc[e] * inv);
     }
     if (cq == 0) den[(size_t)(b * Hq + h) * N + tok] = accz;
   }
@@ -427,14 +433,18 @@ __global__ __launch_bounds__(256) void k_q_bwd(const T* __restrict__ q, const T*
 // (reference _kv_side_vjp :1031-1452 and _add_kv_cross_term_ :911-1028; the
 // local term here uses the group-sum derivative instead of feature GEMMs).
 // ---------------------------------------------------------------------------
-template <typename T, int GMAX>
+// STATE = false (the matrix-core fp32 route): the local parts only, written
+// in fp32 to dkl_out / dvl_out for k3_fold / k3_readout to add.
+template <typename T, int GMAX, bool STATE = true>
 __global__ __launch_bounds__(256) void k_kv_bwd(const T* __restrict__ q, const T* __restrict__ k,
                                                 const T* __restrict__ v, const float* __restrict__ dT,
                                                 const float* __restrict__ dTz, const float* __restrict__ Gv,
                                                 const float* __restrict__ Gz, const int32_t* __restrict__ labels,
                                                 const float* __restrict__ c0, const float* __restrict__ lam,
                                                 const float* __restrict__ gam, int G, int Hq, int Hkv, int N,
-                                                int NB, float scale, T* __restrict__ dk, T* __restrict__ dv) {
+                                                int NB, float scale, T* __restrict__ dk, T* __restrict__ dv,
+                                                float* __restrict__ dkl_out = nullptr,
+                                                float* __restrict__ dvl_out = nullptr) {
   __shared__ float kx[kC][kRow];
   __shared__ float vx[kC][kD];
   __shared__ float qx[kC][kRow];
@@ -462,7 +472,7 @@ __global__ __launch_bounds__(256) void k_kv_bwd(const T* __restrict__ q, const T
     dkl[e] = 0.f;
   }
   const size_t crow0 = ((size_t)u * NB + ch) * kFP;
-  for (int f0 = 0; f0 < kFP; f0 += kTile) {
+  for (int f0 = 0; f0 < (STATE ? kFP : 0); f0 += kTile) {
     __syncthreads();
     stage_state_tile(pt, dT, dTz, crow0 + f0);
     __syncthreads();
@@ -536,8 +546,13 @@ __global__ __launch_bounds__(256) void k_kv_bwd(const T* __restrict__ q, const T
     const size_t o = kbase + (size_t)tok * kD + xq * 16;
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
-      if (dk) dk[o + e] = from_f<T>(dka[j][xq * 16 + e] + dkl[e]);
-      if (dv) dv[o + e] = from_f<T>(accv[e]);
+      if constexpr (STATE) {
+        if (dk) dk[o + e] = from_f<T>(dka[j][xq * 16 + e] + dkl[e]);
+        if (dv) dv[o + e] = from_f<T>(accv[e]);
+      } else {
+        dkl_out[o + e] = dkl[e];
+        dvl_out[o + e] = accv[e];
+      }
     }
   }
 }
@@ -559,10 +574,12 @@ __global__ __launch_bounds__(256) void k_dwq_reduce(const float* __restrict__ pa
 // reference gather does (grouped_reference.py:89-93); dgam is then reported in
 // the symmetric-Gam convention (off-diagonal entries carry the mean of the two
 // routings), the gradient of sum_{g,h} Gam_gh s_g s_h.
+// loc (the matrix-core fp32 route, G <= 8): per-head local parts [Hq][73]
+// (c0, lam[8], Gam[8][8] full symmetric, already in these coordinates).
 __global__ __launch_bounds__(256) void k_coef_grad(const float* __restrict__ dwq,
                                                    const int32_t* __restrict__ labels, int G, float scale,
                                                    float* __restrict__ dc0, float* __restrict__ dlam,
-                                                   float* __restrict__ dgam) {
+                                                   float* __restrict__ dgam, const float* __restrict__ loc = nullptr) {
   __shared__ int lab[kD];
   __shared__ float raw[64 * 64];
   const int h = blockIdx.x, t = threadIdx.x;
@@ -572,12 +589,13 @@ __global__ __launch_bounds__(256) void k_coef_grad(const float* __restrict__ dwq
   }
   __syncthreads();
   const float* w = dwq + (size_t)h * kFP;
-  if (t == 0) dc0[h] = w[0];
+  const float* lc = loc ? loc + (size_t)h * 73 : nullptr;
+  if (t == 0) dc0[h] = w[0] + (lc ? lc[0] : 0.f);
   for (int g = t; g < G; g += blockDim.x) {
     float acc = 0.f;
     for (int d = 0; d < kD; ++d)
       if (lab[d] == g) acc += w[1 + d];
-    dlam[(size_t)h * G + g] = acc * scale;
+    dlam[(size_t)h * G + g] = acc * scale + (lc ? lc[1 + g] : 0.f);
   }
   const float s2 = scale * scale;
   for (int e = t; e < G * G; e += blockDim.x) {
@@ -595,7 +613,8 @@ __global__ __launch_bounds__(256) void k_coef_grad(const float* __restrict__ dwq
   __syncthreads();
   for (int e = t; e < G * G; e += blockDim.x) {
     const int gr = e / G, gc = e % G;
-    dgam[(size_t)h * G * G + e] = gr == gc ? raw[e] : 0.5f * (raw[e] + raw[gc * G + gr]);
+    dgam[(size_t)h * G * G + e] =
+        (gr == gc ? raw[e] : 0.5f * (raw[e] + raw[gc * G + gr])) + (lc ? lc[9 + 8 * gr + gc] : 0.f);
   }
 }
 
@@ -661,10 +680,20 @@ struct WorkView {
   float* dTz;
   float* dwq_part;
   float* dwq;
+  // matrix-core fp32 route (G <= 8): local parts and coefficient partials
+  float* dql;    // [B][Hq][N][64]
+  float* dkl;    // [U][N][64]
+  float* dvl;    // [U][N][64]
+  float* coefl;  // [B][Hq][NB][73]
+  float* coefs;  // [Hq][73]
   size_t bytes;
 };
 
-WorkView work_view(const Geometry& g, void* base) {
+// The fp32 route runs on the matrix cores for up to 8 groups; more (per-pair
+// coefficients) take the scalar feature-form kernels.
+bool f32_mma(int groups) { return groups <= 8; }
+
+WorkView work_view(const Geometry& g, void* base, bool mma) {
   char* p = static_cast<char*>(base);
   WorkView w;
   const size_t rows = (size_t)g.B * g.Hq * g.N;
@@ -680,6 +709,11 @@ WorkView work_view(const Geometry& g, void* base) {
   w.dTz = take(sizeof(float) * (size_t)g.U * g.NB * oal::kFP);
   w.dwq_part = take(sizeof(float) * (size_t)g.B * g.Hq * g.NB * oal::kFP);
   w.dwq = take(sizeof(float) * (size_t)g.Hq * oal::kFP);
+  w.dql = mma ? take(sizeof(float) * rows * oal::kD) : nullptr;
+  w.dkl = mma ? take(sizeof(float) * (size_t)g.U * g.N * oal::kD) : nullptr;
+  w.dvl = mma ? take(sizeof(float) * (size_t)g.U * g.N * oal::kD) : nullptr;
+  w.coefl = mma ? take(sizeof(float) * (size_t)g.B * g.Hq * g.NB * 73) : nullptr;
+  w.coefs = mma ? take(sizeof(float) * (size_t)g.Hq * 73) : nullptr;
   w.bytes = off;
   return w;
 }
@@ -750,6 +784,17 @@ int forward_impl(const Geometry& g, const void* q, const void* k, const void* v,
   const T* vt = static_cast<const T*>(v);
   timed("k_feature_coefficients", st, [&] { hipLaunchKernelGGL(k_feature_coefficients, dim3(g.Hq), dim3(256), 0, st, labels, c0, lam, gam, groups, scale,
                      sv.wq); });
+  if constexpr (GMAX <= 8) {
+    // matrix-core route: state scan, intra-chunk part, then the state readout
+    const oal::LaunchGeom lg = launch_geom(g);
+    oal::launch_f32_state_fwd<T>(lg, kt, vt, sv.carry, sv.carry_z, st, make_timer());
+    timed("k_out_local", st, [&] { hipLaunchKernelGGL((k_out_fwd<T, GMAX, false>), dim3(g.R, g.NB, g.U), dim3(256), 0, st, qt, kt, vt, sv.wq,
+                       sv.carry, sv.carry_z, labels, c0, lam, gam, groups, g.Hq, g.Hkv, g.N, g.NB, scale, floor,
+                       static_cast<T*>(out), num, den); });
+    oal::launch_f32_readout_fwd<T>(lg, qt, sv.wq, sv.carry, sv.carry_z, floor, num, den, static_cast<T*>(out), st,
+                                   make_timer());
+    return launch_status("oal_forward launch");
+  }
   timed("k_state_fwd", st, [&] { hipLaunchKernelGGL(k_state_fwd<T>, dim3(kFP / 16, g.U), dim3(256), 0, st, kt, vt, g.N, g.NB, sv.carry,
                      sv.carry_z); });
   timed("k_out_fwd", st, [&] { hipLaunchKernelGGL((k_out_fwd<T, GMAX>), dim3(g.R, g.NB, g.U), dim3(256), 0, st, qt, kt, vt, sv.wq, sv.carry,
@@ -766,7 +811,7 @@ int backward_impl(const Geometry& g, const void* q, const void* k, const void* v
                   void* workspace, hipStream_t st) {
   using namespace oal;
   SavedView sv = saved_view(g, const_cast<void*>(saved));
-  WorkView w = work_view(g, workspace);
+  WorkView w = work_view(g, workspace, GMAX <= 8);
   const T* qt = static_cast<const T*>(q);
   const T* kt = static_cast<const T*>(k);
   const T* vt = static_cast<const T*>(v);
@@ -774,6 +819,27 @@ int backward_impl(const Geometry& g, const void* q, const void* k, const void* v
   timed("k_gvec", st, [&] { hipLaunchKernelGGL(k_gvec<T>, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st, static_cast<const T*>(dout),
                      dnum, dden, num, den, rows, floor, w.G, w.Gz); });
   const bool need_coef = dc0 || dlam || dgam;
+  if constexpr (GMAX <= 8) {
+    // matrix-core route
+    const oal::LaunchGeom lg = launch_geom(g);
+    if (dk || dv) {
+      timed("k_kv_local", st, [&] { hipLaunchKernelGGL((k_kv_bwd<T, GMAX, false>), dim3(g.NB, g.U), dim3(256), 0, st, qt, kt, vt, w.dT, w.dTz,
+                         w.G, w.Gz, labels, c0, lam, gam, groups, g.Hq, g.Hkv, g.N, g.NB, scale, nullptr, nullptr,
+                         w.dkl, w.dvl); });
+    }
+    oal::F32BwdArgs<T> a{qt, kt, vt, w.G, w.Gz, sv.wq, sv.carry, sv.carry_z, labels, c0, lam, gam, groups, scale,
+                         w.dT, w.dTz, need_coef ? w.dwq_part : nullptr, w.dql, w.dkl, w.dvl,
+                         need_coef ? w.coefl : nullptr, w.coefs, static_cast<T*>(dq), static_cast<T*>(dk),
+                         static_cast<T*>(dv)};
+    oal::launch_f32_backward<T>(lg, a, st, make_timer());
+    if (need_coef) {
+      timed("k_dwq_reduce", st, [&] { hipLaunchKernelGGL(k_dwq_reduce, dim3((kFP + 255) / 256, g.Hq), dim3(256), 0, st, w.dwq_part, g.B, g.Hq,
+                         g.NB, w.dwq); });
+      timed("k_coef_grad", st, [&] { hipLaunchKernelGGL(k_coef_grad, dim3(g.Hq), dim3(256), 0, st, w.dwq, labels, groups, scale, dc0, dlam,
+                         dgam, w.coefs); });
+    }
+    return launch_status("oal_backward launch");
+  }
   if (dk || dv) {
     timed("k_state_bwd", st, [&] { hipLaunchKernelGGL(k_state_bwd<T>, dim3(kFP / 16, g.U), dim3(256), 0, st, qt, sv.wq, w.G, w.Gz, g.Hq, g.Hkv,
                        g.N, g.NB, w.dT, w.dTz); });
@@ -912,7 +978,7 @@ size_t oal_backward_workspace_bytes(int batch, int q_heads, int kv_heads, int se
   if (check_geometry(batch, q_heads, kv_heads, seq_len, dtype, &g) || check_common(groups, precision)) return 0;
   if (use_mfma(precision, groups, g))
     return oal::mfma_work_view(nullptr, g.B, g.Hq, g.U, g.N, g.NB, groups > 8).bytes;
-  return work_view(g, nullptr).bytes;
+  return work_view(g, nullptr, f32_mma(groups)).bytes;
 }
 
 int oal_forward(const void* q, const void* k, const void* v, const int32_t* labels, const float* c0,

@@ -615,6 +615,14 @@ __global__ __launch_bounds__(64) void k2_selftest(int* __restrict__ errors) {
       bad += (c[i] != ref);
     }
   }
+  {  // 32x32x2 f32 with K = 2 (the fp32 matrix-core route)
+    const float a = A[l % 32][l / 32], bb = B[l / 32][l % 32];
+    f32x16 c = __builtin_amdgcn_mfma_f32_32x32x2f32(a, bb, f32x16{}, 0, 0, 0);
+    for (int i = 0; i < 16; ++i) {
+      const int r = c32_row(i, l), col = l % 32;
+      bad += (c[i] != A[r][0] * B[0][col] + A[r][1] * B[1][col]);
+    }
+  }
   {  // 16x16x32 with K = 32
     float fa[8], fb[8];
     for (int j = 0; j < 8; ++j) {
