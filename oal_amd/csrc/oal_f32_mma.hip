@@ -11,7 +11,8 @@
 //   k3_readout     num += phi(x) . S (out: num / den), or dv = raw(K) dT + local
 //   k3_fold        dq = fold of (P [G, Gz]^T) through wq o raw(q) + local,
 //                  dk = fold of (dT [V, 1]^T) through raw(k) + local
-//   k3_q_local     local dq and the local coefficient partials (group sums)
+//   k3_local       local dq, dk, dv and coefficient partials (group sums on the
+//                  matrix cores)
 //   k3_coef_reduce per-head sums of those partials
 //
 // Matrix layout of v_mfma_f32_32x32x2f32: lane l supplies A[l % 32][l / 32]
@@ -421,16 +422,23 @@ __global__ __launch_bounds__(256, 2) void k3_readout(const T* __restrict__ x_in,
     }
   } else {
     if (ok) {
-      const float* lrow = dvl + xbase + (size_t)tok * kD + 32 * m + 4 * s;
+      // local part: the unit's query heads in order
+      for (int r2 = 0; r2 < R; ++r2) {
+        const float* lrow = dvl + ((size_t)(b * Hq + kh * R + r2) * N + tok) * kD + 32 * m + 4 * s;
+#pragma unroll
+        for (int a = 0; a < 4; ++a) {
+          const float4 loc = *reinterpret_cast<const float4*>(lrow + 8 * a);
+          acc[4 * a] += loc.x;
+          acc[4 * a + 1] += loc.y;
+          acc[4 * a + 2] += loc.z;
+          acc[4 * a + 3] += loc.w;
+        }
+      }
       T* drow = dv + xbase + (size_t)tok * kD + 32 * m + 4 * s;
 #pragma unroll
-      for (int a = 0; a < 4; ++a) {
-        const float4 loc = *reinterpret_cast<const float4*>(lrow + 8 * a);
-        drow[8 * a] = from_f<T>(acc[4 * a] + loc.x);
-        drow[8 * a + 1] = from_f<T>(acc[4 * a + 1] + loc.y);
-        drow[8 * a + 2] = from_f<T>(acc[4 * a + 2] + loc.z);
-        drow[8 * a + 3] = from_f<T>(acc[4 * a + 3] + loc.w);
-      }
+      for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) drow[8 * a + e] = from_f<T>(acc[4 * a + e]);
     }
   }
 }
@@ -542,154 +550,344 @@ __global__ __launch_bounds__(128, 2) void k3_fold(const T* __restrict__ x_in, co
   float full[32];
   fold::combine_rotation_groups(dx, s, full);
   if (ok) {
-    const size_t o = rowoff + 32 * s;
-    const float4* lf = reinterpret_cast<const float4*>(local + o);
+    // local part: dq's own head (MODE 0), or the unit's heads in order (MODE 1)
+    for (int r2 = 0; r2 < (MODE == 0 ? 1 : R); ++r2) {
+      const size_t lo = MODE == 0 ? rowoff + 32 * s : ((size_t)(b * Hq + kh * R + r2) * N + tok) * kD + 32 * s;
+      const float4* lf = reinterpret_cast<const float4*>(local + lo);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float4 a = lf[j];
-      full[4 * j] += a.x;
-      full[4 * j + 1] += a.y;
-      full[4 * j + 2] += a.z;
-      full[4 * j + 3] += a.w;
+      for (int j = 0; j < 8; ++j) {
+        const float4 a = lf[j];
+        full[4 * j] += a.x;
+        full[4 * j + 1] += a.y;
+        full[4 * j + 2] += a.z;
+        full[4 * j + 3] += a.w;
+      }
     }
-    fold::store32(dx_out + o, full);
+    fold::store32(dx_out + rowoff + 32 * s, full);
   }
 }
 
 // ---------------------------------------------------------------------------
-// Local dq and coefficient partials, one block per (query head, chunk, unit),
-// 256 threads: thread (i = t / 4, quarter xq = t % 4) owns dims 16 xq .. + 15
-// of token i. With s_g = scale sum_{d in g} q_i[d] k_j[d] and
-// ds_ij = g_i . v_j + gz_i (j <= i):
-//   dq_i[d] = sum_j ds_ij scale (lam_g(d) + 2 sum_h Gam_g(d)h s_h) k_j[d]
-// (the fp32 kernels' symmetric-Gam convention), written to dql; the
-// coefficient partials [0] sum ds, [1 + g] sum ds s_g, [9 + 8 g + h] sum ds
-// s_g s_h (full symmetric 8 x 8), each a fixed-order sum over the block.
+// Intra-chunk (local) VJP on the matrix cores, one block of three waves per
+// (query head, chunk, unit); wave w owns the lower 32 x 32 tile (it, jt) =
+// (0,0), (1,0), (1,1) of the (query i, key j) plane. With s_g(i,j) =
+// scale sum_{d in g} q_i[d] k_j[d], ds_ij = g_i . v_j + gz_i (j <= i) and
+// t_g = sum_h Gam_gh s_h (the fp32 kernels' symmetric-Gam convention):
+//   kappa_ij = c0 + sum_g s_g (lam_g + t_g),  X_g = ds scale (lam_g + 2 t_g)
+//   dq_i[d] = sum_j X_g(d)[i][j] k_j[d],  dk_j[d] = sum_i X_g(d)[i][j] q_i[d],
+//   dv_j[e] = sum_i kappa_ij g_i[e]   (dk, dv per query head: dkl, dvl)
+// and the coefficient partials [0] sum ds, [1 + g] sum ds s_g,
+// [9 + 8 g + h] sum ds s_g s_h (full symmetric 8 x 8).
+// The group sums run over the group-sorted dimensions (k-step k holds sorted
+// positions 2k and 2k + 1 in lane groups 0 and 1; a step that straddles two
+// groups runs once for each, masked), the tile in both orientations: C[i][j]
+// (lane column j) for dk, dv and the partials, C[j][i] (lane column i) for
+// dq; the X_g and kappa accumulators then serve as the K-major operand of the
+// output products (K index = accumulator row, step k taking register k).
 // ---------------------------------------------------------------------------
+constexpr int kLRow = kD + 4;
+
+struct LocalCtx {
+  const float (*qx)[kLRow];
+  const float (*kx)[kLRow];
+  const float (*vx)[kLRow];
+  const float (*gs)[kLRow];
+  const float* gz;
+  const int* perm;
+  const int* gstart;
+  int G;
+};
+
+// acc[g] = sum over the group-sorted dims d of g: A[a_row][d] B[b_row][d]
+// (A = the lane row's operand, B = the lane column's), scaled by scale.
+__device__ __forceinline__ void group_sums_mfma(const float (*A)[kLRow], const float (*B)[kLRow], int a_row,
+                                                int b_row, const int* perm, const int* gstart, int G, int s,
+                                                float scale, f32x16 (&acc)[8]) {
+#pragma unroll
+  for (int g = 0; g < 8; ++g) {
+    acc[g] = f32x16{};
+    if (g < G) {
+      const int p0 = gstart[g], p1 = gstart[g + 1];
+      for (int kk = p0 >> 1; kk < (p1 + 1) >> 1; ++kk) {
+        const int p = 2 * kk + s, d = perm[p];
+        const float a = (p >= p0 && p < p1) ? A[a_row][d] : 0.f;
+        acc[g] = mfma_f32(a, B[b_row][d], acc[g]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[g][i] *= scale;
+  }
+}
+
+// ds over K = values: C[row][col] = sum_e Gr[row][e] Vc[col][e], value 32 s + k at step k.
+__device__ __forceinline__ f32x16 dot_rows_mfma(const float (*Ar)[kLRow], const float (*Bc)[kLRow], int a_row,
+                                                int b_row, int s) {
+  f32x16 acc = f32x16{};
+#pragma unroll
+  for (int k4 = 0; k4 < 8; ++k4) {
+    const float4 a = *reinterpret_cast<const float4*>(&Ar[a_row][32 * s + 4 * k4]);
+    const float4 b = *reinterpret_cast<const float4*>(&Bc[b_row][32 * s + 4 * k4]);
+    acc = mfma_f32(a.x, b.x, acc);
+    acc = mfma_f32(a.y, b.y, acc);
+    acc = mfma_f32(a.z, b.z, acc);
+    acc = mfma_f32(a.w, b.w, acc);
+  }
+  return acc;
+}
+
 template <typename T>
-__global__ __launch_bounds__(256) void k3_q_local(const T* __restrict__ q, const T* __restrict__ k,
-                                                  const T* __restrict__ v, const float* __restrict__ G,
-                                                  const float* __restrict__ Gz, const int32_t* __restrict__ labels,
-                                                  const float* __restrict__ c0, const float* __restrict__ lam,
-                                                  const float* __restrict__ gam, int Gn, int Hq, int Hkv, int N,
-                                                  int NB, float scale, float* __restrict__ dql,
-                                                  float* __restrict__ coefl) {
-  __shared__ float qx[kC][kRow];
-  __shared__ float kx[kC][kRow];
-  __shared__ float vx[kC][kD + 1];
-  __shared__ float gs[kC][kD + 1];
-  __shared__ float dsm[kC][kC + 1];
-  __shared__ float cp[kC][46];
+__global__ __launch_bounds__(192) void k3_local(const T* __restrict__ q, const T* __restrict__ k,
+                                                const T* __restrict__ v, const float* __restrict__ G,
+                                                const float* __restrict__ Gz, const int32_t* __restrict__ labels,
+                                                const float* __restrict__ c0, const float* __restrict__ lam,
+                                                const float* __restrict__ gam, int Gn, int Hq, int Hkv, int N,
+                                                int NB, float scale, float* __restrict__ dql,
+                                                float* __restrict__ dkl, float* __restrict__ dvl,
+                                                float* __restrict__ coefl) {
+  __shared__ __attribute__((aligned(16))) float qx[kC][kLRow];
+  __shared__ __attribute__((aligned(16))) float kx[kC][kLRow];
+  __shared__ __attribute__((aligned(16))) float vx[kC][kLRow];
+  __shared__ __attribute__((aligned(16))) float gs[kC][kLRow];
+  __shared__ __attribute__((aligned(16))) float xb[2][kD][33];  // tile (1,0)'s partial outputs
+  __shared__ float gz[kC];
+  __shared__ float cred[3][45];
   __shared__ HeadGroups<8> hg;
   int hh, ch, u;
   head_chunk_unit(Hq / Hkv, NB, (int)(gridDim.x / ((Hq / Hkv) * NB)), hh, ch, u);
   const int R = Hq / Hkv, b = u / Hkv, kh = u % Hkv, h = kh * R + hh;
-  const int t = threadIdx.x, i = t >> 2, xq = t & 3;
+  const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, s = l >> 5, row = l & 31;
+  const int it = wv == 0 ? 0 : 1, jt = wv == 2 ? 1 : 0;
   const int tok0 = ch * kC;
   const size_t qbase = (size_t)(b * Hq + h) * N * kD;
   const size_t kbase = (size_t)u * N * kD;
-  {
-    float a[16];
-    load_chunk_rows(q, qbase, tok0, N, a);
-    store_chunk_rows(qx, a);
-    load_chunk_rows(k, kbase, tok0, N, a);
-    store_chunk_rows(kx, a);
-    load_chunk_rows(v, kbase, tok0, N, a);
-    store_chunk_rows(vx, a);
-    load_chunk_rows(G, qbase, tok0, N, a);
-    store_chunk_rows(gs, a);
-    if (xq == 0) {
-      const int tok = tok0 + i;
-      gs[i][kD] = tok < N ? Gz[(size_t)(b * Hq + h) * N + tok] : 0.f;
-    }
+  // staging: 192 threads, 64 rows x 64 dims per operand, 16 consecutive dims each
+  for (int idx = tid; idx < 4 * kC * 4; idx += 192) {
+    const int op = idx >> 8, rr = (idx >> 2) & 63, q4 = idx & 3, tok = tok0 + rr;
+    const bool ok = tok < N;
+    float vals[16];
+    const size_t off = (op == 0 || op == 3 ? qbase : kbase) + (size_t)(ok ? tok : N - 1) * kD + 16 * q4;
+    if (op == 0) load16(q, off, ok, vals);
+    else if (op == 1) load16(k, off, ok, vals);
+    else if (op == 2) load16(v, off, ok, vals);
+    else load16(G, off, ok, vals);
+    float* dst = op == 0 ? &qx[rr][16 * q4] : op == 1 ? &kx[rr][16 * q4] : op == 2 ? &vx[rr][16 * q4] : &gs[rr][16 * q4];
+#pragma unroll
+    for (int e = 0; e < 16; e += 4)
+      *reinterpret_cast<float4*>(dst + e) = make_float4(vals[e], vals[e + 1], vals[e + 2], vals[e + 3]);
   }
+  if (tid < kC) gz[tid] = tok0 + tid < N ? Gz[(size_t)(b * Hq + h) * N + tok0 + tid] : 0.f;
   load_head_groups(hg, labels, c0, lam, gam, Gn, h);  // synchronizes the block
-  for (int mm = 0; mm < kC / 4; ++mm) {
-    const int j = xq + 4 * mm;
-    float ds = 0.f;
-    if (j <= i && tok0 + i < N) {
-      ds = gs[i][kD];
-      for (int e = 0; e < kD; ++e) ds += gs[i][e] * vx[j][e];
-    }
-    dsm[i][j] = ds;
+  // the head's coefficients, wave-uniform
+  float lm[8], gm[8][8];
+#pragma unroll
+  for (int g = 0; g < 8; ++g) {
+    lm[g] = g < Gn ? hg.lam[g] : 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) gm[g][e] = (g < Gn && e < Gn) ? hg.gam[g * Gn + e] : 0.f;
   }
-  __syncthreads();
-  float dq[16];
+  const float cz = hg.c0;
+  // elementwise step on one entry: s (8 group sums) -> X_g (in place) and kappa
+  auto entry = [&](float (&sv)[8], float ds, bool valid, float& kap) {
+    float tg[8];
 #pragma unroll
-  for (int e = 0; e < 16; ++e) dq[e] = 0.f;
-  // coefficient entries e of the 45 (c0, 8 lam, 36 gam g <= h) with e % 4 == xq
-  float cacc[12];
+    for (int g = 0; g < 8; ++g) {
+      float t = 0.f;
 #pragma unroll
-  for (int e = 0; e < 12; ++e) cacc[e] = 0.f;
-  int lab16[16];
+      for (int e = 0; e < 8; ++e) t = fmaf(gm[g][e], sv[e], t);
+      tg[g] = t;
+    }
+    float kv = cz;
 #pragma unroll
-  for (int e = 0; e < 16; ++e) lab16[e] = hg.lab[16 * xq + e];
-  for (int j = 0; j <= i; ++j) {
-    const float ds = dsm[i][j];
-    float sg[8];
-    group_sums(hg, Gn, qx[i], kx[j], scale, sg);
-    float kg[8];
-#pragma unroll
-    for (int g = 0; g < 8; ++g) kg[g] = g < Gn ? kappa_grad(hg, Gn, g, sg) : 0.f;
+    for (int g = 0; g < 8; ++g) kv = fmaf(sv[g], lm[g] + tg[g], kv);
     const float dss = ds * scale;
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      float kgd = 0.f;
+    for (int g = 0; g < 8; ++g) sv[g] = valid ? dss * (lm[g] + 2.f * tg[g]) : 0.f;
+    kap = valid ? kv : 0.f;
+  };
+
+  f32x16 S[8];
+  // ---- orientation C[j][i] (lane column = query i): dq ----
+  {
+    const int jr = 32 * jt + row, ic = 32 * it + row;
+    group_sums_mfma(kx, qx, jr, ic, hg.perm, hg.gstart, Gn, s, scale, S);
+    f32x16 dsT = dot_rows_mfma(vx, gs, jr, ic, s);  // sum_e v_j[e] g_i[e]
+    const float gzi = gz[ic];
 #pragma unroll
-      for (int g = 0; g < 8; ++g) kgd = lab16[e] == g ? kg[g] : kgd;
-      dq[e] += dss * kgd * kx[j][16 * xq + e];
+    for (int r = 0; r < 16; ++r) {
+      const int jl = c32_row(r, l);
+      const bool valid = 32 * jt + jl <= ic;
+      float sv[8];
+#pragma unroll
+      for (int g = 0; g < 8; ++g) sv[g] = S[g][r];
+      float kap;
+      entry(sv, dsT[r] + gzi, valid, kap);
+#pragma unroll
+      for (int g = 0; g < 8; ++g) S[g][r] = sv[g];
     }
-    // entry index e: 0 -> ds, 1 + g -> ds s_g, 9 + idx(g <= h) -> ds s_g s_h
+    // dq^T[d][i] = sum_g sum_j (K o m_g)^T[d][j] X_g^T[j][i]; j = 32 jt + c32_row(k, 32 s) at step k
+    f32x16 dq[2] = {f32x16{}, f32x16{}};
 #pragma unroll
-    for (int c = 0; c < 12; ++c) {
-      const int e = xq + 4 * c;
-      if (e >= 45) break;
-      float val;
-      if (e == 0) {
-        val = ds;
-      } else if (e <= 8) {
-        val = ds * sg[e - 1];
-      } else {
-        int rem = e - 9, g = 0;
-        while (rem >= 8 - g) {
-          rem -= 8 - g;
-          ++g;
+    for (int dt = 0; dt < 2; ++dt) {
+      const int d = 32 * dt + row, gd = hg.lab[d];
+#pragma unroll
+      for (int g = 0; g < 8; ++g) {
+        if (g < Gn) {
+#pragma unroll
+          for (int kk = 0; kk < 16; ++kk) {
+            const int j = 32 * jt + c32_row(kk, 32 * s);
+            dq[dt] = mfma_f32(gd == g ? kx[j][d] : 0.f, S[g][kk], dq[dt]);
+          }
         }
-        val = ds * sg[g] * sg[g + rem];
       }
-      cacc[c] += val;
     }
-  }
-  const int tok = tok0 + i;
-  if (tok < N) {
-    float* dst = dql + qbase + (size_t)tok * kD + 16 * xq;
+    // i-tile 1 gets tiles (1,0) and (1,1): wave 1 hands its part to wave 2
+    if (wv == 1) {
 #pragma unroll
-    for (int e = 0; e < 16; e += 4) *reinterpret_cast<float4*>(dst + e) = make_float4(dq[e], dq[e + 1], dq[e + 2], dq[e + 3]);
-  }
-  if (coefl) {
+      for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
-    for (int c = 0; c < 12; ++c) {
-      const int e = xq + 4 * c;
-      if (e < 45) cp[i][e] = cacc[c];
+        for (int r = 0; r < 16; ++r) xb[0][32 * dt + c32_row(r, l)][row] = dq[dt][r];
     }
     __syncthreads();
-    float* out = coefl + ((size_t)(b * Hq + h) * NB + ch) * 73;
-    for (int e = t; e < 45; e += 256) {
-      float acc = 0.f;
-      for (int r = 0; r < kC; ++r) acc += cp[r][e];
-      if (e == 0) {
-        out[0] = acc;
-      } else if (e <= 8) {
-        out[e] = acc;
+    if (wv != 1) {
+      const int i = 32 * it + row, tok = tok0 + i;
+      if (wv == 2) {
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) dq[dt][r] = xb[0][32 * dt + c32_row(r, l)][row] + dq[dt][r];
+      }
+      if (tok < N) {
+        float* dst = dql + qbase + (size_t)tok * kD;
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+          for (int a = 0; a < 4; ++a)
+            *reinterpret_cast<float4*>(dst + 32 * dt + 8 * a + 4 * s) =
+                make_float4(dq[dt][4 * a], dq[dt][4 * a + 1], dq[dt][4 * a + 2], dq[dt][4 * a + 3]);
+      }
+    }
+    __syncthreads();
+  }
+  // ---- orientation C[i][j] (lane column = key j): dk, dv, coefficient partials ----
+  {
+    const int ir = 32 * it + row, jc = 32 * jt + row;
+    group_sums_mfma(qx, kx, ir, jc, hg.perm, hg.gstart, Gn, s, scale, S);
+    f32x16 ds = dot_rows_mfma(gs, vx, ir, jc, s);  // sum_e g_i[e] v_j[e]
+    f32x16 kap16;
+    float cacc[45];
+#pragma unroll
+    for (int e = 0; e < 45; ++e) cacc[e] = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int i = 32 * it + c32_row(r, l);
+      const bool valid = jc <= i;
+      const float dsv = valid ? ds[r] + gz[i] : 0.f;
+      float sv[8];
+#pragma unroll
+      for (int g = 0; g < 8; ++g) sv[g] = S[g][r];
+      if (coefl) {
+        cacc[0] += dsv;
+        int e = 9;
+#pragma unroll
+        for (int g = 0; g < 8; ++g) {
+          const float pg = dsv * sv[g];
+          cacc[1 + g] += pg;
+#pragma unroll
+          for (int h2 = g; h2 < 8; ++h2) cacc[e++] += pg * sv[h2];
+        }
+      }
+      float kap;
+      entry(sv, dsv, valid, kap);
+      kap16[r] = kap;
+#pragma unroll
+      for (int g = 0; g < 8; ++g) S[g][r] = sv[g];
+    }
+    // dk^T[d][j] = sum_g sum_i (Q o m_g)^T[d][i] X_g[i][j]; dv^T[e][j] = sum_i G^T[e][i] kappa[i][j]
+    f32x16 dk[2] = {f32x16{}, f32x16{}}, dv[2] = {f32x16{}, f32x16{}};
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt) {
+      const int d = 32 * dt + row, gd = hg.lab[d];
+#pragma unroll
+      for (int g = 0; g < 8; ++g) {
+        if (g < Gn) {
+#pragma unroll
+          for (int kk = 0; kk < 16; ++kk) {
+            const int i = 32 * it + c32_row(kk, 32 * s);
+            dk[dt] = mfma_f32(gd == g ? qx[i][d] : 0.f, S[g][kk], dk[dt]);
+          }
+        }
+      }
+#pragma unroll
+      for (int kk = 0; kk < 16; ++kk) {
+        const int i = 32 * it + c32_row(kk, 32 * s);
+        dv[dt] = mfma_f32(gs[i][d], kap16[kk], dv[dt]);
+      }
+    }
+    // coefficient partials: lane sums (fixed butterfly), then the waves in order
+    if (coefl) {
+#pragma unroll
+      for (int e = 0; e < 45; ++e) {
+        float x = cacc[e];
+        x += __shfl_xor(x, 1, 64);
+        x += __shfl_xor(x, 2, 64);
+        x += __shfl_xor(x, 4, 64);
+        x += __shfl_xor(x, 8, 64);
+        x += __shfl_xor(x, 16, 64);
+        x += __shfl_xor(x, 32, 64);
+        if (l == 0) cred[wv][e] = x;
+      }
+    }
+    // j-tile 0 gets tiles (0,0) and (1,0): wave 1 hands its part to wave 0
+    if (wv == 1) {
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          xb[0][32 * dt + c32_row(r, l)][row] = dk[dt][r];
+          xb[1][32 * dt + c32_row(r, l)][row] = dv[dt][r];
+        }
+    }
+    __syncthreads();
+    if (wv != 1) {
+      const int j = 32 * jt + row, tok = tok0 + j;
+      if (wv == 0) {
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            dk[dt][r] += xb[0][32 * dt + c32_row(r, l)][row];
+            dv[dt][r] += xb[1][32 * dt + c32_row(r, l)][row];
+          }
+      }
+      if (tok < N) {
+        float* dkd = dkl + qbase + (size_t)tok * kD;
+        float* dvd = dvl + qbase + (size_t)tok * kD;
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+          for (int a = 0; a < 4; ++a) {
+            *reinterpret_cast<float4*>(dkd + 32 * dt + 8 * a + 4 * s) =
+                make_float4(dk[dt][4 * a], dk[dt][4 * a + 1], dk[dt][4 * a + 2], dk[dt][4 * a + 3]);
+            *reinterpret_cast<float4*>(dvd + 32 * dt + 8 * a + 4 * s) =
+                make_float4(dv[dt][4 * a], dv[dt][4 * a + 1], dv[dt][4 * a + 2], dv[dt][4 * a + 3]);
+          }
+      }
+    }
+    if (coefl && tid < 45) {
+      const float x = (cred[0][tid] + cred[1][tid]) + cred[2][tid];
+      float* out = coefl + ((size_t)(b * Hq + h) * NB + ch) * 73;
+      if (tid == 0) {
+        out[0] = x;
+      } else if (tid <= 8) {
+        out[tid] = x;
       } else {
-        int rem = e - 9, g = 0;
+        int rem = tid - 9, g = 0;
         while (rem >= 8 - g) {
           rem -= 8 - g;
           ++g;
         }
-        const int hgi = g + rem;
-        out[9 + 8 * g + hgi] = acc;
-        out[9 + 8 * hgi + g] = acc;
+        out[9 + 8 * g + g + rem] = x;
+        out[9 + 8 * (g + rem) + g] = x;
       }
     }
   }
@@ -736,12 +934,10 @@ void launch_f32_backward(const LaunchGeom& g, const F32BwdArgs<T>& a, hipStream_
                          g.Hq, g.Hkv, g.N, g.NB, a.dT, a.dTz, a.dwq_part);
     });
   }
-  if (a.dq || a.coefl) {
-    timed("k3_q_local", st, [&] {
-      hipLaunchKernelGGL(k3_q_local<T>, dim3(g.R * g.NB * g.U), dim3(256), 0, st, a.q, a.k, a.v, a.G, a.Gz, a.labels,
-                         a.c0, a.lam, a.gam, a.groups, g.Hq, g.Hkv, g.N, g.NB, a.scale, a.dql, a.coefl);
-    });
-  }
+  timed("k3_local", st, [&] {
+    hipLaunchKernelGGL(k3_local<T>, dim3(g.R * g.NB * g.U), dim3(192), 0, st, a.q, a.k, a.v, a.G, a.Gz, a.labels,
+                       a.c0, a.lam, a.gam, a.groups, g.Hq, g.Hkv, g.N, g.NB, a.scale, a.dql, a.dkl, a.dvl, a.coefl);
+  });
   if (a.dq) {
     timed("k3_fold_q", st, [&] {
       hipLaunchKernelGGL((k3_fold<T, 0>), dim3(g.R * g.NB * g.U), dim3(128), 0, st, a.q, a.G, nullptr, a.Gz, a.wq,

@@ -157,7 +157,7 @@ struct F32BwdArgs {
   float scale;
   float *dT, *dTz;    // [U][NB][kFP][64], [U][NB][kFP]
   float* dwq_part;    // state coefficient partials [B][Hq][NB][kFP] (nullptr: not requested)
-  float *dql, *dkl, *dvl;  // local parts (dkl, dvl written by the scalar local kernel)
+  float *dql, *dkl, *dvl;  // local parts, [B][Hq][N][64] per query head
   float* coefl;       // local coefficient partials [B][Hq][NB][73] (nullptr: not requested)
   float* coefs;       // their per-head sums [Hq][73]
   T *dq, *dk, *dv;

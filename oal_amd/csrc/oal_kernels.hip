@@ -433,18 +433,14 @@ __global__ __launch_bounds__(256) void k_q_bwd(const T* __restrict__ q, const T*
 // (reference _kv_side_vjp :1031-1452 and _add_kv_cross_term_ :911-1028; the
 // local term here uses the group-sum derivative instead of feature GEMMs).
 // ---------------------------------------------------------------------------
-// STATE = false (the matrix-core fp32 route): the local parts only, written
-// in fp32 to dkl_out / dvl_out for k3_fold / k3_readout to add.
-template <typename T, int GMAX, bool STATE = true>
+template <typename T, int GMAX>
 __global__ __launch_bounds__(256) void k_kv_bwd(const T* __restrict__ q, const T* __restrict__ k,
                                                 const T* __restrict__ v, const float* __restrict__ dT,
                                                 const float* __restrict__ dTz, const float* __restrict__ Gv,
                                                 const float* __restrict__ Gz, const int32_t* __restrict__ labels,
                                                 const float* __restrict__ c0, const float* __restrict__ lam,
                                                 const float* __restrict__ gam, int G, int Hq, int Hkv, int N,
-                                                int NB, float scale, T* __restrict__ dk, T* __restrict__ dv,
-                                                float* __restrict__ dkl_out = nullptr,
-                                                float* __restrict__ dvl_out = nullptr) {
+                                                int NB, float scale, T* __restrict__ dk, T* __restrict__ dv) {
   __shared__ float kx[kC][kRow];
   __shared__ float vx[kC][kD];
   __shared__ float qx[kC][kRow];
@@ -472,7 +468,7 @@ __global__ __launch_bounds__(256) void k_kv_bwd(const T* __restrict__ q, const T
     dkl[e] = 0.f;
   }
   const size_t crow0 = ((size_t)u * NB + ch) * kFP;
-  for (int f0 = 0; f0 < (STATE ? kFP : 0); f0 += kTile) {
+  for (int f0 = 0; f0 < kFP; f0 += kTile) {
     __syncthreads();
     stage_state_tile(pt, dT, dTz, crow0 + f0);
     __syncthreads();
@@ -546,13 +542,8 @@ __global__ __launch_bounds__(256) void k_kv_bwd(const T* __restrict__ q, const T
     const size_t o = kbase + (size_t)tok * kD + xq * 16;
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
-      if constexpr (STATE) {
-        if (dk) dk[o + e] = from_f<T>(dka[j][xq * 16 + e] + dkl[e]);
-        if (dv) dv[o + e] = from_f<T>(accv[e]);
-      } else {
-        dkl_out[o + e] = dkl[e];
-        dvl_out[o + e] = accv[e];
-      }
+      if (dk) dk[o + e] = from_f<T>(dka[j][xq * 16 + e] + dkl[e]);
+      if (dv) dv[o + e] = from_f<T>(accv[e]);
     }
   }
 }
@@ -682,8 +673,8 @@ struct WorkView {
   float* dwq;
   // matrix-core fp32 route (G <= 8): local parts and coefficient partials
   float* dql;    // [B][Hq][N][64]
-  float* dkl;    // [U][N][64]
-  float* dvl;    // [U][N][64]
+  float* dkl;    // [B][Hq][N][64] per query head
+  float* dvl;    // [B][Hq][N][64] per query head
   float* coefl;  // [B][Hq][NB][73]
   float* coefs;  // [Hq][73]
   size_t bytes;
@@ -710,8 +701,8 @@ WorkView work_view(const Geometry& g, void* base, bool mma) {
   w.dwq_part = take(sizeof(float) * (size_t)g.B * g.Hq * g.NB * oal::kFP);
   w.dwq = take(sizeof(float) * (size_t)g.Hq * oal::kFP);
   w.dql = mma ? take(sizeof(float) * rows * oal::kD) : nullptr;
-  w.dkl = mma ? take(sizeof(float) * (size_t)g.U * g.N * oal::kD) : nullptr;
-  w.dvl = mma ? take(sizeof(float) * (size_t)g.U * g.N * oal::kD) : nullptr;
+  w.dkl = mma ? take(sizeof(float) * rows * oal::kD) : nullptr;
+  w.dvl = mma ? take(sizeof(float) * rows * oal::kD) : nullptr;
   w.coefl = mma ? take(sizeof(float) * (size_t)g.B * g.Hq * g.NB * 73) : nullptr;
   w.coefs = mma ? take(sizeof(float) * (size_t)g.Hq * 73) : nullptr;
   w.bytes = off;
@@ -822,11 +813,6 @@ int backward_impl(const Geometry& g, const void* q, const void* k, const void* v
   if constexpr (GMAX <= 8) {
     // matrix-core route
     const oal::LaunchGeom lg = launch_geom(g);
-    if (dk || dv) {
-      timed("k_kv_local", st, [&] { hipLaunchKernelGGL((k_kv_bwd<T, GMAX, false>), dim3(g.NB, g.U), dim3(256), 0, st, qt, kt, vt, w.dT, w.dTz,
-                         w.G, w.Gz, labels, c0, lam, gam, groups, g.Hq, g.Hkv, g.N, g.NB, scale, nullptr, nullptr,
-                         w.dkl, w.dvl); });
-    }
     oal::F32BwdArgs<T> a{qt, kt, vt, w.G, w.Gz, sv.wq, sv.carry, sv.carry_z, labels, c0, lam, gam, groups, scale,
                          w.dT, w.dTz, need_coef ? w.dwq_part : nullptr, w.dql, w.dkl, w.dvl,
                          need_coef ? w.coefl : nullptr, w.coefs, static_cast<T*>(dq), static_cast<T*>(dk),
