@@ -240,6 +240,17 @@ __global__ __launch_bounds__(64 * NW, (NW + 1) / 2) void k2_scan(const uint16_t*
   // Emission of tile t's state into state block cb (unit u and chunk ch: the
   // exclusive prefix / suffix before ch, cb = u * NB + ch; MODE 4: the carry of
   // segment seg, cb = u * Sg + seg).
+  // A lane holds 4-value words at positions 4 s (word "even") and 8 + 4 s
+  // (word "odd") of a 16-position row; swapping the odd words of lane group 0
+  // with the even words of lane group 1 gives lane group s positions
+  // 8 s .. 8 s + 7, stored as one 16-byte piece (the 64 lanes then write 32
+  // consecutive rows, 1 KiB).
+  auto store_row16 = [&](uint16_t* rowp, uint2 ev, uint2 od) {
+    const auto x = __builtin_amdgcn_permlane32_swap(ev.x, od.x, false, false);
+    const auto y = __builtin_amdgcn_permlane32_swap(ev.y, od.y, false, false);
+    // lanes 0-31: (own even, group 1's even); lanes 32-63: (group 0's odd, own odd)
+    *reinterpret_cast<uint4*>(rowp + 8 * s) = make_uint4(x[0], y[0], x[1], y[1]);
+  };
   auto emit = [&](int t, size_t cb) {
     // R layout straight from the accumulators: lane = slot, 4 values a word pair
     uint32_t wd[2][4][2];
@@ -254,9 +265,10 @@ __global__ __launch_bounds__(64 * NW, (NW + 1) / 2) void k2_scan(const uint16_t*
 #pragma unroll
     for (int n = 0; n < 2; ++n)
 #pragma unroll
-      for (int a = 0; a < 4; ++a) {
-        const int kk = 2 * n + (a >> 1), pos = 8 * (a & 1) + 4 * s;
-        *reinterpret_cast<uint2*>(tr + ((size_t)kk * 32 + row) * 16 + pos) = make_uint2(wd[n][a][0], wd[n][a][1]);
+      for (int a = 0; a < 4; a += 2) {
+        const int kk = 2 * n + (a >> 1);
+        store_row16(tr + ((size_t)kk * 32 + row) * 16, make_uint2(wd[n][a][0], wd[n][a][1]),
+                    make_uint2(wd[n][a + 1][0], wd[n][a + 1][1]));
       }
     // T layout [kstep][64 values][16 slots]: the matrix cores transpose the
     // packed tile (D = A P, one nonzero product per output, exact), giving
@@ -272,10 +284,11 @@ __global__ __launch_bounds__(64 * NW, (NW + 1) / 2) void k2_scan(const uint16_t*
       }
       const int e = 32 * nh + row;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int tp = q >> 1, pos = 8 * (q & 1) + 4 * s;
-        *reinterpret_cast<uint2*>(tt + ((size_t)tp * 64 + e) * 16 + pos) =
-            make_uint2(pack_bf16x2(D[4 * q], D[4 * q + 1]), pack_bf16x2(D[4 * q + 2], D[4 * q + 3]));
+      for (int q = 0; q < 4; q += 2) {
+        const int tp = q >> 1;
+        store_row16(tt + ((size_t)tp * 64 + e) * 16,
+                    make_uint2(pack_bf16x2(D[4 * q], D[4 * q + 1]), pack_bf16x2(D[4 * q + 2], D[4 * q + 3])),
+                    make_uint2(pack_bf16x2(D[4 * q + 4], D[4 * q + 5]), pack_bf16x2(D[4 * q + 6], D[4 * q + 7])));
       }
     }
   };
