@@ -161,12 +161,12 @@ struct ReadoutOps {
   float4 w0, w1;
   bf16x8 b0, b1;
 };
-template <int T>
-__device__ __forceinline__ void readout_read(const float* wl, const LdsRing<kNSR>& ring, int lane, ReadoutOps& o) {
+template <int T, int NS>
+__device__ __forceinline__ void readout_read(const float* wl, const LdsRing<NS>& ring, int lane, ReadoutOps& o) {
   const int s = lane >> 5, row = lane & 31;
   o.w0 = *reinterpret_cast<const float4*>(wl + 16 * T + 8 * s);
   o.w1 = *reinterpret_cast<const float4*>(wl + 16 * T + 8 * s + 4);
-  const __bf16* tile = ring.st[(T / kRG) % kNSR] + (T % kRG) * kRingStep;
+  const __bf16* tile = ring.st[(T / kRG) % NS] + (T % kRG) * kRingStep;
   o.b0 = *reinterpret_cast<const bf16x8*>(tile + row * 16 + 8 * s);
   o.b1 = *reinterpret_cast<const bf16x8*>(tile + (32 + row) * 16 + 8 * s);
 }
@@ -590,6 +590,139 @@ __global__ __launch_bounds__(128, 2) void k2_out_fwd(const T* __restrict__ q, co
 }
 
 // ---------------------------------------------------------------------------
+// Forward readout with the query heads of a unit sharing each copy of P_c: one
+// block per (token half, chunk, unit) of R + 1 waves (R <= kMaxRS query heads
+// per kv head). Wave w < R reads out head kh R + w for the half's 32 tokens as
+// k2_out_fwd does; wave R only streams the P^T tiles into an LDS ring of kNSS
+// stages (it issues every copy, so its vmcnt alone paces the ring). Each
+// chunk's state then leaves L2 twice, once per token half, instead of once per
+// query head, and the deeper ring keeps more of it in flight.
+// ---------------------------------------------------------------------------
+constexpr int kNSS = 4;
+constexpr int kMaxRS = 7;
+
+// Ring group G into stage G % kNSS by the copy wave: two 1 KiB wave copies per
+// k-step tile.
+template <int G>
+__device__ __forceinline__ void ring_issue_shared(const uint16_t* pt, const LdsRing<kNSS>& ring, int lane) {
+  __bf16* st = ring.st[G % kNSS];
+#pragma unroll
+  for (int i = 0; i < kRG; ++i) {
+    const int t = G * kRG + i;
+    if (t < kKS) {
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf)
+        copy16_to_lds(pt + (size_t)t * kRingStep + (64 * hf + lane) * 8, st + i * kRingStep + 64 * hf * 8);
+    }
+  }
+}
+template <int G, int... I>
+constexpr int shared_copies_in_flight(std::integer_sequence<int, I...>) {
+  return ((2 * group_copies<G + 1 + I>()) + ... + 0);
+}
+// The copy wave: one ring barrier per group (as many as the readout waves),
+// then the copies of the group kNSS - 1 ahead into the stage just released.
+template <int G>
+__device__ __forceinline__ void ring_produce(const uint16_t* pt, const LdsRing<kNSS>& ring, int lane) {
+  ring_sync<shared_copies_in_flight<G>(std::make_integer_sequence<int, kNSS - 2>{})>();
+  if constexpr (G + kNSS - 1 < kRingGroups) ring_issue_shared<G + kNSS - 1>(pt, ring, lane);
+  if constexpr (G + 1 < kRingGroups) ring_produce<G + 1>(pt, ring, lane);
+}
+template <int G>
+__device__ __forceinline__ void readout_group_shared(const float (&x)[kD], const float* wl,
+                                                     const LdsRing<kNSS>& ring, int lane, f32x16 (&acc)[2]) {
+  ring_sync<shared_copies_in_flight<G>(std::make_integer_sequence<int, kNSS - 2>{})>();
+  constexpr int n = (G + 1) * kRG <= kKS ? kRG : kKS - G * kRG;
+  ReadoutOps o[2];
+  readout_read<G * kRG>(wl, ring, lane, o[0]);
+  [&]<int... I>(std::integer_sequence<int, I...>) {
+    (([&] {
+       if constexpr (I + 1 < n) readout_read<G * kRG + I + 1>(wl, ring, lane, o[(I + 1) & 1]);
+       readout_step<G * kRG + I>(x, o[I & 1], acc);
+     }()),
+     ...);
+  }(std::make_integer_sequence<int, n>{});
+  if constexpr (G + 1 < kRingGroups) readout_group_shared<G + 1>(x, wl, ring, lane, acc);
+}
+
+template <typename T>
+__global__ __launch_bounds__(64 * (kMaxRS + 1), 1) void k2_out_fwd_shared(
+    const T* __restrict__ q, const float* __restrict__ wqs, const uint16_t* __restrict__ PT, int Hq, int Hkv, int N,
+    int NB, float floor, T* __restrict__ out, float* __restrict__ num, const float* __restrict__ den) {
+  __shared__ __attribute__((aligned(16))) __bf16 rs[kNSS][kRG * kRingStep];
+  __shared__ __attribute__((aligned(16))) float wl[kMaxRS][kS];
+  LdsRing<kNSS> ring;
+#pragma unroll
+  for (int i = 0; i < kNSS; ++i) ring.st[i] = rs[i];
+
+  int th, ch, u;
+  head_chunk_unit(2, NB, (int)(gridDim.x / (2 * NB)), th, ch, u);
+  const int R = Hq / Hkv, b = u / Hkv, kh = u % Hkv;
+  const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, s = l >> 5, row = l & 31;
+  const int tok0 = ch * kC + 32 * th;
+  const uint16_t* pt = PT + ((size_t)u * NB + ch) * ((size_t)kKS * kRingStep);
+
+  if (wv == R) {
+    // the copy wave
+    [&]<int... I>(std::integer_sequence<int, I...>) {
+      (ring_issue_shared<I>(pt, ring, l), ...);
+    }(std::make_integer_sequence<int, kNSS - 1>{});
+    ring_produce<0>(pt, ring, l);
+    return;
+  }
+  const int h = kh * R + wv;
+  const size_t qbase = (size_t)(b * Hq + h) * N * kD;
+  float* wlh = wl[wv];
+  for (int i = l; i < kS / 4; i += 64)
+    reinterpret_cast<float4*>(wlh)[i] = reinterpret_cast<const float4*>(wqs + (size_t)h * kS)[i];
+  float x[kD];
+  {
+    const int tok = tok0 + row;
+    const bool ok = tok < N;
+    const int tc = ok ? tok : N - 1;
+    bf16x8 qr[8];
+    load_row(q, qbase + (size_t)tc * kD, ok, qr);
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) x[(8 * i + j) & 63] = (float)qr[i][j];
+    if (s == 1) {
+#pragma unroll
+      for (int m = 0; m < 32; ++m) {
+        const float t = x[m];
+        x[m] = x[m + 32];
+        x[m + 32] = t;
+      }
+    }
+  }
+  f32x16 acc[2];
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int tok = tok0 + c32_row(i, l);
+      acc[nt][i] = tok < N ? num[qbase + (size_t)tok * kD + 32 * nt + row] : 0.f;
+    }
+  readout_group_shared<0>(x, wlh, ring, l, acc);
+
+  const size_t dbase = (size_t)(b * Hq + h) * N;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int tok = tok0 + c32_row(i, l);
+    if (tok < N) {
+      const float dd = den[dbase + tok];
+      const float inv = 1.f / (floor > 0.f ? fmaxf(dd, floor) : dd);
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        const size_t o = qbase + (size_t)tok * kD + 32 * nt + row;
+        num[o] = acc[nt][i];
+        out[o] = from_f<T>(acc[nt][i] * inv);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // MFMA layout self-test: checks the accumulator layouts assumed above.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(64) void k2_selftest(int* __restrict__ errors) {
@@ -707,6 +840,14 @@ void launch_mfma_forward(const LaunchGeom& g, const void* q, const void* k, cons
                          sv.KAP);
   });
   timed("k2_out_fwd", st, [&] {
+#ifndef OAL_OUT_PER_HEAD
+    // up to kMaxRS query heads per kv head: the heads share each copy of P_c
+    if (g.R <= kMaxRS) {
+      hipLaunchKernelGGL(k2_out_fwd_shared<T>, dim3(2 * g.NB * g.U), dim3(64 * (g.R + 1)), 0, st, qt, sv.wqs, sv.PT,
+                         g.Hq, g.Hkv, g.N, g.NB, floor, static_cast<T*>(out), num, den);
+      return;
+    }
+#endif
     hipLaunchKernelGGL(k2_out_fwd<T>, dim3(g.R * g.NB * g.U), dim3(128), 0, st, qt, sv.wqs, sv.PT, g.Hq, g.Hkv, g.N,
                        g.NB, floor, static_cast<T*>(out), num, den);
   });
