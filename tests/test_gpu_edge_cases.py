@@ -97,8 +97,11 @@ def test_sequence_lengths_at_chunk_boundaries(n):
     _run(2, 14, 2, n, _labels(14, 8), seed=n)
 
 
-@pytest.mark.parametrize("hq,hkv", [(2, 2), (16, 2), (18, 2)])
+@pytest.mark.parametrize("hq,hkv", [(2, 2), (6, 2), (4, 1), (10, 2), (12, 2), (16, 2), (18, 2)])
 def test_heads_per_kv_head(hq, hkv):
+    """1 to 9 query heads per KV head: the shared-copy readout for 1 to 7 (one
+    readout wave per head plus the copy wave), per-head readout blocks for 8, the
+    fp32 kernels for 9."""
     _run(1, hq, hkv, 130, _labels(hq, 4), seed=hq)
 
 
