@@ -171,30 +171,35 @@ __global__ __launch_bounds__(256) void k3_state_fwd(const T* __restrict__ k, con
 }
 
 // ---------------------------------------------------------------------------
-// Backward state scan: block (64-feature slice, unit), waves as above; walks
-// the chunks downwards, the unit's query heads within a chunk. Per item
-// (chunk, head): H = raw(Q)^T [G, Gz] (kept apart), dT += wq_h o H; before a
-// chunk's first item the suffix of the later chunks is emitted. With dwq_part
-// the item also writes <P_c[f], H[f]> (values of both waves and the ones
-// column, in a fixed order).
+// Backward state scan: block (64-feature slice, unit, segment), waves as
+// above; walks the segment's chunks downwards, the unit's query heads within a
+// chunk. Per item (chunk, head): H = raw(Q)^T [G, Gz] (kept apart),
+// dT += wq_h o H; before a chunk's first item the suffix of the segment's later
+// chunks is emitted, and after the segment its total goes to segt (several
+// segments: k3_seg_carry and k3_add_carry then add each segment's carry, the
+// sum of the later segments' totals). With dwq_part the item also writes
+// <P_c[f], H[f]> (values of both waves and the ones column, in a fixed order).
 // ---------------------------------------------------------------------------
 template <typename T>
 __global__ __launch_bounds__(256) void k3_state_bwd(const T* __restrict__ q, const float* __restrict__ G,
                                                     const float* __restrict__ Gz, const float* __restrict__ wq,
                                                     const float* __restrict__ P, const float* __restrict__ Pz, int Hq,
-                                                    int Hkv, int N, int NB, float* __restrict__ dT,
-                                                    float* __restrict__ dTz, float* __restrict__ dwq_part) {
+                                                    int Hkv, int N, int NB, int SL, float* __restrict__ dT,
+                                                    float* __restrict__ dTz, float* __restrict__ segt,
+                                                    float* __restrict__ segtz, float* __restrict__ dwq_part) {
   __shared__ float qx[kC][kRow];
   __shared__ float gs[kC][kD + 1];  // [G, Gz]
   __shared__ float xch[2][32];
   const int u = blockIdx.y, R = Hq / Hkv, b = u / Hkv, kh = u % Hkv;
+  const int seg = blockIdx.z, S = gridDim.z;
   const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, s = l >> 5, row = l & 31;
   const int m = wv & 1, ft = wv >> 1, f = blockIdx.x * 64 + 32 * ft + row;
   const int r = kTab3.r[f], c = kTab3.c[f];
-  const int NI = NB * R;
+  const int c_lo = seg * SL, c_hi = min(NB, c_lo + SL);
+  const int NI = (c_hi - c_lo) * R;
   float qr[16], gr[16], gzr = 0.f;
   auto load_item = [&](int it) {
-    const int ch = NB - 1 - it / R, h = kh * R + it % R;
+    const int ch = c_hi - 1 - it / R, h = kh * R + it % R;
     const size_t hb = (size_t)(b * Hq + h) * N;
     load_chunk_rows(q, hb * kD, ch * kC, N, qr);
     load_chunk_rows(G, hb * kD, ch * kC, N, gr);
@@ -207,7 +212,7 @@ __global__ __launch_bounds__(256) void k3_state_bwd(const T* __restrict__ q, con
   float pr[16];
   float pz = 0.f;
   for (int it = 0; it < NI; ++it) {
-    const int ch = NB - 1 - it / R, hh = it % R, h = kh * R + hh;
+    const int ch = c_hi - 1 - it / R, hh = it % R, h = kh * R + hh;
     const size_t cb = (size_t)u * NB + ch;
     if (hh == 0) {
       store_state_row(dT + (cb * kFP + f) * kD, m, s, acc);
@@ -261,6 +266,60 @@ __global__ __launch_bounds__(256) void k3_state_bwd(const T* __restrict__ q, con
       if (m == 0 && s == 0) dwq_part[((size_t)(b * Hq + h) * NB + ch) * kFP + f] = p + xch[ft][row] + pz * hzt;
     }
   }
+  if (S > 1) {
+    const size_t sb = (size_t)u * S + seg;
+    store_state_row(segt + (sb * kFP + f) * kD, m, s, acc);
+    const float zt = accz + partner(accz);
+    if (m == 0 && s == 0) segtz[sb * kFP + f] = zt;
+  }
+}
+
+// Segment totals -> carries, in place: entry (u, seg) becomes the sum of the
+// totals of the segments after seg (a running sum from the last segment, so a
+// fixed order). One thread per (unit, feature, value or ones column).
+__global__ __launch_bounds__(256) void k3_seg_carry(float* __restrict__ segt, float* __restrict__ segtz, int U, int S) {
+  const size_t per_u = (size_t)kFP * (kD + 1);
+  const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= per_u * U) return;
+  const int u = (int)(idx / per_u);
+  const size_t e = idx % per_u;
+  float* base;
+  size_t stride;
+  if (e < (size_t)kFP * kD) {
+    base = segt + (size_t)u * S * kFP * kD + e;
+    stride = (size_t)kFP * kD;
+  } else {
+    base = segtz + (size_t)u * S * kFP + (e - (size_t)kFP * kD);
+    stride = kFP;
+  }
+  float run = 0.f;
+  for (int sg = S - 1; sg >= 0; --sg) {
+    const float t = base[sg * stride];
+    base[sg * stride] = run;
+    run += t;
+  }
+}
+
+// dT[u][c] += carry[u][c / SL] for every chunk of every segment but the last
+// (whose carry is zero). Block (chunk, unit), float4 per thread and step.
+__global__ __launch_bounds__(256) void k3_add_carry(float* __restrict__ dT, float* __restrict__ dTz,
+                                                    const float* __restrict__ segt, const float* __restrict__ segtz,
+                                                    int NB, int SL, int S) {
+  const int ch = blockIdx.x, u = blockIdx.y, sg = ch / SL;
+  if (sg >= S - 1) return;
+  const size_t cb = (size_t)u * NB + ch, sb = (size_t)u * S + sg;
+  float4* d = reinterpret_cast<float4*>(dT + cb * kFP * kD);
+  const float4* cr = reinterpret_cast<const float4*>(segt + sb * kFP * kD);
+  for (int i = threadIdx.x; i < kFP * kD / 4; i += 256) {
+    float4 a = d[i];
+    const float4 x = cr[i];
+    a.x += x.x;
+    a.y += x.y;
+    a.z += x.z;
+    a.w += x.w;
+    d[i] = a;
+  }
+  for (int i = threadIdx.x; i < kFP; i += 256) dTz[cb * kFP + i] += segtz[sb * kFP + i];
 }
 
 // ---------------------------------------------------------------------------
@@ -929,10 +988,20 @@ template <typename T>
 void launch_f32_backward(const LaunchGeom& g, const F32BwdArgs<T>& a, hipStream_t st, const Timer& timed) {
   // the scan also forms the state coefficient partials (its per-item products)
   if (a.dk || a.dv || a.dwq_part) {
+    const int S = a.plan.S, SL = a.plan.SL;
     timed("k3_state_bwd", st, [&] {
-      hipLaunchKernelGGL(k3_state_bwd<T>, dim3(kFP / 64, g.U), dim3(256), 0, st, a.q, a.G, a.Gz, a.wq, a.P, a.Pz,
-                         g.Hq, g.Hkv, g.N, g.NB, a.dT, a.dTz, a.dwq_part);
+      hipLaunchKernelGGL(k3_state_bwd<T>, dim3(kFP / 64, g.U, S), dim3(256), 0, st, a.q, a.G, a.Gz, a.wq, a.P, a.Pz,
+                         g.Hq, g.Hkv, g.N, g.NB, SL, a.dT, a.dTz, a.segt, a.segtz, a.dwq_part);
     });
+    if (S > 1 && (a.dk || a.dv)) {
+      timed("k3_state_bwd_carry", st, [&] {
+        const size_t n = (size_t)g.U * kFP * (kD + 1);
+        hipLaunchKernelGGL(k3_seg_carry, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a.segt, a.segtz, g.U,
+                           S);
+        hipLaunchKernelGGL(k3_add_carry, dim3(g.NB, g.U), dim3(256), 0, st, a.dT, a.dTz, a.segt, a.segtz, g.NB,
+                           SL, S);
+      });
+    }
   }
   timed("k3_local", st, [&] {
     hipLaunchKernelGGL(k3_local<T>, dim3(g.R * g.NB * g.U), dim3(192), 0, st, a.q, a.k, a.v, a.G, a.Gz, a.labels,

@@ -147,6 +147,33 @@ void launch_f32_state_fwd(const LaunchGeom& g, const T* k, const T* v, float* ca
 template <typename T>
 void launch_f32_readout_fwd(const LaunchGeom& g, const T* q, const float* wq, const float* carry, const float* carry_z,
                             float floor, float* num, float* den, T* out, hipStream_t st, const Timer& timed);
+// Chunk segments of the fp32 backward state scan, a function of the geometry
+// alone (the workspace holds the segment totals): each (64-feature slice,
+// unit, segment) block walks its segment's chunks and the unit's R heads.
+// Model: four resident blocks per CU on a 256-CU MI355X, a block's time
+// proportional to its items (plus a start of two), a partial last round costing
+// a full one, and the carry pass (suffix of the segment totals, added to every
+// chunk's state) about 40 items plus one per segment.
+struct F32ScanPlan {
+  int S, SL;
+};
+inline F32ScanPlan f32_bwd_plan(int U, int NB, int R) {
+  constexpr int kSlices = 2176 / 64, kResident = 4 * 256;
+  F32ScanPlan best{1, NB};
+  double best_t = 0.0;
+  for (int want = 1; want <= NB && want <= 64; ++want) {
+    const int SL = (NB + want - 1) / want, S = (NB + SL - 1) / SL;
+    const int blocks = kSlices * U * S;
+    const double rounds = (double)((blocks + kResident - 1) / kResident);
+    const double t = rounds * (SL * R + 2.0) + (S > 1 ? 40.0 + S : 0.0);
+    if (want == 1 || t < best_t) {
+      best_t = t;
+      best = F32ScanPlan{S, SL};
+    }
+  }
+  return best;
+}
+
 template <typename T>
 struct F32BwdArgs {
   const T *q, *k, *v;
@@ -156,6 +183,8 @@ struct F32BwdArgs {
   int groups;
   float scale;
   float *dT, *dTz;    // [U][NB][kFP][64], [U][NB][kFP]
+  F32ScanPlan plan;   // f32_bwd_plan of the geometry
+  float *segt, *segtz;  // segment totals, then carries: [U][S][kFP][64], [U][S][kFP] (S > 1)
   float* dwq_part;    // state coefficient partials [B][Hq][NB][kFP] (nullptr: not requested)
   float *dql, *dkl, *dvl;  // local parts, [B][Hq][N][64] per query head
   float* coefl;       // local coefficient partials [B][Hq][NB][73] (nullptr: not requested)

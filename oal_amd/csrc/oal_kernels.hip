@@ -677,6 +677,8 @@ struct WorkView {
   float* dvl;    // [B][Hq][N][64] per query head
   float* coefl;  // [B][Hq][NB][73]
   float* coefs;  // [Hq][73]
+  float* segt;   // backward scan segment totals [U][S][kFP][64] (S > 1)
+  float* segtz;  // [U][S][kFP]
   size_t bytes;
 };
 
@@ -705,6 +707,9 @@ WorkView work_view(const Geometry& g, void* base, bool mma) {
   w.dvl = mma ? take(sizeof(float) * rows * oal::kD) : nullptr;
   w.coefl = mma ? take(sizeof(float) * (size_t)g.B * g.Hq * g.NB * 73) : nullptr;
   w.coefs = mma ? take(sizeof(float) * (size_t)g.Hq * 73) : nullptr;
+  const int S = mma ? oal::f32_bwd_plan(g.U, g.NB, g.R).S : 1;
+  w.segt = S > 1 ? take(sizeof(float) * (size_t)g.U * S * oal::kFP * oal::kD) : nullptr;
+  w.segtz = S > 1 ? take(sizeof(float) * (size_t)g.U * S * oal::kFP) : nullptr;
   w.bytes = off;
   return w;
 }
@@ -814,7 +819,8 @@ int backward_impl(const Geometry& g, const void* q, const void* k, const void* v
     // matrix-core route
     const oal::LaunchGeom lg = launch_geom(g);
     oal::F32BwdArgs<T> a{qt, kt, vt, w.G, w.Gz, sv.wq, sv.carry, sv.carry_z, labels, c0, lam, gam, groups, scale,
-                         w.dT, w.dTz, need_coef ? w.dwq_part : nullptr, w.dql, w.dkl, w.dvl,
+                         w.dT, w.dTz, oal::f32_bwd_plan(g.U, g.NB, g.R), w.segt, w.segtz,
+                         need_coef ? w.dwq_part : nullptr, w.dql, w.dkl, w.dvl,
                          need_coef ? w.coefl : nullptr, w.coefs, static_cast<T*>(dq), static_cast<T*>(dk),
                          static_cast<T*>(dv)};
     oal::launch_f32_backward<T>(lg, a, st, make_timer());
