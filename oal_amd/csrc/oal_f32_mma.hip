@@ -5,9 +5,11 @@
 // the matrix cores and the intra-chunk terms in group-sum form.
 //
 //   k3_state_fwd   P_c = sum_{c' < c} raw(K_c')^T [V_c', 1]          (exclusive prefix)
+//   k3_intra_fwd   intra-chunk num and den (group sums on the matrix cores)
 //   k3_state_bwd   dT_c = sum_{c' > c} sum_h wq_h o raw(Q_h,c')^T [G, Gz]_h,c'
-//                  and the state part of the feature-coefficient gradient
-//                  dwq_part[b][h][c][f] = <P_c[f], raw(Q_h,c)^T [G, Gz]_h,c[f]>
+//                  in chunk segments (k3_seg_carry / k3_add_carry add each
+//                  segment's carry) and the state part of the feature-coefficient
+//                  gradient dwq_part[b][h][c][f] = <P_c[f], raw(Q_h,c)^T [G, Gz]_h,c[f]>
 //   k3_readout     num += phi(x) . S (out: num / den), or dv = raw(K) dT + local
 //   k3_fold        dq = fold of (P [G, Gz]^T) through wq o raw(q) + local,
 //                  dk = fold of (dT [V, 1]^T) through raw(k) + local
@@ -694,6 +696,123 @@ __device__ __forceinline__ f32x16 dot_rows_mfma(const float (*Ar)[kLRow], const 
   return acc;
 }
 
+// ---------------------------------------------------------------------------
+// Intra-chunk forward on the matrix cores, one block of 3 waves per (query
+// head, chunk, unit); wave w owns the lower tile (j-tile, i-tile) = (0,0),
+// (0,1), (1,1) in orientation C[j][i] (lane column = query i):
+//   kappa(i, j) = c0 + sum_g s_g (lam_g + sum_h Gam_gh s_h),  j <= i,
+// with the group sums s_g on the matrix cores over the group-sorted dims, then
+//   num^T[e][i] = sum_j V^T[e][j] kappa^T[j][i] (the kappa accumulators as the
+//   K-major operand, step k taking register k),  den[i] = sum_j kappa(i, j).
+// Writes the intra-chunk num and den, to which k3_readout adds the state part
+// (reference: the local terms of grouped_reference.py:214-318 in group-sum form).
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(192) void k3_intra_fwd(const T* __restrict__ q, const T* __restrict__ k,
+                                                    const T* __restrict__ v, const int32_t* __restrict__ labels,
+                                                    const float* __restrict__ c0, const float* __restrict__ lam,
+                                                    const float* __restrict__ gam, int Gn, int Hq, int Hkv, int N,
+                                                    int NB, float scale, float* __restrict__ num,
+                                                    float* __restrict__ den) {
+  __shared__ __attribute__((aligned(16))) float qx[kC][kLRow];
+  __shared__ __attribute__((aligned(16))) float kx[kC][kLRow];
+  __shared__ __attribute__((aligned(16))) float vx[kC][kLRow];
+  __shared__ __attribute__((aligned(16))) float xb[kD][33];  // tile (1,0)'s num^T
+  __shared__ float xz[32];                                    // and its den
+  __shared__ HeadGroups<8> hg;
+  int hh, ch, u;
+  head_chunk_unit(Hq / Hkv, NB, (int)(gridDim.x / ((Hq / Hkv) * NB)), hh, ch, u);
+  const int R = Hq / Hkv, b = u / Hkv, kh = u % Hkv, h = kh * R + hh;
+  const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, s = l >> 5, row = l & 31;
+  const int it = wv == 0 ? 0 : 1, jt = wv == 2 ? 1 : 0;
+  const int tok0 = ch * kC;
+  const size_t qbase = (size_t)(b * Hq + h) * N * kD;
+  const size_t kbase = (size_t)u * N * kD;
+  // staging: 192 threads, 64 rows x 64 dims per operand, 16 consecutive dims each
+  for (int idx = tid; idx < 3 * kC * 4; idx += 192) {
+    const int op = idx >> 8, rr = (idx >> 2) & 63, q4 = idx & 3, tok = tok0 + rr;
+    const bool ok = tok < N;
+    float vals[16];
+    const size_t off = (op == 0 ? qbase : kbase) + (size_t)(ok ? tok : N - 1) * kD + 16 * q4;
+    if (op == 0) load16(q, off, ok, vals);
+    else if (op == 1) load16(k, off, ok, vals);
+    else load16(v, off, ok, vals);
+    float* dst = op == 0 ? &qx[rr][16 * q4] : op == 1 ? &kx[rr][16 * q4] : &vx[rr][16 * q4];
+#pragma unroll
+    for (int e = 0; e < 16; e += 4)
+      *reinterpret_cast<float4*>(dst + e) = make_float4(vals[e], vals[e + 1], vals[e + 2], vals[e + 3]);
+  }
+  load_head_groups(hg, labels, c0, lam, gam, Gn, h);  // synchronizes the block
+  // the head's coefficients, wave-uniform: kept in scalar registers
+  auto uni = [](float x) { return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(x))); };
+  float lm[8], gm[8][8];
+#pragma unroll
+  for (int g = 0; g < 8; ++g) {
+    lm[g] = uni(g < Gn ? hg.lam[g] : 0.f);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) gm[g][e] = uni((g < Gn && e < Gn) ? hg.gam[g * Gn + e] : 0.f);
+  }
+  const float cz = uni(hg.c0);
+
+  const int jr = 32 * jt + row, ic = 32 * it + row;
+  f32x16 S[8];
+  group_sums_mfma(kx, qx, jr, ic, hg.perm, hg.gstart, Gn, s, scale, S);
+  f32x16 kap;
+  float dsum = 0.f;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const bool valid = 32 * jt + c32_row(r, l) <= ic;
+    float kv = cz;
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+      float inner = lm[g];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) inner = fmaf(gm[g][e], S[e][r], inner);
+      kv = fmaf(S[g][r], inner, kv);
+    }
+    kap[r] = valid ? kv : 0.f;
+    dsum += kap[r];
+  }
+  dsum += partner(dsum);
+  // num^T[e][i] = sum_j V^T[e][j] kappa^T[j][i]; j = 32 jt + c32_row(k, 32 s) at step k
+  f32x16 nm[2] = {f32x16{}, f32x16{}};
+#pragma unroll
+  for (int dt = 0; dt < 2; ++dt) {
+    const int e = 32 * dt + row;
+#pragma unroll
+    for (int kk = 0; kk < 16; ++kk) nm[dt] = mfma_f32(vx[32 * jt + c32_row(kk, 32 * s)][e], kap[kk], nm[dt]);
+  }
+  // i-tile 1 gets tiles (1,0) and (1,1): wave 1 hands its part to wave 2
+  if (wv == 1) {
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) xb[32 * dt + c32_row(r, l)][row] = nm[dt][r];
+    if (s == 0) xz[row] = dsum;
+  }
+  __syncthreads();
+  if (wv != 1) {
+    const int i = 32 * it + row, tok = tok0 + i;
+    if (wv == 2) {
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) nm[dt][r] = xb[32 * dt + c32_row(r, l)][row] + nm[dt][r];
+      dsum = xz[row] + dsum;
+    }
+    if (tok < N) {
+      float* dst = num + qbase + (size_t)tok * kD;
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+          *reinterpret_cast<float4*>(dst + 32 * dt + 8 * a + 4 * s) =
+              make_float4(nm[dt][4 * a], nm[dt][4 * a + 1], nm[dt][4 * a + 2], nm[dt][4 * a + 3]);
+      if (s == 0) den[(size_t)(b * Hq + h) * N + tok] = dsum;
+    }
+  }
+}
+
 template <typename T>
 __global__ __launch_bounds__(192) void k3_local(const T* __restrict__ q, const T* __restrict__ k,
                                                 const T* __restrict__ v, const float* __restrict__ G,
@@ -976,6 +1095,16 @@ void launch_f32_state_fwd(const LaunchGeom& g, const T* k, const T* v, float* ca
 }
 
 template <typename T>
+void launch_f32_intra_fwd(const LaunchGeom& g, const T* q, const T* k, const T* v, const int32_t* labels, const float* c0,
+                          const float* lam, const float* gam, int groups, float scale, float* num, float* den,
+                          hipStream_t st, const Timer& timed) {
+  timed("k3_intra_fwd", st, [&] {
+    hipLaunchKernelGGL(k3_intra_fwd<T>, dim3(g.R * g.NB * g.U), dim3(192), 0, st, q, k, v, labels, c0, lam, gam,
+                       groups, g.Hq, g.Hkv, g.N, g.NB, scale, num, den);
+  });
+}
+
+template <typename T>
 void launch_f32_readout_fwd(const LaunchGeom& g, const T* q, const float* wq, const float* carry, const float* carry_z,
                             float floor, float* num, float* den, T* out, hipStream_t st, const Timer& timed) {
   timed("k3_readout", st, [&] {
@@ -1035,6 +1164,9 @@ void launch_f32_backward(const LaunchGeom& g, const F32BwdArgs<T>& a, hipStream_
 #define OAL_F32MMA_INST(T)                                                                                        \
   template void launch_f32_state_fwd<T>(const LaunchGeom&, const T*, const T*, float*, float*, hipStream_t,        \
                                         const Timer&);                                                            \
+  template void launch_f32_intra_fwd<T>(const LaunchGeom&, const T*, const T*, const T*, const int32_t*,         \
+                                        const float*, const float*, const float*, int, float, float*, float*,       \
+                                        hipStream_t, const Timer&);                                                 \
   template void launch_f32_readout_fwd<T>(const LaunchGeom&, const T*, const float*, const float*, const float*, \
                                           float, float*, float*, T*, hipStream_t, const Timer&);                  \
   template void launch_f32_backward<T>(const LaunchGeom&, const F32BwdArgs<T>&, hipStream_t, const Timer&);

@@ -145,6 +145,10 @@ template <typename T>
 void launch_f32_state_fwd(const LaunchGeom& g, const T* k, const T* v, float* carry, float* carry_z, hipStream_t st,
                           const Timer& timed);
 template <typename T>
+void launch_f32_intra_fwd(const LaunchGeom& g, const T* q, const T* k, const T* v, const int32_t* labels, const float* c0,
+                          const float* lam, const float* gam, int groups, float scale, float* num, float* den,
+                          hipStream_t st, const Timer& timed);
+template <typename T>
 void launch_f32_readout_fwd(const LaunchGeom& g, const T* q, const float* wq, const float* carry, const float* carry_z,
                             float floor, float* num, float* den, T* out, hipStream_t st, const Timer& timed);
 // Chunk segments of the fp32 backward state scan, a function of the geometry

@@ -151,9 +151,7 @@ __global__ __launch_bounds__(256) void k_state_fwd(const T* __restrict__ k, cons
 // (reference _contract_query_wave :411-614 and _write_and_normalize_query_wave
 // :351-385). Thread t owns token i = t/4 and value columns 16*(t%4) .. +15.
 // ---------------------------------------------------------------------------
-// STATE = false (the matrix-core fp32 route): the intra-chunk part only, num and
-// den written unnormalized; k3_readout adds the state part and writes out.
-template <typename T, int GMAX, bool STATE = true>
+template <typename T, int GMAX>
 __global__ __launch_bounds__(256) void k_out_fwd(const T* __restrict__ q, const T* __restrict__ k,
                                                  const T* __restrict__ v, const float* __restrict__ wq,
                                                  const float* __restrict__ carry,
@@ -201,21 +199,17 @@ __global__ __launch_bounds__(256) void k_out_fwd(const T* __restrict__ q, const 
   float accz = 0.f;
   const size_t crow0 = ((size_t)u * NB + ch) * kFP;
   const float* wqh = wq + (size_t)h * kFP;
-  if constexpr (STATE) {
-    for (int f0 = 0; f0 < kFP; f0 += kTile) {
-      __syncthreads();
-      stage_state_tile(pt, carry, carry_z, crow0 + f0);
-      __syncthreads();
-      for (int fl = 0; fl < kTile; ++fl) {
-        const int f = f0 + fl;
-        const float phi = wqh[f] * qx[i][kTab.r[f]] * qx[i][kTab.c[f]];
-#pragma unroll
-        for (int e = 0; e < 16; ++e) acc[e] += phi * pt[fl][cq * 16 + e];
-        accz += phi * pt[fl][kD];
-      }
-    }
-  } else {
+  for (int f0 = 0; f0 < kFP; f0 += kTile) {
     __syncthreads();
+    stage_state_tile(pt, carry, carry_z, crow0 + f0);
+    __syncthreads();
+    for (int fl = 0; fl < kTile; ++fl) {
+      const int f = f0 + fl;
+      const float phi = wqh[f] * qx[i][kTab.r[f]] * qx[i][kTab.c[f]];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[e] += phi * pt[fl][cq * 16 + e];
+      accz += phi * pt[fl][kD];
+    }
   }
   for (int j = 0; j <= i; ++j) {
     const float kv = kap[i][j];
@@ -231,7 +225,7 @@ __global__ __launch_bounds__(256) void k_out_fwd(const T* __restrict__ q, const 
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
       num[o + e] = acc[e];
-      if constexpr (STATE) out[o + e] = from_f<T>(acc[e] * inv);
+      out[o + e] = from_f<T>(acc[e] * inv);
     }
     if (cq == 0) den[(size_t)(b * Hq + h) * N + tok] = accz;
   }
@@ -784,9 +778,7 @@ int forward_impl(const Geometry& g, const void* q, const void* k, const void* v,
     // matrix-core route: state scan, intra-chunk part, then the state readout
     const oal::LaunchGeom lg = launch_geom(g);
     oal::launch_f32_state_fwd<T>(lg, kt, vt, sv.carry, sv.carry_z, st, make_timer());
-    timed("k_out_local", st, [&] { hipLaunchKernelGGL((k_out_fwd<T, GMAX, false>), dim3(g.R, g.NB, g.U), dim3(256), 0, st, qt, kt, vt, sv.wq,
-                       sv.carry, sv.carry_z, labels, c0, lam, gam, groups, g.Hq, g.Hkv, g.N, g.NB, scale, floor,
-                       static_cast<T*>(out), num, den); });
+    oal::launch_f32_intra_fwd<T>(lg, qt, kt, vt, labels, c0, lam, gam, groups, scale, num, den, st, make_timer());
     oal::launch_f32_readout_fwd<T>(lg, qt, sv.wq, sv.carry, sv.carry_z, floor, num, den, static_cast<T*>(out), st,
                                    make_timer());
     return launch_status("oal_forward launch");
