@@ -118,6 +118,39 @@ def test_fp32_forward_backward_ragged_gqa_matches_oracle(upstream):
         assert rel(got, want) <= FP32_TOL, (rel(got, want), got.shape)
 
 
+def test_fp32_state_scan_segments_match_oracle():
+    """The fp32 route's backward state scan walks its chunks in segments when a
+    geometry has few (feature slice, unit) blocks for a long chunk walk: at B=1,
+    Hq=8, Hkv=1, N=1080 (17 chunks, the last one ragged) it runs 9 segments of 2
+    chunks (the last of 1), then turns the segment totals into carries and adds
+    each chunk's carry. Outputs and every gradient must match the oracle to the
+    fp32 bar, the coefficient gradients (formed from the per-item products inside
+    the segments) included."""
+    from oal_amd.hd_block_gemm_autograd import grouped_oal
+
+    dev = _dev()
+    q, k, v, labels, c0, lam, gam = _random_grouped(1, 8, 1, 1080, 4, seed=21)
+    scale = 0.125
+    qg, kg, vg = (t.to(dev).requires_grad_() for t in (q, k, v))
+    c0g, lamg, gamg = (t.to(dev).requires_grad_() for t in (c0, lam, gam))
+    out, num, den = grouped_oal(qg, kg, vg, labels.to(dev), c0g, lamg, gamg, scale=scale, floor=0.0)
+    wq, (out_r, num_r, den_r) = _oracle_fwd(q, k, v, labels, c0, lam, gam, scale)
+    errs = {"num": rel(num, num_r), "den": rel(den, den_r)}
+    gen = torch.Generator().manual_seed(22)
+    dnum = torch.randn(num.shape, generator=gen, dtype=torch.float64)
+    dden = torch.randn(den.shape, generator=gen, dtype=torch.float64)
+    ((num * dnum.float().to(dev)).sum() + (den * dden.float().to(dev)).sum()).backward()
+    dq_r, dk_r, dv_r, dwq_r = go.chunked_backward(q.double(), k.double(), v.double(), wq, num_r, den_r,
+                                                  None, dnum, dden)
+    dc0_r, dlam_r, dgam_r = go.coefficient_gradients_from_wq(dwq_r, labels, 4, scale=scale, head_dim=64)
+    dgam_r = go.symmetrize_gamma_gradient(dgam_r)
+    for name, got, want in (("dq", qg.grad, dq_r), ("dk", kg.grad, dk_r), ("dv", vg.grad, dv_r),
+                            ("dc0", c0g.grad, dc0_r), ("dlam", lamg.grad, dlam_r), ("dgam", gamg.grad, dgam_r)):
+        errs[name] = rel(got, want)
+    print("fp32 segmented scan: " + " ".join(f"{k_}={e:.1e}" for k_, e in errs.items()), flush=True)
+    assert all(e <= FP32_TOL for e in errs.values()), errs
+
+
 def test_logical_abc_function_matches_oracle_small_head_dim():
     from oal_amd.hd_block_gemm import build_hd_block_gemm_plan, canonical_pair_layout
     from oal_amd.hd_block_gemm_autograd import _HDParallelBlockGemmFunction
