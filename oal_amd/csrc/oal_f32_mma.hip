@@ -303,16 +303,21 @@ __global__ __launch_bounds__(256) void k3_seg_carry(float* __restrict__ segt, fl
 }
 
 // dT[u][c] += carry[u][c / SL] for every chunk of every segment but the last
-// (whose carry is zero). Block (chunk, unit), float4 per thread and step.
+// (whose carry is zero). Block (chunk, unit, part): part p of kAddParts covers
+// a contiguous 1 / kAddParts of the chunk's state, a float4 per thread and step;
+// part 0 also adds the ones column.
+constexpr int kAddParts = 8;
 __global__ __launch_bounds__(256) void k3_add_carry(float* __restrict__ dT, float* __restrict__ dTz,
                                                     const float* __restrict__ segt, const float* __restrict__ segtz,
                                                     int NB, int SL, int S) {
   const int ch = blockIdx.x, u = blockIdx.y, sg = ch / SL;
   if (sg >= S - 1) return;
   const size_t cb = (size_t)u * NB + ch, sb = (size_t)u * S + sg;
-  float4* d = reinterpret_cast<float4*>(dT + cb * kFP * kD);
-  const float4* cr = reinterpret_cast<const float4*>(segt + sb * kFP * kD);
-  for (int i = threadIdx.x; i < kFP * kD / 4; i += 256) {
+  constexpr int per = kFP * kD / 4 / kAddParts;
+  static_assert(per * kAddParts * 4 == kFP * kD, "parts must tile the chunk state");
+  float4* d = reinterpret_cast<float4*>(dT + cb * kFP * kD) + blockIdx.z * per;
+  const float4* cr = reinterpret_cast<const float4*>(segt + sb * kFP * kD) + blockIdx.z * per;
+  for (int i = threadIdx.x; i < per; i += 256) {
     float4 a = d[i];
     const float4 x = cr[i];
     a.x += x.x;
@@ -321,7 +326,8 @@ __global__ __launch_bounds__(256) void k3_add_carry(float* __restrict__ dT, floa
     a.w += x.w;
     d[i] = a;
   }
-  for (int i = threadIdx.x; i < kFP; i += 256) dTz[cb * kFP + i] += segtz[sb * kFP + i];
+  if (blockIdx.z == 0)
+    for (int i = threadIdx.x; i < kFP; i += 256) dTz[cb * kFP + i] += segtz[sb * kFP + i];
 }
 
 // ---------------------------------------------------------------------------
@@ -1073,14 +1079,22 @@ __global__ __launch_bounds__(192) void k3_local(const T* __restrict__ q, const T
 
 // Per-head sums of the local coefficient partials over (batch, chunk), in a
 // fixed order: coefs[h][e].
-__global__ __launch_bounds__(128) void k3_coef_reduce(const float* __restrict__ coefl, int B, int Hq, int NB,
+__global__ __launch_bounds__(256) void k3_coef_reduce(const float* __restrict__ coefl, int B, int Hq, int NB,
                                                       float* __restrict__ coefs) {
-  const int h = blockIdx.x, e = threadIdx.x;
-  if (e >= 73) return;
+  __shared__ float ps[256];
+  const int e = blockIdx.x, h = blockIdx.y, t = threadIdx.x;
   float acc = 0.f;
-  for (int b = 0; b < B; ++b)
-    for (int ch = 0; ch < NB; ++ch) acc += coefl[((size_t)(b * Hq + h) * NB + ch) * 73 + e];
-  coefs[(size_t)h * 73 + e] = acc;
+  for (int r = t; r < B * NB; r += 256) {
+    const int b = r / NB, ch = r - b * NB;
+    acc += coefl[((size_t)(b * Hq + h) * NB + ch) * 73 + e];
+  }
+  ps[t] = acc;
+  __syncthreads();
+  for (int w = 128; w >= 1; w >>= 1) {
+    if (t < w) ps[t] += ps[t + w];
+    __syncthreads();
+  }
+  if (t == 0) coefs[(size_t)h * 73 + e] = ps[0];
 }
 
 // ---------------------------------------------------------------------------
@@ -1127,7 +1141,7 @@ void launch_f32_backward(const LaunchGeom& g, const F32BwdArgs<T>& a, hipStream_
         const size_t n = (size_t)g.U * kFP * (kD + 1);
         hipLaunchKernelGGL(k3_seg_carry, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a.segt, a.segtz, g.U,
                            S);
-        hipLaunchKernelGGL(k3_add_carry, dim3(g.NB, g.U), dim3(256), 0, st, a.dT, a.dTz, a.segt, a.segtz, g.NB,
+        hipLaunchKernelGGL(k3_add_carry, dim3(g.NB, g.U, kAddParts), dim3(256), 0, st, a.dT, a.dTz, a.segt, a.segtz, g.NB,
                            SL, S);
       });
     }
@@ -1156,7 +1170,7 @@ void launch_f32_backward(const LaunchGeom& g, const F32BwdArgs<T>& a, hipStream_
   }
   if (a.coefl) {
     timed("k3_coef_reduce", st, [&] {
-      hipLaunchKernelGGL(k3_coef_reduce, dim3(g.Hq), dim3(128), 0, st, a.coefl, g.B, g.Hq, g.NB, a.coefs);
+      hipLaunchKernelGGL(k3_coef_reduce, dim3(73, g.Hq), dim3(256), 0, st, a.coefl, g.B, g.Hq, g.NB, a.coefs);
     });
   }
 }

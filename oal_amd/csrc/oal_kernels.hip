@@ -542,16 +542,27 @@ __global__ __launch_bounds__(256) void k_kv_bwd(const T* __restrict__ q, const T
   }
 }
 
-// dwq[h][f] = sum_{b, chunk} dwq_part[b][h][chunk][f] in a fixed order.
-__global__ __launch_bounds__(256) void k_dwq_reduce(const float* __restrict__ part, int B, int Hq, int NB,
-                                                    float* __restrict__ dwq) {
-  const int h = blockIdx.y;
-  const int f = blockIdx.x * blockDim.x + threadIdx.x;
-  if (f >= kFP) return;
+// dwq[h][f] = sum_{b, chunk} dwq_part[b][h][chunk][f] in a fixed order. Block
+// (64 features, head): 16 row sets, row set q sums rows q, q + 16, ... (row r =
+// batch r / NB, chunk r % NB), then a fixed pairwise tree over the 16 sums.
+__global__ __launch_bounds__(1024) void k_dwq_reduce(const float* __restrict__ part, int B, int Hq, int NB,
+                                                     float* __restrict__ dwq) {
+  __shared__ float ps[16][64];
+  const int h = blockIdx.y, fl = threadIdx.x & 63, q = threadIdx.x >> 6;
+  const int f = blockIdx.x * 64 + fl;
   float acc = 0.f;
-  for (int b = 0; b < B; ++b)
-    for (int ch = 0; ch < NB; ++ch) acc += part[((size_t)(b * Hq + h) * NB + ch) * kFP + f];
-  dwq[(size_t)h * kFP + f] = acc;
+  if (f < kFP)
+    for (int r = q; r < B * NB; r += 16) {
+      const int b = r / NB, ch = r - b * NB;
+      acc += part[((size_t)(b * Hq + h) * NB + ch) * kFP + f];
+    }
+  ps[q][fl] = acc;
+  __syncthreads();
+  for (int w = 8; w >= 1; w >>= 1) {
+    if (q < w) ps[q][fl] += ps[q + w][fl];
+    __syncthreads();
+  }
+  if (q == 0 && f < kFP) dwq[(size_t)h * kFP + f] = ps[0][fl];
 }
 
 // Adjoint of k_feature_coefficients: dc0, dlam[g], dgam[g][g'] in a fixed
@@ -567,30 +578,42 @@ __global__ __launch_bounds__(256) void k_coef_grad(const float* __restrict__ dwq
                                                    float* __restrict__ dgam, const float* __restrict__ loc = nullptr) {
   __shared__ int lab[kD];
   __shared__ float raw[64 * 64];
+  __shared__ float w[kFP];           // the head's slot gradients
+  __shared__ uint8_t mem[64][kD];    // mem[g][0..cnt[g]): dims of group g, ascending
+  __shared__ int cnt[64];
   const int h = blockIdx.x, t = threadIdx.x;
   if (t < kD) {
     int g = labels[h * kD + t];
     lab[t] = g < 0 ? 0 : (g >= G ? G - 1 : g);
   }
+  for (int i = t; i < kFP; i += blockDim.x) w[i] = dwq[(size_t)h * kFP + i];
   __syncthreads();
-  const float* w = dwq + (size_t)h * kFP;
+  for (int g = t; g < G; g += blockDim.x) {
+    int n = 0;
+    for (int d = 0; d < kD; ++d)
+      if (lab[d] == g) mem[g][n++] = (uint8_t)d;
+    cnt[g] = n;
+  }
+  __syncthreads();
   const float* lc = loc ? loc + (size_t)h * 73 : nullptr;
   if (t == 0) dc0[h] = w[0] + (lc ? lc[0] : 0.f);
+  // Both sums below visit dims in ascending order, the order of a plain scan over d / (r, c<=r).
   for (int g = t; g < G; g += blockDim.x) {
     float acc = 0.f;
-    for (int d = 0; d < kD; ++d)
-      if (lab[d] == g) acc += w[1 + d];
+    for (int i = 0; i < cnt[g]; ++i) acc += w[1 + mem[g][i]];
     dlam[(size_t)h * G + g] = acc * scale + (lc ? lc[1 + g] : 0.f);
   }
   const float s2 = scale * scale;
   for (int e = t; e < G * G; e += blockDim.x) {
     const int gr = e / G, gc = e % G;
     float acc = 0.f;
-    for (int r = 0; r < kD; ++r) {
-      if (lab[r] != gr) continue;
-      for (int c = 0; c <= r; ++c) {
-        if (lab[c] != gc) continue;
-        acc += (r == c ? 1.f : 2.f) * w[1 + kD + r * (r + 1) / 2 + c];
+    for (int i = 0; i < cnt[gr]; ++i) {
+      const int r = mem[gr][i];
+      const float* row = w + 1 + kD + r * (r + 1) / 2;
+      for (int j = 0; j < cnt[gc]; ++j) {
+        const int c = mem[gc][j];
+        if (c > r) break;
+        acc += (r == c ? 1.f : 2.f) * row[c];
       }
     }
     raw[e] = acc * s2;
@@ -817,7 +840,7 @@ int backward_impl(const Geometry& g, const void* q, const void* k, const void* v
                          static_cast<T*>(dv)};
     oal::launch_f32_backward<T>(lg, a, st, make_timer());
     if (need_coef) {
-      timed("k_dwq_reduce", st, [&] { hipLaunchKernelGGL(k_dwq_reduce, dim3((kFP + 255) / 256, g.Hq), dim3(256), 0, st, w.dwq_part, g.B, g.Hq,
+      timed("k_dwq_reduce", st, [&] { hipLaunchKernelGGL(k_dwq_reduce, dim3((kFP + 63) / 64, g.Hq), dim3(1024), 0, st, w.dwq_part, g.B, g.Hq,
                          g.NB, w.dwq); });
       timed("k_coef_grad", st, [&] { hipLaunchKernelGGL(k_coef_grad, dim3(g.Hq), dim3(256), 0, st, w.dwq, labels, groups, scale, dc0, dlam,
                          dgam, w.coefs); });
@@ -836,7 +859,7 @@ int backward_impl(const Geometry& g, const void* q, const void* k, const void* v
                        sv.carry_z, w.G, w.Gz, g.Hq, g.Hkv, g.N, g.NB, static_cast<T*>(dq), w.dwq_part); });
   }
   if (need_coef) {
-    timed("k_dwq_reduce", st, [&] { hipLaunchKernelGGL(k_dwq_reduce, dim3((kFP + 255) / 256, g.Hq), dim3(256), 0, st, w.dwq_part, g.B, g.Hq, g.NB,
+    timed("k_dwq_reduce", st, [&] { hipLaunchKernelGGL(k_dwq_reduce, dim3((kFP + 63) / 64, g.Hq), dim3(1024), 0, st, w.dwq_part, g.B, g.Hq, g.NB,
                        w.dwq); });
     timed("k_coef_grad", st, [&] { hipLaunchKernelGGL(k_coef_grad, dim3(g.Hq), dim3(256), 0, st, w.dwq, labels, groups, scale, dc0, dlam, dgam); });
   }
