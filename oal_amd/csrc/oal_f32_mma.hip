@@ -7,8 +7,9 @@
 //   k3_state_fwd   P_c = sum_{c' < c} raw(K_c')^T [V_c', 1]          (exclusive prefix)
 //   k3_intra_fwd   intra-chunk num and den (group sums on the matrix cores)
 //   k3_state_bwd   dT_c = sum_{c' > c} sum_h wq_h o raw(Q_h,c')^T [G, Gz]_h,c'
-//                  in chunk segments (k3_seg_carry / k3_add_carry add each
-//                  segment's carry) and the state part of the feature-coefficient
+//                  in chunk segments (k3_seg_carry turns the segment totals
+//                  into carries, which the dk and dv kernels add as they
+//                  stage dT) and the state part of the feature-coefficient
 //                  gradient dwq_part[b][h][c][f] = <P_c[f], raw(Q_h,c)^T [G, Gz]_h,c[f]>
 //   k3_readout     num += phi(x) . S (out: num / den), or dv = raw(K) dT + local
 //   k3_fold        dq = fold of (P [G, Gz]^T) through wq o raw(q) + local,
@@ -178,8 +179,8 @@ __global__ __launch_bounds__(256) void k3_state_fwd(const T* __restrict__ k, con
 // chunk. Per item (chunk, head): H = raw(Q)^T [G, Gz] (kept apart),
 // dT += wq_h o H; before a chunk's first item the suffix of the segment's later
 // chunks is emitted, and after the segment its total goes to segt (several
-// segments: k3_seg_carry and k3_add_carry then add each segment's carry, the
-// sum of the later segments' totals). With dwq_part the item also writes
+// segments: k3_seg_carry turns the totals into each segment's carry, the sum
+// of the later segments' totals, which the readers of dT add). With dwq_part the item also writes
 // <P_c[f], H[f]> (values of both waves and the ones column, in a fixed order).
 // ---------------------------------------------------------------------------
 template <typename T>
@@ -302,34 +303,6 @@ __global__ __launch_bounds__(256) void k3_seg_carry(float* __restrict__ segt, fl
   }
 }
 
-// dT[u][c] += carry[u][c / SL] for every chunk of every segment but the last
-// (whose carry is zero). Block (chunk, unit, part): part p of kAddParts covers
-// a contiguous 1 / kAddParts of the chunk's state, a float4 per thread and step;
-// part 0 also adds the ones column.
-constexpr int kAddParts = 8;
-__global__ __launch_bounds__(256) void k3_add_carry(float* __restrict__ dT, float* __restrict__ dTz,
-                                                    const float* __restrict__ segt, const float* __restrict__ segtz,
-                                                    int NB, int SL, int S) {
-  const int ch = blockIdx.x, u = blockIdx.y, sg = ch / SL;
-  if (sg >= S - 1) return;
-  const size_t cb = (size_t)u * NB + ch, sb = (size_t)u * S + sg;
-  constexpr int per = kFP * kD / 4 / kAddParts;
-  static_assert(per * kAddParts * 4 == kFP * kD, "parts must tile the chunk state");
-  float4* d = reinterpret_cast<float4*>(dT + cb * kFP * kD) + blockIdx.z * per;
-  const float4* cr = reinterpret_cast<const float4*>(segt + sb * kFP * kD) + blockIdx.z * per;
-  for (int i = threadIdx.x; i < per; i += 256) {
-    float4 a = d[i];
-    const float4 x = cr[i];
-    a.x += x.x;
-    a.y += x.y;
-    a.z += x.z;
-    a.w += x.w;
-    d[i] = a;
-  }
-  if (blockIdx.z == 0)
-    for (int i = threadIdx.x; i < kFP; i += 256) dTz[cb * kFP + i] += segtz[sb * kFP + i];
-}
-
 // ---------------------------------------------------------------------------
 // Slot-ordered state tiles. M-tile M holds the 32 slots 32 M .. 32 M + 31
 // (bases 16 M .. 16 M + 15): row j = the natural-order state row of slot
@@ -343,15 +316,21 @@ constexpr int kMT = kS / 32;  // 69
 // for t < 32, the ones column of row t. With wqh (a query head's feature
 // coefficients) each row is scaled by its slot's coefficient: the products
 // that read the tile are linear in it, so the weighted tile gives the
-// weighted readout or fold directly.
+// weighted readout or fold directly. With C (the backward state's segment
+// carry, row block sb) each row also adds its carry row.
 template <int NT>
 struct TileRegs {
   float4 v[512 / NT];
   float z;
 };
-template <int NT>
+struct SegCarry {
+  const float* C;   // [unit * segments + segment][kFP][kD], or null (no carry)
+  const float* Cz;  // [unit * segments + segment][kFP]
+  size_t sb;
+};
+template <int NT, bool ADD = false>
 __device__ __forceinline__ void load_tile(const float* __restrict__ S, const float* __restrict__ Sz, size_t cb, int M,
-                                          const float* __restrict__ wqh, TileRegs<NT>& tr) {
+                                          const float* __restrict__ wqh, TileRegs<NT>& tr, const SegCarry& sc = {}) {
   const int t = threadIdx.x;
 #pragma unroll
   for (int i = 0; i < 512 / NT; ++i) {
@@ -360,6 +339,12 @@ __device__ __forceinline__ void load_tile(const float* __restrict__ S, const flo
     float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
     if (nat >= 0) {
       a = *reinterpret_cast<const float4*>(S + (cb * kFP + nat) * kD + 4 * c4);
+      if constexpr (ADD) {
+        if (sc.C) {
+          const float4 c = *reinterpret_cast<const float4*>(sc.C + (sc.sb * kFP + nat) * kD + 4 * c4);
+          a = make_float4(a.x + c.x, a.y + c.y, a.z + c.z, a.w + c.w);
+        }
+      }
       if (wqh) {
         const float w = wqh[nat];
         a = make_float4(a.x * w, a.y * w, a.z * w, a.w * w);
@@ -369,7 +354,15 @@ __device__ __forceinline__ void load_tile(const float* __restrict__ S, const flo
   }
   if (t < 32) {
     const int nat = kSlot3.nat[32 * M + t];
-    tr.z = nat >= 0 ? Sz[cb * kFP + nat] * (wqh ? wqh[nat] : 1.f) : 0.f;
+    float z = 0.f;
+    if (nat >= 0) {
+      z = Sz[cb * kFP + nat];
+      if constexpr (ADD) {
+        if (sc.C) z += sc.Cz[sc.sb * kFP + nat];
+      }
+      z *= wqh ? wqh[nat] : 1.f;
+    }
+    tr.z = z;
   }
 }
 template <int NT>
@@ -381,6 +374,17 @@ __device__ __forceinline__ void store_tile(float* __restrict__ st, const TileReg
     *reinterpret_cast<float4*>(st + j * kStRow + 4 * c4) = tr.v[i];
   }
   if (t < 32) st[t * kStRow + kD] = tr.z;
+}
+
+// The carry chunk ch of unit u adds: that of its segment (segments of SL
+// chunks, nseg of them); none in the last segment or without cS.
+__device__ __forceinline__ SegCarry seg_carry(const float* cS, const float* cSz, int u, int ch, int SL, int nseg) {
+  const int sg = ch / SL;
+  SegCarry sc;
+  sc.C = (cS && sg < nseg - 1) ? cS : nullptr;
+  sc.Cz = cSz;
+  sc.sb = (size_t)u * nseg + sg;
+  return sc;
 }
 
 
@@ -413,17 +417,17 @@ template <int M, int MODE>
 __device__ __forceinline__ void readout_tiles(const float (&x)[kD], float* st0, float* st1,
                                               const float* __restrict__ S, const float* __restrict__ Sz, size_t cb,
                                               const float* wqh, int m, int s, int row, TileRegs<256>& tr,
-                                              f32x16& acc, float& zacc) {
+                                              f32x16& acc, float& zacc, const SegCarry& sc) {
   const float* st = (M & 1) ? st1 : st0;
   [&]<int... J>(std::integer_sequence<int, J...>) {
     (readout_base<16 * M + J, MODE>(x, st, m, s, row, acc, zacc), ...);
   }(std::make_integer_sequence<int, 16>{});
   if constexpr (M + 1 < kMT) {
     store_tile<256>((M & 1) ? st0 : st1, tr);
-    if constexpr (M + 2 < kMT) load_tile<256>(S, Sz, cb, M + 2, wqh, tr);
+    if constexpr (M + 2 < kMT) load_tile<256, MODE == 1>(S, Sz, cb, M + 2, wqh, tr, sc);
     __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
-    readout_tiles<M + 1, MODE>(x, st0, st1, S, Sz, cb, wqh, m, s, row, tr, acc, zacc);
+    readout_tiles<M + 1, MODE>(x, st0, st1, S, Sz, cb, wqh, m, s, row, tr, acc, zacc, sc);
   }
 }
 
@@ -432,7 +436,9 @@ __global__ __launch_bounds__(256, 2) void k3_readout(const T* __restrict__ x_in,
                                                      const float* __restrict__ S, const float* __restrict__ Sz, int Hq,
                                                      int Hkv, int N, int NB, float floor, float* __restrict__ num,
                                                      float* __restrict__ den, T* __restrict__ out,
-                                                     const float* __restrict__ dvl, T* __restrict__ dv) {
+                                                     const float* __restrict__ dvl, T* __restrict__ dv,
+                                                     const float* __restrict__ cS, const float* __restrict__ cSz,
+                                                     int SL, int nseg) {
   __shared__ __attribute__((aligned(16))) float st0[32 * kStRow], st1[32 * kStRow];
   __shared__ float zd[kC];
   int hh = 0, ch, u;
@@ -455,14 +461,15 @@ __global__ __launch_bounds__(256, 2) void k3_readout(const T* __restrict__ x_in,
   const bool ok = tok < N;
   float x[kD];
   load_rotated_f32(x_in, xbase + (size_t)(ok ? tok : N - 1) * kD, ok, s, x);
+  const SegCarry sc = seg_carry(cS, cSz, u, ch, SL, nseg);
   TileRegs<256> tr;
-  load_tile<256>(S, Sz, cb, 0, wqh, tr);
+  load_tile<256, MODE == 1>(S, Sz, cb, 0, wqh, tr, sc);
   store_tile<256>(st0, tr);
-  load_tile<256>(S, Sz, cb, 1, wqh, tr);
+  load_tile<256, MODE == 1>(S, Sz, cb, 1, wqh, tr, sc);
   __syncthreads();
   f32x16 acc = f32x16{};
   float zacc = 0.f;
-  readout_tiles<0, MODE>(x, st0, st1, S, Sz, cb, wqh, m, s, row, tr, acc, zacc);
+  readout_tiles<0, MODE>(x, st0, st1, S, Sz, cb, wqh, m, s, row, tr, acc, zacc, sc);
 
   if constexpr (MODE == 0) {
     const size_t dbase = (size_t)(b * Hq + h) * N;
@@ -540,19 +547,19 @@ __device__ __forceinline__ void fold_tile_f32(const float (&x)[kD], float (&dx)[
   fold::fold_tile<M>(D, x, dx, w16);
 }
 
-template <int M>
+template <int M, bool ADD>
 __device__ __forceinline__ void fold_tiles(const float (&x)[kD], float (&dx)[kD], const float (&yv)[32], float yz,
                                            float* st0, float* st1, const float* __restrict__ S,
                                            const float* __restrict__ Sz, size_t cb, const float* wqh, int s, int row,
-                                           TileRegs<128>& tr) {
+                                           TileRegs<128>& tr, const SegCarry& sc) {
   pin64(dx);
   fold_tile_f32<M>(x, dx, yv, yz, (M & 1) ? st1 : st0, s, row);
   if constexpr (M + 1 < kMT) {
     store_tile<128>((M & 1) ? st0 : st1, tr);
-    if constexpr (M + 2 < kMT) load_tile<128>(S, Sz, cb, M + 2, wqh, tr);
+    if constexpr (M + 2 < kMT) load_tile<128, ADD>(S, Sz, cb, M + 2, wqh, tr, sc);
     __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
-    fold_tiles<M + 1>(x, dx, yv, yz, st0, st1, S, Sz, cb, wqh, s, row, tr);
+    fold_tiles<M + 1, ADD>(x, dx, yv, yz, st0, st1, S, Sz, cb, wqh, s, row, tr, sc);
   }
 }
 
@@ -561,7 +568,9 @@ __global__ __launch_bounds__(128, 2) void k3_fold(const T* __restrict__ x_in, co
                                                   const T* __restrict__ v_in, const float* __restrict__ yz_in,
                                                   const float* __restrict__ wq, const float* __restrict__ S,
                                                   const float* __restrict__ Sz, const float* __restrict__ local,
-                                                  int Hq, int Hkv, int N, int NB, T* __restrict__ dx_out) {
+                                                  int Hq, int Hkv, int N, int NB, T* __restrict__ dx_out,
+                                                  const float* __restrict__ cS, const float* __restrict__ cSz, int SL,
+                                                  int nseg) {
   __shared__ __attribute__((aligned(16))) float st0[32 * kStRow], st1[32 * kStRow];
   int hh = 0, ch, u;
   if constexpr (MODE == 0) {
@@ -608,12 +617,13 @@ __global__ __launch_bounds__(128, 2) void k3_fold(const T* __restrict__ x_in, co
   }
 #pragma unroll
   for (int i = 0; i < kD; ++i) dx[i] = 0.f;
+  const SegCarry sc = seg_carry(cS, cSz, u, ch, SL, nseg);
   TileRegs<128> tr;
-  load_tile<128>(S, Sz, cb, 0, wqh, tr);
+  load_tile<128, MODE == 1>(S, Sz, cb, 0, wqh, tr, sc);
   store_tile<128>(st0, tr);
-  load_tile<128>(S, Sz, cb, 1, wqh, tr);
+  load_tile<128, MODE == 1>(S, Sz, cb, 1, wqh, tr, sc);
   __syncthreads();
-  fold_tiles<0>(x, dx, yv, yz, st0, st1, S, Sz, cb, wqh, s, row, tr);
+  fold_tiles<0, MODE == 1>(x, dx, yv, yz, st0, st1, S, Sz, cb, wqh, s, row, tr, sc);
   float full[32];
   fold::combine_rotation_groups(dx, s, full);
   if (ok) {
@@ -1123,7 +1133,7 @@ void launch_f32_readout_fwd(const LaunchGeom& g, const T* q, const float* wq, co
                             float floor, float* num, float* den, T* out, hipStream_t st, const Timer& timed) {
   timed("k3_readout", st, [&] {
     hipLaunchKernelGGL((k3_readout<T, 0>), dim3(g.R * g.NB * g.U), dim3(256), 0, st, q, wq, carry, carry_z, g.Hq,
-                       g.Hkv, g.N, g.NB, floor, num, den, out, nullptr, nullptr);
+                       g.Hkv, g.N, g.NB, floor, num, den, out, nullptr, nullptr, nullptr, nullptr, 1, 1);
   });
 }
 
@@ -1131,21 +1141,22 @@ template <typename T>
 void launch_f32_backward(const LaunchGeom& g, const F32BwdArgs<T>& a, hipStream_t st, const Timer& timed) {
   // the scan also forms the state coefficient partials (its per-item products)
   if (a.dk || a.dv || a.dwq_part) {
-    const int S = a.plan.S, SL = a.plan.SL;
     timed("k3_state_bwd", st, [&] {
-      hipLaunchKernelGGL(k3_state_bwd<T>, dim3(kFP / 64, g.U, S), dim3(256), 0, st, a.q, a.G, a.Gz, a.wq, a.P, a.Pz,
-                         g.Hq, g.Hkv, g.N, g.NB, SL, a.dT, a.dTz, a.segt, a.segtz, a.dwq_part);
+      hipLaunchKernelGGL(k3_state_bwd<T>, dim3(kFP / 64, g.U, a.plan.S), dim3(256), 0, st, a.q, a.G, a.Gz, a.wq, a.P, a.Pz,
+                         g.Hq, g.Hkv, g.N, g.NB, a.plan.SL, a.dT, a.dTz, a.segt, a.segtz, a.dwq_part);
     });
-    if (S > 1 && (a.dk || a.dv)) {
-      timed("k3_state_bwd_carry", st, [&] {
+    if (a.plan.S > 1 && (a.dk || a.dv)) {
+      timed("k3_seg_carry", st, [&] {
         const size_t n = (size_t)g.U * kFP * (kD + 1);
         hipLaunchKernelGGL(k3_seg_carry, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a.segt, a.segtz, g.U,
-                           S);
-        hipLaunchKernelGGL(k3_add_carry, dim3(g.NB, g.U, kAddParts), dim3(256), 0, st, a.dT, a.dTz, a.segt, a.segtz, g.NB,
-                           SL, S);
+                           a.plan.S);
       });
     }
   }
+  // dT holds each segment's own suffix; the dk and dv kernels add the segment
+  // carries (the later segments' totals) as they stage the state
+  const float* cS = a.plan.S > 1 ? a.segt : nullptr;
+  const float* cSz = a.plan.S > 1 ? a.segtz : nullptr;
   timed("k3_local", st, [&] {
     hipLaunchKernelGGL(k3_local<T>, dim3(g.R * g.NB * g.U), dim3(192), 0, st, a.q, a.k, a.v, a.G, a.Gz, a.labels,
                        a.c0, a.lam, a.gam, a.groups, g.Hq, g.Hkv, g.N, g.NB, a.scale, a.dql, a.dkl, a.dvl, a.coefl);
@@ -1153,19 +1164,19 @@ void launch_f32_backward(const LaunchGeom& g, const F32BwdArgs<T>& a, hipStream_
   if (a.dq) {
     timed("k3_fold_q", st, [&] {
       hipLaunchKernelGGL((k3_fold<T, 0>), dim3(g.R * g.NB * g.U), dim3(128), 0, st, a.q, a.G, nullptr, a.Gz, a.wq,
-                         a.P, a.Pz, a.dql, g.Hq, g.Hkv, g.N, g.NB, a.dq);
+                         a.P, a.Pz, a.dql, g.Hq, g.Hkv, g.N, g.NB, a.dq, nullptr, nullptr, 1, 1);
     });
   }
   if (a.dk) {
     timed("k3_fold_k", st, [&] {
       hipLaunchKernelGGL((k3_fold<T, 1>), dim3(g.NB * g.U), dim3(128), 0, st, a.k, nullptr, a.v, nullptr, nullptr,
-                         a.dT, a.dTz, a.dkl, g.Hq, g.Hkv, g.N, g.NB, a.dk);
+                         a.dT, a.dTz, a.dkl, g.Hq, g.Hkv, g.N, g.NB, a.dk, cS, cSz, a.plan.SL, a.plan.S);
     });
   }
   if (a.dv) {
     timed("k3_readout_v", st, [&] {
       hipLaunchKernelGGL((k3_readout<T, 1>), dim3(g.NB * g.U), dim3(256), 0, st, a.k, nullptr, a.dT, a.dTz, g.Hq,
-                         g.Hkv, g.N, g.NB, 0.f, nullptr, nullptr, nullptr, a.dvl, a.dv);
+                         g.Hkv, g.N, g.NB, 0.f, nullptr, nullptr, nullptr, a.dvl, a.dv, cS, cSz, a.plan.SL, a.plan.S);
     });
   }
   if (a.coefl) {
