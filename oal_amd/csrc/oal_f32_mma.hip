@@ -151,14 +151,14 @@ __global__ __launch_bounds__(256) void k3_state_fwd(const T* __restrict__ k, con
     store_state_row(carry + (cb * kFP + f) * kD, m, s, acc);
     const float zt = accz + partner(accz);
     if (m == 0 && s == 0) carry_z[cb * kFP + f] = zt;
-    __syncthreads();
+    lds_sync();
     store_chunk_rows(kx, kr);
     store_chunk_rows(vx, vr);
     if ((tid & 3) == 0) {
       kx[tid >> 2][kD] = ch * kC + (tid >> 2) < N ? 1.f : 0.f;
       kx[tid >> 2][kD + 1] = 0.f;
     }
-    __syncthreads();
+    lds_sync();
     if (ch + 1 < NB) {
       load_chunk_rows(k, base, (ch + 1) * kC, N, kr);
       load_chunk_rows(v, base, (ch + 1) * kC, N, vr);
@@ -235,7 +235,7 @@ __global__ __launch_bounds__(256) void k3_state_bwd(const T* __restrict__ q, con
       }
     }
     const float w = wq[(size_t)h * kFP + f];
-    __syncthreads();
+    lds_sync();
     store_chunk_rows(qx, qr);
     store_chunk_rows(gs, gr);
     if ((tid & 3) == 0) {
@@ -243,7 +243,7 @@ __global__ __launch_bounds__(256) void k3_state_bwd(const T* __restrict__ q, con
       qx[tid >> 2][kD + 1] = 0.f;
       gs[tid >> 2][kD] = gzr;
     }
-    __syncthreads();
+    lds_sync();
     if (it + 1 < NI) load_item(it + 1);
     f32x16 hT = f32x16{};
     float hz = 0.f;
@@ -265,7 +265,7 @@ __global__ __launch_bounds__(256) void k3_state_bwd(const T* __restrict__ q, con
       p += partner(p);
       const float hzt = hz + partner(hz);
       if (m == 1 && s == 0) xch[ft][row] = p;
-      __syncthreads();
+      lds_sync();
       if (m == 0 && s == 0) dwq_part[((size_t)(b * Hq + h) * NB + ch) * kFP + f] = p + xch[ft][row] + pz * hzt;
     }
   }
@@ -316,74 +316,71 @@ constexpr int kMT = kS / 32;  // 69
 // for t < 32, the ones column of row t. With wqh (a query head's feature
 // coefficients) each row is scaled by its slot's coefficient: the products
 // that read the tile are linear in it, so the weighted tile gives the
-// weighted readout or fold directly. With C (the backward state's segment
-// carry, row block sb) each row also adds its carry row.
+// weighted readout or fold directly. With ADD each row also adds its row of
+// the backward state's segment carry (row block sb). load_tile only
+// issues the loads; store_tile, a tile later, forms (row + carry) * weight and
+// writes LDS, so the loads stay in flight over a whole tile of products.
 template <int NT>
 struct TileRegs {
   float4 v[512 / NT];
-  float z;
+  float4 c[512 / NT];  // carry rows (ADD)
+  float w[512 / NT];   // slot weights (W)
+  float z, zc, zw;
 };
 struct SegCarry {
-  const float* C;   // [unit * segments + segment][kFP][kD], or null (no carry)
+  const float* C;   // [unit * segments + segment][kFP][kD] (read only with ADD)
   const float* Cz;  // [unit * segments + segment][kFP]
   size_t sb;
 };
-template <int NT, bool ADD = false>
+// natl: the slot table's natural indices staged in LDS (a lane-indexed read of
+// the constant table is a global load, and each one's wait would also wait for
+// every state load issued before it). Every load is issued unconditionally: an
+// invalid slot reads feature row kFeat, a padding row, which every state, carry
+// and coefficient buffer holds as zero, so the loads stay whole 16-byte loads
+// with no branches between them.
+template <int NT, bool ADD, bool W>
 __device__ __forceinline__ void load_tile(const float* __restrict__ S, const float* __restrict__ Sz, size_t cb, int M,
-                                          const float* __restrict__ wqh, TileRegs<NT>& tr, const SegCarry& sc = {}) {
+                                          const float* __restrict__ wqh, const int16_t* natl, TileRegs<NT>& tr,
+                                          const SegCarry& sc) {
   const int t = threadIdx.x;
 #pragma unroll
   for (int i = 0; i < 512 / NT; ++i) {
     const int idx = t + NT * i, j = idx >> 4, c4 = idx & 15;
-    const int nat = kSlot3.nat[32 * M + j];
-    float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (nat >= 0) {
-      a = *reinterpret_cast<const float4*>(S + (cb * kFP + nat) * kD + 4 * c4);
-      if constexpr (ADD) {
-        if (sc.C) {
-          const float4 c = *reinterpret_cast<const float4*>(sc.C + (sc.sb * kFP + nat) * kD + 4 * c4);
-          a = make_float4(a.x + c.x, a.y + c.y, a.z + c.z, a.w + c.w);
-        }
-      }
-      if (wqh) {
-        const float w = wqh[nat];
-        a = make_float4(a.x * w, a.y * w, a.z * w, a.w * w);
-      }
-    }
-    tr.v[i] = a;
+    const int nat = natl[32 * M + j], natc = nat >= 0 ? nat : kFeat;
+    tr.v[i] = *reinterpret_cast<const float4*>(S + (cb * kFP + natc) * kD + 4 * c4);
+    if constexpr (ADD) tr.c[i] = *reinterpret_cast<const float4*>(sc.C + (sc.sb * kFP + natc) * kD + 4 * c4);
+    if constexpr (W) tr.w[i] = wqh[natc];
   }
-  if (t < 32) {
-    const int nat = kSlot3.nat[32 * M + t];
-    float z = 0.f;
-    if (nat >= 0) {
-      z = Sz[cb * kFP + nat];
-      if constexpr (ADD) {
-        if (sc.C) z += sc.Cz[sc.sb * kFP + nat];
-      }
-      z *= wqh ? wqh[nat] : 1.f;
-    }
-    tr.z = z;
-  }
+  // every thread loads the ones column of row t % 32 (threads t < 32 store it)
+  const int nat = natl[32 * M + (t & 31)], natc = nat >= 0 ? nat : kFeat;
+  tr.z = Sz[cb * kFP + natc];
+  if constexpr (ADD) tr.zc = sc.Cz[sc.sb * kFP + natc];
+  if constexpr (W) tr.zw = wqh[natc];
 }
-template <int NT>
+template <int NT, bool ADD, bool W>
 __device__ __forceinline__ void store_tile(float* __restrict__ st, const TileRegs<NT>& tr) {
   const int t = threadIdx.x;
 #pragma unroll
   for (int i = 0; i < 512 / NT; ++i) {
     const int idx = t + NT * i, j = idx >> 4, c4 = idx & 15;
-    *reinterpret_cast<float4*>(st + j * kStRow + 4 * c4) = tr.v[i];
+    float4 a = tr.v[i];
+    if constexpr (ADD) a = make_float4(a.x + tr.c[i].x, a.y + tr.c[i].y, a.z + tr.c[i].z, a.w + tr.c[i].w);
+    if constexpr (W) a = make_float4(a.x * tr.w[i], a.y * tr.w[i], a.z * tr.w[i], a.w * tr.w[i]);
+    *reinterpret_cast<float4*>(st + j * kStRow + 4 * c4) = a;
   }
-  if (t < 32) st[t * kStRow + kD] = tr.z;
+  float z = tr.z;
+  if constexpr (ADD) z += tr.zc;
+  if constexpr (W) z *= tr.zw;
+  if (t < 32) st[t * kStRow + kD] = z;
 }
 
 // The carry chunk ch of unit u adds: that of its segment (segments of SL
-// chunks, nseg of them); none in the last segment or without cS.
+// chunks, nseg of them; the last segment's carry is zero).
 __device__ __forceinline__ SegCarry seg_carry(const float* cS, const float* cSz, int u, int ch, int SL, int nseg) {
-  const int sg = ch / SL;
   SegCarry sc;
-  sc.C = (cS && sg < nseg - 1) ? cS : nullptr;
+  sc.C = cS;
   sc.Cz = cSz;
-  sc.sb = (size_t)u * nseg + sg;
+  sc.sb = (size_t)u * nseg + ch / SL;
   return sc;
 }
 
@@ -413,25 +410,25 @@ __device__ __forceinline__ void readout_base(const float (&x)[kD], const float* 
   }
 }
 
-template <int M, int MODE>
+template <int M, int MODE, bool ADD>
 __device__ __forceinline__ void readout_tiles(const float (&x)[kD], float* st0, float* st1,
                                               const float* __restrict__ S, const float* __restrict__ Sz, size_t cb,
                                               const float* wqh, int m, int s, int row, TileRegs<256>& tr,
-                                              f32x16& acc, float& zacc, const SegCarry& sc) {
+                                              f32x16& acc, float& zacc, const int16_t* natl, const SegCarry& sc) {
   const float* st = (M & 1) ? st1 : st0;
   [&]<int... J>(std::integer_sequence<int, J...>) {
     (readout_base<16 * M + J, MODE>(x, st, m, s, row, acc, zacc), ...);
   }(std::make_integer_sequence<int, 16>{});
   if constexpr (M + 1 < kMT) {
-    store_tile<256>((M & 1) ? st0 : st1, tr);
-    if constexpr (M + 2 < kMT) load_tile<256, MODE == 1>(S, Sz, cb, M + 2, wqh, tr, sc);
-    __syncthreads();
+    store_tile<256, ADD, MODE == 0>((M & 1) ? st0 : st1, tr);
+    if constexpr (M + 2 < kMT) load_tile<256, ADD, MODE == 0>(S, Sz, cb, M + 2, wqh, natl, tr, sc);
+    lds_sync();
     __builtin_amdgcn_sched_barrier(0);
-    readout_tiles<M + 1, MODE>(x, st0, st1, S, Sz, cb, wqh, m, s, row, tr, acc, zacc, sc);
+    readout_tiles<M + 1, MODE, ADD>(x, st0, st1, S, Sz, cb, wqh, m, s, row, tr, acc, zacc, natl, sc);
   }
 }
 
-template <typename T, int MODE>
+template <typename T, int MODE, bool CARRY = false>
 __global__ __launch_bounds__(256, 2) void k3_readout(const T* __restrict__ x_in, const float* __restrict__ wq,
                                                      const float* __restrict__ S, const float* __restrict__ Sz, int Hq,
                                                      int Hkv, int N, int NB, float floor, float* __restrict__ num,
@@ -441,6 +438,7 @@ __global__ __launch_bounds__(256, 2) void k3_readout(const T* __restrict__ x_in,
                                                      int SL, int nseg) {
   __shared__ __attribute__((aligned(16))) float st0[32 * kStRow], st1[32 * kStRow];
   __shared__ float zd[kC];
+  __shared__ int16_t natl[kS];
   int hh = 0, ch, u;
   if constexpr (MODE == 0) {
     head_chunk_unit(Hq / Hkv, NB, (int)(gridDim.x / ((Hq / Hkv) * NB)), hh, ch, u);
@@ -462,14 +460,16 @@ __global__ __launch_bounds__(256, 2) void k3_readout(const T* __restrict__ x_in,
   float x[kD];
   load_rotated_f32(x_in, xbase + (size_t)(ok ? tok : N - 1) * kD, ok, s, x);
   const SegCarry sc = seg_carry(cS, cSz, u, ch, SL, nseg);
+  for (int i = tid; i < kS; i += 256) natl[i] = kSlot3.nat[i];
+  __syncthreads();
   TileRegs<256> tr;
-  load_tile<256, MODE == 1>(S, Sz, cb, 0, wqh, tr, sc);
-  store_tile<256>(st0, tr);
-  load_tile<256, MODE == 1>(S, Sz, cb, 1, wqh, tr, sc);
+  load_tile<256, CARRY, MODE == 0>(S, Sz, cb, 0, wqh, natl, tr, sc);
+  store_tile<256, CARRY, MODE == 0>(st0, tr);
+  load_tile<256, CARRY, MODE == 0>(S, Sz, cb, 1, wqh, natl, tr, sc);
   __syncthreads();
   f32x16 acc = f32x16{};
   float zacc = 0.f;
-  readout_tiles<0, MODE>(x, st0, st1, S, Sz, cb, wqh, m, s, row, tr, acc, zacc, sc);
+  readout_tiles<0, MODE, CARRY>(x, st0, st1, S, Sz, cb, wqh, m, s, row, tr, acc, zacc, natl, sc);
 
   if constexpr (MODE == 0) {
     const size_t dbase = (size_t)(b * Hq + h) * N;
@@ -477,7 +477,7 @@ __global__ __launch_bounds__(256, 2) void k3_readout(const T* __restrict__ x_in,
       const float z = zacc + partner(zacc);
       if (s == 0) zd[32 * n + row] = (ok ? den[dbase + tok] : 0.f) + z;
     }
-    __syncthreads();
+    lds_sync();
     if (ok) {
       const float dd = zd[32 * n + row];
       if (m == 0 && s == 0) den[dbase + tok] = dd;
@@ -547,23 +547,23 @@ __device__ __forceinline__ void fold_tile_f32(const float (&x)[kD], float (&dx)[
   fold::fold_tile<M>(D, x, dx, w16);
 }
 
-template <int M, bool ADD>
+template <int M, bool ADD, bool W>
 __device__ __forceinline__ void fold_tiles(const float (&x)[kD], float (&dx)[kD], const float (&yv)[32], float yz,
                                            float* st0, float* st1, const float* __restrict__ S,
                                            const float* __restrict__ Sz, size_t cb, const float* wqh, int s, int row,
-                                           TileRegs<128>& tr, const SegCarry& sc) {
+                                           TileRegs<128>& tr, const int16_t* natl, const SegCarry& sc) {
   pin64(dx);
   fold_tile_f32<M>(x, dx, yv, yz, (M & 1) ? st1 : st0, s, row);
   if constexpr (M + 1 < kMT) {
-    store_tile<128>((M & 1) ? st0 : st1, tr);
-    if constexpr (M + 2 < kMT) load_tile<128, ADD>(S, Sz, cb, M + 2, wqh, tr, sc);
-    __syncthreads();
+    store_tile<128, ADD, W>((M & 1) ? st0 : st1, tr);
+    if constexpr (M + 2 < kMT) load_tile<128, ADD, W>(S, Sz, cb, M + 2, wqh, natl, tr, sc);
+    lds_sync();
     __builtin_amdgcn_sched_barrier(0);
-    fold_tiles<M + 1, ADD>(x, dx, yv, yz, st0, st1, S, Sz, cb, wqh, s, row, tr, sc);
+    fold_tiles<M + 1, ADD, W>(x, dx, yv, yz, st0, st1, S, Sz, cb, wqh, s, row, tr, natl, sc);
   }
 }
 
-template <typename T, int MODE>
+template <typename T, int MODE, bool CARRY = false>
 __global__ __launch_bounds__(128, 2) void k3_fold(const T* __restrict__ x_in, const float* __restrict__ y_in,
                                                   const T* __restrict__ v_in, const float* __restrict__ yz_in,
                                                   const float* __restrict__ wq, const float* __restrict__ S,
@@ -572,6 +572,7 @@ __global__ __launch_bounds__(128, 2) void k3_fold(const T* __restrict__ x_in, co
                                                   const float* __restrict__ cS, const float* __restrict__ cSz, int SL,
                                                   int nseg) {
   __shared__ __attribute__((aligned(16))) float st0[32 * kStRow], st1[32 * kStRow];
+  __shared__ int16_t natl[kS];
   int hh = 0, ch, u;
   if constexpr (MODE == 0) {
     head_chunk_unit(Hq / Hkv, NB, (int)(gridDim.x / ((Hq / Hkv) * NB)), hh, ch, u);
@@ -618,12 +619,14 @@ __global__ __launch_bounds__(128, 2) void k3_fold(const T* __restrict__ x_in, co
 #pragma unroll
   for (int i = 0; i < kD; ++i) dx[i] = 0.f;
   const SegCarry sc = seg_carry(cS, cSz, u, ch, SL, nseg);
-  TileRegs<128> tr;
-  load_tile<128, MODE == 1>(S, Sz, cb, 0, wqh, tr, sc);
-  store_tile<128>(st0, tr);
-  load_tile<128, MODE == 1>(S, Sz, cb, 1, wqh, tr, sc);
+  for (int i = tid; i < kS; i += 128) natl[i] = kSlot3.nat[i];
   __syncthreads();
-  fold_tiles<0, MODE == 1>(x, dx, yv, yz, st0, st1, S, Sz, cb, wqh, s, row, tr, sc);
+  TileRegs<128> tr;
+  load_tile<128, CARRY, MODE == 0>(S, Sz, cb, 0, wqh, natl, tr, sc);
+  store_tile<128, CARRY, MODE == 0>(st0, tr);
+  load_tile<128, CARRY, MODE == 0>(S, Sz, cb, 1, wqh, natl, tr, sc);
+  __syncthreads();
+  fold_tiles<0, CARRY, MODE == 0>(x, dx, yv, yz, st0, st1, S, Sz, cb, wqh, s, row, tr, natl, sc);
   float full[32];
   fold::combine_rotation_groups(dx, s, full);
   if (ok) {
@@ -1169,13 +1172,15 @@ void launch_f32_backward(const LaunchGeom& g, const F32BwdArgs<T>& a, hipStream_
   }
   if (a.dk) {
     timed("k3_fold_k", st, [&] {
-      hipLaunchKernelGGL((k3_fold<T, 1>), dim3(g.NB * g.U), dim3(128), 0, st, a.k, nullptr, a.v, nullptr, nullptr,
+      auto* kern = cS ? k3_fold<T, 1, true> : k3_fold<T, 1, false>;
+      hipLaunchKernelGGL(kern, dim3(g.NB * g.U), dim3(128), 0, st, a.k, nullptr, a.v, nullptr, nullptr,
                          a.dT, a.dTz, a.dkl, g.Hq, g.Hkv, g.N, g.NB, a.dk, cS, cSz, a.plan.SL, a.plan.S);
     });
   }
   if (a.dv) {
     timed("k3_readout_v", st, [&] {
-      hipLaunchKernelGGL((k3_readout<T, 1>), dim3(g.NB * g.U), dim3(256), 0, st, a.k, nullptr, a.dT, a.dTz, g.Hq,
+      auto* kern = cS ? k3_readout<T, 1, true> : k3_readout<T, 1, false>;
+      hipLaunchKernelGGL(kern, dim3(g.NB * g.U), dim3(256), 0, st, a.k, nullptr, a.dT, a.dTz, g.Hq,
                          g.Hkv, g.N, g.NB, 0.f, nullptr, nullptr, nullptr, a.dvl, a.dv, cS, cSz, a.plan.SL, a.plan.S);
     });
   }
