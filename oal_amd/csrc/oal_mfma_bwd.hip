@@ -415,15 +415,23 @@ __global__ __launch_bounds__(128, 2) void k2_kv_fold(const T* __restrict__ k, co
     du_issue<UPG, CARRY, 1>(dTT + cbase, csrc, ring, tid);
     du_issue<UPG, CARRY, 2>(dTT + cbase, csrc, ring, tid);
     du_group<0, UPG, CARRY>(x, ring, dTT + cbase, csrc, tid, l, acc);
+    // the local parts are loaded together (rows clamped into range), then
+    // stored for the rows below N: a load inside the row test would wait for
+    // each one in turn
+    float lv[2][16];
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int tj = min(tok0 + 32 * wv + c32_row(i, l), N - 1);
+        lv[nt][i] = dvl[kbase + (size_t)tj * kD + 32 * nt + row];
+      }
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int tj = tok0 + 32 * wv + c32_row(i, l);
-        if (tj < N) {
-          const size_t o = kbase + (size_t)tj * kD + 32 * nt + row;
-          dv[o] = from_f<T>(acc[nt][i] + dvl[o]);
-        }
+        if (tj < N) dv[kbase + (size_t)tj * kD + 32 * nt + row] = from_f<T>(acc[nt][i] + lv[nt][i]);
       }
     return;
   }

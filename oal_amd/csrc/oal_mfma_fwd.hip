@@ -573,11 +573,16 @@ __global__ __launch_bounds__(128, 2) void k2_out_fwd(const T* __restrict__ q, co
   readout_group<0>(x, wl, ring, pt, tid, l, acc);
 
   const size_t dbase = (size_t)(b * Hq + h) * N;
+  // the row denominators are loaded together (rows clamped into range): a load
+  // inside the row test would wait for each one in turn
+  float dv16[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) dv16[i] = den[dbase + min(tok0 + 32 * wv + c32_row(i, l), N - 1)];
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int tok = tok0 + 32 * wv + c32_row(i, l);
     if (tok < N) {
-      const float dd = den[dbase + tok];
+      const float dd = dv16[i];
       const float inv = 1.f / (floor > 0.f ? fmaxf(dd, floor) : dd);
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt) {
@@ -706,11 +711,16 @@ __global__ __launch_bounds__(64 * (kMaxRS + 1), 1) void k2_out_fwd_shared(
   readout_group_shared<0>(x, wlh, ring, l, acc);
 
   const size_t dbase = (size_t)(b * Hq + h) * N;
+  // the row denominators are loaded together (rows clamped into range): a load
+  // inside the row test would wait for each one in turn
+  float dv16[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) dv16[i] = den[dbase + min(tok0 + c32_row(i, l), N - 1)];
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int tok = tok0 + c32_row(i, l);
     if (tok < N) {
-      const float dd = den[dbase + tok];
+      const float dd = dv16[i];
       const float inv = 1.f / (floor > 0.f ? fmaxf(dd, floor) : dd);
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt) {
