@@ -832,8 +832,8 @@ __global__ __launch_bounds__(192) void k3_intra_fwd(const T* __restrict__ q, con
   }
 }
 
-template <typename T>
-__global__ __launch_bounds__(192) void k3_local(const T* __restrict__ q, const T* __restrict__ k,
+template <typename T, int PART>
+__global__ __launch_bounds__(192, PART == 0 ? 2 : 1) void k3_local(const T* __restrict__ q, const T* __restrict__ k,
                                                 const T* __restrict__ v, const float* __restrict__ G,
                                                 const float* __restrict__ Gz, const int32_t* __restrict__ labels,
                                                 const float* __restrict__ c0, const float* __restrict__ lam,
@@ -845,9 +845,10 @@ __global__ __launch_bounds__(192) void k3_local(const T* __restrict__ q, const T
   __shared__ __attribute__((aligned(16))) float kx[kC][kLRow];
   __shared__ __attribute__((aligned(16))) float vx[kC][kLRow];
   __shared__ __attribute__((aligned(16))) float gs[kC][kLRow];
-  __shared__ __attribute__((aligned(16))) float xb[2][kD][33];  // tile (1,0)'s partial outputs
+  // tile (1,0)'s partial outputs: dq (PART 0), dk and dv (PART 1)
+  __shared__ __attribute__((aligned(16))) float xb[PART == 0 ? 1 : 2][kD][33];
   __shared__ float gz[kC];
-  __shared__ float cred[3][45];
+  __shared__ float cred[PART == 1 ? 3 : 1][45];
   __shared__ HeadGroups<8> hg;
   int hh, ch, u;
   head_chunk_unit(Hq / Hkv, NB, (int)(gridDim.x / ((Hq / Hkv) * NB)), hh, ch, u);
@@ -874,15 +875,16 @@ __global__ __launch_bounds__(192) void k3_local(const T* __restrict__ q, const T
   }
   if (tid < kC) gz[tid] = tok0 + tid < N ? Gz[(size_t)(b * Hq + h) * N + tok0 + tid] : 0.f;
   load_head_groups(hg, labels, c0, lam, gam, Gn, h);  // synchronizes the block
-  // the head's coefficients, wave-uniform
+  // the head's coefficients, wave-uniform (scalar registers)
+  auto uni = [](float x) { return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(x))); };
   float lm[8], gm[8][8];
 #pragma unroll
   for (int g = 0; g < 8; ++g) {
-    lm[g] = g < Gn ? hg.lam[g] : 0.f;
+    lm[g] = uni(g < Gn ? hg.lam[g] : 0.f);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) gm[g][e] = (g < Gn && e < Gn) ? hg.gam[g * Gn + e] : 0.f;
+    for (int e = 0; e < 8; ++e) gm[g][e] = uni((g < Gn && e < Gn) ? hg.gam[g * Gn + e] : 0.f);
   }
-  const float cz = hg.c0;
+  const float cz = uni(hg.c0);
   // elementwise step on one entry: s (8 group sums) -> X_g (in place) and kappa
   auto entry = [&](float (&sv)[8], float ds, bool valid, float& kap) {
     float tg[8];
@@ -903,8 +905,8 @@ __global__ __launch_bounds__(192) void k3_local(const T* __restrict__ q, const T
   };
 
   f32x16 S[8];
-  // ---- orientation C[j][i] (lane column = query i): dq ----
-  {
+  // ---- PART 0, orientation C[j][i] (lane column = query i): dq ----
+  if constexpr (PART == 0) {
     const int jr = 32 * jt + row, ic = 32 * it + row;
     group_sums_mfma(kx, qx, jr, ic, hg.perm, hg.gstart, Gn, s, scale, S);
     f32x16 dsT = dot_rows_mfma(vx, gs, jr, ic, s);  // sum_e v_j[e] g_i[e]
@@ -965,8 +967,8 @@ __global__ __launch_bounds__(192) void k3_local(const T* __restrict__ q, const T
     }
     __syncthreads();
   }
-  // ---- orientation C[i][j] (lane column = key j): dk, dv, coefficient partials ----
-  {
+  // ---- PART 1, orientation C[i][j] (lane column = key j): dk, dv, coefficient partials ----
+  if constexpr (PART == 1) {
     const int ir = 32 * it + row, jc = 32 * jt + row;
     group_sums_mfma(qx, kx, ir, jc, hg.perm, hg.gstart, Gn, s, scale, S);
     f32x16 ds = dot_rows_mfma(gs, vx, ir, jc, s);  // sum_e g_i[e] v_j[e]
@@ -1160,9 +1162,17 @@ void launch_f32_backward(const LaunchGeom& g, const F32BwdArgs<T>& a, hipStream_
   // carries (the later segments' totals) as they stage the state
   const float* cS = a.plan.S > 1 ? a.segt : nullptr;
   const float* cSz = a.plan.S > 1 ? a.segtz : nullptr;
-  timed("k3_local", st, [&] {
-    hipLaunchKernelGGL(k3_local<T>, dim3(g.R * g.NB * g.U), dim3(192), 0, st, a.q, a.k, a.v, a.G, a.Gz, a.labels,
-                       a.c0, a.lam, a.gam, a.groups, g.Hq, g.Hkv, g.N, g.NB, a.scale, a.dql, a.dkl, a.dvl, a.coefl);
+  // the two orientations in separate launches: the dq part fits two blocks per
+  // CU, the dk / dv / coefficient part one
+  timed("k3_local_dq", st, [&] {
+    hipLaunchKernelGGL((k3_local<T, 0>), dim3(g.R * g.NB * g.U), dim3(192), 0, st, a.q, a.k, a.v, a.G, a.Gz,
+                       a.labels, a.c0, a.lam, a.gam, a.groups, g.Hq, g.Hkv, g.N, g.NB, a.scale, a.dql, a.dkl, a.dvl,
+                       a.coefl);
+  });
+  timed("k3_local_kv", st, [&] {
+    hipLaunchKernelGGL((k3_local<T, 1>), dim3(g.R * g.NB * g.U), dim3(192), 0, st, a.q, a.k, a.v, a.G, a.Gz,
+                       a.labels, a.c0, a.lam, a.gam, a.groups, g.Hq, g.Hkv, g.N, g.NB, a.scale, a.dql, a.dkl, a.dvl,
+                       a.coefl);
   });
   if (a.dq) {
     timed("k3_fold_q", st, [&] {
