@@ -14,8 +14,8 @@
 //   k3_readout     num += phi(x) . S (out: num / den), or dv = raw(K) dT + local
 //   k3_fold        dq = fold of (P [G, Gz]^T) through wq o raw(q) + local,
 //                  dk = fold of (dT [V, 1]^T) through raw(k) + local
-//   k3_local       local dq, dk, dv and coefficient partials (group sums on the
-//                  matrix cores)
+//   k3_local       local dq (part 0), and dk, dv and coefficient partials
+//                  (part 1), group sums on the matrix cores
 //   k3_coef_reduce per-head sums of those partials
 //
 // Matrix layout of v_mfma_f32_32x32x2f32: lane l supplies A[l % 32][l / 32]
