@@ -161,12 +161,12 @@ struct ReadoutOps {
   float4 w0, w1;
   bf16x8 b0, b1;
 };
-template <int T, int NS>
+template <int T, int NS, int RG = kRG>
 __device__ __forceinline__ void readout_read(const float* wl, const LdsRing<NS>& ring, int lane, ReadoutOps& o) {
   const int s = lane >> 5, row = lane & 31;
   o.w0 = *reinterpret_cast<const float4*>(wl + 16 * T + 8 * s);
   o.w1 = *reinterpret_cast<const float4*>(wl + 16 * T + 8 * s + 4);
-  const __bf16* tile = ring.st[(T / kRG) % NS] + (T % kRG) * kRingStep;
+  const __bf16* tile = ring.st[(T / RG) % NS] + (T % RG) * kRingStep;
   o.b0 = *reinterpret_cast<const bf16x8*>(tile + row * 16 + 8 * s);
   o.b1 = *reinterpret_cast<const bf16x8*>(tile + (32 + row) * 16 + 8 * s);
 }
@@ -601,10 +601,19 @@ __global__ __launch_bounds__(128, 2) void k2_out_fwd(const T* __restrict__ q, co
 // k2_out_fwd does; wave R only streams the P^T tiles into an LDS ring of kNSS
 // stages (it issues every copy, so its vmcnt alone paces the ring). Each
 // chunk's state then leaves L2 twice, once per token half, instead of once per
-// query head, and the deeper ring keeps more of it in flight.
+// query head, and the deeper ring keeps more of it in flight. The ring holds
+// kNSS stages of kRGS k-steps (48 KB): one ring barrier per eight k-steps.
 // ---------------------------------------------------------------------------
-constexpr int kNSS = 4;
+constexpr int kNSS = 3;
+constexpr int kRGS = 8;  // k-steps per ring group of the shared readout
+constexpr int kRingGroupsS = (kKS + kRGS - 1) / kRGS;
 constexpr int kMaxRS = 7;
+
+// Copies per k-step tile (two 1 KiB wave copies) of ring group G.
+template <int G>
+constexpr int group_steps_shared() {
+  return (G < kRingGroupsS) ? ((G + 1) * kRGS <= kKS ? kRGS : kKS - G * kRGS) : 0;
+}
 
 // Ring group G into stage G % kNSS by the copy wave: two 1 KiB wave copies per
 // k-step tile.
@@ -612,8 +621,8 @@ template <int G>
 __device__ __forceinline__ void ring_issue_shared(const uint16_t* pt, const LdsRing<kNSS>& ring, int lane) {
   __bf16* st = ring.st[G % kNSS];
 #pragma unroll
-  for (int i = 0; i < kRG; ++i) {
-    const int t = G * kRG + i;
+  for (int i = 0; i < kRGS; ++i) {
+    const int t = G * kRGS + i;
     if (t < kKS) {
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf)
@@ -623,38 +632,38 @@ __device__ __forceinline__ void ring_issue_shared(const uint16_t* pt, const LdsR
 }
 template <int G, int... I>
 constexpr int shared_copies_in_flight(std::integer_sequence<int, I...>) {
-  return ((2 * group_copies<G + 1 + I>()) + ... + 0);
+  return ((2 * group_steps_shared<G + 1 + I>()) + ... + 0);
 }
 // The copy wave: one ring barrier per group (as many as the readout waves),
 // then the copies of the group kNSS - 1 ahead into the stage just released.
 template <int G>
 __device__ __forceinline__ void ring_produce(const uint16_t* pt, const LdsRing<kNSS>& ring, int lane) {
   ring_sync<shared_copies_in_flight<G>(std::make_integer_sequence<int, kNSS - 2>{})>();
-  if constexpr (G + kNSS - 1 < kRingGroups) ring_issue_shared<G + kNSS - 1>(pt, ring, lane);
-  if constexpr (G + 1 < kRingGroups) ring_produce<G + 1>(pt, ring, lane);
+  if constexpr (G + kNSS - 1 < kRingGroupsS) ring_issue_shared<G + kNSS - 1>(pt, ring, lane);
+  if constexpr (G + 1 < kRingGroupsS) ring_produce<G + 1>(pt, ring, lane);
 }
 template <int G>
 __device__ __forceinline__ void readout_group_shared(const float (&x)[kD], const float* wl,
                                                      const LdsRing<kNSS>& ring, int lane, f32x16 (&acc)[2]) {
   ring_sync<shared_copies_in_flight<G>(std::make_integer_sequence<int, kNSS - 2>{})>();
-  constexpr int n = (G + 1) * kRG <= kKS ? kRG : kKS - G * kRG;
+  constexpr int n = group_steps_shared<G>();
   ReadoutOps o[2];
-  readout_read<G * kRG>(wl, ring, lane, o[0]);
+  readout_read<G * kRGS, kNSS, kRGS>(wl, ring, lane, o[0]);
   [&]<int... I>(std::integer_sequence<int, I...>) {
     (([&] {
-       if constexpr (I + 1 < n) readout_read<G * kRG + I + 1>(wl, ring, lane, o[(I + 1) & 1]);
-       readout_step<G * kRG + I>(x, o[I & 1], acc);
+       if constexpr (I + 1 < n) readout_read<G * kRGS + I + 1, kNSS, kRGS>(wl, ring, lane, o[(I + 1) & 1]);
+       readout_step<G * kRGS + I>(x, o[I & 1], acc);
      }()),
      ...);
   }(std::make_integer_sequence<int, n>{});
-  if constexpr (G + 1 < kRingGroups) readout_group_shared<G + 1>(x, wl, ring, lane, acc);
+  if constexpr (G + 1 < kRingGroupsS) readout_group_shared<G + 1>(x, wl, ring, lane, acc);
 }
 
 template <typename T>
 __global__ __launch_bounds__(64 * (kMaxRS + 1), 1) void k2_out_fwd_shared(
     const T* __restrict__ q, const float* __restrict__ wqs, const uint16_t* __restrict__ PT, int Hq, int Hkv, int N,
     int NB, float floor, T* __restrict__ out, float* __restrict__ num, const float* __restrict__ den) {
-  __shared__ __attribute__((aligned(16))) __bf16 rs[kNSS][kRG * kRingStep];
+  __shared__ __attribute__((aligned(16))) __bf16 rs[kNSS][kRGS * kRingStep];
   __shared__ __attribute__((aligned(16))) float wl[kMaxRS][kS];
   LdsRing<kNSS> ring;
 #pragma unroll
