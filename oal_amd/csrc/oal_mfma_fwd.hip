@@ -142,16 +142,24 @@ __device__ __forceinline__ bf16x8 load8(const float* p) {
 // the register limit) fit a CU; one group of four k-steps stays in flight.
 constexpr int kNSR = 3;
 
+// A k-step tile in LDS is [4 value blocks][16 slots][16 values] bf16: the four
+// 512-byte pieces of the R layout ([tile][4][32 slots][16 values]) that hold
+// its 16 slots. Element offset in the chunk's R state of piece p (value block)
+// of k-step t, for the 32 lanes r of a 512-byte copy:
+__device__ __forceinline__ size_t rpiece(int t, int p, int r) {
+  return (size_t)(t >> 1) * 2048 + p * 512 + (t & 1) * 256 + r * 8;
+}
+
 // Ring group G (k-steps G * kRG ..) into LDS stage G % kNSR; each k-step tile is
-// 64 values x 16 slots = 128 lanes x 16 bytes.
+// 4 pieces of 512 bytes = 128 lanes x 16 bytes (wave w copies pieces 2w, 2w + 1).
 template <int G>
-__device__ __forceinline__ void ring_issue(const uint16_t* pt, const LdsRing<kNSR>& ring, int tid) {
-  const int wv = tid >> 6;
+__device__ __forceinline__ void ring_issue(const uint16_t* pr, const LdsRing<kNSR>& ring, int tid) {
+  const int wv = tid >> 6, l = tid & 63;
   __bf16* st = ring.st[G % kNSR];
 #pragma unroll
   for (int i = 0; i < kRG; ++i) {
     const int t = G * kRG + i;
-    if (t < kKS) copy16_to_lds(pt + (size_t)t * kRingStep + tid * 8, st + i * kRingStep + 64 * wv * 8);
+    if (t < kKS) copy16_to_lds(pr + rpiece(t, 2 * wv + (l >> 5), l & 31), st + i * kRingStep + 64 * wv * 8);
   }
 }
 
@@ -161,14 +169,31 @@ struct ReadoutOps {
   float4 w0, w1;
   bf16x8 b0, b1;
 };
+
+// B fragment of value half n of a staged k-step tile: lane l supplies slots
+// 8 (l / 32) .. + 7 of value 32 n + l % 32. ds_read_b64_tr_b16 hands lane i of
+// each 16-lane group column i of the 4 x 16 block whose row j the group's lanes
+// 4 j .. 4 j + 3 address (four values each), so the 16-lane group g reads rows =
+// slots 8 (g / 2) + 0..3, then + 4..7, of value block 2 n + g % 2.
+typedef short trv4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ bf16x8 tr_fragment(const __bf16* tile, int lane, int n) {
+  const int g = lane >> 4, i = lane & 15;
+  const __bf16* p = tile + (2 * n + (g & 1)) * 256 + (8 * (g >> 1) + (i >> 2)) * 16 + 4 * (i & 3);
+  typedef __attribute__((address_space(3))) trv4 lds_trv4;
+  const trv4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_trv4*)(p));
+  const trv4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_trv4*)(p + 4 * 16));
+  typedef short trv8 __attribute__((ext_vector_type(8)));
+  const trv8 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return __builtin_bit_cast(bf16x8, v);
+}
 template <int T, int NS, int RG = kRG>
 __device__ __forceinline__ void readout_read(const float* wl, const LdsRing<NS>& ring, int lane, ReadoutOps& o) {
   const int s = lane >> 5, row = lane & 31;
   o.w0 = *reinterpret_cast<const float4*>(wl + 16 * T + 8 * s);
   o.w1 = *reinterpret_cast<const float4*>(wl + 16 * T + 8 * s + 4);
   const __bf16* tile = ring.st[(T / RG) % NS] + (T % RG) * kRingStep;
-  o.b0 = *reinterpret_cast<const bf16x8*>(tile + row * 16 + 8 * s);
-  o.b1 = *reinterpret_cast<const bf16x8*>(tile + (32 + row) * 16 + 8 * s);
+  o.b0 = tr_fragment(tile, lane, 0);
+  o.b1 = tr_fragment(tile, lane, 1);
 }
 template <int T>
 __device__ __forceinline__ void readout_step(const float (&x)[kD], const ReadoutOps& o, f32x16 (&acc)[2]) {
@@ -510,7 +535,7 @@ __global__ __launch_bounds__(256) void k2_intra_fwd(const T* __restrict__ q, con
 // ---------------------------------------------------------------------------
 template <typename T>
 __global__ __launch_bounds__(128, 2) void k2_out_fwd(const T* __restrict__ q, const float* __restrict__ wqs,
-                                                  const uint16_t* __restrict__ PT, int Hq, int Hkv, int N, int NB,
+                                                  const uint16_t* __restrict__ PR, int Hq, int Hkv, int N, int NB,
                                                   float floor, T* __restrict__ out, float* __restrict__ num,
                                                   const float* __restrict__ den) {
   __shared__ __attribute__((aligned(16))) __bf16 ring0[kRG * kRingStep], ring1[kRG * kRingStep],
@@ -529,7 +554,7 @@ __global__ __launch_bounds__(128, 2) void k2_out_fwd(const T* __restrict__ q, co
   const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, s = l >> 5, row = l & 31;
   const int tok0 = ch * kC;
   const size_t qbase = (size_t)(b * Hq + h) * N * kD;
-  const uint16_t* pt = PT + ((size_t)u * NB + ch) * ((size_t)kKS * kRingStep);
+  const uint16_t* pt = PR + ((size_t)u * NB + ch) * ((size_t)kKS * kRingStep);
 
   for (int i = tid; i < kS / 4; i += 128)
     reinterpret_cast<float4*>(wl)[i] = reinterpret_cast<const float4*>(wqs + (size_t)h * kS)[i];
@@ -626,7 +651,7 @@ __device__ __forceinline__ void ring_issue_shared(const uint16_t* pt, const LdsR
     if (t < kKS) {
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf)
-        copy16_to_lds(pt + (size_t)t * kRingStep + (64 * hf + lane) * 8, st + i * kRingStep + 64 * hf * 8);
+        copy16_to_lds(pt + rpiece(t, 2 * hf + (lane >> 5), lane & 31), st + i * kRingStep + 64 * hf * 8);
     }
   }
 }
@@ -661,7 +686,7 @@ __device__ __forceinline__ void readout_group_shared(const float (&x)[kD], const
 
 template <typename T>
 __global__ __launch_bounds__(64 * (kMaxRS + 1), 1) void k2_out_fwd_shared(
-    const T* __restrict__ q, const float* __restrict__ wqs, const uint16_t* __restrict__ PT, int Hq, int Hkv, int N,
+    const T* __restrict__ q, const float* __restrict__ wqs, const uint16_t* __restrict__ PR, int Hq, int Hkv, int N,
     int NB, float floor, T* __restrict__ out, float* __restrict__ num, const float* __restrict__ den) {
   __shared__ __attribute__((aligned(16))) __bf16 rs[kNSS][kRGS * kRingStep];
   __shared__ __attribute__((aligned(16))) float wl[kMaxRS][kS];
@@ -674,7 +699,7 @@ __global__ __launch_bounds__(64 * (kMaxRS + 1), 1) void k2_out_fwd_shared(
   const int R = Hq / Hkv, b = u / Hkv, kh = u % Hkv;
   const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, s = l >> 5, row = l & 31;
   const int tok0 = ch * kC + 32 * th;
-  const uint16_t* pt = PT + ((size_t)u * NB + ch) * ((size_t)kKS * kRingStep);
+  const uint16_t* pt = PR + ((size_t)u * NB + ch) * ((size_t)kKS * kRingStep);
 
   if (wv == R) {
     // the copy wave
@@ -844,7 +869,7 @@ void launch_mfma_forward(const LaunchGeom& g, const void* q, const void* k, cons
     // segment scratch
     const ScanPlan plan = scan_plan(g.U, g.NB, sizeof(float) * (size_t)g.B * g.Hq * g.N * kD, true);
     ScanArgs a{sv.KT16, kD, sv.VT16, kD + 1, nullptr, nullptr, g.U, g.Hq, g.Hkv, g.N, g.NB,
-               sv.PT, sv.PR, num, nullptr, nullptr, nullptr};
+               nullptr, sv.PR, num, nullptr, nullptr, nullptr};
     launch_scan<true>(plan, a, st, timed);
   }
   timed("k2_intra_fwd", st, [&] {
@@ -862,12 +887,12 @@ void launch_mfma_forward(const LaunchGeom& g, const void* q, const void* k, cons
 #ifndef OAL_OUT_PER_HEAD
     // up to kMaxRS query heads per kv head: the heads share each copy of P_c
     if (g.R <= kMaxRS) {
-      hipLaunchKernelGGL(k2_out_fwd_shared<T>, dim3(2 * g.NB * g.U), dim3(64 * (g.R + 1)), 0, st, qt, sv.wqs, sv.PT,
+      hipLaunchKernelGGL(k2_out_fwd_shared<T>, dim3(2 * g.NB * g.U), dim3(64 * (g.R + 1)), 0, st, qt, sv.wqs, sv.PR,
                          g.Hq, g.Hkv, g.N, g.NB, floor, static_cast<T*>(out), num, den);
       return;
     }
 #endif
-    hipLaunchKernelGGL(k2_out_fwd<T>, dim3(g.R * g.NB * g.U), dim3(128), 0, st, qt, sv.wqs, sv.PT, g.Hq, g.Hkv, g.N,
+    hipLaunchKernelGGL(k2_out_fwd<T>, dim3(g.R * g.NB * g.U), dim3(128), 0, st, qt, sv.wqs, sv.PR, g.Hq, g.Hkv, g.N,
                        g.NB, floor, static_cast<T*>(out), num, den);
   });
 }

@@ -270,9 +270,12 @@ __global__ __launch_bounds__(64 * NW, (NW + 1) / 2) void k2_scan(const uint16_t*
         store_row16(tr + ((size_t)kk * 32 + row) * 16, make_uint2(wd[n][a][0], wd[n][a][1]),
                     make_uint2(wd[n][a + 1][0], wd[n][a + 1][1]));
       }
-    // T layout [kstep][64 values][16 slots]: the matrix cores transpose the
-    // packed tile (D = A P, one nonzero product per output, exact), giving
-    // lane = value and registers = slots 8 (i / 4) + 4 s + i % 4.
+    // T layout [kstep][64 values][16 slots] (backward only: the forward's
+    // readers take their fragments from the R layout with transposed LDS
+    // reads): the matrix cores transpose the packed tile (D = A P, one nonzero
+    // product per output, exact), giving lane = value and registers = slots
+    // 8 (i / 4) + 4 s + i % 4.
+    if constexpr (FWD) return;
     uint16_t* tt = outT + cb * kChunkElems + (size_t)(2 * tile[t]) * 64 * 16;
 #pragma unroll
     for (int nh = 0; nh < 2; ++nh) {
