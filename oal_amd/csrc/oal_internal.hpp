@@ -31,8 +31,7 @@ struct MfmaSaved {
   float* ic;      // [Hq][kIC] intra-chunk coefficient pack
   float* gm;      // [Hq][64][64] scale^2 Gam[g(r)][g(c)]
   float* lb;      // [Hq][64] scale lam[g(d)]
-  uint16_t* PT;   // [U][NB][kKS][64][16] bf16
-  uint16_t* PR;   // [U][NB][kS/32][4][32][16] bf16
+  uint16_t* PR;   // [U][NB][kS/32][4][32][16] bf16 (the readouts' and the backward's state)
   float* PZ;      // [U][NB][kFP] denominator column, natural order
   float* PZm;     // [U][NB][64][64] denominator column as a symmetric pair matrix
   uint16_t* KT16; // [U][64][NB * 64] bf16 k^T (tokens >= N zero)

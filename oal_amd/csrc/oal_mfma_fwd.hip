@@ -11,8 +11,9 @@
 //                        registers, added to num, then out = num / den.
 //
 // Saved layouts (per unit u and chunk c; "tile" = 32 slots, "k-step" = 16 slots):
-//   PT [u][c][kKS][64 e][16]        bf16  (readout B operand: slots contiguous)
-//   PR [u][c][kS/32][4][32][16 e]   bf16  (backward A operand: values contiguous)
+//   PR [u][c][kS/32][4][32][16 e]   bf16  (backward A operand: values contiguous; the
+//                                          readouts take their B fragments from it
+//                                          with transposed LDS reads)
 //   PZ [u][c][kFP]                  f32   (denominator state, natural feature order)
 //   PZm [u][c][64][64]              f32   (its pair entries as a symmetric matrix; PZ and
 //                                          PZm are k2_den_scan's prefixes of k2_fwd_prep's
@@ -835,7 +836,6 @@ MfmaSaved mfma_saved_view(void* base, int Hq, int U, int NB, int R) {
   v.ic = static_cast<float*>(take(sizeof(float) * (size_t)Hq * kIC));
   v.gm = static_cast<float*>(take(sizeof(float) * (size_t)Hq * kD * kD));
   v.lb = static_cast<float*>(take(sizeof(float) * (size_t)Hq * kD));
-  v.PT = static_cast<uint16_t*>(take(chunk * units));
   v.PR = static_cast<uint16_t*>(take(chunk * units));
   v.PZ = static_cast<float*>(take(sizeof(float) * units * kFP));
   v.PZm = static_cast<float*>(take(sizeof(float) * units * kD * kD));
