@@ -55,7 +55,6 @@ struct MfmaWork {
   float* Gz;      // [B][Hq][N]
   uint16_t* GT16; // [B][Hq][66][NB * 64] bf16: G^T, Gz, 0
   uint16_t* QT16; // [B][Hq][66][NB * 64] bf16: q^T, 1 (token < N), 0
-  uint16_t* dTT;  // [U][NB][kKS][64][16] bf16
   uint16_t* dTR;  // [U][NB][kS/32][4][32][16] bf16
   float* dTz;     // [U][NB][kFP] exclusive suffix of the denominator state (natural order)
   float* dCt;     // [U][NB][kZt] per-chunk denominator dCarry (pair-matrix form)
@@ -71,7 +70,6 @@ struct MfmaWork {
   float* coefs;   // [Hq][73] their sums over the chunks
   float* dkp;     // per-pair path: [B][Hq][N][64] local dk per query head
   float* dwql;    // per-pair path: [Hq][B * NB * 2][kS] local slot-coefficient partials
-  uint16_t* dCT;  // [U][S][kKS][64][16] bf16 segment carries of dT (S > 1), T layout
   uint16_t* dCR;  // [U][S][kS/32][4][32][16] bf16, R layout
   int S, SL;      // segments of the backward state scan and chunks per segment
   size_t bytes;
@@ -205,11 +203,9 @@ struct ScanArgs {
   const float* wqs;   // backward: [Hq][kS] slot coefficients
   const uint16_t* PR; // backward: forward state (R layout), for the coefficient partials
   int U, Hq, Hkv, N, NB;
-  uint16_t* outT;     // emitted state, T layout
   uint16_t* outR;     // emitted state, R layout
   float* segtot;      // [U][S][kS][64] scratch when S > 1
   float* dwqs;        // backward: [S][B][Hq][kS] coefficient partials
-  uint16_t* carryT;   // backward with S > 1: [U][S] segment carries, T layout
   uint16_t* carryR;   // backward with S > 1: [U][S] segment carries, R layout
 };
 template <bool FWD>

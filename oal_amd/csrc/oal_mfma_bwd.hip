@@ -154,7 +154,8 @@ __global__ __launch_bounds__(256) void k2_bwd_prep(const T* __restrict__ q, cons
 
 // ---------------------------------------------------------------------------
 // Ring staging of k-blocked tiles (shared by the two waves of a fold block).
-// One unit = 1024 bf16 (a PR M-tile k-slice of 32 x 16 or a PT k-step 64 x 16).
+// One unit = 1024 bf16 (a PR M-tile k-slice of 32 x 16, or the four 512-byte
+// R-layout pieces of a k-step).
 // ---------------------------------------------------------------------------
 constexpr int kFG = 4;  // units per ring group
 constexpr int kNS = 4;  // LDS stages of a ring
@@ -300,21 +301,21 @@ __global__ __launch_bounds__(128, 2) void k2_q_fold(const T* __restrict__ q, con
 // dk, dv: state parts (fold of dT V^T, dU = raw(K) dT, dTz quadratic form) plus
 // the per-head local parts. grid (NB, U), 2 waves; wave w owns tokens 32w..+31.
 // ---------------------------------------------------------------------------
-// dU = raw(K) dT: k-step T of the T-layout state in LDS; with CARRY the same
-// k-step of the segment carry follows the UPG state units of each ring stage,
-// and its products accumulate into the same accumulators.
+// dU = raw(K) dT: k-step T of the state staged in LDS from its R-layout pieces
+// (B fragments by transposed reads); with CARRY the same k-step of the segment
+// carry follows the UPG state units of each ring stage, and its products
+// accumulate into the same accumulators.
 template <int T, int UPG, bool CARRY>
 __device__ __forceinline__ void du_step(const float (&x)[kD], const LdsRing<4>& ring, int lane, f32x16 (&acc)[2]) {
-  const int s = lane >> 5, row = lane & 31;
   const __bf16* tile = ring.st[(T / UPG) % kNS] + (T % UPG) * 1024;
-  const bf16x8 b0 = *reinterpret_cast<const bf16x8*>(tile + row * 16 + 8 * s);
-  const bf16x8 b1 = *reinterpret_cast<const bf16x8*>(tile + (32 + row) * 16 + 8 * s);
+  const bf16x8 b0 = tr_fragment(tile, lane, 0);
+  const bf16x8 b1 = tr_fragment(tile, lane, 1);
   const bf16x8 a = raw_fragment<T>(x);
   acc[0] = mfma32(a, b0, acc[0]);
   acc[1] = mfma32(a, b1, acc[1]);
   if constexpr (CARRY) {
-    const bf16x8 c0 = *reinterpret_cast<const bf16x8*>(tile + UPG * 1024 + row * 16 + 8 * s);
-    const bf16x8 c1 = *reinterpret_cast<const bf16x8*>(tile + UPG * 1024 + (32 + row) * 16 + 8 * s);
+    const bf16x8 c0 = tr_fragment(tile + UPG * 1024, lane, 0);
+    const bf16x8 c1 = tr_fragment(tile + UPG * 1024, lane, 1);
     acc[0] = mfma32(a, c0, acc[0]);
     acc[1] = mfma32(a, c1, acc[1]);
   }
@@ -333,14 +334,16 @@ constexpr int du_copies() {
 template <int UPG, bool CARRY, int G>
 __device__ __forceinline__ void du_issue(const uint16_t* src, const uint16_t* csrc, const LdsRing<4>& ring,
                                          int tid) {
-  const int wv = tid >> 6;
+  const int wv = tid >> 6, l = tid & 63;
   __bf16* st = ring.st[G % kNS];
 #pragma unroll
   for (int i = 0; i < UPG; ++i) {
     const int u = G * UPG + i;
     if (u < kKS) {
-      copy16_to_lds(src + (size_t)u * 1024 + tid * 8, st + i * 1024 + 64 * wv * 8);
-      if constexpr (CARRY) copy16_to_lds(csrc + (size_t)u * 1024 + tid * 8, st + (UPG + i) * 1024 + 64 * wv * 8);
+      // wave w copies the k-step's R-layout pieces 2 w, 2 w + 1
+      const size_t o = rpiece(u, 2 * wv + (l >> 5), l & 31);
+      copy16_to_lds(src + o, st + i * 1024 + 64 * wv * 8);
+      if constexpr (CARRY) copy16_to_lds(csrc + o, st + (UPG + i) * 1024 + 64 * wv * 8);
     }
   }
 }
@@ -367,13 +370,12 @@ __device__ __forceinline__ void du_group(const float (&x)[kD], const LdsRing<4>&
 // both parts of a unit, so that the chunks of a segment read its carry through
 // one L2.
 // CARRY: dT of chunk ch is the backward scan's segment-local state plus the
-// carry of the chunk's segment (ch / SL, cR / cT [U][S]); both products of each
+// carry of the chunk's segment (ch / SL, cR [U][S]); both products of each
 // step accumulate into the same registers, so the carry costs matrix products
 // and staging only (the feature and fold arithmetic is shared).
 template <typename T, bool CARRY>
 __global__ __launch_bounds__(128, 2) void k2_kv_fold(const T* __restrict__ k, const T* __restrict__ v,
-                                                     const uint16_t* __restrict__ dTR, const uint16_t* __restrict__ dTT,
-                                                     const uint16_t* __restrict__ cR, const uint16_t* __restrict__ cT,
+                                                     const uint16_t* __restrict__ dTR, const uint16_t* __restrict__ cR,
                                                      int SL, int S, const float* __restrict__ dTz,
                                                      const float* __restrict__ dkl, const float* __restrict__ dvl,
                                                      int Hq, int Hkv, int N, int NB, T* __restrict__ dk,
@@ -410,11 +412,11 @@ __global__ __launch_bounds__(128, 2) void k2_kv_fold(const T* __restrict__ k, co
     f32x16 acc[2] = {f32x16{}, f32x16{}};
     // four k-steps of dT per ring stage, or two of dT and two of the carry
     constexpr int UPG = CARRY ? 2 : 4;
-    const uint16_t* csrc = CARRY ? cT + sbase : nullptr;
-    du_issue<UPG, CARRY, 0>(dTT + cbase, csrc, ring, tid);
-    du_issue<UPG, CARRY, 1>(dTT + cbase, csrc, ring, tid);
-    du_issue<UPG, CARRY, 2>(dTT + cbase, csrc, ring, tid);
-    du_group<0, UPG, CARRY>(x, ring, dTT + cbase, csrc, tid, l, acc);
+    const uint16_t* csrc = CARRY ? cR + sbase : nullptr;
+    du_issue<UPG, CARRY, 0>(dTR + cbase, csrc, ring, tid);
+    du_issue<UPG, CARRY, 1>(dTR + cbase, csrc, ring, tid);
+    du_issue<UPG, CARRY, 2>(dTR + cbase, csrc, ring, tid);
+    du_group<0, UPG, CARRY>(x, ring, dTR + cbase, csrc, tid, l, acc);
     // the local parts are loaded together (rows clamped into range), then
     // stored for the rows below N: a load inside the row test would wait for
     // each one in turn
@@ -718,7 +720,6 @@ MfmaWork mfma_work_view(void* base, int B, int Hq, int U, int N, int NB, bool pa
   w.Gz = static_cast<float*>(take(rows * sizeof(float)));
   w.GT16 = static_cast<uint16_t*>(take(trows * sizeof(uint16_t)));
   w.QT16 = static_cast<uint16_t*>(take(trows * sizeof(uint16_t)));
-  w.dTT = static_cast<uint16_t*>(take(chunk * U * NB));
   w.dTR = static_cast<uint16_t*>(take(chunk * U * NB));
   w.dTz = static_cast<float*>(take(sizeof(float) * (size_t)U * NB * kFP));
   w.dCt = static_cast<float*>(take(sizeof(float) * (size_t)U * NB * kZt));
@@ -734,7 +735,6 @@ MfmaWork mfma_work_view(void* base, int B, int Hq, int U, int N, int NB, bool pa
   w.coefs = static_cast<float*>(take(sizeof(float) * (size_t)Hq * 73));
   w.dkp = pairwise ? static_cast<float*>(take(rows * kD * sizeof(float))) : nullptr;
   w.dwql = pairwise ? static_cast<float*>(take(sizeof(float) * (size_t)Hq * B * NB * 2 * kS)) : nullptr;
-  w.dCT = plan.S > 1 ? static_cast<uint16_t*>(take(chunk * U * plan.S)) : nullptr;
   w.dCR = plan.S > 1 ? static_cast<uint16_t*>(take(chunk * U * plan.S)) : nullptr;
   w.bytes = off;
   return w;
@@ -763,7 +763,7 @@ int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, cons
     const ScanPlan plan{w.S, w.SL, 0};
     // without a coefficient gradient the scan forms no coefficient partials
     ScanArgs a{w.QT16, kTRows, w.GT16, kTRows, sv.wqs, sv.PR, g.U, g.Hq, g.Hkv, g.N, g.NB,
-               w.dTT, w.dTR, w.segtot, need_coef ? w.dwqs : nullptr, w.dCT, w.dCR};
+               w.dTR, w.segtot, need_coef ? w.dwqs : nullptr, w.dCR};
     launch_scan<false>(plan, a, st, timed);
     // denominator state (pair-matrix form): per-chunk dCarry and coefficient
     // partials, then dTz as the exclusive chunk suffix
@@ -786,13 +786,13 @@ int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, cons
   if (dk) {
     timed("k2_kv_fold", st, [&] {
       if (w.S > 1)
-        hipLaunchKernelGGL((k2_kv_fold<T, true>), dim3(g.NB * g.U * 2), dim3(128), 0, st, kt, vt, w.dTR, w.dTT, w.dCR,
-                           w.dCT, w.SL, w.S, w.dTz, w.dkl, w.dvl, g.Hq, g.Hkv, g.N, g.NB, static_cast<T*>(dk),
+        hipLaunchKernelGGL((k2_kv_fold<T, true>), dim3(g.NB * g.U * 2), dim3(128), 0, st, kt, vt, w.dTR, w.dCR,
+                           w.SL, w.S, w.dTz, w.dkl, w.dvl, g.Hq, g.Hkv, g.N, g.NB, static_cast<T*>(dk),
                            static_cast<T*>(dv));
       else
-        hipLaunchKernelGGL((k2_kv_fold<T, false>), dim3(g.NB * g.U * 2), dim3(128), 0, st, kt, vt, w.dTR, w.dTT,
-                           nullptr, nullptr, 1, 1, w.dTz, w.dkl, w.dvl, g.Hq, g.Hkv, g.N, g.NB,
-                           static_cast<T*>(dk), static_cast<T*>(dv));
+        hipLaunchKernelGGL((k2_kv_fold<T, false>), dim3(g.NB * g.U * 2), dim3(128), 0, st, kt, vt, w.dTR, nullptr,
+                           1, 1, w.dTz, w.dkl, w.dvl, g.Hq, g.Hkv, g.N, g.NB, static_cast<T*>(dk),
+                           static_cast<T*>(dv));
     });
   }
   if (need_coef) {

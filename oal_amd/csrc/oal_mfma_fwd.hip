@@ -143,14 +143,6 @@ __device__ __forceinline__ bf16x8 load8(const float* p) {
 // the register limit) fit a CU; one group of four k-steps stays in flight.
 constexpr int kNSR = 3;
 
-// A k-step tile in LDS is [4 value blocks][16 slots][16 values] bf16: the four
-// 512-byte pieces of the R layout ([tile][4][32 slots][16 values]) that hold
-// its 16 slots. Element offset in the chunk's R state of piece p (value block)
-// of k-step t, for the 32 lanes r of a 512-byte copy:
-__device__ __forceinline__ size_t rpiece(int t, int p, int r) {
-  return (size_t)(t >> 1) * 2048 + p * 512 + (t & 1) * 256 + r * 8;
-}
-
 // Ring group G (k-steps G * kRG ..) into LDS stage G % kNSR; each k-step tile is
 // 4 pieces of 512 bytes = 128 lanes x 16 bytes (wave w copies pieces 2w, 2w + 1).
 template <int G>
@@ -171,22 +163,6 @@ struct ReadoutOps {
   bf16x8 b0, b1;
 };
 
-// B fragment of value half n of a staged k-step tile: lane l supplies slots
-// 8 (l / 32) .. + 7 of value 32 n + l % 32. ds_read_b64_tr_b16 hands lane i of
-// each 16-lane group column i of the 4 x 16 block whose row j the group's lanes
-// 4 j .. 4 j + 3 address (four values each), so the 16-lane group g reads rows =
-// slots 8 (g / 2) + 0..3, then + 4..7, of value block 2 n + g % 2.
-typedef short trv4 __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ bf16x8 tr_fragment(const __bf16* tile, int lane, int n) {
-  const int g = lane >> 4, i = lane & 15;
-  const __bf16* p = tile + (2 * n + (g & 1)) * 256 + (8 * (g >> 1) + (i >> 2)) * 16 + 4 * (i & 3);
-  typedef __attribute__((address_space(3))) trv4 lds_trv4;
-  const trv4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_trv4*)(p));
-  const trv4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_trv4*)(p + 4 * 16));
-  typedef short trv8 __attribute__((ext_vector_type(8)));
-  const trv8 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-  return __builtin_bit_cast(bf16x8, v);
-}
 template <int T, int NS, int RG = kRG>
 __device__ __forceinline__ void readout_read(const float* wl, const LdsRing<NS>& ring, int lane, ReadoutOps& o) {
   const int s = lane >> 5, row = lane & 31;
@@ -869,7 +845,7 @@ void launch_mfma_forward(const LaunchGeom& g, const void* q, const void* k, cons
     // segment scratch
     const ScanPlan plan = scan_plan(g.U, g.NB, sizeof(float) * (size_t)g.B * g.Hq * g.N * kD, true);
     ScanArgs a{sv.KT16, kD, sv.VT16, kD + 1, nullptr, nullptr, g.U, g.Hq, g.Hkv, g.N, g.NB,
-               nullptr, sv.PR, num, nullptr, nullptr, nullptr};
+               sv.PR, num, nullptr, nullptr};
     launch_scan<true>(plan, a, st, timed);
   }
   timed("k2_intra_fwd", st, [&] {

@@ -37,15 +37,16 @@
 //           backward state, k2_kv_fold, adds the carry with matrix products of
 //           its own, so the backward contracts every item once.
 //   MODE 4 (backward): the carry of each segment, the sum of the totals of the
-//           segments after it, emitted once per (unit, segment) in the R and T
-//           layouts; no items. A block walks its tiles' segments from the last
+//           segments after it, emitted once per (unit, segment); no items. A block walks its tiles' segments from the last
 //           one backwards with a running sum, so each total is read once.
 // PART (backward, MODE 0 and 2): form the coefficient partials; without them
 // (no coefficient gradient requested) the forward state is not read. The
 // per-head products stay apart either way, so that the state -- and every
 // gradient -- is bit-identical whichever gradients are requested.
-// Emitted layouts per (unit, chunk), identical in both directions:
-//   R [kS/32][4][32][16 values] bf16, T [kKS][64 values][16 slots] bf16.
+// Emitted layout per (unit, chunk), identical in both directions:
+//   R [kS/32][4][32][16 values] bf16. Readers that contract over the slots
+//   stage a k-step's four 512-byte pieces and read their fragments transposed
+//   (ds_read_b64_tr_b16), so no second, slot-contiguous copy is written.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -76,7 +77,7 @@ __global__ __launch_bounds__(64 * NW, (NW + 1) / 2) void k2_scan(const uint16_t*
                                                const uint16_t* __restrict__ V, int vrows,
                                                const float* __restrict__ wqs, const uint16_t* __restrict__ PRin,
                                                const float* __restrict__ carry, int Hq, int Hkv, int N, int NB, int SL,
-                                               int Sg, uint16_t* __restrict__ outT, uint16_t* __restrict__ outR,
+                                               int Sg, uint16_t* __restrict__ outR,
                                                float* __restrict__ segtot, float* __restrict__ dwqs) {
   constexpr bool EMIT = MODE == 1 || MODE == 2 || MODE == 3;
   // per-head products kept apart (needed for the partials)
@@ -224,19 +225,6 @@ __global__ __launch_bounds__(64 * NW, (NW + 1) / 2) void k2_scan(const uint16_t*
     }
   };
 
-  // Permutation matrices of the T-layout transposition (see emit): for value
-  // block kk, K position 8 s' + j of a lane group s' holds the state value
-  // 16 kk + 4 s' + j (j < 4) or 16 kk + 8 + 4 s' + (j - 4) (j >= 4); B routes it
-  // to output column 16 (kk % 2) + that offset of the 32-value half kk / 2.
-  bf16x8 perm[2];
-#pragma unroll
-  for (int p = 0; p < 2; ++p)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int off = j < 4 ? 4 * s + j : 8 + 4 * s + (j - 4);
-      perm[p][j] = (__bf16)(16 * p + off == row ? 1.f : 0.f);
-    }
-
   // Emission of tile t's state into state block cb (unit u and chunk ch: the
   // exclusive prefix / suffix before ch, cb = u * NB + ch; MODE 4: the carry of
   // segment seg, cb = u * Sg + seg).
@@ -270,30 +258,6 @@ __global__ __launch_bounds__(64 * NW, (NW + 1) / 2) void k2_scan(const uint16_t*
         store_row16(tr + ((size_t)kk * 32 + row) * 16, make_uint2(wd[n][a][0], wd[n][a][1]),
                     make_uint2(wd[n][a + 1][0], wd[n][a + 1][1]));
       }
-    // T layout [kstep][64 values][16 slots] (backward only: the forward's
-    // readers take their fragments from the R layout with transposed LDS
-    // reads): the matrix cores transpose the packed tile (D = A P, one nonzero
-    // product per output, exact), giving lane = value and registers = slots
-    // 8 (i / 4) + 4 s + i % 4.
-    if constexpr (FWD) return;
-    uint16_t* tt = outT + cb * kChunkElems + (size_t)(2 * tile[t]) * 64 * 16;
-#pragma unroll
-    for (int nh = 0; nh < 2; ++nh) {
-      f32x16 D = f32x16{};
-#pragma unroll
-      for (int p = 0; p < 2; ++p) {
-        const uint4 av = make_uint4(wd[nh][2 * p][0], wd[nh][2 * p][1], wd[nh][2 * p + 1][0], wd[nh][2 * p + 1][1]);
-        D = mfma32(__builtin_bit_cast(bf16x8, av), perm[p], D);
-      }
-      const int e = 32 * nh + row;
-#pragma unroll
-      for (int q = 0; q < 4; q += 2) {
-        const int tp = q >> 1;
-        store_row16(tt + ((size_t)tp * 64 + e) * 16,
-                    make_uint2(pack_bf16x2(D[4 * q], D[4 * q + 1]), pack_bf16x2(D[4 * q + 2], D[4 * q + 3])),
-                    make_uint2(pack_bf16x2(D[4 * q + 4], D[4 * q + 5]), pack_bf16x2(D[4 * q + 6], D[4 * q + 7])));
-      }
-    }
   };
 
   if constexpr (MODE == 4) {
@@ -708,8 +672,7 @@ static void launch_scan_impl(const ScanPlan& p, const ScanArgs& a, hipStream_t s
   if (p.S == 1) {
     timed(name, st, [&] {
       hipLaunchKernelGGL((k2_scan<FWD, 2, T2, W2, PART>), grid(T2, W2), dim3(64 * W2), 0, st, a.F, a.frows, a.V,
-                         a.vrows, a.wqs, a.PR, nullptr, a.Hq, a.Hkv, a.N, a.NB, p.SL, p.S, a.outT, a.outR, nullptr,
-                         a.dwqs);
+                         a.vrows, a.wqs, a.PR, nullptr, a.Hq, a.Hkv, a.N, a.NB, p.SL, p.S, a.outR, nullptr, a.dwqs);
     });
     return;
   }
@@ -719,14 +682,13 @@ static void launch_scan_impl(const ScanPlan& p, const ScanArgs& a, hipStream_t s
     constexpr int T4 = scan_tpw(false, 4), W4 = scan_nw(false, 4);
     timed(name, st, [&] {
       hipLaunchKernelGGL((k2_scan<false, 3, T3, W3, PART>), grid(T3, W3), dim3(64 * W3), 0, st, a.F, a.frows, a.V,
-                         a.vrows, a.wqs, a.PR, nullptr, a.Hq, a.Hkv, a.N, a.NB, p.SL, p.S, a.outT, a.outR, a.segtot,
-                         a.dwqs);
+                         a.vrows, a.wqs, a.PR, nullptr, a.Hq, a.Hkv, a.N, a.NB, p.SL, p.S, a.outR, a.segtot, a.dwqs);
     });
     timed("k2_state_bwd_carry", st, [&] {
       const dim3 g4((unsigned)(scan_tile_groups(T4, W4) * a.U));  // one block per (unit, tile group)
       hipLaunchKernelGGL((k2_scan<false, 4, T4, W4, false>), g4, dim3(64 * W4), 0, st, a.F, a.frows,
-                         a.V, a.vrows, a.wqs, a.PR, a.segtot, a.Hq, a.Hkv, a.N, a.NB, p.SL, p.S, a.carryT,
-                         a.carryR, nullptr, nullptr);
+                         a.V, a.vrows, a.wqs, a.PR, a.segtot, a.Hq, a.Hkv, a.N, a.NB, p.SL, p.S, a.carryR,
+                         nullptr, nullptr);
     });
     return;
   }
@@ -734,12 +696,12 @@ static void launch_scan_impl(const ScanPlan& p, const ScanArgs& a, hipStream_t s
     // segment totals, then each segment's replay from the totals before it
     timed("k2_state_fwd_totals", st, [&] {
       hipLaunchKernelGGL((k2_scan<true, 0, T0, W0, false>), grid(T0, W0), dim3(64 * W0), 0, st, a.F, a.frows, a.V,
-                         a.vrows, a.wqs, a.PR, nullptr, a.Hq, a.Hkv, a.N, a.NB, p.SL, p.S, nullptr, nullptr,
-                         a.segtot, nullptr);
+                         a.vrows, a.wqs, a.PR, nullptr, a.Hq, a.Hkv, a.N, a.NB, p.SL, p.S, nullptr, a.segtot,
+                         nullptr);
     });
     timed(name, st, [&] {
       hipLaunchKernelGGL((k2_scan<true, 1, T1, W1, false>), grid(T1, W1), dim3(64 * W1), 0, st, a.F, a.frows, a.V,
-                         a.vrows, a.wqs, a.PR, a.segtot, a.Hq, a.Hkv, a.N, a.NB, p.SL, p.S, a.outT, a.outR, nullptr,
+                         a.vrows, a.wqs, a.PR, a.segtot, a.Hq, a.Hkv, a.N, a.NB, p.SL, p.S, a.outR, nullptr,
                          nullptr);
     });
   }
