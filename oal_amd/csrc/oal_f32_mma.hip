@@ -410,21 +410,26 @@ __device__ __forceinline__ void readout_base(const float (&x)[kD], const float* 
   }
 }
 
-template <int M, int MODE, bool ADD>
+// PD (1 or 2) tiles of loads in flight: set (M + 1) % PD holds tile M + 1 and
+// then takes tile M + 1 + PD. Two help the dv readout (one block per chunk and
+// unit, few waves per CU); the query readout, with seven times the blocks,
+// keeps one and its fourth wave per SIMD.
+template <int M, int MODE, bool ADD, int PD>
 __device__ __forceinline__ void readout_tiles(const float (&x)[kD], float* st0, float* st1,
                                               const float* __restrict__ S, const float* __restrict__ Sz, size_t cb,
-                                              const float* wqh, int m, int s, int row, TileRegs<256>& tr,
+                                              const float* wqh, int m, int s, int row, TileRegs<256> (&tr)[PD],
                                               f32x16& acc, float& zacc, const int16_t* natl, const SegCarry& sc) {
   const float* st = (M & 1) ? st1 : st0;
   [&]<int... J>(std::integer_sequence<int, J...>) {
     (readout_base<16 * M + J, MODE>(x, st, m, s, row, acc, zacc), ...);
   }(std::make_integer_sequence<int, 16>{});
   if constexpr (M + 1 < kMT) {
-    store_tile<256, ADD, MODE == 0>((M & 1) ? st0 : st1, tr);
-    if constexpr (M + 2 < kMT) load_tile<256, ADD, MODE == 0>(S, Sz, cb, M + 2, wqh, natl, tr, sc);
+    store_tile<256, ADD, MODE == 0>((M & 1) ? st0 : st1, tr[(M + 1) % PD]);
+    if constexpr (M + 1 + PD < kMT)
+      load_tile<256, ADD, MODE == 0>(S, Sz, cb, M + 1 + PD, wqh, natl, tr[(M + 1) % PD], sc);
     lds_sync();
     __builtin_amdgcn_sched_barrier(0);
-    readout_tiles<M + 1, MODE, ADD>(x, st0, st1, S, Sz, cb, wqh, m, s, row, tr, acc, zacc, natl, sc);
+    readout_tiles<M + 1, MODE, ADD, PD>(x, st0, st1, S, Sz, cb, wqh, m, s, row, tr, acc, zacc, natl, sc);
   }
 }
 
@@ -462,14 +467,16 @@ __global__ __launch_bounds__(256, 2) void k3_readout(const T* __restrict__ x_in,
   const SegCarry sc = seg_carry(cS, cSz, u, ch, SL, nseg);
   for (int i = tid; i < kS; i += 256) natl[i] = kSlot3.nat[i];
   __syncthreads();
-  TileRegs<256> tr;
-  load_tile<256, CARRY, MODE == 0>(S, Sz, cb, 0, wqh, natl, tr, sc);
-  store_tile<256, CARRY, MODE == 0>(st0, tr);
-  load_tile<256, CARRY, MODE == 0>(S, Sz, cb, 1, wqh, natl, tr, sc);
+  constexpr int PD = MODE == 1 ? 2 : 1;
+  TileRegs<256> tr[PD];
+  load_tile<256, CARRY, MODE == 0>(S, Sz, cb, 0, wqh, natl, tr[0], sc);
+  store_tile<256, CARRY, MODE == 0>(st0, tr[0]);
+#pragma unroll
+  for (int i = 1; i <= PD; ++i) load_tile<256, CARRY, MODE == 0>(S, Sz, cb, i, wqh, natl, tr[i % PD], sc);
   __syncthreads();
   f32x16 acc = f32x16{};
   float zacc = 0.f;
-  readout_tiles<0, MODE, CARRY>(x, st0, st1, S, Sz, cb, wqh, m, s, row, tr, acc, zacc, natl, sc);
+  readout_tiles<0, MODE, CARRY, PD>(x, st0, st1, S, Sz, cb, wqh, m, s, row, tr, acc, zacc, natl, sc);
 
   if constexpr (MODE == 0) {
     const size_t dbase = (size_t)(b * Hq + h) * N;
