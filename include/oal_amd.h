@@ -149,8 +149,9 @@ int oal_backward_noalloc(const void* q, const void* k, const void* v,
                          void* stream);
 
 /*
- * Matrix-core self-test: one wave checks the MFMA accumulator layouts the bf16
- * kernels assume and adds the number of mismatching elements to
+ * Matrix-core self-test: one wave checks the MFMA accumulator layouts and the
+ * transposed LDS read (ds_read_b64_tr_b16) lane mapping the bf16 kernels
+ * assume, and adds the number of mismatching elements to
  * *device_errors (a device int the caller zeroed). No counterpart in the
  * reference; it lets a deployment verify the device before trusting results.
  */

@@ -744,7 +744,8 @@ __global__ __launch_bounds__(64 * (kMaxRS + 1), 1) void k2_out_fwd_shared(
 }
 
 // ---------------------------------------------------------------------------
-// MFMA layout self-test: checks the accumulator layouts assumed above.
+// MFMA layout self-test: checks the accumulator layouts assumed above and the
+// lane mapping of the transposed LDS reads (tr_fragment).
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(64) void k2_selftest(int* __restrict__ errors) {
   __shared__ float A[32][32], B[32][32];
@@ -789,6 +790,24 @@ __global__ __launch_bounds__(64) void k2_selftest(int* __restrict__ errors) {
       float ref = 0.f;
       for (int kk = 0; kk < 32; ++kk) ref += A[r][kk] * B[kk][col];
       bad += (c[i] != ref);
+    }
+  }
+  {  // transposed LDS reads (tr_fragment) of a staged k-step tile: entry
+     // (slot, value) holds the bits slot * 64 + value
+    __shared__ __attribute__((aligned(16))) uint16_t tile[4 * 16 * 16];
+    for (int i = l; i < 4 * 16 * 16; i += 64) {
+      const int vb = i / 256, slot = (i / 16) % 16, vv = i % 16;
+      tile[i] = (uint16_t)(slot * 64 + 16 * vb + vv);
+    }
+    __syncthreads();
+    for (int n = 0; n < 2; ++n) {
+      // compared as 32-bit words (two 16-bit elements each)
+      typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+      const u32x4 w = __builtin_bit_cast(u32x4, tr_fragment(reinterpret_cast<const __bf16*>(tile), l, n));
+      for (int j = 0; j < 8; ++j) {
+        const uint32_t got = (w[j >> 1] >> (16 * (j & 1))) & 0xffffu;
+        bad += (got != (uint32_t)((8 * (l / 32) + j) * 64 + 32 * n + l % 32));
+      }
     }
   }
   atomicAdd(errors, bad);
