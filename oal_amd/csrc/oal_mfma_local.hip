@@ -116,7 +116,10 @@ __global__ __launch_bounds__(192, COEF ? 2 : 3) void k2_local_dq(const T* __rest
   constexpr int LD = kD + 8;
   __shared__ __attribute__((aligned(16))) uint32_t mk[4][8][2][4];
   __shared__ __attribute__((aligned(16))) __bf16 Mz[kD][LD];
+  __shared__ __attribute__((aligned(16))) uint16_t kts[kD][LD];  // k^T of the chunk
+  __shared__ float cft[9][kD];  // coef_h(d), h = 0..8
   __shared__ float bz[kD];
+  __shared__ float gzs[kC];
   __shared__ float red[2][16][64];  // wave 2's dq (query tile 1)
   __shared__ float cp[COEF ? 3 * 64 : 1][45];  // per-lane coefficient partials
   __shared__ float cred[COEF ? 4 * 45 : 1];
@@ -131,45 +134,97 @@ __global__ __launch_bounds__(192, COEF ? 2 : 3) void k2_local_dq(const T* __rest
   const size_t cbase = (size_t)u * NB + ch;
   const size_t np = (size_t)NB * kC;
 
-  build_masks(mk, labels, h, G, tid);
-  for (int e = tid; e < kD * 4; e += 192) {
-    // Mz = gm o PZm (bf16): row r = e / 4, columns 16 (e % 4) .. + 15
-    const int r = e >> 2, qq = e & 3;
+  // The prologue's global loads are issued together, labels first (the
+  // coefficient rows depend on them), and the lane's operand rows right after
+  // the Mz stores: two round trips in all instead of one per loop. Loads and
+  // LDS stores are unconditional: a thread past an item count wraps onto an
+  // item another thread also holds and stores the same value there.
+  // masks: thread t = tid & 31 covers dims d, d + 1, d = 16 kk + 8 ss + 2 w
+  const int mt = tid & 31, mkk = mt >> 3, mss = (mt >> 2) & 1, mw = mt & 3;
+  const int md = 16 * mkk + 8 * mss + 2 * mw;
+  const int ml0 = labels[h * kD + md], ml1 = labels[h * kD + md + 1];
+  const int cd = tid & 63;  // dim of the coefficient table, bz and token of gzs
+  const int cl = clamp_label(labels[h * kD + cd], G);
+  // Mz = gm o PZm (bf16): items e = tid, tid + 192 (< 256): row e / 4, columns 16 (e % 4) .. + 15
+  float4 mg[2][4], mz[2][4];
+#pragma unroll
+  for (int x = 0; x < 2; ++x) {
+    const int e = (tid + 192 * x) & 255, r = e >> 2, qq = e & 3;
     const float4* gp = reinterpret_cast<const float4*>(gm + ((size_t)h * kD + r) * kD + 16 * qq);
     const float4* zp = reinterpret_cast<const float4*>(PZm + (cbase * kD + r) * kD + 16 * qq);
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const float4 g0 = gp[2 * i], g1 = gp[2 * i + 1], z0 = zp[2 * i], z1 = zp[2 * i + 1];
-      float y[8] = {g0.x * z0.x, g0.y * z0.y, g0.z * z0.z, g0.w * z0.w,
-                    g1.x * z1.x, g1.y * z1.y, g1.z * z1.z, g1.w * z1.w};
-      *reinterpret_cast<bf16x8*>(&Mz[r][16 * qq + 8 * i]) = pack8(y);
+    for (int y = 0; y < 4; ++y) {
+      mg[x][y] = gp[y];
+      mz[x][y] = zp[y];
     }
   }
-  if (tid < kD) bz[tid] = lb[(size_t)h * kD + tid] * PZ[cbase * kFP + 1 + tid];
-  __syncthreads();
+  const float lbv = lb[(size_t)h * kD + cd], pzv = PZ[cbase * kFP + 1 + cd];
+  const float gzv = Gz[(size_t)(b * Hq + h) * N + min(tok0 + cd, N - 1)];
+  // k^T of the chunk: 512 pieces of 8 tokens, pieces tid, tid + 192, tid + 384 (< 512)
+  bf16x8 ktv[3];
+#pragma unroll
+  for (int x = 0; x < 3; ++x) {
+    const int pc = (tid + 192 * x) & 511, d = pc >> 3, c = 8 * (pc & 7);
+    ktv[x] = *reinterpret_cast<const bf16x8*>(KT16 + ((size_t)u * kD + d) * np + tok0 + c);
+  }
+  // coefficient rows of dim cd: gam[g(cd)][0..7], lam[g(cd)] (group index clamped)
+  float cg[9];
+#pragma unroll
+  for (int h2 = 0; h2 < 8; ++h2) cg[h2] = gam[((size_t)h * G + cl) * G + min(h2, G - 1)];
+  cg[8] = lam[(size_t)h * G + cl];
 
+  {
+    const int g0 = clamp_label(ml0, G), g1 = clamp_label(ml1, G);
+#pragma unroll
+    for (int g = 0; g < 8; ++g) mk[mkk][g][mss][mw] = (g0 == g ? 0x0000ffffu : 0u) | (g1 == g ? 0xffff0000u : 0u);
+  }
+#pragma unroll
+  for (int x = 0; x < 2; ++x) {
+    const int e = (tid + 192 * x) & 255, r = e >> 2, qq = e & 3;
+#pragma unroll
+    for (int i2 = 0; i2 < 2; ++i2) {
+      const float4 g0 = mg[x][2 * i2], g1 = mg[x][2 * i2 + 1], z0 = mz[x][2 * i2], z1 = mz[x][2 * i2 + 1];
+      float y[8] = {g0.x * z0.x, g0.y * z0.y, g0.z * z0.z, g0.w * z0.w,
+                    g1.x * z1.x, g1.y * z1.y, g1.z * z1.z, g1.w * z1.w};
+      *reinterpret_cast<bf16x8*>(&Mz[r][16 * qq + 8 * i2]) = pack8(y);
+    }
+  }
   const int tp = wv, jt = tile_jt(tp), it = tile_it(tp);
   const int jr = tok0 + 32 * jt + row, ir = tok0 + 32 * it + row;  // this lane's operand rows
   const bool jok = jr < N, iok = ir < N;
   const size_t jo = (size_t)(jok ? jr : N - 1) * kD, io = (size_t)(iok ? ir : N - 1) * kD;
-  bf16x8 kf[4], qf[4];
-  f32x16 ds = f32x16{};
+  bf16x8 kf[4], qf[4], vf[4], gf[4];
 #pragma unroll
   for (int kk = 0; kk < 4; ++kk) {
     const int c = 16 * kk + 8 * s;
     kf[kk] = row8(k + kbase + jo + c, jok);
     qf[kk] = row8(q + qbase + io + c, iok);
-    ds = mfma32(row8(v + kbase + jo + c, jok), row8(G16 + qbase + io + c, iok), ds);
+    vf[kk] = row8(v + kbase + jo + c, jok);
+    gf[kk] = row8(G16 + qbase + io + c, iok);
   }
+#pragma unroll
+  for (int x = 0; x < 3; ++x) {
+    const int pc = (tid + 192 * x) & 511;
+    *reinterpret_cast<bf16x8*>(&kts[pc >> 3][8 * (pc & 7)]) = ktv[x];
+  }
+  bz[cd] = lbv * pzv;
+  gzs[cd] = tok0 + cd < N ? gzv : 0.f;
+#pragma unroll
+  for (int h2 = 0; h2 < 8; ++h2) cft[h2][cd] = h2 < G ? 2.f * scale * scale * cg[h2] : 0.f;
+  cft[8][cd] = scale * cg[8];
+  lds_sync();
+
+  f32x16 ds = f32x16{};
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) ds = mfma32(vf[kk], gf[kk], ds);
   // lane column i = 32 it + row; register rows j = 32 jt + c32_row(r)
   const int i = 32 * it + row;
-  const bool icol = tok0 + i < N;
-  const float gzi = icol ? Gz[(size_t)(b * Hq + h) * N + tok0 + i] : 0.f;
+  const float gzi = gzs[i];  // zero past N
   float dsv[16];
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int j = 32 * jt + c32_row(r, l);
-    dsv[r] = (j <= i && icol) ? ds[r] + gzi : 0.f;
+    dsv[r] = j <= i ? ds[r] + gzi : 0.f;
   }
   f32x16 sgs[COEF ? 8 : 1];
   if constexpr (COEF) {
@@ -212,26 +267,7 @@ __global__ __launch_bounds__(192, COEF ? 2 : 3) void k2_local_dq(const T* __rest
   for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
     for (int t = 0; t < 2; ++t)
-      kt[dt][t] = *reinterpret_cast<const bf16x8*>(KT16 + ((size_t)u * kD + 32 * dt + row) * np + tok0 + 32 * jt +
-                                                    16 * t + 8 * s);
-  // coefficient loads issued together: both labels, then every gam / lam entry
-  // unconditionally (group index clamped, so in bounds) and masked afterwards
-  float cf[9][2];
-  int gd[2];
-#pragma unroll
-  for (int dt = 0; dt < 2; ++dt) gd[dt] = clamp_label(labels[h * kD + 32 * dt + row], G);
-#pragma unroll
-  for (int dt = 0; dt < 2; ++dt) {
-#pragma unroll
-    for (int h2 = 0; h2 < 8; ++h2) cf[h2][dt] = gam[((size_t)h * G + gd[dt]) * G + min(h2, G - 1)];
-    cf[8][dt] = lam[(size_t)h * G + gd[dt]];
-  }
-#pragma unroll
-  for (int dt = 0; dt < 2; ++dt) {
-#pragma unroll
-    for (int h2 = 0; h2 < 8; ++h2) cf[h2][dt] = h2 < G ? 2.f * scale * scale * cf[h2][dt] : 0.f;
-    cf[8][dt] *= scale;
-  }
+      kt[dt][t] = *reinterpret_cast<const bf16x8*>(&kts[32 * dt + row][32 * jt + 16 * t + 8 * s]);
   f32x16 dq[2] = {f32x16{}, f32x16{}};
 #pragma unroll
   for (int h2 = 0; h2 < 9; ++h2) {
@@ -246,7 +282,7 @@ __global__ __launch_bounds__(192, COEF ? 2 : 3) void k2_local_dq(const T* __rest
         for (int kk = 0; kk < 4; ++kk) sh = mfma32(masked(kf[kk], &mk[kk][h2][s][0]), qf[kk], sh);
       }
 #pragma unroll
-      for (int r = 0; r < 16; ++r) x[r] = dsv[r] * sh[r];  // the scale of s_h is in cf
+      for (int r = 0; r < 16; ++r) x[r] = dsv[r] * sh[r];  // the scale of s_h is in cft
     } else {
 #pragma unroll
       for (int r = 0; r < 16; ++r) x[r] = dsv[r];
@@ -256,8 +292,9 @@ __global__ __launch_bounds__(192, COEF ? 2 : 3) void k2_local_dq(const T* __rest
     for (int dt = 0; dt < 2; ++dt) {
       f32x16 p = mfma32(f0, kt[dt][0], f32x16{});
       p = mfma32(f1, kt[dt][1], p);
+      const float cf = cft[h2][32 * dt + row];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) dq[dt][r] = fmaf(cf[h2][dt], p[r], dq[dt][r]);
+      for (int r = 0; r < 16; ++r) dq[dt][r] = fmaf(cf, p[r], dq[dt][r]);
     }
   }
   if (wv == 2) {
@@ -270,11 +307,9 @@ __global__ __launch_bounds__(192, COEF ? 2 : 3) void k2_local_dq(const T* __rest
     // query fragments qf are this lane's row i = 32 it + row
     float gzr[16];
 #pragma unroll
-    for (int a = 0; a < 4; ++a) {
-      const int i0 = tok0 + 32 * it + 8 * a + 4 * s;
+    for (int a = 0; a < 4; ++a)
 #pragma unroll
-      for (int vv = 0; vv < 4; ++vv) gzr[4 * a + vv] = i0 + vv < N ? Gz[(size_t)(b * Hq + h) * N + i0 + vv] : 0.f;
-    }
+      for (int vv = 0; vv < 4; ++vv) gzr[4 * a + vv] = gzs[32 * it + 8 * a + 4 * s + vv];
 #pragma unroll
     for (int dt = 0; dt < 2; ++dt) {
       f32x16 z = f32x16{};
