@@ -265,8 +265,7 @@ __global__ __launch_bounds__(128, 2) void k2_q_fold(const T* __restrict__ q, con
   const size_t qbase = (size_t)(b * Hq + h) * N * kD;
   const uint16_t* src = PR + ((size_t)u * NB + ch) * ((size_t)kKS * 64 * 16);
 
-  for (int i = tid; i < kS / 4; i += 128)
-    reinterpret_cast<float4*>(wl)[i] = reinterpret_cast<const float4*>(wqs + (size_t)h * kS)[i];
+  stage_f4<128, kS / 4>(reinterpret_cast<float4*>(wl), reinterpret_cast<const float4*>(wqs + (size_t)h * kS), tid);
   const int tok = tok0 + 32 * wv + row;
   const bool ok = tok < N;
   const size_t rowoff = qbase + (size_t)(ok ? tok : N - 1) * kD;

@@ -292,6 +292,21 @@ __device__ __forceinline__ void ring_sync() {
   asm volatile("" ::: "memory");
 }
 
+// Copies N4 float4 from global memory to LDS over NT threads with every load
+// of a thread issued before its first store (a strided loop waits for each
+// load before issuing the next). Items t + NT x past the end are clamped onto
+// the last item, which its own thread also copies: the same value to the same
+// place.
+template <int NT, int N4>
+__device__ __forceinline__ void stage_f4(float4* dst, const float4* __restrict__ src, int t) {
+  constexpr int kIt = (N4 + NT - 1) / NT;
+  float4 v[kIt];
+#pragma unroll
+  for (int x = 0; x < kIt; ++x) v[x] = src[min(t + NT * x, N4 - 1)];
+#pragma unroll
+  for (int x = 0; x < kIt; ++x) dst[min(t + NT * x, N4 - 1)] = v[x];
+}
+
 // Workgroup barrier over LDS only: this wave's LDS reads and writes are done
 // (lgkmcnt(0)), then s_barrier. Unlike __syncthreads() it does not wait for
 // outstanding global loads and stores (vmcnt counts both on gfx950), so

@@ -343,8 +343,7 @@ __global__ __launch_bounds__(256) void k2_intra_fwd(const T* __restrict__ q, con
       *reinterpret_cast<bf16x8*>(&Mz[r][16 * qq + 8 * i]) = pack8(y);
     }
     if constexpr (PAIRWISE) {
-      for (int i = tid; i < kS / 4; i += 256)
-        reinterpret_cast<float4*>(wl)[i] = reinterpret_cast<const float4*>(wqs + (size_t)h * kS)[i];
+      stage_f4<256, kS / 4>(reinterpret_cast<float4*>(wl), reinterpret_cast<const float4*>(wqs + (size_t)h * kS), tid);
     }
     // group masks: entry (kk, g, ss, w) covers dims d, d + 1 with d = 16 kk + 8 ss + 2 w
     if constexpr (!PAIRWISE) {
@@ -533,8 +532,7 @@ __global__ __launch_bounds__(128, 2) void k2_out_fwd(const T* __restrict__ q, co
   const size_t qbase = (size_t)(b * Hq + h) * N * kD;
   const uint16_t* pt = PR + ((size_t)u * NB + ch) * ((size_t)kKS * kRingStep);
 
-  for (int i = tid; i < kS / 4; i += 128)
-    reinterpret_cast<float4*>(wl)[i] = reinterpret_cast<const float4*>(wqs + (size_t)h * kS)[i];
+  stage_f4<128, kS / 4>(reinterpret_cast<float4*>(wl), reinterpret_cast<const float4*>(wqs + (size_t)h * kS), tid);
   // rotated query row of this lane's token
   float x[kD];
   {
@@ -566,8 +564,10 @@ __global__ __launch_bounds__(128, 2) void k2_out_fwd(const T* __restrict__ q, co
   for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const int tok = tok0 + 32 * wv + c32_row(i, l);
-      acc[nt][i] = tok < N ? num[qbase + (size_t)tok * kD + 32 * nt + row] : 0.f;
+      // rows past N read row N - 1 and are never stored: a load inside the
+      // row test would wait for each one in turn
+      const int tok = min(tok0 + 32 * wv + c32_row(i, l), N - 1);
+      acc[nt][i] = num[qbase + (size_t)tok * kD + 32 * nt + row];
     }
   [&]<int... I>(std::integer_sequence<int, I...>) {
     (ring_issue<I>(pt, ring, tid), ...);
@@ -689,8 +689,7 @@ __global__ __launch_bounds__(64 * (kMaxRS + 1), 1) void k2_out_fwd_shared(
   const int h = kh * R + wv;
   const size_t qbase = (size_t)(b * Hq + h) * N * kD;
   float* wlh = wl[wv];
-  for (int i = l; i < kS / 4; i += 64)
-    reinterpret_cast<float4*>(wlh)[i] = reinterpret_cast<const float4*>(wqs + (size_t)h * kS)[i];
+  stage_f4<64, kS / 4>(reinterpret_cast<float4*>(wlh), reinterpret_cast<const float4*>(wqs + (size_t)h * kS), l);
   float x[kD];
   {
     const int tok = tok0 + row;
@@ -716,8 +715,10 @@ __global__ __launch_bounds__(64 * (kMaxRS + 1), 1) void k2_out_fwd_shared(
   for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const int tok = tok0 + c32_row(i, l);
-      acc[nt][i] = tok < N ? num[qbase + (size_t)tok * kD + 32 * nt + row] : 0.f;
+      // rows past N read row N - 1 and are never stored: a load inside the
+      // row test would wait for each one in turn
+      const int tok = min(tok0 + c32_row(i, l), N - 1);
+      acc[nt][i] = num[qbase + (size_t)tok * kD + 32 * nt + row];
     }
   readout_group_shared<0>(x, wlh, ring, l, acc);
 
