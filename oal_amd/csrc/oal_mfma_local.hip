@@ -268,6 +268,14 @@ __global__ __launch_bounds__(192, COEF ? 2 : 3) void k2_local_dq(const T* __rest
 #pragma unroll
     for (int t = 0; t < 2; ++t)
       kt[dt][t] = *reinterpret_cast<const bf16x8*>(&kts[32 * dt + row][32 * jt + 16 * t + 8 * s]);
+  // this lane's query row again for the den-state term: the prologue's copy
+  // would stay live across the partials and spill. The pointer goes through an
+  // empty asm so that the compiler cannot fold the reload into the first load.
+  const T* qre = q;
+  asm volatile("" : "+s"(qre));
+  bf16x8 qz[4];
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) qz[kk] = row8(qre + qbase + io + 16 * kk + 8 * s, iok);
   f32x16 dq[2] = {f32x16{}, f32x16{}};
 #pragma unroll
   for (int h2 = 0; h2 < 9; ++h2) {
@@ -304,7 +312,7 @@ __global__ __launch_bounds__(192, COEF ? 2 : 3) void k2_local_dq(const T* __rest
       for (int r = 0; r < 16; ++r) red[dt][r][l] = dq[dt][r];
   } else {
     // den-state dq of query tile it = wv: gz_i (bz_d + 2 Z[i][d]), Z = q Mz; the
-    // query fragments qf are this lane's row i = 32 it + row
+    // query fragments qz are this lane's row i = 32 it + row
     float gzr[16];
 #pragma unroll
     for (int a = 0; a < 4; ++a)
@@ -315,7 +323,7 @@ __global__ __launch_bounds__(192, COEF ? 2 : 3) void k2_local_dq(const T* __rest
       f32x16 z = f32x16{};
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk)
-        z = mfma32(qf[kk], *reinterpret_cast<const bf16x8*>(&Mz[32 * dt + row][16 * kk + 8 * s]), z);
+        z = mfma32(qz[kk], *reinterpret_cast<const bf16x8*>(&Mz[32 * dt + row][16 * kk + 8 * s]), z);
       const float bzd = bz[32 * dt + row];
 #pragma unroll
       for (int r = 0; r < 16; ++r) dq[dt][r] = fmaf(gzr[r], bzd + 2.f * z[r], dq[dt][r]);
