@@ -559,16 +559,10 @@ __global__ __launch_bounds__(128, 2) void k2_out_fwd(const T* __restrict__ q, co
     }
   }
   // accumulators start from the intra-chunk numerator
-  f32x16 acc[2];
-#pragma unroll
-  for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      // rows past N read row N - 1 and are never stored: a load inside the
-      // row test would wait for each one in turn
-      const int tok = min(tok0 + 32 * wv + c32_row(i, l), N - 1);
-      acc[nt][i] = num[qbase + (size_t)tok * kD + 32 * nt + row];
-    }
+  // the state part accumulates from zero; the intra part already in num is
+  // added in the epilogue, its loads sharing the denominators' round trip
+  // (as the accumulators' initial value the first product waited for them)
+  f32x16 acc[2] = {f32x16{}, f32x16{}};
   [&]<int... I>(std::integer_sequence<int, I...>) {
     (ring_issue<I>(pt, ring, tid), ...);
   }(std::make_integer_sequence<int, kNSR - 1>{});
@@ -580,6 +574,13 @@ __global__ __launch_bounds__(128, 2) void k2_out_fwd(const T* __restrict__ q, co
   float dv16[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) dv16[i] = den[dbase + min(tok0 + 32 * wv + c32_row(i, l), N - 1)];
+  // rows past N read row N - 1 and are never stored: a load inside the row
+  // test would wait for each one in turn
+  float nm[2][16];
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) nm[nt][i] = num[qbase + (size_t)min(tok0 + 32 * wv + c32_row(i, l), N - 1) * kD + 32 * nt + row];
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int tok = tok0 + 32 * wv + c32_row(i, l);
@@ -589,6 +590,7 @@ __global__ __launch_bounds__(128, 2) void k2_out_fwd(const T* __restrict__ q, co
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt) {
         const size_t o = qbase + (size_t)tok * kD + 32 * nt + row;
+        acc[nt][i] += nm[nt][i];
         num[o] = acc[nt][i];
         out[o] = from_f<T>(acc[nt][i] * inv);
       }
@@ -710,16 +712,10 @@ __global__ __launch_bounds__(64 * (kMaxRS + 1), 1) void k2_out_fwd_shared(
       }
     }
   }
-  f32x16 acc[2];
-#pragma unroll
-  for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      // rows past N read row N - 1 and are never stored: a load inside the
-      // row test would wait for each one in turn
-      const int tok = min(tok0 + c32_row(i, l), N - 1);
-      acc[nt][i] = num[qbase + (size_t)tok * kD + 32 * nt + row];
-    }
+  // the state part accumulates from zero; the intra part already in num is
+  // added in the epilogue, its loads sharing the denominators' round trip
+  // (as the accumulators' initial value the first product waited for them)
+  f32x16 acc[2] = {f32x16{}, f32x16{}};
   readout_group_shared<0>(x, wlh, ring, l, acc);
 
   const size_t dbase = (size_t)(b * Hq + h) * N;
@@ -728,6 +724,13 @@ __global__ __launch_bounds__(64 * (kMaxRS + 1), 1) void k2_out_fwd_shared(
   float dv16[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) dv16[i] = den[dbase + min(tok0 + c32_row(i, l), N - 1)];
+  // rows past N read row N - 1 and are never stored: a load inside the row
+  // test would wait for each one in turn
+  float nm[2][16];
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) nm[nt][i] = num[qbase + (size_t)min(tok0 + c32_row(i, l), N - 1) * kD + 32 * nt + row];
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int tok = tok0 + c32_row(i, l);
@@ -737,6 +740,7 @@ __global__ __launch_bounds__(64 * (kMaxRS + 1), 1) void k2_out_fwd_shared(
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt) {
         const size_t o = qbase + (size_t)tok * kD + 32 * nt + row;
+        acc[nt][i] += nm[nt][i];
         num[o] = acc[nt][i];
         out[o] = from_f<T>(acc[nt][i] * inv);
       }
