@@ -11,7 +11,10 @@ One JSON line on stdout:
   roofline   = dominant kernel's credited state-contraction FLOPs per launch
                / its average launch time (HIP events on its launch stream,
                recorded by the library during a second pass of the same K steps)
-               against the MI355X dense bf16 MFMA peak
+               against the MI355X dense bf16 MFMA peak (the fp32 MFMA peak for
+               --precision fp32); state_frac = the whole step's state work
+               (6 F DA B N (Hq + Hkv) FLOP) over the summed time of the
+               state kernels, the north star's figure
   cpu_baseline = the CPU oracle (oracle/grouped_oracle.py chunked fwd+bwd), one step
                of the same workload on this host's cores
 """
@@ -35,6 +38,7 @@ DA = 65  # value columns + the denominator column
 DA_MC = 64  # columns the matrix-core state kernels contract (the denominator column runs
 # apart, as a 64 x 64 pair matrix per chunk, in k2_fwd_prep / k2_den_bwd / k2_den_scan)
 BF16_PEAK_TFLOPS = 2516.6  # MI355X dense bf16 MFMA (256 CU x 2.4 GHz x 4096 FLOP/clk)
+FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X fp32 matrix (MFMA) peak
 METRIC = "OAL attn fwd+bwd tokens/s at N=4096 d=64 bf16; % bf16 MFMA peak"
 
 
@@ -44,8 +48,12 @@ def credited_flops(kernel: str, b: int, hq: int, hkv: int, n: int) -> float:
     fwd:  T_c update 2*F*DA per kv token; readout 2*F*DA per query token
     bwd:  dCarry and dphi_Q 2*F*DA each per query token; dphi_K and dU
           2*F*DA each per kv token.   Sum = 6*F*DA*B*N*(Hq+Hkv).
-    The matrix-core kernels (k2_*) are credited with the DA_MC = 64 value
-    columns they contract; the denominator column's work is done elsewhere.
+    Each contraction is credited once, to the kernel that produces its result:
+    the bf16 forward scan's segment-totals pass (k2_state_fwd_totals) contracts
+    every chunk a second time to give the replay its carries, and is credited
+    nothing. The matrix-core kernels (k2_*) are credited with the DA_MC = 64
+    value columns they contract (the denominator column runs apart); the fp32
+    route's matrix-core kernels (k3_*) contract all DA = 65 columns.
     """
     unit = 2.0 * F_LOGICAL * DA
     mc = 2.0 * F_LOGICAL * DA_MC
@@ -57,15 +65,34 @@ def credited_flops(kernel: str, b: int, hq: int, hkv: int, n: int) -> float:
         "k_state_bwd": unit * q_tok,
         "k_q_bwd": unit * q_tok,
         "k_kv_bwd": 2 * unit * kv_tok,
-        # matrix-core kernels
+        # bf16 matrix-core kernels
         "k2_state_fwd": mc * kv_tok,
-        "k2_state_fwd_totals": mc * kv_tok,
         "k2_out_fwd": mc * q_tok,
         "k2_state_bwd": mc * q_tok,
-        "k2_state_bwd_totals": mc * q_tok,
         "k2_q_fold": mc * q_tok,
         "k2_kv_fold": 2 * mc * kv_tok,
+        # fp32 matrix-core kernels
+        "k3_state_fwd": unit * kv_tok,
+        "k3_readout": unit * q_tok,
+        "k3_state_bwd": unit * q_tok,
+        "k3_fold_q": unit * q_tok,
+        "k3_fold_k": unit * kv_tok,
+        "k3_readout_v": unit * kv_tok,
     }.get(kernel, 0.0)
+
+
+# Kernels that form, scan or contract the chunk states (every launch on the
+# path from the operands to the state results, the denominator column's
+# pair-matrix kernels included); state_frac credits the whole 6*F*DA state
+# work to their summed time. The rest of a step is the intra-chunk terms,
+# the normalization VJP and the coefficient reductions.
+STATE_KERNELS = {
+    "bf16": ("k2_fwd_prep", "k2_den_fwd_scan", "k2_state_fwd_totals", "k2_state_fwd", "k2_out_fwd",
+             "k2_den_bwd", "k2_den_bwd_scan", "k2_state_bwd", "k2_state_bwd_carry", "k2_q_fold", "k2_kv_fold"),
+    "fp32": ("k3_state_fwd", "k3_readout", "k3_state_bwd", "k3_seg_carry", "k3_fold_q", "k3_fold_k",
+             "k3_readout_v"),
+}
+PEAK_TFLOPS = {"bf16": BF16_PEAK_TFLOPS, "fp32": FP32_MFMA_PEAK_TFLOPS}
 
 
 def measured_traffic(kernel: str, b: int, n: int):
@@ -260,6 +287,79 @@ def bench_model(args) -> int:
     return 0
 
 
+def bench_pairwise(args) -> int:
+    """The reference-contract HD Function with logical per-pair coefficients
+    (a [Hq], b [Hq, 64], c [Hq, 2080]; one group per dimension, so the
+    intra-chunk local score runs in feature form) through a bf16_tensorcore
+    plan, fwd+bwd at the configuration-2 shape. q, k, v as in configuration 2;
+    the coefficients come from a random lower-triangular factor over [1, x]
+    (x = scale q o k), so every denominator is positive and the plan's
+    positivity check (two host syncs per forward, as the reference) passes.
+    """
+    from oal_amd import _native
+    from oal_amd.hd_block_gemm import build_hd_block_gemm_plan, canonical_pair_layout
+    from oal_amd.hd_block_gemm_autograd import _hd_parallel_block_gemm_autograd
+
+    dev = torch.device("cuda:0")
+    b, n = args.batch, args.seq_len
+    hq, d = 14, 64
+    base = make_inputs(b, n, dev)
+    gen = torch.Generator().manual_seed(5)
+    rows, cols = torch.tril_indices(d, d)
+    av, bv, cv = [], [], []
+    for _ in range(hq):
+        low = torch.tril(torch.randn(d + 1, d + 1, generator=gen, dtype=torch.float64) * 0.08)
+        low.diagonal().copy_(0.4 + 0.3 * torch.rand(d + 1, generator=gen, dtype=torch.float64))
+        m = low @ low.T
+        av.append(m[0, 0] + 1e-3)
+        bv.append(2 * m[0, 1:])
+        cv.append(m[1:, 1:][rows, cols])
+    coefs = [torch.stack(x).float().to(dev).requires_grad_() for x in (av, bv, cv)]
+    ts = [base["q"], base["k"], base["v"], *coefs]
+    plan = build_hd_block_gemm_plan(ts[0], ts[1], ts[2], precision="bf16_tensorcore",
+                                    requested_gradient_mask=(True,) * 6)
+    layout = canonical_pair_layout(d)
+
+    def one():
+        for t in ts:
+            t.grad = None
+        out, _, _ = _hd_parallel_block_gemm_autograd(*ts, scale=d ** -0.5, eps=1e-30, layout=layout, plan=plan)
+        out.backward(base["dout"])
+
+    for _ in range(args.warmup):
+        one()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        one()
+    torch.cuda.synchronize()
+    sec = (time.perf_counter() - t0) / args.steps
+    _native.profile_collect()
+    _native.profile_enable(True)
+    for _ in range(args.steps):
+        one()
+    torch.cuda.synchronize()
+    _native.profile_enable(False)
+    kernels = _native.profile_collect()
+    result = {
+        "metric": "OAL HD Function (per-pair coefficients, bf16_tensorcore plan) fwd+bwd tokens/s",
+        "value": round(b * n / sec, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(sec * 1e3, 4),
+        "higher_is_better": True,
+        "dtype": "bf16",
+        "data": "synthetic (configuration-2 q, k, v; per-pair coefficients from a random PSD factor over [1, x])",
+        "config": {"workload": "reference-contract HD Function, per-pair coefficients", "batch": b, "q_heads": hq,
+                   "kv_heads": 2, "seq_len": n, "head_dim": d, "groups": d},
+        "kernels": {k_: {"launches": c, "avg_ms": round(t / max(c, 1), 4)} for k_, (c, t) in kernels.items()},
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -274,9 +374,10 @@ def main() -> int:
     ap.add_argument("--cpu-materialized", action="store_true",
                     help="also time the materializing reference algorithm at B=1, N=512 and 1024 (about a minute)")
     ap.add_argument(
-        "--workload", choices=("attention", "model"), default="attention",
+        "--workload", choices=("attention", "model", "pairwise"), default="attention",
         help="attention: the OAL operator fwd+bwd (BASELINE config 2, the headline metric); "
-             "model: one LoRA training step of the Qwen-shaped OAL model (BASELINE config 4)",
+             "model: one LoRA training step of the Qwen-shaped OAL model (BASELINE config 4); "
+             "pairwise: the reference-contract HD Function with per-pair coefficients",
     )
     ap.add_argument(
         "--copy-calibration-mib", type=int, default=0,
@@ -295,6 +396,8 @@ def main() -> int:
 
     if args.workload == "model":
         return bench_model(args)
+    if args.workload == "pairwise":
+        return bench_pairwise(args)
 
     from oal_amd import _native
 
@@ -344,7 +447,13 @@ def main() -> int:
     dom_avg_s = kernels[dominant][1] / kernels[dominant][0] * 1e-3
     dom_flops = credited_flops(dominant, b, 14, 2, n)
     achieved = dom_flops / dom_avg_s / 1e12
+    peak = PEAK_TFLOPS[args.precision]
     total_credited = 6.0 * F_LOGICAL * DA * b * n * (14 + 2)
+    # the north star's own figure: the whole state work over the summed time of
+    # the state kernels (per-step averages of the event-timed pass)
+    state_names = [k_ for k_ in STATE_KERNELS[args.precision] if k_ in kernels]
+    state_ms = sum(kernels[k_][1] for k_ in state_names) / args.steps
+    state_tflops = total_credited / (state_ms * 1e-3) / 1e12 if state_ms > 0 else 0.0
 
     result = {
         "metric": METRIC,
@@ -377,13 +486,18 @@ def main() -> int:
             "bound": "mfma",
             "kernel": dominant,
             "achieved": round(achieved, 3),
-            "peak": BF16_PEAK_TFLOPS,
+            "peak": peak,
             "unit": "TFLOP/s",
-            "frac": round(achieved / BF16_PEAK_TFLOPS, 5),
-            "traffic": measured_traffic(dominant, b, n),
+            "frac": round(achieved / peak, 5),
+            "traffic": measured_traffic(dominant, b, n) if args.precision == "bf16" else None,
             "traffic_unit": "bytes per launch (profiles/config2_traffic.json)",
+            "peak_kind": "dense bf16 MFMA" if args.precision == "bf16" else "fp32 MFMA",
+            "state_kernels": state_names,
+            "state_ms_per_step": round(state_ms, 4),
+            "state_credited_tflops": round(state_tflops, 3),
+            "state_frac": round(state_tflops / peak, 5),
             "step_credited_tflops": round(total_credited / sec / 1e12, 3),
-            "step_frac": round(total_credited / sec / 1e12 / BF16_PEAK_TFLOPS, 5),
+            "step_frac": round(total_credited / sec / 1e12 / peak, 5),
         },
         "kernels": per_kernel,
     }

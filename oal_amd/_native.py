@@ -4,6 +4,11 @@ PyTorch supplies device memory and the current HIP stream; every byte of the
 operator's arithmetic runs in the HIP kernels behind this library. There is no
 fallback: if the library is missing or the tensors are not on a ROCm device,
 the call raises.
+
+Each call sits in a ``torch.profiler.record_function`` range
+("oal_amd::forward", "oal_amd::backward"), and the library brackets its own
+launches with roctx ranges, as the reference brackets its stages
+(``oal_attention/hd_block_gemm_profiling.py:195-226``).
 """
 
 from __future__ import annotations
@@ -290,7 +295,7 @@ def forward(q, k, v, labels, c0, lam, gam, *, scale: float, floor: float, precis
     q, k, v = (_aligned(t) for t in (q, k, v))
     code = _dtype_code(q.dtype)
     dev = q.device
-    with torch.cuda.device(dev):
+    with torch.cuda.device(dev), torch.profiler.record_function("oal_amd::forward"):
         nbytes = lib.oal_forward_saved_bytes(b, hq, hkv, n, groups, code, pcode)
         if nbytes == 0:
             _check(1, lib, "oal_forward_saved_bytes")
@@ -329,7 +334,7 @@ def backward(q, k, v, labels, c0, lam, gam, num, den, saved, dout, dnum, dden, *
     _require_device(q)
     code = _dtype_code(q.dtype)
     dev = q.device
-    with torch.cuda.device(dev):
+    with torch.cuda.device(dev), torch.profiler.record_function("oal_amd::backward"):
         sbytes = lib.oal_forward_saved_bytes(b, hq, hkv, n, groups, code, pcode)
         wbytes = lib.oal_backward_workspace_bytes(b, hq, hkv, n, groups, code, pcode)
         if sbytes == 0 or wbytes == 0:

@@ -45,6 +45,12 @@ def compile_flags() -> list[str]:
     ]
 
 
+def link_flags() -> list[str]:
+    rocm = os.path.dirname(os.path.dirname(os.path.realpath(hipcc())))
+    libdir = os.path.join(rocm, "lib")
+    return ["-L" + libdir, "-Wl,-rpath," + libdir, "-lrocprofiler-sdk-roctx"]
+
+
 def _run(cmd: list[str], verbose: bool) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
@@ -65,7 +71,8 @@ def build(verbose: bool = False) -> str:
         for fut in [pool.submit(_run, j, verbose) for j in jobs]:
             fut.result()
     tmp = OUTPUT + ".tmp"
-    _run([cc, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp], verbose)
+    # librocprofiler-sdk-roctx: the host-side stage ranges (roctx) of every launch
+    _run([cc, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp, *link_flags()], verbose)
     os.replace(tmp, OUTPUT)
     return OUTPUT
 

@@ -17,8 +17,10 @@
 //   dwq_part [B][Hq][NB][kFP], dwq [Hq][kFP]         feature-coefficient gradients
 
 #include <hip/hip_runtime.h>
+#include <rocprofiler-sdk-roctx/roctx.h>
 #include <stdint.h>
 
+#include <atomic>
 #include <cstdio>
 #include <cstring>
 #include <map>
@@ -739,12 +741,14 @@ int launch_status(const char* what) {
 
 // Opt-in per-kernel timing: each launch is bracketed by HIP events recorded
 // on its own stream; oal_profile_collect() waits for them and aggregates.
+// The switch is atomic, so a launch with timing off takes no lock; the record
+// list and the event pool are guarded by g_prof_mu.
 struct ProfRecord {
   const char* name;
   hipEvent_t start, stop;
 };
 std::mutex g_prof_mu;
-bool g_prof_on = false;
+std::atomic<bool> g_prof_on{false};
 std::vector<ProfRecord> g_prof_records;
 std::vector<hipEvent_t> g_prof_pool;
 
@@ -759,13 +763,27 @@ hipEvent_t prof_event() {
   return e;
 }
 
+// Host-side stage ranges (roctx): every launch sits in a range named after its
+// kernel, inside a range per entry point ("oal_forward", "oal_backward"), so a
+// profiler's marker trace (rocprofv3 --marker-trace) shows the stages of a call
+// next to its kernels, as the reference brackets its stages with
+// record_function (oal_attention/hd_block_gemm_profiling.py:195-226). Without a
+// profiler attached a range costs a call into an empty dispatch.
+struct Range {
+  explicit Range(const char* name) { roctxRangePushA(name); }
+  ~Range() { roctxRangePop(); }
+  Range(const Range&) = delete;
+  Range& operator=(const Range&) = delete;
+};
+
 template <typename F>
 void timed(const char* name, hipStream_t st, F&& launch) {
-  std::lock_guard<std::mutex> lock(g_prof_mu);
-  if (!g_prof_on) {
+  Range range(name);
+  if (!g_prof_on.load(std::memory_order_acquire)) {
     launch();
     return;
   }
+  std::lock_guard<std::mutex> lock(g_prof_mu);
   hipEvent_t a = prof_event(), b = prof_event();
   if (a) hipEventRecord(a, st);
   launch();
@@ -911,7 +929,7 @@ int oal_abi_version(void) { return 2; }
 
 int oal_profile_enable(int enable) {
   std::lock_guard<std::mutex> lock(g_prof_mu);
-  g_prof_on = enable != 0;
+  g_prof_on.store(enable != 0, std::memory_order_release);
   return 0;
 }
 
@@ -992,6 +1010,7 @@ int oal_forward(const void* q, const void* k, const void* v, const int32_t* labe
                 const float* lam, const float* gam, int groups, int batch, int q_heads, int kv_heads, int seq_len,
                 int dtype, int precision, float scale, float floor, void* out, float* num, float* den, void* saved,
                 void* stream) {
+  Range range("oal_forward");
   Geometry g;
   if (check_geometry(batch, q_heads, kv_heads, seq_len, dtype, &g)) return 1;
   if (!q || !k || !v || !labels || !c0 || !lam || !gam || !out || !num || !den || !saved)
@@ -1026,6 +1045,7 @@ int oal_backward(const void* q, const void* k, const void* v, const int32_t* lab
                  int dtype, int precision, float scale, float floor, const float* num, const float* den,
                  const void* saved, const void* dout, const float* dnum, const float* dden, void* dq, void* dk,
                  void* dv, float* dc0, float* dlam, float* dgam, void* workspace, void* stream) {
+  Range range("oal_backward");
   Geometry g;
   if (check_geometry(batch, q_heads, kv_heads, seq_len, dtype, &g)) return 1;
   if (!q || !k || !v || !labels || !c0 || !lam || !gam || !num || !den || !saved || !workspace)

@@ -884,14 +884,12 @@ void launch_mfma_forward(const LaunchGeom& g, const void* q, const void* k, cons
                          sv.KAP);
   });
   timed("k2_out_fwd", st, [&] {
-#ifndef OAL_OUT_PER_HEAD
     // up to kMaxRS query heads per kv head: the heads share each copy of P_c
     if (g.R <= kMaxRS) {
       hipLaunchKernelGGL(k2_out_fwd_shared<T>, dim3(2 * g.NB * g.U), dim3(64 * (g.R + 1)), 0, st, qt, sv.wqs, sv.PR,
                          g.Hq, g.Hkv, g.N, g.NB, floor, static_cast<T*>(out), num, den);
       return;
     }
-#endif
     hipLaunchKernelGGL(k2_out_fwd<T>, dim3(g.R * g.NB * g.U), dim3(128), 0, st, qt, sv.wqs, sv.PR, g.Hq, g.Hkv, g.N,
                        g.NB, floor, static_cast<T*>(out), num, den);
   });

@@ -19,6 +19,8 @@ from math import ceil
 import torch
 
 _PRECISIONS = ("fp32_ieee", "bf16_tensorcore")
+# Token block (chunk) of every HIP kernel, liboal_amd.so's oal_chunk_size().
+KERNEL_TOKEN_BLOCK = 64
 
 
 @dataclass(frozen=True)
@@ -77,7 +79,7 @@ class HDParallelBlockPlan:
     model_residency_bytes: int
     options: tuple[tuple[str, object], ...]
     require_positive_denominator: bool = True
-    physical_token_block: int = 64
+    requested_token_block: int | None = None
     feature_dimension: int = field(init=False)
     pair_count: int = field(init=False)
     number_blocks: int = field(init=False)
@@ -154,6 +156,11 @@ def build_hd_block_gemm_plan(
         raise ValueError("feature_wave_blocks must be a positive int")
     if feature_wave_blocks > nb:
         raise ValueError("feature_wave_blocks cannot exceed the number of blocks")
+    # the kernels run one token block, KERNEL_TOKEN_BLOCK (the library's
+    # oal_chunk_size()); the plan reports that block and its block count, and
+    # keeps the caller's request (results do not depend on the block size;
+    # feature_wave_blocks, at most the requested block count, is at most the
+    # kernel's as well)
     if precision not in _PRECISIONS:
         raise ValueError(f"precision must be one of {_PRECISIONS}")
     mask = tuple(bool(x) for x in requested_gradient_mask)
@@ -170,13 +177,13 @@ def build_hd_block_gemm_plan(
         device=str(q.device),
         precision=precision,
         requested_gradient_mask=mask,
-        token_block=token_block,
+        token_block=KERNEL_TOKEN_BLOCK,
         feature_wave_blocks=feature_wave_blocks,
         memory_budget_bytes=memory_budget_bytes,
         model_residency_bytes=model_residency_bytes,
         options=tuple(sorted((k_, v_ if not isinstance(v_, list) else tuple(v_)) for k_, v_ in options.items())),
         require_positive_denominator=bool(require_positive_denominator),
-        physical_token_block=64,
+        requested_token_block=token_block,
     )
 
 

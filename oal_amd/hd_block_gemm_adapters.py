@@ -32,12 +32,7 @@ from .grouped_quadratic import (
     _validate_qkv,
 )
 from .hd_block_gemm import HDParallelBlockPlan, build_hd_block_gemm_plan, canonical_pair_layout
-from .hd_block_gemm_autograd import (
-    _hd_parallel_block_gemm,
-    _hd_parallel_block_gemm_autograd,
-    _require_positive_denominator,
-    grouped_oal,
-)
+from .hd_block_gemm_autograd import _require_positive_denominator, grouped_oal
 
 _POSITIVE_FP32_FLOOR = torch.finfo(torch.float32).tiny * torch.finfo(torch.float32).eps
 
@@ -116,7 +111,6 @@ def prepare_grouped_hd_block_gemm(
         require_positive_denominator=require_positive_denominator, **options,
     )
     full = (groups.unsqueeze(0).expand(q.shape[1], -1) if groups.ndim == 1 else groups).detach().clone()
-    canonical_pair_layout(plan.head_dimension)
     return _PreparedGroupedHdBlockGemm(
         plan=plan,
         groups=full,
@@ -153,13 +147,6 @@ def run_prepared_grouped_hd_block_gemm(prepared, q, k, v, factor):
     if plan.require_positive_denominator:
         _require_positive_denominator(den)
     return out, num, den
-
-
-def _run_logical_coefficients(q, k, v, a, b, c, *, plan, scale, normalization_floor):
-    """Logical (a, b, c) route through the reference-contract Function."""
-    layout = canonical_pair_layout(plan.head_dimension)
-    run = _hd_parallel_block_gemm_autograd if any(plan.requested_gradient_mask) else _hd_parallel_block_gemm
-    return run(q, k, v, a, b, c, scale=scale, eps=normalization_floor, layout=layout, plan=plan)
 
 
 def grouped_causal_attention(q, k, v, dim_groups, factor, **kwargs):

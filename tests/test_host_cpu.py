@@ -35,6 +35,10 @@ def test_library_loads_and_exports_every_declared_symbol():
     assert loaded.oal_feature_count() == 2145
     assert loaded.oal_feature_stride() % 64 == 0
     assert loaded.oal_chunk_size() > 0
+    # the plan reports the token block the kernels run
+    from oal_amd.hd_block_gemm import KERNEL_TOKEN_BLOCK
+
+    assert loaded.oal_chunk_size() == KERNEL_TOKEN_BLOCK
 
 
 def test_size_queries_and_argument_errors_without_a_gpu():
@@ -151,6 +155,15 @@ def test_plan_records_caller_options_and_pair_layout():
     assert plan.number_blocks == 1 and plan.gqa_ratio == 2 and plan.pair_count == 10
     with pytest.raises(ValueError, match="precision"):
         build_hd_block_gemm_plan(q, k, v, precision="tf32", requested_gradient_mask=(False,) * 6)
+    # a request of 128 (the reference planner's default) is recorded; the plan
+    # reports the kernels' token block and its block count
+    q2 = torch.zeros((1, 2, 300, 4))
+    k2 = torch.zeros((1, 1, 300, 4))
+    plan128 = build_hd_block_gemm_plan(q2, k2, k2, token_block=128, feature_wave_blocks=3,
+                                       requested_gradient_mask=(True,) * 6)
+    assert plan128.requested_token_block == 128
+    assert plan128.token_block == 64 and plan128.number_blocks == 5
+    assert plan128.feature_wave_blocks == 3
     layout = canonical_pair_layout(64)
     assert layout.pair_count == 2080
     assert layout.rows[:4] == (0, 1, 1, 2) and layout.columns[:4] == (0, 0, 1, 0)

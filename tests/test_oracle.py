@@ -149,6 +149,55 @@ def test_closed_form_chunked_backward_matches_autograd(use_dnum):
     torch.testing.assert_close(dgam, gam.grad, atol=1e-10, rtol=1e-9)
 
 
+def _floor_between(den: torch.Tensor, quantile: float) -> float:
+    """A floor between two sorted denominators near the given quantile, at the
+    middle of the widest gap there, so that no denominator sits on it."""
+    vals = den.detach().flatten().sort().values
+    lo = int(quantile * (vals.numel() - 1))
+    window = range(max(lo - 8, 0), min(lo + 8, vals.numel() - 1))
+    best = max(window, key=lambda i: float(vals[i + 1] - vals[i]))
+    return float(0.5 * (vals[best] + vals[best + 1]))
+
+
+def test_floor_branch_matches_autograd_of_clamped_denominator():
+    # reference hd_block_gemm_normalization_ops.py:13-71: out = num / max(den, eps), and the
+    # VJP masks the dout part of the denominator gradient where den < eps (the gradient of
+    # clamp_min), while dden is added unmasked
+    q, k, v, labels, _ = _random_case(seed=11)
+    gen = torch.Generator().manual_seed(4)
+    c0 = torch.rand(4, generator=gen, dtype=torch.float64) + 2
+    lam = torch.rand((4, 3), generator=gen, dtype=torch.float64)
+    g0 = torch.rand((4, 3, 3), generator=gen, dtype=torch.float64)
+    gam = 0.5 * (g0 + g0.transpose(-1, -2))
+    qa, ka, va = (t.clone().requires_grad_() for t in (q, k, v))
+    c0a, lama, gama = (t.clone().requires_grad_() for t in (c0, lam, gam))
+    scale = 0.3
+    num, den = go.dense_forward_coefficients(qa, ka, va, labels, c0a, lama, gama, scale=scale)
+    floor = _floor_between(den, 0.4)
+    below = int((den < floor).sum())
+    assert 0.2 * den.numel() < below < 0.6 * den.numel()
+    out = num / den.clamp_min(floor)
+    dout = torch.randn(out.shape, generator=gen, dtype=torch.float64)
+    dnum = torch.randn(num.shape, generator=gen, dtype=torch.float64)
+    dden = torch.randn(den.shape, generator=gen, dtype=torch.float64)
+    ((out * dout).sum() + (num * dnum).sum() + (den * dden).sum()).backward()
+    wq = go.feature_coefficients(labels, c0, lam, gam, scale=scale, head_dim=6)
+    out_c, num_c, den_c = go.chunked_forward(q, k, v, wq, chunk=4, floor=floor)
+    torch.testing.assert_close(out_c, out.detach(), atol=1e-12, rtol=1e-11)
+    dq, dk, dv, dwq = go.chunked_backward(q, k, v, wq, num_c, den_c, dout, dnum, dden, chunk=4, floor=floor)
+    torch.testing.assert_close(dq, qa.grad, atol=1e-10, rtol=1e-9)
+    torch.testing.assert_close(dk, ka.grad, atol=1e-10, rtol=1e-9)
+    torch.testing.assert_close(dv, va.grad, atol=1e-10, rtol=1e-9)
+    dc0, dlam, dgam = go.coefficient_gradients_from_wq(dwq, labels, 3, scale=scale, head_dim=6)
+    torch.testing.assert_close(dc0, c0a.grad, atol=1e-10, rtol=1e-9)
+    torch.testing.assert_close(dlam, lama.grad, atol=1e-10, rtol=1e-9)
+    torch.testing.assert_close(dgam, gama.grad, atol=1e-10, rtol=1e-9)
+    # the mask matters: without it (the floor's gradient passed through) dq differs
+    dq0, _, _, _ = go.chunked_backward(q, k, v, wq, num_c, den_c.clamp_min(floor), dout, dnum, dden, chunk=4,
+                                       floor=0.0)
+    assert (dq0 - qa.grad).abs().max() > 1e-3
+
+
 def test_factor_expansion_known_answer():
     # tests/operators/test_grouped_quadratic.py:476-488
     factor = torch.tensor((1.1, 0.5, 0.9, 0.4, 0.8, 0.7), dtype=torch.float64)

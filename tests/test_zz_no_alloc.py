@@ -3,8 +3,10 @@
 Called through the C ABI with ctypes. Two calls in a row on one device, the
 second with a smaller input (the static scratch keeps the first call's
 contents), each compared with oal_backward on the same inputs and a
-caller-allocated workspace: bitwise on the bf16 matrix-core path (fixed-order
-reductions), and to 1e-6 rel-L2 on the fp32 route. A geometry whose workspace
+caller-allocated workspace, bitwise (every reduction of both routes has a fixed
+order), for 8 groups, 12 groups and per-pair coefficients (64 groups), whose
+workspaces differ (the per-pair bf16 layout adds per-head dk partials and local
+slot partials; more than 8 groups run the fp32 route's scalar kernels). A geometry whose workspace
 exceeds the 256 MiB scratch is refused with an error before anything runs.
 """
 
@@ -25,14 +27,36 @@ def _dev():
     return torch.device("cuda:0")
 
 
-def _inputs(b, n, dtype, seed, dev):
-    inp = go.config_inputs(1, batch=b, seq_len=n, seed=seed)
-    q, k, v = (inp[x].to(dtype).to(dev).contiguous() for x in ("q", "k", "v"))
-    labels, c0, lam, gam = (inp[x].to(dev).contiguous() for x in ("groups", "c0", "lam", "gam"))
+def _inputs(b, n, dtype, seed, dev, gcount=8):
+    """8 groups: the configuration-1 inputs; 12 groups: random labels and a factor;
+    64 groups: labels d -> d (the per-pair layout, whose bf16 workspace adds the
+    per-head dk partials and the local slot partials)."""
+    if gcount == 8:
+        inp = go.config_inputs(1, batch=b, seq_len=n, seed=seed)
+        q, k, v = (inp[x].to(dtype).to(dev).contiguous() for x in ("q", "k", "v"))
+        labels, c0, lam, gam = (inp[x].to(dev).contiguous() for x in ("groups", "c0", "lam", "gam"))
+        scale = inp["scale"]
+    else:
+        gen = torch.Generator().manual_seed(seed)
+        q = (torch.randn((b, 14, n, 64), generator=gen) * 0.6).to(dtype).to(dev)
+        k = (torch.randn((b, 2, n, 64), generator=gen) * 0.6).to(dtype).to(dev)
+        v = torch.randn((b, 2, n, 64), generator=gen).to(dtype).to(dev)
+        if gcount == 64:
+            labels = torch.arange(64, dtype=torch.int32).unsqueeze(0).expand(14, -1).contiguous()
+        else:
+            labels = torch.randint(0, gcount, (14, 64), generator=gen, dtype=torch.int32)
+            labels[:, :gcount] = torch.arange(gcount, dtype=torch.int32)
+        side = gcount + 1
+        factor = torch.randn((14, side * (side + 1) // 2), generator=gen, dtype=torch.float64)
+        factor *= 0.05 if gcount == 64 else 0.3
+        c0, lam, gam = (t.float().to(dev).contiguous()
+                        for t in go.expand_factor(factor, query_heads=14, kernel_eps=0.05))
+        labels = labels.to(dev)
+        scale = 0.125
     gen = torch.Generator().manual_seed(seed + 1)
     dout = torch.randn(q.shape, generator=gen).to(dtype).to(dev)
     dden = torch.randn(q.shape[:3] + (1,), generator=gen).to(dev)
-    return q, k, v, labels, c0, lam, gam, inp["scale"], dout, dden
+    return q, k, v, labels, c0, lam, gam, scale, dout, dden
 
 
 def _noalloc(lib, q, k, v, labels, c0, lam, gam, num, den, saved, dout, dden, scale, precision):
@@ -54,13 +78,16 @@ def _rel(a, b):
     return float((a.double() - b.double()).norm() / b.double().norm())
 
 
-@pytest.mark.parametrize("precision,dtype", [("bf16", torch.bfloat16), ("fp32", torch.float32)])
-def test_noalloc_backward_matches_the_workspace_entry_point(precision, dtype):
+@pytest.mark.parametrize("precision,dtype,gcount", [
+    ("bf16", torch.bfloat16, 8), ("fp32", torch.float32, 8), ("bf16", torch.bfloat16, 12),
+    ("fp32", torch.float32, 12), ("bf16", torch.bfloat16, 64), ("fp32", torch.float32, 64)])
+def test_noalloc_backward_matches_the_workspace_entry_point(precision, dtype, gcount):
     dev = _dev()
     lib = _native.load_library()
-    for call, (b, n, seed) in enumerate(((1, 1024, 3), (1, 200, 4))):
-        print(f"noalloc call {call}: precision={precision} B={b} N={n}", flush=True)
-        q, k, v, labels, c0, lam, gam, scale, dout, dden = _inputs(b, n, dtype, seed, dev)
+    shapes = ((1, 1024, 3), (1, 200, 4)) if gcount <= 12 else ((1, 640, 3), (1, 130, 4))
+    for call, (b, n, seed) in enumerate(shapes):
+        print(f"noalloc call {call}: precision={precision} groups={gcount} B={b} N={n}", flush=True)
+        q, k, v, labels, c0, lam, gam, scale, dout, dden = _inputs(b, n, dtype, seed, dev, gcount)
         _, num, den, saved = _native.forward(q, k, v, labels, c0, lam, gam, scale=scale, floor=0.0,
                                              precision=precision)
         want = _native.backward(q, k, v, labels, c0, lam, gam, num, den, saved, dout, None, dden, scale=scale,
@@ -70,10 +97,8 @@ def test_noalloc_backward_matches_the_workspace_entry_point(precision, dtype):
         torch.cuda.synchronize()
         for name, g, w in zip(("dq", "dk", "dv", "dc0", "dlam", "dgam"), got, want):
             assert torch.isfinite(g.float()).all(), name
-            if precision == "bf16":
-                assert torch.equal(g, w), (call, name, _rel(g, w))
-            else:
-                assert _rel(g, w) <= 1e-6, (call, name, _rel(g, w))
+            # every reduction of both routes has a fixed order: bitwise
+            assert torch.equal(g, w), (call, name, _rel(g, w))
 
 
 def test_noalloc_refuses_a_geometry_beyond_the_scratch():
