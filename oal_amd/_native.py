@@ -282,11 +282,15 @@ def selftest() -> int:
     return int(errors.item())
 
 
-def forward(q, k, v, labels, c0, lam, gam, *, scale: float, floor: float, precision: str = "fp32"):
+def forward(q, k, v, labels, c0, lam, gam, *, scale: float, floor: float, precision: str = "fp32",
+            zero_saved: bool = False):
     """Run the HIP forward. q [B,Hq,N,64], k/v [B,Hkv,N,64] contiguous, same dtype;
     labels int32 [Hq,64]; c0 [Hq], lam [Hq,G], gam [Hq,G,G] float32.
 
-    Returns (out [dtype], num f32, den f32 [B,Hq,N,1], saved uint8).
+    Returns (out [dtype], num f32, den f32 [B,Hq,N,1], saved uint8). The kernels
+    leave the saved state's alignment gaps and padding tails unwritten;
+    ``zero_saved`` allocates it zero-filled, so that every byte is defined (the
+    registered operator's output, which tracing compares bytewise).
     """
     lib = load_library()
     b, hq, hkv, n, groups = check_forward_args(q, k, v, labels, c0, lam, gam)
@@ -302,7 +306,7 @@ def forward(q, k, v, labels, c0, lam, gam, *, scale: float, floor: float, precis
         out = torch.empty((b, hq, n, HEAD_DIM), dtype=q.dtype, device=dev)
         num = torch.empty((b, hq, n, HEAD_DIM), dtype=torch.float32, device=dev)
         den = torch.empty((b, hq, n, 1), dtype=torch.float32, device=dev)
-        saved = torch.empty((nbytes,), dtype=torch.uint8, device=dev)
+        saved = (torch.zeros if zero_saved else torch.empty)((nbytes,), dtype=torch.uint8, device=dev)
         rc = lib.oal_forward(
             _ptr(q), _ptr(k), _ptr(v), _ptr(labels), _ptr(c0), _ptr(lam), _ptr(gam), groups,
             b, hq, hkv, n, code, pcode, float(scale), float(floor),
