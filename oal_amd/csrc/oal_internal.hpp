@@ -77,12 +77,24 @@ struct MfmaWork {
 // pairwise: more than 8 groups (the per-pair path's local buffers)
 MfmaWork mfma_work_view(void* base, int B, int Hq, int U, int N, int NB, bool pairwise);
 
+// Independent kernels of one entry point may run on a second stream of the
+// device: aux_stream(st) is that stream (default priority, created once per
+// device), or st itself when per-kernel timing is on (timed kernels never
+// overlap) or the stream cannot be had; stream_wait(w, s) makes stream w wait
+// for the work enqueued on s so far (a fork or a join; both are captured into
+// a graph like any stream dependency).
+hipStream_t aux_stream(hipStream_t st);
+void stream_wait(hipStream_t waiter, hipStream_t signaller);
+
+// aux: a second stream for the kernels that do not depend on each other (the
+// intra-chunk VJP beside the state scan, the key-side fold beside the query
+// side), or st to run every kernel on st.
 template <typename T>
 int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, const void* v, const int32_t* labels,
                          const float* c0, const float* lam, const float* gam, int groups, float scale, float floor,
                          const float* num, const float* den, const void* saved, const void* dout, const float* dnum,
                          const float* dden, void* dq, void* dk, void* dv, float* dc0, float* dlam, float* dgam,
-                         void* workspace, hipStream_t st, const Timer& timed);
+                         void* workspace, hipStream_t st, hipStream_t aux, const Timer& timed);
 
 struct LocalBwdArgs {
   const uint16_t* G16;

@@ -800,6 +800,74 @@ bool use_mfma(int precision, int groups, const Geometry& g) {
 
 oal::LaunchGeom launch_geom(const Geometry& g) { return oal::LaunchGeom{g.B, g.Hq, g.Hkv, g.N, g.NB, g.U, g.R}; }
 
+// Second stream and fork/join events per device, created on first use and kept
+// until the process ends. An event is recorded on the signalling stream and
+// waited for at once; the ring is long enough that an event is recorded again
+// only after its earlier waits were enqueued (a wait takes the record at the
+// time it is enqueued).
+constexpr int kAuxDevices = 64;
+constexpr int kAuxEvents = 64;
+struct AuxState {
+  hipStream_t stream = nullptr;
+  hipEvent_t events[kAuxEvents] = {};
+  unsigned next = 0;
+  bool failed = false;
+};
+std::mutex g_aux_mu;
+AuxState g_aux[kAuxDevices];
+
+}  // namespace
+
+namespace oal {
+
+hipStream_t aux_stream(hipStream_t st) {
+  if (g_prof_on.load(std::memory_order_acquire)) return st;
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kAuxDevices) return st;
+  if (st) {
+    int sdev = -1;
+    if (hipStreamGetDevice(st, &sdev) != hipSuccess || sdev != dev) return st;
+  }
+  std::lock_guard<std::mutex> lock(g_aux_mu);
+  AuxState& a = g_aux[dev];
+  if (a.failed) return st;
+  if (!a.stream) {
+    // the stream and its events are not created while st is being captured
+    // into a graph (that call then runs on st alone)
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (st && (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)) {
+      (void)hipGetLastError();
+      return st;
+    }
+    bool ok = hipStreamCreateWithFlags(&a.stream, hipStreamNonBlocking) == hipSuccess;
+    for (int i = 0; ok && i < kAuxEvents; ++i)
+      ok = hipEventCreateWithFlags(&a.events[i], hipEventDisableTiming) == hipSuccess;
+    if (!ok) {
+      a.failed = true;
+      (void)hipGetLastError();
+      return st;
+    }
+  }
+  return a.stream;
+}
+
+void stream_wait(hipStream_t waiter, hipStream_t signaller) {
+  int dev = -1;
+  (void)hipGetDevice(&dev);
+  hipEvent_t ev = nullptr;
+  {
+    std::lock_guard<std::mutex> lock(g_aux_mu);
+    AuxState& a = g_aux[dev];
+    ev = a.events[a.next++ % kAuxEvents];
+  }
+  (void)hipEventRecord(ev, signaller);
+  (void)hipStreamWaitEvent(waiter, ev, 0);
+}
+
+}  // namespace oal
+
+namespace {
+
 oal::Timer make_timer() {
   return [](const char* name, hipStream_t st, const std::function<void()>& launch) { timed(name, st, launch); };
 }
@@ -1040,11 +1108,18 @@ int oal_forward(const void* q, const void* k, const void* v, const int32_t* labe
   return forward_impl<uint16_t, 64>(g, q, k, v, labels, c0, lam, gam, groups, scale, floor, out, num, den, saved, st);
 }
 
-int oal_backward(const void* q, const void* k, const void* v, const int32_t* labels, const float* c0,
-                 const float* lam, const float* gam, int groups, int batch, int q_heads, int kv_heads, int seq_len,
-                 int dtype, int precision, float scale, float floor, const float* num, const float* den,
-                 const void* saved, const void* dout, const float* dnum, const float* dden, void* dq, void* dk,
-                 void* dv, float* dc0, float* dlam, float* dgam, void* workspace, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// The backward of both entry points; may_fork: the matrix-core path may put
+// independent kernels on the device's second stream (the allocation-free entry
+// point keeps every kernel on the caller's stream).
+int backward_entry(const void* q, const void* k, const void* v, const int32_t* labels, const float* c0,
+                   const float* lam, const float* gam, int groups, int batch, int q_heads, int kv_heads, int seq_len,
+                   int dtype, int precision, float scale, float floor, const float* num, const float* den,
+                   const void* saved, const void* dout, const float* dnum, const float* dden, void* dq, void* dk,
+                   void* dv, float* dc0, float* dlam, float* dgam, void* workspace, void* stream, bool may_fork) {
   Range range("oal_backward");
   Geometry g;
   if (check_geometry(batch, q_heads, kv_heads, seq_len, dtype, &g)) return 1;
@@ -1061,15 +1136,16 @@ int oal_backward(const void* q, const void* k, const void* v, const int32_t* lab
     if ((dk != nullptr) != (dv != nullptr))
       return fail("oal_backward: dk and dv must be requested together on the matrix-core path");
     const oal::LaunchGeom lg = launch_geom(g);
+    const hipStream_t aux = may_fork ? oal::aux_stream(st) : st;
     int rc;
     if (dtype == OAL_DTYPE_F32)
       rc = oal::launch_mfma_backward<float>(lg, q, k, v, labels, c0, lam, gam, groups, scale, floor, num, den, saved,
-                                            dout, dnum, dden, dq, dk, dv, dc0, dlam, dgam, workspace, st,
+                                            dout, dnum, dden, dq, dk, dv, dc0, dlam, dgam, workspace, st, aux,
                                             make_timer());
     else
       rc = oal::launch_mfma_backward<uint16_t>(lg, q, k, v, labels, c0, lam, gam, groups, scale, floor, num, den,
                                                saved, dout, dnum, dden, dq, dk, dv, dc0, dlam, dgam, workspace, st,
-                                               make_timer());
+                                               aux, make_timer());
     if (rc == 2) return fail("oal_backward: dk and dv must be requested together on the matrix-core path");
     if (rc == 3) return fail("dc0, dlam and dgam must be given together");
     return launch_status("oal_backward launch");
@@ -1084,6 +1160,20 @@ int oal_backward(const void* q, const void* k, const void* v, const int32_t* lab
   if (groups <= 8) return backward_impl<uint16_t, 8>(OAL_BWD_ARGS);
   return backward_impl<uint16_t, 64>(OAL_BWD_ARGS);
 #undef OAL_BWD_ARGS
+}
+
+}  // namespace
+
+extern "C" {
+
+int oal_backward(const void* q, const void* k, const void* v, const int32_t* labels, const float* c0,
+                 const float* lam, const float* gam, int groups, int batch, int q_heads, int kv_heads, int seq_len,
+                 int dtype, int precision, float scale, float floor, const float* num, const float* den,
+                 const void* saved, const void* dout, const float* dnum, const float* dden, void* dq, void* dk,
+                 void* dv, float* dc0, float* dlam, float* dgam, void* workspace, void* stream) {
+  return backward_entry(q, k, v, labels, c0, lam, gam, groups, batch, q_heads, kv_heads, seq_len, dtype, precision,
+                        scale, floor, num, den, saved, dout, dnum, dden, dq, dk, dv, dc0, dlam, dgam, workspace,
+                        stream, true);
 }
 
 int oal_backward_noalloc(const void* q, const void* k, const void* v, const int32_t* labels, const float* c0,
@@ -1111,9 +1201,11 @@ int oal_backward_noalloc(const void* q, const void* k, const void* v, const int3
   void* ws = scratch_address();
   if (!ws) return 1;
   // every workspace byte the backward reads it has written first in the same
-  // call, so the scratch needs no clearing between calls
-  return oal_backward(q, k, v, labels, c0, lam, gam, groups, batch, q_heads, kv_heads, seq_len, dtype, precision,
-                      scale, floor, num, den, saved, dout, dnum, dden, dq, dk, dv, dc0, dlam, dgam, ws, stream);
+  // call, so the scratch needs no clearing between calls; every kernel stays
+  // on the caller's stream (no second stream or event is created)
+  return backward_entry(q, k, v, labels, c0, lam, gam, groups, batch, q_heads, kv_heads, seq_len, dtype, precision,
+                        scale, floor, num, den, saved, dout, dnum, dden, dq, dk, dv, dc0, dlam, dgam, ws, stream,
+                        false);
 }
 
 int oal_selftest(int* device_errors, void* stream) {

@@ -744,7 +744,7 @@ int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, cons
                          const float* c0, const float* lam, const float* gam, int groups, float scale, float floor,
                          const float* num, const float* den, const void* saved, const void* dout, const float* dnum,
                          const float* dden, void* dq, void* dk, void* dv, float* dc0, float* dlam, float* dgam,
-                         void* workspace, hipStream_t st, const Timer& timed) {
+                         void* workspace, hipStream_t st, hipStream_t aux, const Timer& timed) {
   if ((dk != nullptr) != (dv != nullptr)) return 2;
   const bool need_coef = dc0 || dlam || dgam;
   if (need_coef && !(dc0 && dlam && dgam)) return 3;
@@ -754,10 +754,23 @@ int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, cons
   const T* qt = static_cast<const T*>(q);
   const T* kt = static_cast<const T*>(k);
   const T* vt = static_cast<const T*>(v);
+  const bool forked = aux != st;
   timed("k2_bwd_prep", st, [&] {
     hipLaunchKernelGGL(k2_bwd_prep<T>, dim3(g.B * g.Hq * g.NB), dim3(256), 0, st, qt, static_cast<const T*>(dout),
                        dnum, dden, num, den, g.N, g.NB, floor, w.G16, w.Gz, w.GT16, w.QT16);
   });
+  // The state side (the backward scan, its carries and the denominator
+  // column) and the intra-chunk VJP read only what k2_bwd_prep and the forward
+  // wrote: the latter runs on the second stream meanwhile. (Measured: the
+  // denominator kernels or the coefficient reductions on the second stream as
+  // well made the step slower.)
+  if (forked) stream_wait(aux, st);
+  {
+    LocalBwdArgs la{w.G16, w.Gz, w.QT16, w.GT16, sv.KT16, sv.KAP, sv.PZ, sv.PZm, labels, lam, gam, sv.ic, sv.gm, sv.lb,
+                    groups, scale, w.dqf, w.dkl, w.dvl, (need_coef && !pairwise) ? w.coefl : nullptr,
+                    pairwise, sv.wqs, w.dkp, (need_coef && pairwise) ? w.dwql : nullptr};
+    launch_local_bwd<T>(g, qt, kt, vt, la, dq != nullptr, dk != nullptr, aux, timed);
+  }
   {
     const ScanPlan plan{w.S, w.SL, 0};
     // without a coefficient gradient the scan forms no coefficient partials
@@ -770,11 +783,12 @@ int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, cons
                    need_coef ? w.dwz : nullptr, st, timed);
     launch_den_scan(false, g, w.dCt, w.dTz, nullptr, st, timed);
   }
-  {
-    LocalBwdArgs la{w.G16, w.Gz, w.QT16, w.GT16, sv.KT16, sv.KAP, sv.PZ, sv.PZm, labels, lam, gam, sv.ic, sv.gm, sv.lb,
-                    groups, scale, w.dqf, w.dkl, w.dvl, (need_coef && !pairwise) ? w.coefl : nullptr,
-                    pairwise, sv.wqs, w.dkp, (need_coef && pairwise) ? w.dwql : nullptr};
-    launch_local_bwd<T>(g, qt, kt, vt, la, dq != nullptr, dk != nullptr, st, timed);
+  // join, then fork again: the folds need both sides; the key-side fold runs
+  // on the second stream beside the query-side one (whose last round of blocks
+  // would otherwise leave half the CUs idle)
+  if (forked) {
+    stream_wait(st, aux);
+    stream_wait(aux, st);
   }
   if (dq) {
     timed("k2_q_fold", st, [&] {
@@ -783,13 +797,13 @@ int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, cons
     });
   }
   if (dk) {
-    timed("k2_kv_fold", st, [&] {
+    timed("k2_kv_fold", aux, [&] {
       if (w.S > 1)
-        hipLaunchKernelGGL((k2_kv_fold<T, true>), dim3(g.NB * g.U * 2), dim3(128), 0, st, kt, vt, w.dTR, w.dCR,
+        hipLaunchKernelGGL((k2_kv_fold<T, true>), dim3(g.NB * g.U * 2), dim3(128), 0, aux, kt, vt, w.dTR, w.dCR,
                            w.SL, w.S, w.dTz, w.dkl, w.dvl, g.Hq, g.Hkv, g.N, g.NB, static_cast<T*>(dk),
                            static_cast<T*>(dv));
       else
-        hipLaunchKernelGGL((k2_kv_fold<T, false>), dim3(g.NB * g.U * 2), dim3(128), 0, st, kt, vt, w.dTR, nullptr,
+        hipLaunchKernelGGL((k2_kv_fold<T, false>), dim3(g.NB * g.U * 2), dim3(128), 0, aux, kt, vt, w.dTR, nullptr,
                            1, 1, w.dTz, w.dkl, w.dvl, g.Hq, g.Hkv, g.N, g.NB, static_cast<T*>(dk),
                            static_cast<T*>(dv));
     });
@@ -812,17 +826,20 @@ int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, cons
       });
     }
   }
+  // the caller's stream ends after every kernel of the call
+  if (forked) stream_wait(st, aux);
   return 0;
 }
 
 template int launch_mfma_backward<float>(const LaunchGeom&, const void*, const void*, const void*, const int32_t*,
                                          const float*, const float*, const float*, int, float, float, const float*,
                                          const float*, const void*, const void*, const float*, const float*, void*,
-                                         void*, void*, float*, float*, float*, void*, hipStream_t, const Timer&);
+                                         void*, void*, float*, float*, float*, void*, hipStream_t, hipStream_t,
+                                         const Timer&);
 template int launch_mfma_backward<uint16_t>(const LaunchGeom&, const void*, const void*, const void*, const int32_t*,
                                             const float*, const float*, const float*, int, float, float,
                                             const float*, const float*, const void*, const void*, const float*,
                                             const float*, void*, void*, void*, float*, float*, float*, void*,
-                                            hipStream_t, const Timer&);
+                                            hipStream_t, hipStream_t, const Timer&);
 
 }  // namespace oal
