@@ -5,8 +5,10 @@
  * takes plain device pointers and sizes; no framework types cross this boundary.
  * Callers own every buffer (inputs, outputs, the forward's saved state and the
  * backward's workspace; sizes come from the *_bytes queries). Work is enqueued on
- * the caller's HIP stream and nothing is synchronized. The library allocates no
- * device memory.
+ * the caller's HIP stream and nothing is synchronized (oal_backward may run part
+ * of its work on a second stream of the library's own, forked from and joined
+ * back to the caller's stream by events, so the caller sees one stream). The
+ * library allocates no device memory.
  *
  * Operator (reference oal_attention/grouped_reference.py:102-211):
  *   s_g(i,j)   = scale * sum_{d: labels[h][d] == g} q[i][d] * k[j][d]
@@ -114,7 +116,14 @@ int oal_forward(const void* q, const void* k, const void* v,
  * gather, grouped_reference.py:89-93, routes pair (r, c), r >= c, to
  * [g(r)][g(c)] only; gradients reaching a factor L with gam = L L^T, or a
  * per-pair coefficient, are the same under both.) Invalid combinations are
- * refused before anything is enqueued.
+ * refused before anything is enqueued. On the matrix-core path the intra-chunk
+ * VJP and the key-side fold run on a second stream (one per device, default
+ * priority, created with its fork/join events on the first call; not created
+ * while the caller's stream is capturing a graph, whose call then stays on the
+ * caller's stream). Every kernel on it waits for an event recorded on the
+ * caller's stream, and at the end of the call the caller's stream waits for the
+ * last of them, so work enqueued after the call, or an event recorded after it,
+ * covers all of it.
  */
 int oal_backward(const void* q, const void* k, const void* v,
                  const int32_t* labels, const float* c0, const float* lam, const float* gam,
@@ -131,7 +140,9 @@ int oal_backward(const void* q, const void* k, const void* v,
  * capture, tight serving loops, harnesses that forbid hipMalloc). Same
  * arguments and results as oal_backward, without the workspace: the workspace
  * is a file-scope device array of OAL_NOALLOC_SCRATCH_BYTES (256 MiB) that each
- * GPU the library runs on holds until the process ends. A geometry whose
+ * GPU the library runs on holds until the process ends, whether or not this
+ * entry point is called (the array is part of the loaded code object). It runs
+ * all its kernels on the caller's stream (no second stream). A geometry whose
  * oal_backward_workspace_bytes exceeds it is refused with an error (B = 1,
  * N = 4096, 14/2 heads needs 146 MiB on the bf16 path). Nothing is allocated or
  * freed. The stream must belong to the current device. Every call on a GPU
