@@ -168,6 +168,40 @@ int oal_backward_noalloc(const void* q, const void* k, const void* v,
  */
 int oal_selftest(int* device_errors, void* stream);
 
+/*
+ * FP64 evaluation, the route of oal_attention(execution="reference") when the
+ * working dtype is float64. Replaces the reference's float64 evaluation of
+ * grouped_quadratic_reference (oal_attention/grouped_quadratic.py:332-355,
+ * grouped_reference.py:102-211) and, for the backward, torch autograd of it.
+ * Same operator and layouts as oal_forward with every tensor float64: q, k, v
+ * (padded to 64 features), c0 [Hq], lam [Hq][groups], gam [Hq][groups][groups]
+ * (symmetric), out and num [B][Hq][N][64], den [B][Hq][N]; out = num / den, no
+ * floor. Evaluated over token pairs in 32-token tiles (O(N^2) per head), for
+ * validation in double precision rather than speed. No saved state: the
+ * backward recomputes from q, k, v.
+ */
+int oal_forward_f64(const double* q, const double* k, const double* v,
+                    const int32_t* labels, const double* c0, const double* lam, const double* gam,
+                    int groups, int batch, int q_heads, int kv_heads, int seq_len, double scale,
+                    double* out, double* num, double* den, void* stream);
+
+/* Workspace of oal_backward_f64 in bytes (0 on invalid geometry). */
+size_t oal_backward_f64_workspace_bytes(int batch, int q_heads, int kv_heads, int seq_len, int groups);
+
+/*
+ * VJP of oal_forward_f64, every tensor float64: dout [B][Hq][N][64], dnum
+ * [B][Hq][N][64] and dden [B][Hq][N] may each be NULL; dq, dk, dv, and the
+ * coefficient gradients dc0, dlam, dgam (requested together) may be NULL when
+ * not requested. dgam is in the symmetric convention of oal_backward.
+ */
+int oal_backward_f64(const double* q, const double* k, const double* v,
+                     const int32_t* labels, const double* c0, const double* lam, const double* gam,
+                     int groups, int batch, int q_heads, int kv_heads, int seq_len, double scale,
+                     const double* num, const double* den,
+                     const double* dout, const double* dnum, const double* dden,
+                     double* dq, double* dk, double* dv, double* dc0, double* dlam, double* dgam,
+                     void* workspace, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

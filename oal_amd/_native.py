@@ -60,6 +60,16 @@ _SIGNATURES = {
         _i,
     ),
     "oal_selftest": ([_vp, _vp], _i),
+    "oal_forward_f64": (
+        [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, ctypes.c_double, _vp, _vp, _vp, _vp],
+        _i,
+    ),
+    "oal_backward_f64_workspace_bytes": ([_i, _i, _i, _i, _i], _sz),
+    "oal_backward_f64": (
+        [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, ctypes.c_double, _vp, _vp, _vp, _vp, _vp, _vp,
+         _vp, _vp, _vp, _vp, _vp, _vp, _vp],
+        _i,
+    ),
 }
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)
@@ -369,3 +379,103 @@ def backward(q, k, v, labels, c0, lam, gam, num, den, saved, dout, dnum, dden, *
         )
         _check(rc, lib, "oal_backward")
     return dq, dk if need_k else None, dv if need_v else None, dc0, dlam, dgam
+
+
+# ---------------------------------------------------------------------------
+# FP64 route (oal_forward_f64 / oal_backward_f64): every tensor float64.
+# ---------------------------------------------------------------------------
+def check_forward_args_f64(q, k, v, labels, c0, lam, gam) -> tuple[int, int, int, int, int]:
+    """Validate the FP64 operands; returns (B, Hq, Hkv, N, groups)."""
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        if not isinstance(t, torch.Tensor):
+            raise RuntimeError(f"{name} must be a torch.Tensor")
+        if t.ndim != 4:
+            raise RuntimeError(f"{name} must be rank 4 [B, H, N, {HEAD_DIM}]")
+    b, hq, n, d = q.shape
+    hkv = k.shape[1]
+    if min(b, hq, hkv, n) <= 0:
+        raise RuntimeError("batch, head counts and sequence length must be positive")
+    if hq % hkv != 0:
+        raise RuntimeError("query head count must be divisible by KV head count")
+    if d != HEAD_DIM:
+        raise RuntimeError(f"q, k and v must be padded to {HEAD_DIM} features")
+    dev = q.device
+    f64 = torch.float64
+    _check_tensor(q, "q", dtype=f64, shape=(b, hq, n, HEAD_DIM))
+    _check_tensor(k, "k", dtype=f64, shape=(b, hkv, n, HEAD_DIM), device=dev)
+    _check_tensor(v, "v", dtype=f64, shape=(b, hkv, n, HEAD_DIM), device=dev)
+    if not isinstance(lam, torch.Tensor) or lam.ndim != 2:
+        raise RuntimeError("lam must be a [Hq, G] tensor")
+    groups = lam.shape[1]
+    if not 1 <= groups <= 64:
+        raise RuntimeError("the group count must be in [1, 64]")
+    _check_tensor(labels, "labels", dtype=torch.int32, shape=(hq, HEAD_DIM), device=dev)
+    _check_tensor(c0, "c0", dtype=f64, shape=(hq,), device=dev)
+    _check_tensor(lam, "lam", dtype=f64, shape=(hq, groups), device=dev)
+    _check_tensor(gam, "gam", dtype=f64, shape=(hq, groups, groups), device=dev)
+    return b, hq, hkv, n, groups
+
+
+def forward_f64(q, k, v, labels, c0, lam, gam, *, scale: float):
+    """FP64 forward: q [B,Hq,N,64], k/v [B,Hkv,N,64], c0/lam/gam float64, labels
+    int32 [Hq,64]. Returns (out, num [B,Hq,N,64], den [B,Hq,N,1]), all float64."""
+    lib = load_library()
+    b, hq, hkv, n, groups = check_forward_args_f64(q, k, v, labels, c0, lam, gam)
+    _require_device(q)
+    q, k, v = (_aligned(t) for t in (q, k, v))
+    dev = q.device
+    with torch.cuda.device(dev), torch.profiler.record_function("oal_amd::forward_f64"):
+        out = torch.empty((b, hq, n, HEAD_DIM), dtype=torch.float64, device=dev)
+        num = torch.empty((b, hq, n, HEAD_DIM), dtype=torch.float64, device=dev)
+        den = torch.empty((b, hq, n, 1), dtype=torch.float64, device=dev)
+        rc = lib.oal_forward_f64(
+            _ptr(q), _ptr(k), _ptr(v), _ptr(labels), _ptr(c0), _ptr(lam), _ptr(gam), groups,
+            b, hq, hkv, n, float(scale), _ptr(out), _ptr(num), _ptr(den), _stream(dev),
+        )
+        _check(rc, lib, "oal_forward_f64")
+    return out, num, den
+
+
+def backward_f64(q, k, v, labels, c0, lam, gam, num, den, dout, dnum, dden, *, scale: float, need_q: bool,
+                 need_kv: bool, need_coef: bool):
+    """FP64 VJP; returns (dq, dk, dv, dc0, dlam, dgam) with None where not requested."""
+    lib = load_library()
+    f64 = torch.float64
+    if dout is not None:
+        dout = dout.to(f64).contiguous()
+    if dnum is not None:
+        dnum = dnum.to(f64).contiguous()
+    if dden is not None:
+        dden = dden.to(f64)
+        dden = (dden.unsqueeze(-1) if dden.ndim == 3 else dden).contiguous()
+    b, hq, hkv, n, groups = check_forward_args_f64(q, k, v, labels, c0, lam, gam)
+    dev = q.device
+    _check_tensor(num, "num", dtype=f64, shape=(b, hq, n, HEAD_DIM), device=dev)
+    _check_tensor(den, "den", dtype=f64, shape=(b, hq, n, 1), device=dev)
+    if dout is not None:
+        _check_tensor(dout, "dout", dtype=f64, shape=(b, hq, n, HEAD_DIM), device=dev)
+    if dnum is not None:
+        _check_tensor(dnum, "dnum", dtype=f64, shape=(b, hq, n, HEAD_DIM), device=dev)
+    if dden is not None:
+        _check_tensor(dden, "dden", dtype=f64, shape=(b, hq, n, 1), device=dev)
+    _require_device(q)
+    with torch.cuda.device(dev), torch.profiler.record_function("oal_amd::backward_f64"):
+        wbytes = lib.oal_backward_f64_workspace_bytes(b, hq, hkv, n, groups)
+        if wbytes == 0:
+            _check(1, lib, "oal_backward_f64_workspace_bytes")
+        work = torch.empty((wbytes,), dtype=torch.uint8, device=dev)
+        dq = torch.empty_like(q) if need_q else None
+        dk = torch.empty_like(k) if need_kv else None
+        dv = torch.empty_like(v) if need_kv else None
+        if need_coef:
+            dc0, dlam, dgam = torch.empty_like(c0), torch.empty_like(lam), torch.empty_like(gam)
+        else:
+            dc0 = dlam = dgam = None
+        q, k, v, num, den, dout, dnum, dden = (_aligned(t) for t in (q, k, v, num, den, dout, dnum, dden))
+        rc = lib.oal_backward_f64(
+            _ptr(q), _ptr(k), _ptr(v), _ptr(labels), _ptr(c0), _ptr(lam), _ptr(gam), groups,
+            b, hq, hkv, n, float(scale), _ptr(num), _ptr(den), _ptr(dout), _ptr(dnum), _ptr(dden),
+            _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dc0), _ptr(dlam), _ptr(dgam), _ptr(work), _stream(dev),
+        )
+        _check(rc, lib, "oal_backward_f64")
+    return dq, dk, dv, dc0, dlam, dgam

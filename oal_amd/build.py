@@ -18,7 +18,8 @@ ROOT = os.path.dirname(PKG)
 SOURCES = [os.path.join(PKG, "csrc", "oal_kernels.hip"), os.path.join(PKG, "csrc", "oal_mfma_fwd.hip"),
            os.path.join(PKG, "csrc", "oal_mfma_bwd.hip"), os.path.join(PKG, "csrc", "oal_mfma_local.hip"),
            os.path.join(PKG, "csrc", "oal_mfma_scan.hip"), os.path.join(PKG, "csrc", "oal_mfma_den.hip"),
-           os.path.join(PKG, "csrc", "oal_mfma_pair.hip"), os.path.join(PKG, "csrc", "oal_f32_mma.hip")]
+           os.path.join(PKG, "csrc", "oal_mfma_pair.hip"), os.path.join(PKG, "csrc", "oal_f32_mma.hip"),
+           os.path.join(PKG, "csrc", "oal_f64.hip")]
 HEADERS = [os.path.join(PKG, "csrc", "oal_common.hpp"), os.path.join(ROOT, "include", "oal_amd.h")]
 OUTPUT = os.path.join(PKG, "liboal_amd.so")
 OBJDIR = os.path.join(PKG, "_build")

@@ -236,4 +236,18 @@ void launch_den_bwd(const LaunchGeom& g, const uint16_t* QT16, const uint16_t* G
 
 int run_mfma_selftest(int* dev_errors, hipStream_t st);
 
+// FP64 route (oal_f64.hip): pairwise evaluation over 32-token tiles.
+struct F64Geom {
+  int B, Hq, Hkv, N;
+};
+size_t f64_workspace_bytes(int B, int Hq, int N);
+void launch_f64_forward(const F64Geom& g, const double* q, const double* k, const double* v, const int32_t* labels,
+                        const double* c0, const double* lam, const double* gam, int G, double scale, double* out,
+                        double* num, double* den, hipStream_t st, const Timer& timed);
+void launch_f64_backward(const F64Geom& g, const double* q, const double* k, const double* v,
+                         const int32_t* labels, const double* c0, const double* lam, const double* gam, int G,
+                         double scale, const double* num, const double* den, const double* dout,
+                         const double* dnum, const double* dden, double* dq, double* dk, double* dv, double* dc0,
+                         double* dlam, double* dgam, void* workspace, hipStream_t st, const Timer& timed);
+
 }  // namespace oal

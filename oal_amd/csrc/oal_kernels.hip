@@ -1215,4 +1215,58 @@ int oal_selftest(int* device_errors, void* stream) {
   return 0;
 }
 
+
+// FP64 route. Geometry checks as the other entry points (any group count in
+// [1, 64]); the kernels are in oal_f64.hip.
+static int check_f64(int groups, int batch, int q_heads, int kv_heads, int seq_len, oal::F64Geom* g) {
+  Geometry geo;
+  if (check_geometry(batch, q_heads, kv_heads, seq_len, OAL_DTYPE_F32, &geo)) return 1;
+  if (groups < 1 || groups > 64) return fail("groups must be in [1, 64]");
+  const long tiles = (seq_len + 31) / 32;
+  if (tiles > 65535 || (long)batch * q_heads > 65535) return fail("grid too large");
+  *g = oal::F64Geom{batch, q_heads, kv_heads, seq_len};
+  return 0;
+}
+
+int oal_forward_f64(const double* q, const double* k, const double* v, const int32_t* labels, const double* c0,
+                    const double* lam, const double* gam, int groups, int batch, int q_heads, int kv_heads,
+                    int seq_len, double scale, double* out, double* num, double* den, void* stream) {
+  Range range("oal_forward_f64");
+  oal::F64Geom g;
+  if (check_f64(groups, batch, q_heads, kv_heads, seq_len, &g)) return 1;
+  if (!q || !k || !v || !labels || !c0 || !lam || !gam || !out || !num || !den)
+    return fail("oal_forward_f64: null pointer argument");
+  const void* ptrs[] = {q, k, v, out, num, den};
+  for (const void* p : ptrs)
+    if (!aligned16(p)) return fail("oal_forward_f64: tensor pointers must be 16-byte aligned");
+  oal::launch_f64_forward(g, q, k, v, labels, c0, lam, gam, groups, scale, out, num, den,
+                          static_cast<hipStream_t>(stream), make_timer());
+  return launch_status("oal_forward_f64 launch");
+}
+
+size_t oal_backward_f64_workspace_bytes(int batch, int q_heads, int kv_heads, int seq_len, int groups) {
+  oal::F64Geom g;
+  if (check_f64(groups, batch, q_heads, kv_heads, seq_len, &g)) return 0;
+  return oal::f64_workspace_bytes(g.B, g.Hq, g.N);
+}
+
+int oal_backward_f64(const double* q, const double* k, const double* v, const int32_t* labels, const double* c0,
+                     const double* lam, const double* gam, int groups, int batch, int q_heads, int kv_heads,
+                     int seq_len, double scale, const double* num, const double* den, const double* dout,
+                     const double* dnum, const double* dden, double* dq, double* dk, double* dv, double* dc0,
+                     double* dlam, double* dgam, void* workspace, void* stream) {
+  Range range("oal_backward_f64");
+  oal::F64Geom g;
+  if (check_f64(groups, batch, q_heads, kv_heads, seq_len, &g)) return 1;
+  if (!q || !k || !v || !labels || !c0 || !lam || !gam || !num || !den || !workspace)
+    return fail("oal_backward_f64: null pointer argument");
+  const void* ptrs[] = {q, k, v, num, den, dout, dnum, dden, dq, dk, dv, workspace};
+  for (const void* p : ptrs)
+    if (p && !aligned16(p)) return fail("oal_backward_f64: tensor pointers must be 16-byte aligned");
+  if ((dc0 || dlam || dgam) && !(dc0 && dlam && dgam)) return fail("dc0, dlam and dgam must be given together");
+  oal::launch_f64_backward(g, q, k, v, labels, c0, lam, gam, groups, scale, num, den, dout, dnum, dden, dq, dk, dv,
+                           dc0, dlam, dgam, workspace, static_cast<hipStream_t>(stream), make_timer());
+  return launch_status("oal_backward_f64 launch");
+}
+
 }  // extern "C"

@@ -19,7 +19,7 @@ from typing import Literal
 
 import torch
 
-from .hd_block_gemm_autograd import grouped_oal
+from .hd_block_gemm_autograd import grouped_oal, grouped_oal_f64
 
 _SUPPORTED_FLOATING_DTYPES = frozenset({torch.float16, torch.bfloat16, torch.float32, torch.float64})
 _SUPPORTED_FACTOR_DTYPES = frozenset({torch.float32, torch.float64})
@@ -203,9 +203,11 @@ def oal_attention(
     """Evaluate OAL's grouped PSD quadratic attention kernel on the HIP path.
 
     q [B, Hq, N, D], k/v [B, Hkv, N, D | DV] (D, DV <= 64), dim_groups [D] or
-    [Hq, D] int32/int64, factor [P] or [Hq, P] float32 packed lower-triangular.
-    Returns out (v.dtype or output_dtype), or (out, num, den) with num
-    [B, Hq, N, DV] and den [B, Hq, N, 1] in float32.
+    [Hq, D] int32/int64, factor [P] or [Hq, P] packed lower-triangular (float32
+    for the HIP executions; float32 or float64 for "reference", which evaluates
+    in the working dtype). Returns out (v.dtype or output_dtype), or (out, num,
+    den) with num [B, Hq, N, DV] and den [B, Hq, N, 1] in float32 (float64 for
+    the float64 "reference" execution).
     """
     q, k, v = _validate_qkv(q, k, v)
     causal, execution = _validate_public_options(
@@ -237,20 +239,23 @@ def oal_attention(
             )
         raise RuntimeError("grouped quadratic HIP execution requires ROCm device input")
     if execution == "reference":
-        # the reference evaluates in the working dtype (:332-355); the HIP reference
-        # route is the fp32 kernels, so an FP64 working dtype cannot be honoured
-        if working_dtype != torch.float32:
-            raise TypeError("grouped quadratic HIP reference execution computes in FP32; FP64 inputs are unsupported")
+        # the reference evaluates in the working dtype (:332-355): the fp32 HIP
+        # kernels for FP32, the FP64 route (oal_f64.hip) for FP64
         if q.shape[-1] > 64 or v.shape[-1] > 64:
             raise ValueError("grouped quadratic HIP execution supports D<=64")
         q_work, k_work, v_work = (t.to(dtype=working_dtype) for t in (q, k, v))
         constant, linear, quadratic = _expand_factor_coefficients(
             factor, query_heads=q.shape[1], gmax=gmax, kernel_eps=resolved_eps, working_dtype=working_dtype
         )
-        output, numerator, denominator = grouped_oal(
-            q_work, k_work, v_work, dim_groups, constant, linear, quadratic, scale=resolved_scale, floor=0.0,
-            precision="fp32",
-        )
+        if working_dtype == torch.float64:
+            output, numerator, denominator = grouped_oal_f64(
+                q_work, k_work, v_work, dim_groups, constant, linear, quadratic, scale=resolved_scale
+            )
+        else:
+            output, numerator, denominator = grouped_oal(
+                q_work, k_work, v_work, dim_groups, constant, linear, quadratic, scale=resolved_scale, floor=0.0,
+                precision="fp32",
+            )
     else:
         if q.dtype not in _HIP_INPUT_DTYPES:
             raise TypeError("grouped quadratic HIP execution supports float16, bfloat16 and float32")

@@ -23,7 +23,8 @@ Two ``torch.autograd.Function`` classes share the same HIP forward/VJP:
   (or no plan) the fp32 kernels.
 
 Both pad D and DV up to 64 with zeros (padding contributes nothing) and slice
-the results back.
+the results back. :class:`_GroupedOALF64Function` is the grouped Function's
+float64 counterpart (the FP64 route, ``oal_f64.hip``).
 """
 
 from __future__ import annotations
@@ -130,6 +131,66 @@ def grouped_oal(q, k, v, labels, c0, lam, gam, *, scale: float, floor: float, pr
         out = out[..., :dv_orig]
         num = num[..., :dv_orig]
     return out.to(q.dtype), num, den
+
+
+class _GroupedOALF64Function(torch.autograd.Function):
+    """(q, k, v, c0, lam, gam, labels, scale) -> (out, num, den), all float64.
+
+    The FP64 route (``oal_forward_f64`` / ``oal_backward_f64``): the working
+    dtype of ``oal_attention(execution="reference")`` for float64 inputs, as the
+    reference evaluates that execution in the working dtype
+    (``oal_attention/grouped_quadratic.py:332-355``). q, k, v [B, H, N, 64]
+    contiguous float64 on one ROCm device; labels int32 [Hq, 64]. dGam in the
+    symmetric convention of :class:`_GroupedOALFunction`.
+    """
+
+    @staticmethod
+    def forward(ctx: Any, q, k, v, c0, lam, gam, labels, scale: float):
+        ctx.set_materialize_grads(False)
+        c0c, lamc, gamc = (t.detach().to(torch.float64).contiguous() for t in (c0, lam, gam))
+        out, num, den = _native.forward_f64(q, k, v, labels, c0c, lamc, gamc, scale=scale)
+        ctx.save_for_backward(q, k, v, c0c, lamc, gamc, labels, num, den)
+        ctx.scale = float(scale)
+        ctx.coef_dtypes = (c0.dtype, lam.dtype, gam.dtype)
+        return out, num, den
+
+    @staticmethod
+    def backward(ctx: Any, dout, dnum, dden):
+        if torch.is_grad_enabled():
+            raise RuntimeError("the OAL HIP operator does not support double backward")
+        q, k, v, c0, lam, gam, labels, num, den = ctx.saved_tensors
+        needs = ctx.needs_input_grad
+        if dout is None and dnum is None and dden is None:
+            return (None,) * 8
+        dq, dk, dv, dc0, dlam, dgam = _native.backward_f64(
+            q, k, v, labels, c0, lam, gam, num, den, dout, dnum, dden, scale=ctx.scale,
+            need_q=needs[0], need_kv=needs[1] or needs[2], need_coef=any(needs[3:6]),
+        )
+        cd = ctx.coef_dtypes
+        return (
+            dq,
+            dk if needs[1] else None,
+            dv if needs[2] else None,
+            dc0.to(cd[0]) if needs[3] else None,
+            dlam.to(cd[1]) if needs[4] else None,
+            dgam.to(cd[2]) if needs[5] else None,
+            None,
+            None,
+        )
+
+
+def grouped_oal_f64(q, k, v, labels, c0, lam, gam, *, scale: float):
+    """The grouped operator in float64 throughout (the FP64 route): [B, H, N, D<=64]
+    q, k, v, labels [D] or [Hq, D], grouped coefficients. Returns (out, num, den)
+    in float64, num [B, Hq, N, DV], den [B, Hq, N, 1]."""
+    dv_orig = v.shape[-1]
+    qp, kp, vp = (_pad_last(t.to(torch.float64)) for t in (q, k, v))
+    lab = pad_labels(labels, q.shape[1])
+    out, num, den = _GroupedOALF64Function.apply(qp, kp, vp, c0, lam, gam, lab, float(scale))
+    if dv_orig != HEAD_DIM:
+        out = out[..., :dv_orig]
+        num = num[..., :dv_orig]
+    return out, num, den
 
 
 def _pair_rows_cols(d: int, device) -> tuple[torch.Tensor, torch.Tensor]:

@@ -169,3 +169,60 @@ def test_caller_workspace_is_checked(monkeypatch):
         _native.backward(*[a[n] for n in ("q", "k", "v", "labels", "c0", "lam", "gam", "num", "den", "saved",
                                           "dout", "dnum", "dden")], scale=0.1, floor=0.0, need_q=True, need_k=True,
                          need_v=True, need_coef=False, workspace=base[8:200])
+
+
+# FP64 route (oal_forward_f64 / oal_backward_f64): every tensor float64.
+def _valid64(b=1, hq=2, hkv=1, n=5, g=3):
+    a = _valid(b, hq, hkv, n, g)
+    for key in ("q", "k", "v", "c0", "lam", "gam"):
+        a[key] = a[key].double()
+    return a
+
+
+def _fwd64(a):
+    return _native.forward_f64(a["q"], a["k"], a["v"], a["labels"], a["c0"], a["lam"], a["gam"], scale=0.125)
+
+
+def test_valid_f64_operands_reach_the_device_check():
+    a = _valid64()
+    assert _native.check_forward_args_f64(a["q"], a["k"], a["v"], a["labels"], a["c0"], a["lam"],
+                                          a["gam"]) == (1, 2, 1, 5, 3)
+    with pytest.raises(RuntimeError, match="ROCm"):
+        _fwd64(a)
+    n = a["q"].shape[2]
+    num = torch.zeros(1, 2, n, 64, dtype=torch.float64)
+    den = torch.ones(1, 2, n, 1, dtype=torch.float64)
+    with pytest.raises(RuntimeError, match="ROCm"):
+        _native.backward_f64(a["q"], a["k"], a["v"], a["labels"], a["c0"], a["lam"], a["gam"], num, den,
+                             torch.zeros_like(num), None, None, scale=0.125, need_q=True, need_kv=True,
+                             need_coef=True)
+
+
+F64_REJECTIONS = [
+    ("float32 q", lambda a: a.update(q=a["q"].float(), k=a["k"].float(), v=a["v"].float()), "q must be float64"),
+    ("v dtype", lambda a: a.update(v=a["v"].float()), "v must be float64"),
+    ("unpadded head dim", lambda a: a.update(q=a["q"][..., :32].contiguous()), "padded to 64"),
+    ("c0 float32", lambda a: a.update(c0=a["c0"].float()), "c0 must be float64"),
+    ("gam shape", lambda a: a.update(gam=a["gam"][:, :2, :2].contiguous()), r"gam must have shape \[2, 3, 3\]"),
+    ("too many groups", lambda a: a.update(lam=torch.ones(2, 65, dtype=torch.float64)),
+     r"group count must be in \[1, 64\]"),
+    ("labels int64", lambda a: a.update(labels=a["labels"].long()), "labels must be int32"),
+]
+
+
+@pytest.mark.parametrize("case,mutate,message", F64_REJECTIONS, ids=[c[0] for c in F64_REJECTIONS])
+def test_f64_forward_rejects(case, mutate, message):
+    a = _valid64()
+    mutate(a)
+    with pytest.raises(RuntimeError, match=message):
+        _fwd64(a)
+
+
+def test_f64_backward_checks_num_and_den():
+    a = _valid64()
+    n = a["q"].shape[2]
+    num = torch.zeros(1, 2, n, 64, dtype=torch.float32)
+    den = torch.ones(1, 2, n, 1, dtype=torch.float64)
+    with pytest.raises(RuntimeError, match="num must be float64"):
+        _native.backward_f64(a["q"], a["k"], a["v"], a["labels"], a["c0"], a["lam"], a["gam"], num, den, None,
+                             None, None, scale=0.125, need_q=True, need_kv=False, need_coef=False)
