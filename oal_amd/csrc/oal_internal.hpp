@@ -131,9 +131,12 @@ void launch_pair_local_bwd(const LaunchGeom& g, const T* q, const T* k, const T*
 void launch_pair_coef_grad(const LaunchGeom& g, const float* dwq, const float* dwqz, const int32_t* labels, int G,
                            float scale, float* dc0, float* dlam, float* dgam, hipStream_t st, const Timer& timed);
 
+// Parts of the intra-chunk VJP that one call of launch_local_bwd launches:
+// the dq kernel (which also forms the coefficient partials), the dk and dv kernels.
+constexpr unsigned kLocalDq = 1, kLocalDkv = 2;
 template <typename T>
 void launch_local_bwd(const LaunchGeom& g, const T* q, const T* k, const T* v, const LocalBwdArgs& a, bool need_dq,
-                      bool need_dkv, hipStream_t st, const Timer& timed);
+                      bool need_dkv, unsigned parts, hipStream_t st, const Timer& timed);
 
 // Segmentation of a chunk-state scan: S segments of SL chunks, a function of
 // the geometry alone. The forward runs more than one segment as totals, carry,

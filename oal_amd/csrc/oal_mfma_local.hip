@@ -575,15 +575,16 @@ __global__ __launch_bounds__(192, 2) void k2_local_dv(const uint16_t* __restrict
 
 template <typename T>
 void launch_local_bwd(const LaunchGeom& g, const T* q, const T* k, const T* v, const LocalBwdArgs& a, bool need_dq,
-                      bool need_dkv, hipStream_t st, const Timer& timed) {
+                      bool need_dkv, unsigned parts, hipStream_t st, const Timer& timed) {
   // The coefficient partials come from the dq kernel's group sums, also when
   // dq itself is not requested (its dq then goes to the workspace unused), so
   // that every requested gradient is bit-identical whatever else is requested.
-  if (a.pairwise) {
+  // parts: kLocalDq (with the per-pair path's whole local VJP), kLocalDkv.
+  if (a.pairwise && (parts & kLocalDq)) {
     launch_pair_local_bwd<T>(g, q, k, v, a, need_dq, need_dkv, st, timed);
   }
   const bool coef = a.coefl != nullptr;
-  if (!a.pairwise && (need_dq || coef)) {
+  if (!a.pairwise && (need_dq || coef) && (parts & kLocalDq)) {
     timed("k2_local_dq", st, [&] {
       if (coef)
         hipLaunchKernelGGL((k2_local_dq<T, true>), dim3(g.R * g.NB * g.U), dim3(192), 0, st, q, k, v, a.G16, a.Gz,
@@ -595,13 +596,13 @@ void launch_local_bwd(const LaunchGeom& g, const T* q, const T* k, const T* v, c
                            a.scale, a.dqf, nullptr);
     });
   }
-  if (!a.pairwise && need_dkv) {
+  if (!a.pairwise && need_dkv && (parts & kLocalDkv)) {
     timed("k2_local_dk", st, [&] {
       hipLaunchKernelGGL(k2_local_dk<T>, dim3(g.NB * g.U), dim3(192), 0, st, q, k, v, a.G16, a.Gz, a.QT16,
                          a.labels, a.lam, a.gam, a.groups, g.Hq, g.Hkv, g.N, g.NB, a.scale, a.dkl);
     });
   }
-  if (need_dkv) {
+  if (need_dkv && (parts & kLocalDkv)) {
     timed("k2_local_dv", st, [&] {
       hipLaunchKernelGGL(k2_local_dv, dim3(g.NB * g.U), dim3(192), 0, st, a.KAP, a.GT16, g.Hq, g.Hkv, g.N, g.NB,
                          a.dvl);
@@ -610,8 +611,8 @@ void launch_local_bwd(const LaunchGeom& g, const T* q, const T* k, const T* v, c
 }
 
 template void launch_local_bwd<float>(const LaunchGeom&, const float*, const float*, const float*,
-                                      const LocalBwdArgs&, bool, bool, hipStream_t, const Timer&);
+                                      const LocalBwdArgs&, bool, bool, unsigned, hipStream_t, const Timer&);
 template void launch_local_bwd<uint16_t>(const LaunchGeom&, const uint16_t*, const uint16_t*, const uint16_t*,
-                                         const LocalBwdArgs&, bool, bool, hipStream_t, const Timer&);
+                                         const LocalBwdArgs&, bool, bool, unsigned, hipStream_t, const Timer&);
 
 }  // namespace oal
