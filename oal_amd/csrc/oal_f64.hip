@@ -414,6 +414,8 @@ __global__ __launch_bounds__(256) void k64_coef_grad(const double* __restrict__ 
                                                      double* __restrict__ dgam) {
   __shared__ double w[kFP];
   __shared__ int lab[kD];
+  __shared__ uint8_t mem[kD][kD];  // mem[g][0 .. cnt[g]): the dimensions of group g, ascending
+  __shared__ int cnt[kD];
   const int h = blockIdx.x, t = threadIdx.x;
   if (t < kD) {
     const int g = labels[h * kD + t];
@@ -427,21 +429,28 @@ __global__ __launch_bounds__(256) void k64_coef_grad(const double* __restrict__ 
     }
     w[f] = acc;
   }
+  for (int g = t; g < G; g += blockDim.x) {
+    int n = 0;
+    for (int d = 0; d < kD; ++d)
+      if (lab[d] == g) mem[g][n++] = (uint8_t)d;
+    cnt[g] = n;
+  }
   __syncthreads();
   if (t == 0) dc0[h] = w[0];
   for (int g = t; g < G; g += blockDim.x) {
     double acc = 0.0;
-    for (int d = 0; d < kD; ++d)
-      if (lab[d] == g) acc += w[1 + d];
+    for (int i = 0; i < cnt[g]; ++i) acc += w[1 + mem[g][i]];
     dlam[(size_t)h * G + g] = acc;
   }
+  // every (g, h) entry walks only its two groups' members: 64 x 64 terms per
+  // head in all, whatever the group count
   for (int e = t; e < G * G; e += blockDim.x) {
     const int gr = e / G, gc = e % G;
     double acc = 0.0;
-    for (int d = 0; d < kD; ++d) {
-      if (lab[d] != gr) continue;
-      for (int c = 0; c < kD; ++c) {
-        if (lab[c] != gc) continue;
+    for (int i = 0; i < cnt[gr]; ++i) {
+      const int d = mem[gr][i];
+      for (int j = 0; j < cnt[gc]; ++j) {
+        const int c = mem[gc][j];
         const int r0 = d > c ? d : c, c0i = d > c ? c : d;
         acc += w[1 + kD + r0 * (r0 + 1) / 2 + c0i];
       }

@@ -6,8 +6,9 @@
 // (the intra-chunk VJP, k2_local_dq / k2_local_dk / k2_local_dv, is in oal_mfma_local.hip)
 // k2_q_fold     dq state part: D^T = P G^T on the MFMA, folded through the query
 //               features (rotated rows, static register indices) + local dq.
-// k2_kv_fold    dk state part (D^T = dT V^T folded through the key features),
-//               dv = raw(K) dT, the dTz quadratic form, + local dk, dv.
+// k2_kv_fold    dk state part (D^T = dT V^T folded through the key features)
+//               and dv = raw(K) dT from one staged copy of the chunk's state,
+//               the dTz quadratic form, + local dk, dv.
 // k2_dwq_reduce sum of the per-segment slot-coefficient partials.
 // k2_coef_grad  per head: slot gradients -> (dc0, dlam, dGam) + local parts.
 //
@@ -297,155 +298,135 @@ __global__ __launch_bounds__(128, 2) void k2_q_fold(const T* __restrict__ q, con
 }
 
 // ---------------------------------------------------------------------------
-// dk, dv: state parts (fold of dT V^T, dU = raw(K) dT, dTz quadratic form) plus
-// the per-head local parts. grid (NB, U), 2 waves; wave w owns tokens 32w..+31.
+// dk, dv: the key-side state parts plus the per-head local parts, with the
+// chunk's state read once. One block of 4 waves per (chunk, unit):
+//   waves 0, 1 (tokens 32 w ..): dk = fold of dT V^T through the key features
+//     + z1 + Mz k + local dk, Mz[r][c] = dTz[pair(r, c)] (r != c),
+//     2 dTz[pair(r, r)] on the diagonal;
+//   waves 2, 3 (tokens 32 (w - 2) ..): dv = raw(K) dT (values 0..63) + local dv.
+// Both read one LDS ring of 32-slot M-tiles of dT; the dv waves take the B
+// fragments of a tile's two k-steps by transposed reads at the M-tile's
+// value-block stride. (Two blocks per chunk, one per part, each streaming the
+// state: 79.4 -> 75.1 us at config 2.)
+// CARRY: dT of chunk ch is the backward scan's segment-local state plus the
+// carry of the chunk's segment (ch / SL, cR [U][S]); each ring stage holds the
+// same M-tile of both, and both products of each step accumulate into the same
+// registers, so the carry costs matrix products and staging only.
 // ---------------------------------------------------------------------------
-// dU = raw(K) dT: k-step T of the state staged in LDS from its R-layout pieces
-// (B fragments by transposed reads); with CARRY the same k-step of the segment
-// carry follows the UPG state units of each ring stage, and its products
-// accumulate into the same accumulators.
-template <int T, int UPG, bool CARRY>
-__device__ __forceinline__ void du_step(const float (&x)[kD], const LdsRing<4>& ring, int lane, f32x16 (&acc)[2]) {
-  const __bf16* tile = ring.st[(T / UPG) % kNS] + (T % UPG) * 1024;
-  const bf16x8 b0 = tr_fragment(tile, lane, 0);
-  const bf16x8 b1 = tr_fragment(tile, lane, 1);
+// B fragment of value half n of k-step half `half` (slots 16 half ..) of a
+// staged M-tile [4 value blocks][32 slots][16 values]; the lane mapping of
+// tr_fragment.
+__device__ __forceinline__ bf16x8 tr_fragment_mtile(const __bf16* mtile, int half, int lane, int n) {
+  const int g = lane >> 4, i = lane & 15;
+  const __bf16* p = mtile + half * 256 + (2 * n + (g & 1)) * 512 + (8 * (g >> 1) + (i >> 2)) * 16 + 4 * (i & 3);
+  typedef __attribute__((address_space(3))) trv4 lds_trv4;
+  const trv4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_trv4*)(p));
+  const trv4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_trv4*)(p + 4 * 16));
+  typedef short trv8 __attribute__((ext_vector_type(8)));
+  const trv8 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return __builtin_bit_cast(bf16x8, v);
+}
+template <int T, bool CARRY>
+__device__ __forceinline__ void kvm_du_step(const float (&x)[kD], const __bf16* st, int lane, f32x16 (&acc)[2]) {
   const bf16x8 a = raw_fragment<T>(x);
-  acc[0] = mfma32(a, b0, acc[0]);
-  acc[1] = mfma32(a, b1, acc[1]);
+  acc[0] = mfma32(a, tr_fragment_mtile(st, T & 1, lane, 0), acc[0]);
+  acc[1] = mfma32(a, tr_fragment_mtile(st, T & 1, lane, 1), acc[1]);
   if constexpr (CARRY) {
-    const bf16x8 c0 = tr_fragment(tile + UPG * 1024, lane, 0);
-    const bf16x8 c1 = tr_fragment(tile + UPG * 1024, lane, 1);
-    acc[0] = mfma32(a, c0, acc[0]);
-    acc[1] = mfma32(a, c1, acc[1]);
+    acc[0] = mfma32(a, tr_fragment_mtile(st + kTileElems, T & 1, lane, 0), acc[0]);
+    acc[1] = mfma32(a, tr_fragment_mtile(st + kTileElems, T & 1, lane, 1), acc[1]);
   }
 }
-// Units (1024 bf16 each) of ring group G in flight per thread.
-template <int UPG, bool CARRY, int G>
-constexpr int du_copies() {
-  constexpr int NG = (kKS + UPG - 1) / UPG;
-  if constexpr (G >= NG) {
-    return 0;
-  } else {
-    constexpr int n = (G + 1) * UPG <= kKS ? UPG : kKS - G * UPG;
-    return CARRY ? 2 * n : n;
-  }
+// M-tile m of the state (and of the carry) into stage st: 256 threads, one
+// 16-byte copy each per tile.
+template <bool CARRY>
+__device__ __forceinline__ void kvm_issue(const uint16_t* src, const uint16_t* csrc, int m, __bf16* st, int tid) {
+  const int wv = tid >> 6;
+  copy16_to_lds(src + (size_t)m * kTileElems + tid * 8, st + 64 * wv * 8);
+  if constexpr (CARRY) copy16_to_lds(csrc + (size_t)m * kTileElems + tid * 8, st + kTileElems + 64 * wv * 8);
 }
-template <int UPG, bool CARRY, int G>
-__device__ __forceinline__ void du_issue(const uint16_t* src, const uint16_t* csrc, const LdsRing<4>& ring,
-                                         int tid) {
-  const int wv = tid >> 6, l = tid & 63;
-  __bf16* st = ring.st[G % kNS];
+template <bool CARRY>
+constexpr int kvm_copies() {
+  return CARRY ? 2 : 1;
+}
+// Group G: wait for tile G + 1, refill the stage of tile G with tile G + 4,
+// then the dk waves issue the product of tile G + 1 and fold tile G, the dv
+// waves take the products of tile G + 1's two k-steps. The two accumulator
+// tiles acc serve both kinds of wave: the dv waves' dv accumulators, and the
+// dk waves' products in flight (tile G's in acc[G % 2]), so that the kernel
+// needs no more registers than the dk fold alone.
+template <int G, bool CARRY>
+__device__ __forceinline__ void kvm_group(bool dkw, const bf16x8 (&bfr)[4], const float (&x)[kD], float (&dx)[kD],
+                                          f32x16 (&acc)[2], const LdsRing<4>& ring, const uint16_t* src,
+                                          const uint16_t* csrc, int tid, int lane) {
+  constexpr int NS = 4, NT = kS / 32;
+  float w1[16];
 #pragma unroll
-  for (int i = 0; i < UPG; ++i) {
-    const int u = G * UPG + i;
-    if (u < kKS) {
-      // wave w copies the k-step's R-layout pieces 2 w, 2 w + 1
-      const size_t o = rpiece(u, 2 * wv + (l >> 5), l & 31);
-      copy16_to_lds(src + o, st + i * 1024 + 64 * wv * 8);
-      if constexpr (CARRY) copy16_to_lds(csrc + o, st + (UPG + i) * 1024 + 64 * wv * 8);
+  for (int i = 0; i < 16; ++i) w1[i] = 1.f;
+  if constexpr (G + 1 < NT) {
+    constexpr int issued = (G + NS - 1 < NT - 1) ? G + NS - 1 : NT - 1;
+    pin64(dx);
+    ring_sync<kvm_copies<CARRY>() * (issued - (G + 1))>();
+    if constexpr (G + NS < NT) kvm_issue<CARRY>(src, csrc, G + NS, ring.st[(G + NS) % NS], tid);
+    if (dkw) {
+      acc[(G + 1) & 1] = fold_mfma<G + 1, CARRY>(bfr, ring.st[(G + 1) % NS], lane);
+      fold_tile<G>(acc[G & 1], x, dx, w1);
+    } else {
+      kvm_du_step<2 * (G + 1), CARRY>(x, ring.st[(G + 1) % NS], lane, acc);
+      kvm_du_step<2 * (G + 1) + 1, CARRY>(x, ring.st[(G + 1) % NS], lane, acc);
     }
+    kvm_group<G + 1, CARRY>(dkw, bfr, x, dx, acc, ring, src, csrc, tid, lane);
+  } else {
+    if (dkw) fold_tile<G>(acc[G & 1], x, dx, w1);
   }
-}
-template <int G, int UPG, bool CARRY>
-__device__ __forceinline__ void du_group(const float (&x)[kD], const LdsRing<4>& ring, const uint16_t* src,
-                                         const uint16_t* csrc, int tid, int lane, f32x16 (&acc)[2]) {
-  constexpr int NG = (kKS + UPG - 1) / UPG;
-  ring_sync<du_copies<UPG, CARRY, G + 1>() + du_copies<UPG, CARRY, G + 2>()>();
-  if constexpr (G + 3 < NG) du_issue<UPG, CARRY, G + 3>(src, csrc, ring, tid);
-  [&]<int... I>(std::integer_sequence<int, I...>) {
-    ((G * UPG + I < kKS ? du_step<(G * UPG + I < kKS ? G * UPG + I : 0), UPG, CARRY>(x, ring, lane, acc) : void()),
-     ...);
-  }(std::make_integer_sequence<int, UPG>{});
-  if constexpr (G + 1 < NG) du_group<G + 1, UPG, CARRY>(x, ring, src, csrc, tid, lane, acc);
 }
 
-// grid NB * U * 2 blocks of 2 waves; wave w owns tokens 32w..32w+31 of the chunk.
-//   part 0: dk = fold of dT V^T through the key features + z1 + Mz k + local dk,
-//           Mz[r][c] = dTz[pair(r, c)] (r != c), 2 dTz[pair(r, r)] on the diagonal;
-//   part 1: dv = raw(K) dT (values 0..63) + local dv.
-// The two parts share nothing, so they run as independent blocks. Block ids
-// are dealt to the 8 XCDs round-robin; item w = (id % 8) * (total / 8) + id / 8
-// (chunk fastest, then part, then unit) gives each XCD consecutive chunks of
-// both parts of a unit, so that the chunks of a segment read its carry through
-// one L2.
-// CARRY: dT of chunk ch is the backward scan's segment-local state plus the
-// carry of the chunk's segment (ch / SL, cR [U][S]); both products of each
-// step accumulate into the same registers, so the carry costs matrix products
-// and staging only (the feature and fold arithmetic is shared).
+// grid NB * U blocks of 4 waves. Block ids are dealt to the 8 XCDs
+// round-robin; item w = (id % 8) * (total / 8) + id / 8 (chunk fastest, then
+// unit) gives each XCD consecutive chunks of a unit, so that the chunks of a
+// segment read its carry through one L2.
 template <typename T, bool CARRY>
-__global__ __launch_bounds__(128, 2) void k2_kv_fold(const T* __restrict__ k, const T* __restrict__ v,
-                                                     const uint16_t* __restrict__ dTR, const uint16_t* __restrict__ cR,
-                                                     int SL, int S, const float* __restrict__ dTz,
-                                                     const float* __restrict__ dkl, const float* __restrict__ dvl,
-                                                     int Hq, int Hkv, int N, int NB, T* __restrict__ dk,
-                                                     T* __restrict__ dv) {
+__global__ __launch_bounds__(256, 2) void k2_kv_fold(const T* __restrict__ k, const T* __restrict__ v,
+                                                            const uint16_t* __restrict__ dTR,
+                                                            const uint16_t* __restrict__ cR, int SL, int S,
+                                                            const float* __restrict__ dTz,
+                                                            const float* __restrict__ dkl,
+                                                            const float* __restrict__ dvl, int Hq, int Hkv, int N,
+                                                            int NB, T* __restrict__ dk, T* __restrict__ dv) {
   __shared__ __attribute__((aligned(16))) __bf16 ring0[kFG * 1024], ring1[kFG * 1024], ring2[kFG * 1024],
       ring3[kFG * 1024];
-  // mz rows unpadded, 16-byte chunk c of row r stored at chunk c ^ (r & 7) (the
-  // fragment reads stay conflict-free); with the ring that is exactly 40 KiB, so
-  // four blocks (the register limit) fit a CU
   __shared__ __attribute__((aligned(16))) __bf16 mz[kD][kD];
 
-  int ch, u, part;
+  int ch, u;
   {
     const int total = gridDim.x, id = blockIdx.x;
     const int w = (total & 7) == 0 ? (id & 7) * (total >> 3) + (id >> 3) : id;
     ch = w % NB;
-    part = (w / NB) & 1;
-    u = w / (2 * NB);
+    u = w / NB;
   }
   const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, s = l >> 5, row = l & 31;
+  const bool dkw = wv < 2;
+  const int tw = wv & 1;  // token half of the wave
   const int tok0 = ch * kC;
   const size_t kbase = (size_t)u * N * kD;
   const size_t cbase = ((size_t)u * NB + ch) * ((size_t)kKS * 64 * 16);
-  // the carry of the chunk's segment (unused without CARRY)
   const size_t sbase = ((size_t)u * S + (CARRY ? ch / SL : 0)) * ((size_t)kKS * 64 * 16);
-  const int tok = tok0 + 32 * wv + row;
+  const int tok = tok0 + 32 * tw + row;
   const bool ok = tok < N;
   const size_t rowoff = kbase + (size_t)(ok ? tok : N - 1) * kD;
   float x[kD];
   load_rotated(k, rowoff, ok, s, x);
   const LdsRing<4> ring{{ring0, ring1, ring2, ring3}};
-
-  if (part == 1) {
-    f32x16 acc[2] = {f32x16{}, f32x16{}};
-    // four k-steps of dT per ring stage, or two of dT and two of the carry
-    constexpr int UPG = CARRY ? 2 : 4;
-    const uint16_t* csrc = CARRY ? cR + sbase : nullptr;
-    du_issue<UPG, CARRY, 0>(dTR + cbase, csrc, ring, tid);
-    du_issue<UPG, CARRY, 1>(dTR + cbase, csrc, ring, tid);
-    du_issue<UPG, CARRY, 2>(dTR + cbase, csrc, ring, tid);
-    du_group<0, UPG, CARRY>(x, ring, dTR + cbase, csrc, tid, l, acc);
-    // the local parts are loaded together (rows clamped into range), then
-    // stored for the rows below N: a load inside the row test would wait for
-    // each one in turn
-    float lv[2][16];
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int tj = min(tok0 + 32 * wv + c32_row(i, l), N - 1);
-        lv[nt][i] = dvl[kbase + (size_t)tj * kD + 32 * nt + row];
-      }
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int tj = tok0 + 32 * wv + c32_row(i, l);
-        if (tj < N) dv[kbase + (size_t)tj * kD + 32 * nt + row] = from_f<T>(acc[nt][i] + lv[nt][i]);
-      }
-    return;
-  }
+  const uint16_t* src = dTR + cbase;
+  const uint16_t* csrc = CARRY ? cR + sbase : nullptr;
 
   const float* tz = dTz + ((size_t)u * NB + ch) * kFP;
-  for (int idx = tid; idx < kD * kD; idx += 128) {
+  for (int idx = tid; idx < kD * kD; idx += 256) {
     const int r = idx >> 6, c = idx & 63;
     const int d = mz_dim(r >> 5, r & 31);
     const int hi = d > c ? d : c, lo = d > c ? c : d;
     const float val = tz[1 + kD + pair_index(hi, lo)];
     mz[r][(((c >> 3) ^ (r & 7)) << 3) | (c & 7)] = (__bf16)(d == c ? 2.f * val : val);
   }
-  // z1 goes to LDS after the fold, into the then idle ring
   const float zv = tz[1 + (tid & 63)];
   bf16x8 bfr[4];
 #pragma unroll
@@ -453,16 +434,45 @@ __global__ __launch_bounds__(128, 2) void k2_kv_fold(const T* __restrict__ k, co
   float dx[kD];
 #pragma unroll
   for (int m = 0; m < kD; ++m) dx[m] = 0.f;
-  static_assert(2 * kTileElems <= kFG * 1024, "a fold tile and its carry tile fit one ring stage");
-  fold_all<4, false, CARRY>(bfr, x, dx, nullptr, ring, dTR + cbase, CARRY ? cR + sbase : nullptr, tid, l);
+  f32x16 acc[2] = {f32x16{}, f32x16{}};
+  static_assert(2 * kTileElems <= kFG * 1024, "a state tile and its carry tile fit one ring stage");
+  kvm_issue<CARRY>(src, csrc, 0, ring.st[0], tid);
+  kvm_issue<CARRY>(src, csrc, 1, ring.st[1], tid);
+  kvm_issue<CARRY>(src, csrc, 2, ring.st[2], tid);
+  kvm_issue<CARRY>(src, csrc, 3, ring.st[3], tid);
+  ring_sync<kvm_copies<CARRY>() * 3>();
+  if (dkw) {
+    acc[0] = fold_mfma<0, CARRY>(bfr, ring.st[0], l);
+  } else {
+    kvm_du_step<0, CARRY>(x, ring.st[0], l, acc);
+    kvm_du_step<1, CARRY>(x, ring.st[0], l, acc);
+  }
+  kvm_group<0, CARRY>(dkw, bfr, x, dx, acc, ring, src, csrc, tid, l);
+
   float* zl = reinterpret_cast<float*>(ring0);
   __syncthreads();
   if (tid < kD) zl[tid] = zv;
   __syncthreads();
-  // lane group s: dimensions 32 s .. 32 s + 31 of its token
+  if (!dkw) {
+    float lv[2][16];
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int tj = min(tok0 + 32 * tw + c32_row(i, l), N - 1);
+        lv[nt][i] = dvl[kbase + (size_t)tj * kD + 32 * nt + row];
+      }
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int tj = tok0 + 32 * tw + c32_row(i, l);
+        if (tj < N) dv[kbase + (size_t)tj * kD + 32 * nt + row] = from_f<T>(acc[nt][i] + lv[nt][i]);
+      }
+    return;
+  }
   float full[32];
   combine_rotation_groups(dx, s, full);
-  // Z^T [dimension x token] = Mz K^T for this wave's tokens; B = the lane's own k row
   bf16x8 kb[4];
 #pragma unroll
   for (int kk = 0; kk < 4; ++kk) kb[kk] = frag8(k, rowoff + 16 * kk + 8 * s, ok);
@@ -802,12 +812,12 @@ int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, cons
   if (dk) {
     timed("k2_kv_fold", aux, [&] {
       if (w.S > 1)
-        hipLaunchKernelGGL((k2_kv_fold<T, true>), dim3(g.NB * g.U * 2), dim3(128), 0, aux, kt, vt, w.dTR, w.dCR,
-                           w.SL, w.S, w.dTz, w.dkl, w.dvl, g.Hq, g.Hkv, g.N, g.NB, static_cast<T*>(dk),
+        hipLaunchKernelGGL((k2_kv_fold<T, true>), dim3(g.NB * g.U), dim3(256), 0, aux, kt, vt, w.dTR, w.dCR, w.SL,
+                           w.S, w.dTz, w.dkl, w.dvl, g.Hq, g.Hkv, g.N, g.NB, static_cast<T*>(dk),
                            static_cast<T*>(dv));
       else
-        hipLaunchKernelGGL((k2_kv_fold<T, false>), dim3(g.NB * g.U * 2), dim3(128), 0, aux, kt, vt, w.dTR, nullptr,
-                           1, 1, w.dTz, w.dkl, w.dvl, g.Hq, g.Hkv, g.N, g.NB, static_cast<T*>(dk),
+        hipLaunchKernelGGL((k2_kv_fold<T, false>), dim3(g.NB * g.U), dim3(256), 0, aux, kt, vt, w.dTR, nullptr, 1,
+                           1, w.dTz, w.dkl, w.dvl, g.Hq, g.Hkv, g.N, g.NB, static_cast<T*>(dk),
                            static_cast<T*>(dv));
     });
   }
