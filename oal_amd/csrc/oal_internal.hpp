@@ -85,6 +85,10 @@ MfmaWork mfma_work_view(void* base, int B, int Hq, int U, int N, int NB, bool pa
 // a graph like any stream dependency).
 hipStream_t aux_stream(hipStream_t st);
 void stream_wait(hipStream_t waiter, hipStream_t signaller);
+// An event of the device's ring recorded on s now, and a wait for it enqueued
+// on waiter later (stream_wait is the two at once).
+hipEvent_t record_event(hipStream_t s);
+void wait_event(hipStream_t waiter, hipEvent_t ev);
 
 // aux: a second stream for the kernels that do not depend on each other (the
 // intra-chunk VJP beside the state scan, the key-side fold beside the query

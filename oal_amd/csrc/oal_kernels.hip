@@ -802,9 +802,9 @@ oal::LaunchGeom launch_geom(const Geometry& g) { return oal::LaunchGeom{g.B, g.H
 
 // Second stream and fork/join events per device, created on first use and kept
 // until the process ends. An event is recorded on the signalling stream and
-// waited for at once; the ring is long enough that an event is recorded again
-// only after its earlier waits were enqueued (a wait takes the record at the
-// time it is enqueued).
+// waited for within the same call, a few records later at most; the ring is
+// long enough that an event is recorded again only after its earlier waits
+// were enqueued (a wait takes the record at the time it is enqueued).
 constexpr int kAuxDevices = 64;
 constexpr int kAuxEvents = 64;
 struct AuxState {
@@ -851,7 +851,7 @@ hipStream_t aux_stream(hipStream_t st) {
   return a.stream;
 }
 
-void stream_wait(hipStream_t waiter, hipStream_t signaller) {
+hipEvent_t record_event(hipStream_t s) {
   int dev = -1;
   (void)hipGetDevice(&dev);
   hipEvent_t ev = nullptr;
@@ -860,9 +860,13 @@ void stream_wait(hipStream_t waiter, hipStream_t signaller) {
     AuxState& a = g_aux[dev];
     ev = a.events[a.next++ % kAuxEvents];
   }
-  (void)hipEventRecord(ev, signaller);
-  (void)hipStreamWaitEvent(waiter, ev, 0);
+  (void)hipEventRecord(ev, s);
+  return ev;
 }
+
+void wait_event(hipStream_t waiter, hipEvent_t ev) { (void)hipStreamWaitEvent(waiter, ev, 0); }
+
+void stream_wait(hipStream_t waiter, hipStream_t signaller) { wait_event(waiter, record_event(signaller)); }
 
 }  // namespace oal
 

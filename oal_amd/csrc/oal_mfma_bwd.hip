@@ -769,21 +769,32 @@ int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, cons
     hipLaunchKernelGGL(k2_bwd_prep<T>, dim3(g.B * g.Hq * g.NB), dim3(256), 0, st, qt, static_cast<const T*>(dout),
                        dnum, dden, num, den, g.N, g.NB, floor, w.G16, w.Gz, w.GT16, w.QT16);
   });
-  // The state side (the backward scan, its carries and the denominator
-  // column) and the intra-chunk VJP read only what k2_bwd_prep and the forward
-  // wrote: the latter runs on the second stream meanwhile. (Measured: the
-  // denominator kernels or the coefficient reductions on the second stream as
-  // well made the step slower.)
+  // Two streams, joined only at the end. The second stream: the intra-chunk
+  // VJP (dk and dv first: their blocks, 35 KB and 8 KB of LDS, fit on a CU
+  // beside two blocks of the backward scan, 62.5 KB each; the dq kernel's
+  // 66 KB do not), then the query-side fold, which needs only the dq kernel's
+  // local part and what k2_bwd_prep and the forward wrote. The caller's stream:
+  // the state scan, its carry and the denominator kernels, then the key-side
+  // fold after an event that the dk and dv kernels recorded (long past by
+  // then), then the coefficient reductions after the dq kernel's event.
+  // (Measured, per config-2 step: 0.9263-0.9266 -> 0.9035-0.9077 ms against a
+  // join before the two folds, whose cross-stream wait left the GPU idle about
+  // 18 us; moving the denominator kernels or the coefficient reductions to the
+  // second stream was slower.)
   if (forked) stream_wait(aux, st);
   const LocalBwdArgs la{w.G16, w.Gz, w.QT16, w.GT16, sv.KT16, sv.KAP, sv.PZ, sv.PZm, labels, lam, gam, sv.ic, sv.gm,
                         sv.lb, groups, scale, w.dqf, w.dkl, w.dvl, (need_coef && !pairwise) ? w.coefl : nullptr,
                         pairwise, sv.wqs, w.dkp, (need_coef && pairwise) ? w.dwql : nullptr};
-  // dk and dv first: their blocks (35 KB and 8 KB of LDS) fit on a CU beside
-  // two blocks of the backward scan (62.5 KB each), the dq kernel's (66 KB) do
-  // not, so the dq kernel runs after them, beside the scan's tail and the
-  // denominator kernels (measured: 0.946-0.949 -> 0.936-0.938 ms per step).
   launch_local_bwd<T>(g, qt, kt, vt, la, dq != nullptr, dk != nullptr, kLocalDkv, aux, timed);
+  hipEvent_t ev_dkv = forked ? record_event(aux) : nullptr;
   launch_local_bwd<T>(g, qt, kt, vt, la, dq != nullptr, dk != nullptr, kLocalDq, aux, timed);
+  hipEvent_t ev_dq = forked ? record_event(aux) : nullptr;
+  if (dq) {
+    timed("k2_q_fold", aux, [&] {
+      hipLaunchKernelGGL(k2_q_fold<T>, dim3(g.R * g.NB * g.U), dim3(128), 0, aux, qt, w.G16, sv.wqs, sv.PR, w.dqf,
+                         g.Hq, g.Hkv, g.N, g.NB, static_cast<T*>(dq));
+    });
+  }
   {
     const ScanPlan plan{w.S, w.SL, 0};
     // without a coefficient gradient the scan forms no coefficient partials
@@ -796,31 +807,21 @@ int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, cons
                    need_coef ? w.dwz : nullptr, st, timed);
     launch_den_scan(false, g, w.dCt, w.dTz, nullptr, st, timed);
   }
-  // join, then fork again: the folds need both sides; the key-side fold runs
-  // on the second stream beside the query-side one (whose last round of blocks
-  // would otherwise leave half the CUs idle)
-  if (forked) {
-    stream_wait(st, aux);
-    stream_wait(aux, st);
-  }
-  if (dq) {
-    timed("k2_q_fold", st, [&] {
-      hipLaunchKernelGGL(k2_q_fold<T>, dim3(g.R * g.NB * g.U), dim3(128), 0, st, qt, w.G16, sv.wqs, sv.PR, w.dqf,
-                         g.Hq, g.Hkv, g.N, g.NB, static_cast<T*>(dq));
-    });
-  }
   if (dk) {
-    timed("k2_kv_fold", aux, [&] {
+    // the per-pair path forms its local dk in the dq part's launch
+    if (forked) wait_event(st, pairwise ? ev_dq : ev_dkv);
+    timed("k2_kv_fold", st, [&] {
       if (w.S > 1)
-        hipLaunchKernelGGL((k2_kv_fold<T, true>), dim3(g.NB * g.U), dim3(256), 0, aux, kt, vt, w.dTR, w.dCR, w.SL,
+        hipLaunchKernelGGL((k2_kv_fold<T, true>), dim3(g.NB * g.U), dim3(256), 0, st, kt, vt, w.dTR, w.dCR, w.SL,
                            w.S, w.dTz, w.dkl, w.dvl, g.Hq, g.Hkv, g.N, g.NB, static_cast<T*>(dk),
                            static_cast<T*>(dv));
       else
-        hipLaunchKernelGGL((k2_kv_fold<T, false>), dim3(g.NB * g.U), dim3(256), 0, aux, kt, vt, w.dTR, nullptr, 1,
+        hipLaunchKernelGGL((k2_kv_fold<T, false>), dim3(g.NB * g.U), dim3(256), 0, st, kt, vt, w.dTR, nullptr, 1,
                            1, w.dTz, w.dkl, w.dvl, g.Hq, g.Hkv, g.N, g.NB, static_cast<T*>(dk),
                            static_cast<T*>(dv));
     });
   }
+  if (forked && need_coef) wait_event(st, ev_dq);
   if (need_coef) {
     // group-sum path: the 73 local coefficient columns; per-pair path: the
     // local slot partials added to the state's

@@ -1,8 +1,9 @@
 """The C-ABI forward and backward captured into a HIP graph (torch.cuda.graph)
 and replayed: the backward's second-stream fork and join (the intra-chunk VJP
-beside the state scan, the key-side fold beside the query-side one) are
-captured as event dependencies. Each replay follows other eager work and a
-synchronization, and must reproduce the eager results bitwise."""
+and the query-side fold on the second stream, events before the key-side fold
+and the reductions, the final join) are captured as event dependencies. Each
+replay follows other eager work and a synchronization, and must reproduce the
+eager results bitwise."""
 
 import pytest
 import torch

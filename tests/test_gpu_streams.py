@@ -1,12 +1,14 @@
 """The backward's second stream as the caller sees it: one stream.
 
-``oal_backward`` forks the intra-chunk VJP and the key-side fold onto a stream
-of the library's own and joins it back into the caller's stream before it
-returns. These tests call it on caller-created streams (not the default one),
-from two streams in turn, and consume the gradients on the caller's stream
-right after the call with no synchronization in between. Every result must be
-bitwise equal to the same call on the default stream, so a missing join would
-show up as a read of a gradient that is not yet written.
+``oal_backward`` forks the intra-chunk VJP and the query-side fold onto a
+stream of the library's own, makes the caller's stream wait for events the
+second stream recorded before the key-side fold and the coefficient
+reductions, and joins it back into the caller's stream before it returns.
+These tests call it on caller-created streams (not the default one), from two
+streams in turn, and consume the gradients on the caller's stream right after
+the call with no synchronization in between. Every result must be bitwise
+equal to the same call on the default stream, so a missing join would show up
+as a read of a gradient that is not yet written.
 """
 
 import pytest
