@@ -5,10 +5,11 @@
  * takes plain device pointers and sizes; no framework types cross this boundary.
  * Callers own every buffer (inputs, outputs, the forward's saved state and the
  * backward's workspace; sizes come from the *_bytes queries). Work is enqueued on
- * the caller's HIP stream and nothing is synchronized (oal_backward may run part
- * of its work on a second stream of the library's own, forked from and joined
- * back to the caller's stream by events, so the caller sees one stream). The
- * library allocates no device memory.
+ * the caller's HIP stream and nothing is synchronized (oal_backward, and
+ * oal_forward on the fp32 route, may run part of their work on a second stream
+ * of the library's own, forked from and joined back to the caller's stream by
+ * events, so the caller sees one stream). The library allocates no device
+ * memory.
  *
  * Operator (reference oal_attention/grouped_reference.py:102-211):
  *   s_g(i,j)   = scale * sum_{d: labels[h][d] == g} q[i][d] * k[j][d]
@@ -116,8 +117,9 @@ int oal_forward(const void* q, const void* k, const void* v,
  * gather, grouped_reference.py:89-93, routes pair (r, c), r >= c, to
  * [g(r)][g(c)] only; gradients reaching a factor L with gam = L L^T, or a
  * per-pair coefficient, are the same under both.) Invalid combinations are
- * refused before anything is enqueued. On the matrix-core path the intra-chunk
- * VJP and the query-side fold run on a second stream (one per device, default
+ * refused before anything is enqueued. On the matrix-core paths (bf16, and fp32
+ * with up to 8 groups) the intra-chunk VJP and the query-side fold run on a
+ * second stream (one per device, default
  * priority, created with its fork/join events on the first call; not created
  * while the caller's stream is capturing a graph, whose call then stays on the
  * caller's stream). Every kernel on it waits for an event recorded on the

@@ -1150,7 +1150,33 @@ void launch_f32_readout_fwd(const LaunchGeom& g, const T* q, const float* wq, co
 }
 
 template <typename T>
-void launch_f32_backward(const LaunchGeom& g, const F32BwdArgs<T>& a, hipStream_t st, const Timer& timed) {
+void launch_f32_backward(const LaunchGeom& g, const F32BwdArgs<T>& a, hipStream_t st, hipStream_t aux,
+                         const Timer& timed) {
+  // Two streams, as on the bf16 path: the intra-chunk VJP and then the
+  // query-side fold on the second stream beside the state scan; the dk and dv
+  // kernels and the coefficient reduction wait on the caller's stream for the
+  // event the second stream records after the dk / dv / coefficient part.
+  const bool forked = aux != st;
+  if (forked) stream_wait(aux, st);
+  // the two orientations in separate launches: the dq part fits two blocks per
+  // CU, the dk / dv / coefficient part one
+  timed("k3_local_kv", aux, [&] {
+    hipLaunchKernelGGL((k3_local<T, 1>), dim3(g.R * g.NB * g.U), dim3(192), 0, aux, a.q, a.k, a.v, a.G, a.Gz,
+                       a.labels, a.c0, a.lam, a.gam, a.groups, g.Hq, g.Hkv, g.N, g.NB, a.scale, a.dql, a.dkl, a.dvl,
+                       a.coefl);
+  });
+  hipEvent_t ev_kv = forked ? record_event(aux) : nullptr;
+  timed("k3_local_dq", aux, [&] {
+    hipLaunchKernelGGL((k3_local<T, 0>), dim3(g.R * g.NB * g.U), dim3(192), 0, aux, a.q, a.k, a.v, a.G, a.Gz,
+                       a.labels, a.c0, a.lam, a.gam, a.groups, g.Hq, g.Hkv, g.N, g.NB, a.scale, a.dql, a.dkl, a.dvl,
+                       a.coefl);
+  });
+  if (a.dq) {
+    timed("k3_fold_q", aux, [&] {
+      hipLaunchKernelGGL((k3_fold<T, 0>), dim3(g.R * g.NB * g.U), dim3(128), 0, aux, a.q, a.G, nullptr, a.Gz, a.wq,
+                         a.P, a.Pz, a.dql, g.Hq, g.Hkv, g.N, g.NB, a.dq, nullptr, nullptr, 1, 1);
+    });
+  }
   // the scan also forms the state coefficient partials (its per-item products)
   if (a.dk || a.dv || a.dwq_part) {
     timed("k3_state_bwd", st, [&] {
@@ -1169,24 +1195,7 @@ void launch_f32_backward(const LaunchGeom& g, const F32BwdArgs<T>& a, hipStream_
   // carries (the later segments' totals) as they stage the state
   const float* cS = a.plan.S > 1 ? a.segt : nullptr;
   const float* cSz = a.plan.S > 1 ? a.segtz : nullptr;
-  // the two orientations in separate launches: the dq part fits two blocks per
-  // CU, the dk / dv / coefficient part one
-  timed("k3_local_dq", st, [&] {
-    hipLaunchKernelGGL((k3_local<T, 0>), dim3(g.R * g.NB * g.U), dim3(192), 0, st, a.q, a.k, a.v, a.G, a.Gz,
-                       a.labels, a.c0, a.lam, a.gam, a.groups, g.Hq, g.Hkv, g.N, g.NB, a.scale, a.dql, a.dkl, a.dvl,
-                       a.coefl);
-  });
-  timed("k3_local_kv", st, [&] {
-    hipLaunchKernelGGL((k3_local<T, 1>), dim3(g.R * g.NB * g.U), dim3(192), 0, st, a.q, a.k, a.v, a.G, a.Gz,
-                       a.labels, a.c0, a.lam, a.gam, a.groups, g.Hq, g.Hkv, g.N, g.NB, a.scale, a.dql, a.dkl, a.dvl,
-                       a.coefl);
-  });
-  if (a.dq) {
-    timed("k3_fold_q", st, [&] {
-      hipLaunchKernelGGL((k3_fold<T, 0>), dim3(g.R * g.NB * g.U), dim3(128), 0, st, a.q, a.G, nullptr, a.Gz, a.wq,
-                         a.P, a.Pz, a.dql, g.Hq, g.Hkv, g.N, g.NB, a.dq, nullptr, nullptr, 1, 1);
-    });
-  }
+  if (forked) wait_event(st, ev_kv);
   if (a.dk) {
     timed("k3_fold_k", st, [&] {
       auto* kern = cS ? k3_fold<T, 1, true> : k3_fold<T, 1, false>;
@@ -1216,7 +1225,8 @@ void launch_f32_backward(const LaunchGeom& g, const F32BwdArgs<T>& a, hipStream_
                                         hipStream_t, const Timer&);                                                 \
   template void launch_f32_readout_fwd<T>(const LaunchGeom&, const T*, const float*, const float*, const float*, \
                                           float, float*, float*, T*, hipStream_t, const Timer&);                  \
-  template void launch_f32_backward<T>(const LaunchGeom&, const F32BwdArgs<T>&, hipStream_t, const Timer&);
+  template void launch_f32_backward<T>(const LaunchGeom&, const F32BwdArgs<T>&, hipStream_t, hipStream_t,          \
+                                       const Timer&);
 OAL_F32MMA_INST(float)
 OAL_F32MMA_INST(uint16_t)
 #undef OAL_F32MMA_INST

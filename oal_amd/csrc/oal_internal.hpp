@@ -212,7 +212,8 @@ struct F32BwdArgs {
   T *dq, *dk, *dv;
 };
 template <typename T>
-void launch_f32_backward(const LaunchGeom& g, const F32BwdArgs<T>& a, hipStream_t st, const Timer& timed);
+void launch_f32_backward(const LaunchGeom& g, const F32BwdArgs<T>& a, hipStream_t st, hipStream_t aux,
+                         const Timer& timed);
 
 struct ScanArgs {
   const uint16_t* F;  // feature side, [X][frows][NB * 64] bf16 (rows 0..63 used)

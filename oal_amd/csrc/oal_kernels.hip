@@ -879,7 +879,7 @@ oal::Timer make_timer() {
 template <typename T, int GMAX>
 int forward_impl(const Geometry& g, const void* q, const void* k, const void* v, const int32_t* labels,
                  const float* c0, const float* lam, const float* gam, int groups, float scale, float floor,
-                 void* out, float* num, float* den, void* saved, hipStream_t st) {
+                 void* out, float* num, float* den, void* saved, hipStream_t st, hipStream_t aux) {
   using namespace oal;
   SavedView sv = saved_view(g, saved);
   const T* qt = static_cast<const T*>(q);
@@ -890,8 +890,14 @@ int forward_impl(const Geometry& g, const void* q, const void* k, const void* v,
   if constexpr (GMAX <= 8) {
     // matrix-core route: state scan, intra-chunk part, then the state readout
     const oal::LaunchGeom lg = launch_geom(g);
+    // the intra-chunk part on the second stream beside the state scan, whose
+    // 272 blocks leave most CUs idle (measured with the backward's fork:
+    // 3.944-3.953 -> 3.774-3.783 ms per config-2 step)
+    const bool forked = aux != st;
+    if (forked) oal::stream_wait(aux, st);
+    oal::launch_f32_intra_fwd<T>(lg, qt, kt, vt, labels, c0, lam, gam, groups, scale, num, den, aux, make_timer());
     oal::launch_f32_state_fwd<T>(lg, kt, vt, sv.carry, sv.carry_z, st, make_timer());
-    oal::launch_f32_intra_fwd<T>(lg, qt, kt, vt, labels, c0, lam, gam, groups, scale, num, den, st, make_timer());
+    if (forked) oal::stream_wait(st, aux);
     oal::launch_f32_readout_fwd<T>(lg, qt, sv.wq, sv.carry, sv.carry_z, floor, num, den, static_cast<T*>(out), st,
                                    make_timer());
     return launch_status("oal_forward launch");
@@ -909,7 +915,7 @@ int backward_impl(const Geometry& g, const void* q, const void* k, const void* v
                   const float* c0, const float* lam, const float* gam, int groups, float scale, float floor,
                   const float* num, const float* den, const void* saved, const void* dout, const float* dnum,
                   const float* dden, void* dq, void* dk, void* dv, float* dc0, float* dlam, float* dgam,
-                  void* workspace, hipStream_t st) {
+                  void* workspace, hipStream_t st, hipStream_t aux) {
   using namespace oal;
   SavedView sv = saved_view(g, const_cast<void*>(saved));
   WorkView w = work_view(g, workspace, GMAX <= 8);
@@ -928,13 +934,15 @@ int backward_impl(const Geometry& g, const void* q, const void* k, const void* v
                          need_coef ? w.dwq_part : nullptr, w.dql, w.dkl, w.dvl,
                          need_coef ? w.coefl : nullptr, w.coefs, static_cast<T*>(dq), static_cast<T*>(dk),
                          static_cast<T*>(dv)};
-    oal::launch_f32_backward<T>(lg, a, st, make_timer());
+    oal::launch_f32_backward<T>(lg, a, st, aux, make_timer());
     if (need_coef) {
       timed("k_dwq_reduce", st, [&] { hipLaunchKernelGGL(k_dwq_reduce, dim3((kFP + 63) / 64, g.Hq), dim3(1024), 0, st, w.dwq_part, g.B, g.Hq,
                          g.NB, w.dwq); });
       timed("k_coef_grad", st, [&] { hipLaunchKernelGGL(k_coef_grad, dim3(g.Hq), dim3(256), 0, st, w.dwq, labels, groups, scale, dc0, dlam,
                          dgam, w.coefs); });
     }
+    // the caller's stream ends after every kernel of the call
+    if (aux != st) oal::stream_wait(st, aux);
     return launch_status("oal_backward launch");
   }
   if (dk || dv) {
@@ -1104,12 +1112,12 @@ int oal_forward(const void* q, const void* k, const void* v, const int32_t* labe
   }
   if (dtype == OAL_DTYPE_F32) {
     if (groups <= 8)
-      return forward_impl<float, 8>(g, q, k, v, labels, c0, lam, gam, groups, scale, floor, out, num, den, saved, st);
-    return forward_impl<float, 64>(g, q, k, v, labels, c0, lam, gam, groups, scale, floor, out, num, den, saved, st);
+      return forward_impl<float, 8>(g, q, k, v, labels, c0, lam, gam, groups, scale, floor, out, num, den, saved, st, oal::aux_stream(st));
+    return forward_impl<float, 64>(g, q, k, v, labels, c0, lam, gam, groups, scale, floor, out, num, den, saved, st, st);
   }
   if (groups <= 8)
-    return forward_impl<uint16_t, 8>(g, q, k, v, labels, c0, lam, gam, groups, scale, floor, out, num, den, saved, st);
-  return forward_impl<uint16_t, 64>(g, q, k, v, labels, c0, lam, gam, groups, scale, floor, out, num, den, saved, st);
+    return forward_impl<uint16_t, 8>(g, q, k, v, labels, c0, lam, gam, groups, scale, floor, out, num, den, saved, st, oal::aux_stream(st));
+  return forward_impl<uint16_t, 64>(g, q, k, v, labels, c0, lam, gam, groups, scale, floor, out, num, den, saved, st, st);
 }
 
 }  // extern "C"
@@ -1157,12 +1165,15 @@ int backward_entry(const void* q, const void* k, const void* v, const int32_t* l
 #define OAL_BWD_ARGS                                                                                       \
   g, q, k, v, labels, c0, lam, gam, groups, scale, floor, num, den, saved, dout, dnum, dden, dq, dk, dv, dc0, \
       dlam, dgam, workspace, st
+  // the fp32 matrix-core route (up to 8 groups) may fork like the bf16 path;
+  // the scalar kernels for more groups run on the caller's stream
+  const hipStream_t aux8 = may_fork ? oal::aux_stream(st) : st;
   if (dtype == OAL_DTYPE_F32) {
-    if (groups <= 8) return backward_impl<float, 8>(OAL_BWD_ARGS);
-    return backward_impl<float, 64>(OAL_BWD_ARGS);
+    if (groups <= 8) return backward_impl<float, 8>(OAL_BWD_ARGS, aux8);
+    return backward_impl<float, 64>(OAL_BWD_ARGS, st);
   }
-  if (groups <= 8) return backward_impl<uint16_t, 8>(OAL_BWD_ARGS);
-  return backward_impl<uint16_t, 64>(OAL_BWD_ARGS);
+  if (groups <= 8) return backward_impl<uint16_t, 8>(OAL_BWD_ARGS, aux8);
+  return backward_impl<uint16_t, 64>(OAL_BWD_ARGS, st);
 #undef OAL_BWD_ARGS
 }
 
