@@ -41,9 +41,9 @@ def _inputs(dev, n=1000, seed=43):
     return q, k, v, labels.to(dev), c0, lam, gam, dout
 
 
-def _step(inp):
+def _step(inp, precision="bf16"):
     q, k, v, labels, c0, lam, gam, dout = inp
-    kw = dict(scale=0.125, floor=0.0, precision="bf16")
+    kw = dict(scale=0.125, floor=0.0, precision=precision)
     out, num, den, saved = _native.forward(q, k, v, labels, c0, lam, gam, **kw)
     grads = _native.backward(q, k, v, labels, c0, lam, gam, num, den, saved, dout, None, None,
                              need_q=True, need_k=True, need_v=True, need_coef=True, **kw)
@@ -51,10 +51,13 @@ def _step(inp):
     return [t.clone() for t in (out, num, den, *grads)]
 
 
-def test_backward_on_caller_streams_is_joined_before_the_next_work():
+@pytest.mark.parametrize("precision", ["bf16", "fp32"])
+def test_backward_on_caller_streams_is_joined_before_the_next_work(precision):
+    """bf16: the matrix-core backward's fork; fp32: the fp32 route's forward and
+    backward forks."""
     dev = _dev()
     inp = _inputs(dev)
-    ref = _step(inp)
+    ref = _step(inp, precision)
     torch.cuda.synchronize()
     streams = [torch.cuda.Stream(dev), torch.cuda.Stream(dev)]
     results = []
@@ -62,7 +65,7 @@ def test_backward_on_caller_streams_is_joined_before_the_next_work():
         st = streams[rep % 2]
         st.wait_stream(torch.cuda.current_stream(dev))
         with torch.cuda.stream(st):
-            res = _step(inp)
+            res = _step(inp, precision)
             # more work on the same stream right behind the copies
             res.append(res[3].float().sum())
         results.append((st, res))
