@@ -893,11 +893,15 @@ int forward_impl(const Geometry& g, const void* q, const void* k, const void* v,
     // the intra-chunk part on the second stream beside the state scan, whose
     // 272 blocks leave most CUs idle (measured with the backward's fork:
     // 3.944-3.953 -> 3.774-3.783 ms per config-2 step)
-    const bool forked = aux != st;
-    if (forked) oal::stream_wait(aux, st);
-    oal::launch_f32_intra_fwd<T>(lg, qt, kt, vt, labels, c0, lam, gam, groups, scale, num, den, aux, make_timer());
-    oal::launch_f32_state_fwd<T>(lg, kt, vt, sv.carry, sv.carry_z, st, make_timer());
-    if (forked) oal::stream_wait(st, aux);
+    if (aux != st) {
+      oal::stream_wait(aux, st);
+      oal::launch_f32_intra_fwd<T>(lg, qt, kt, vt, labels, c0, lam, gam, groups, scale, num, den, aux, make_timer());
+      oal::launch_f32_state_fwd<T>(lg, kt, vt, sv.carry, sv.carry_z, st, make_timer());
+      oal::stream_wait(st, aux);
+    } else {
+      oal::launch_f32_state_fwd<T>(lg, kt, vt, sv.carry, sv.carry_z, st, make_timer());
+      oal::launch_f32_intra_fwd<T>(lg, qt, kt, vt, labels, c0, lam, gam, groups, scale, num, den, st, make_timer());
+    }
     oal::launch_f32_readout_fwd<T>(lg, qt, sv.wq, sv.carry, sv.carry_z, floor, num, den, static_cast<T*>(out), st,
                                    make_timer());
     return launch_status("oal_forward launch");

@@ -781,19 +781,25 @@ int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, cons
   // join before the two folds, whose cross-stream wait left the GPU idle about
   // 18 us; moving the denominator kernels or the coefficient reductions to the
   // second stream was slower.)
-  if (forked) stream_wait(aux, st);
   const LocalBwdArgs la{w.G16, w.Gz, w.QT16, w.GT16, sv.KT16, sv.KAP, sv.PZ, sv.PZm, labels, lam, gam, sv.ic, sv.gm,
                         sv.lb, groups, scale, w.dqf, w.dkl, w.dvl, (need_coef && !pairwise) ? w.coefl : nullptr,
                         pairwise, sv.wqs, w.dkp, (need_coef && pairwise) ? w.dwql : nullptr};
-  launch_local_bwd<T>(g, qt, kt, vt, la, dq != nullptr, dk != nullptr, kLocalDkv, aux, timed);
-  hipEvent_t ev_dkv = forked ? record_event(aux) : nullptr;
-  launch_local_bwd<T>(g, qt, kt, vt, la, dq != nullptr, dk != nullptr, kLocalDq, aux, timed);
-  hipEvent_t ev_dq = forked ? record_event(aux) : nullptr;
-  if (dq) {
-    timed("k2_q_fold", aux, [&] {
-      hipLaunchKernelGGL(k2_q_fold<T>, dim3(g.R * g.NB * g.U), dim3(128), 0, aux, qt, w.G16, sv.wqs, sv.PR, w.dqf,
-                         g.Hq, g.Hkv, g.N, g.NB, static_cast<T*>(dq));
-    });
+  auto q_fold = [&](hipStream_t s) {
+    if (dq) {
+      timed("k2_q_fold", s, [&] {
+        hipLaunchKernelGGL(k2_q_fold<T>, dim3(g.R * g.NB * g.U), dim3(128), 0, s, qt, w.G16, sv.wqs, sv.PR, w.dqf,
+                           g.Hq, g.Hkv, g.N, g.NB, static_cast<T*>(dq));
+      });
+    }
+  };
+  hipEvent_t ev_dkv = nullptr, ev_dq = nullptr;
+  if (forked) {
+    stream_wait(aux, st);
+    launch_local_bwd<T>(g, qt, kt, vt, la, dq != nullptr, dk != nullptr, kLocalDkv, aux, timed);
+    ev_dkv = record_event(aux);
+    launch_local_bwd<T>(g, qt, kt, vt, la, dq != nullptr, dk != nullptr, kLocalDq, aux, timed);
+    ev_dq = record_event(aux);
+    q_fold(aux);
   }
   {
     const ScanPlan plan{w.S, w.SL, 0};
@@ -806,6 +812,15 @@ int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, cons
     launch_den_bwd(g, w.QT16, w.GT16, kTRows, sv.gm, sv.lb, sv.ic, kIC, sv.PZ, sv.PZm, w.dCt,
                    need_coef ? w.dwz : nullptr, st, timed);
     launch_den_scan(false, g, w.dCt, w.dTz, nullptr, st, timed);
+  }
+  if (!forked) {
+    // one stream (the allocation-free entry point, the profiling mode, a call
+    // made during a graph capture before the second stream exists): the state
+    // side first, then the intra-chunk VJP and the query-side fold (on one
+    // stream 0.950-0.951 ms per config-2 step, against 0.955 with the
+    // intra-chunk VJP first)
+    launch_local_bwd<T>(g, qt, kt, vt, la, dq != nullptr, dk != nullptr, kLocalDq | kLocalDkv, st, timed);
+    q_fold(st);
   }
   if (dk) {
     // the per-pair path forms its local dk in the dq part's launch
