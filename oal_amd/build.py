@@ -20,6 +20,12 @@ SOURCES = [os.path.join(PKG, "csrc", "oal_kernels.hip"), os.path.join(PKG, "csrc
            os.path.join(PKG, "csrc", "oal_mfma_scan.hip"), os.path.join(PKG, "csrc", "oal_mfma_den.hip"),
            os.path.join(PKG, "csrc", "oal_mfma_pair.hip"), os.path.join(PKG, "csrc", "oal_f32_mma.hip"),
            os.path.join(PKG, "csrc", "oal_f64.hip")]
+# Sources whose matrix-core accumulators the compiler would otherwise place in
+# the accumulation registers (AGPRs): there every VALU use of a group sum needs
+# a v_accvgpr_read copy first (256 of them per tile in the intra-chunk forward).
+# In VGPRs the VALU reads them directly; each kernel in these files stays
+# within 256 VGPRs without spilling.
+VGPR_FORM = {"oal_mfma_fwd.hip", "oal_mfma_local.hip"}
 HEADERS = [os.path.join(PKG, "csrc", "oal_common.hpp"), os.path.join(ROOT, "include", "oal_amd.h")]
 OUTPUT = os.path.join(PKG, "liboal_amd.so")
 OBJDIR = os.path.join(PKG, "_build")
@@ -46,6 +52,10 @@ def compile_flags() -> list[str]:
     ]
 
 
+def source_flags(src: str) -> list[str]:
+    return ["-mllvm", "-amdgpu-mfma-vgpr-form"] if os.path.basename(src) in VGPR_FORM else []
+
+
 def link_flags() -> list[str]:
     rocm = os.path.dirname(os.path.dirname(os.path.realpath(hipcc())))
     libdir = os.path.join(rocm, "lib")
@@ -66,7 +76,7 @@ def build(verbose: bool = False) -> str:
     os.makedirs(OBJDIR, exist_ok=True)
     objs = [os.path.join(OBJDIR, os.path.splitext(os.path.basename(s))[0] + ".o") for s in SOURCES]
     cc = hipcc()
-    jobs = [[cc, *compile_flags(), "-c", src, "-o", obj] for src, obj in zip(SOURCES, objs)]
+    jobs = [[cc, *compile_flags(), *source_flags(src), "-c", src, "-o", obj] for src, obj in zip(SOURCES, objs)]
     workers = max(1, min(len(jobs), os.cpu_count() or 1))
     with ThreadPoolExecutor(max_workers=workers) as pool:
         for fut in [pool.submit(_run, j, verbose) for j in jobs]:
