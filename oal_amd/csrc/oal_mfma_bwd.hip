@@ -202,16 +202,16 @@ __device__ __forceinline__ f32x16 fold_mfma(const bf16x8 (&bfr)[4], const __bf16
 }
 
 // Ring pipeline over the 69 M-tiles with NS LDS stages. Group G enters with
-// the product of tile G in flight (Dc) and its weights read (wc); it waits for
-// tile G + 1, refills the stage of tile G (whose reads ended before the
-// barrier) with tile G + NS, issues the product of tile G + 1 and reads its
-// weights, then folds tile G, so the fold's VALU work overlaps the next tile's
-// matrix products and LDS reads. Up to NS - 2 tiles stay in flight.
-template <int G, int NS, bool WEIGHTED, bool CARRY>
+// the product of tile G in flight (Dc) and its slot weights read (wc, one
+// register: fold_weight_row); it waits for tile G + 1, refills the stage of
+// tile G (whose reads ended before the barrier) with tile G + NS, issues the
+// product of tile G + 1 and reads its weights, then folds tile G, so the fold's
+// VALU work overlaps the next tile's matrix products and LDS reads. Up to
+// NS - 2 tiles stay in flight.
+template <int G, int NS, bool CARRY>
 __device__ __forceinline__ void fold_group(const bf16x8 (&bfr)[4], const float (&x)[kD], float (&dx)[kD],
                                            const float* wl, const LdsRing<NS>& ring, const uint16_t* src,
-                                           const uint16_t* csrc, int tid, int lane, const f32x16& Dc,
-                                           const float (&wc)[16]) {
+                                           const uint16_t* csrc, int tid, int lane, const f32x16& Dc, float wc) {
   constexpr int NT = kS / 32;  // 69 M-tiles
   if constexpr (G + 1 < NT) {
     constexpr int issued = (G + NS - 1 < NT - 1) ? G + NS - 1 : NT - 1;  // last tile issued so far
@@ -219,17 +219,16 @@ __device__ __forceinline__ void fold_group(const bf16x8 (&bfr)[4], const float (
     ring_sync<fold_copies<CARRY>() * (issued - (G + 1))>();
     if constexpr (G + NS < NT) fold_issue<CARRY>(src, csrc, G + NS, ring.st[(G + NS) % NS], tid);
     const f32x16 Dn = fold_mfma<G + 1, CARRY>(bfr, ring.st[(G + 1) % NS], lane);
-    float wn[16];
-    fold_weights<G + 1, WEIGHTED>(wl, lane >> 5, wn);
-    fold_tile<G>(Dc, x, dx, wc);
-    fold_group<G + 1, NS, WEIGHTED, CARRY>(bfr, x, dx, wl, ring, src, csrc, tid, lane, Dn, wn);
+    const float wn = fold_weight_row<G + 1>(wl, lane);
+    fold_tile_row<G>(Dc, x, dx, wc);
+    fold_group<G + 1, NS, CARRY>(bfr, x, dx, wl, ring, src, csrc, tid, lane, Dn, wn);
   } else {
-    fold_tile<G>(Dc, x, dx, wc);
+    fold_tile_row<G>(Dc, x, dx, wc);
   }
 }
 
 // Whole fold: tiles 0 .. NS - 1 in flight, product of tile 0, then the groups.
-template <int NS, bool WEIGHTED, bool CARRY>
+template <int NS, bool CARRY>
 __device__ __forceinline__ void fold_all(const bf16x8 (&bfr)[4], const float (&x)[kD], float (&dx)[kD],
                                          const float* wl, const LdsRing<NS>& ring, const uint16_t* src,
                                          const uint16_t* csrc, int tid, int lane) {
@@ -239,9 +238,8 @@ __device__ __forceinline__ void fold_all(const bf16x8 (&bfr)[4], const float (&x
   }(std::make_integer_sequence<int, NS>{});
   ring_sync<fold_copies<CARRY>() * (NS - 1)>();
   const f32x16 D0 = fold_mfma<0, CARRY>(bfr, ring.st[0], lane);
-  float w0[16];
-  fold_weights<0, WEIGHTED>(wl, lane >> 5, w0);
-  fold_group<0, NS, WEIGHTED, CARRY>(bfr, x, dx, wl, ring, src, csrc, tid, lane, D0, w0);
+  const float w0 = fold_weight_row<0>(wl, lane);
+  fold_group<0, NS, CARRY>(bfr, x, dx, wl, ring, src, csrc, tid, lane, D0, w0);
 }
 
 // ---------------------------------------------------------------------------
@@ -277,7 +275,7 @@ __global__ __launch_bounds__(128, 2) void k2_q_fold(const T* __restrict__ q, con
   for (int kk = 0; kk < 4; ++kk) bfr[kk] = frag8(G16, rowoff + 16 * kk + 8 * s, ok);
 #pragma unroll
   for (int m = 0; m < kD; ++m) dx[m] = 0.f;
-  fold_all<6, true, false>(bfr, x, dx, wl, ring, src, nullptr, tid, l);
+  fold_all<6, false>(bfr, x, dx, wl, ring, src, nullptr, tid, l);
 
   // lane group s writes dimensions 32 s .. 32 s + 31 of its token
   float full[32];

@@ -171,6 +171,46 @@ template <int T>
 __device__ __forceinline__ bf16x8 feature_fragment(const float (&x)[kD], const float (&w)[8]) {
   return feature_fragment_impl<T>(x, w, std::make_integer_sequence<int, 8>{});
 }
+// Lane J of this lane's 16-lane row (DPP row_newbcast:J). Used as an operand
+// of a VALU instruction it folds into that instruction's DPP source, so a
+// per-slot weight reaches the lanes that need it without its own instruction:
+// one register can hold the 16 weights a row of lanes uses in turn, in place
+// of an LDS read of every weight by every lane.
+template <int J>
+__device__ __forceinline__ float row_bcast(float w) {
+  static_assert(J >= 0 && J < 16, "a row has 16 lanes");
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(w), 0x150 + J, 0xf, 0xf, true));
+}
+// Weighted feature of base B with the weight wb applied to the first factor:
+// the instruction that reads the broadcast weight then reads no register
+// written by the VALU just before it (a DPP read of such a register needs two
+// wait states).
+template <int B>
+__device__ __forceinline__ float weighted_base(const float (&x)[kD], float wb) {
+  constexpr int rb = kSlotHost.rb[B], cb = kSlotHost.cb[B];
+  if constexpr (rb == 65) {
+    return 0.f * wb;
+  } else if constexpr (rb == 64) {
+    return wb;
+  } else if constexpr (cb == 64) {
+    return x[rb] * wb;
+  } else {
+    return (x[rb] * wb) * x[cb];
+  }
+}
+// feature_fragment with the weights in one register: lane OFF + j of each row
+// holds the weight of slot 8 s + j of k-step T (j < 8; s = the row's lane
+// group; OFF = 0 or 8, so that a register can serve two k-steps).
+template <int T, int OFF, int... J>
+__device__ __forceinline__ bf16x8 feature_fragment_row_impl(const float (&x)[kD], float wrow,
+                                                            std::integer_sequence<int, J...>) {
+  float v[8] = {weighted_base<8 * T + J>(x, row_bcast<OFF + J>(wrow))...};
+  return pack8(v);
+}
+template <int T, int OFF = 0>
+__device__ __forceinline__ bf16x8 feature_fragment_row(const float (&x)[kD], float wrow) {
+  return feature_fragment_row_impl<T, OFF>(x, wrow, std::make_integer_sequence<int, 8>{});
+}
 template <int T, int... J>
 __device__ __forceinline__ bf16x8 raw_fragment_impl(const float (&x)[kD], std::integer_sequence<int, J...>) {
   float v[8] = {base_value<8 * T + J>(x)...};

@@ -77,6 +77,15 @@ __device__ __forceinline__ void fold_weights(const float* wl, int s, float (&w16
   }
 }
 
+// Slot weights of M-tile M in one register: lane j of each 16-lane row holds
+// the weight of accumulator register j of the row's lane group s (slot
+// 32 M + 16 (j / 8) + 8 s + j % 8), for fold_tile_row.
+template <int M>
+__device__ __forceinline__ float fold_weight_row(const float* wl, int lane) {
+  const int j = lane & 15, s = lane >> 5;
+  return wl[32 * M + 16 * (j >> 3) + 8 * s + (j & 7)];
+}
+
 // Fold of one 32-slot M-tile (rows permuted so that the rows a lane holds are
 // slots of its rotation group): dx[rb] += d x[cb], dx[cb] += d x[rb].
 template <int M>
@@ -88,6 +97,26 @@ __device__ __forceinline__ void fold_tile(const f32x16& D, const float (&x)[kD],
        constexpr int base = 8 * (2 * M + a / 2) + 4 * (a % 2) + v;
        constexpr int rb = kSlotHost.rb[base], cb = kSlotHost.cb[base];
        const float d = D[I] * w16[I];
+       if constexpr (rb < 64 && cb < 64) {
+         dx[rb] += d * x[cb];
+         dx[cb] += d * x[rb];
+       } else if constexpr (rb < 64 && cb == 64) {
+         dx[rb] += d;
+       }
+     }()),
+     ...);
+  }(std::make_integer_sequence<int, 16>{});
+}
+
+// fold_tile with the slot weights of fold_weight_row.
+template <int M>
+__device__ __forceinline__ void fold_tile_row(const f32x16& D, const float (&x)[kD], float (&dx)[kD], float wrow) {
+  [&]<int... I>(std::integer_sequence<int, I...>) {
+    (([&] {
+       constexpr int a = I / 4, v = I % 4;
+       constexpr int base = 8 * (2 * M + a / 2) + 4 * (a % 2) + v;
+       constexpr int rb = kSlotHost.rb[base], cb = kSlotHost.cb[base];
+       const float d = D[I] * row_bcast<I>(wrow);
        if constexpr (rb < 64 && cb < 64) {
          dx[rb] += d * x[cb];
          dx[cb] += d * x[rb];

@@ -156,26 +156,26 @@ __device__ __forceinline__ void ring_issue(const uint16_t* pr, const LdsRing<kNS
   }
 }
 
-// Operands of k-step T: this lane group's 8 slot weights and the two P^T
+// Operands of k-step T: the slot weights of this lane's row (lane j of the row
+// holds the weight of slot 16 T + 8 s + j, j < 8; one 4-byte read per lane
+// instead of the 32 bytes of every weight of its lane group) and the two P^T
 // fragments (value halves) of the staged tile.
 struct ReadoutOps {
-  float4 w0, w1;
+  float w;
   bf16x8 b0, b1;
 };
 
 template <int T, int NS, int RG = kRG>
 __device__ __forceinline__ void readout_read(const float* wl, const LdsRing<NS>& ring, int lane, ReadoutOps& o) {
-  const int s = lane >> 5, row = lane & 31;
-  o.w0 = *reinterpret_cast<const float4*>(wl + 16 * T + 8 * s);
-  o.w1 = *reinterpret_cast<const float4*>(wl + 16 * T + 8 * s + 4);
+  const int s = lane >> 5;
+  o.w = wl[16 * T + 8 * s + (lane & 7)];
   const __bf16* tile = ring.st[(T / RG) % NS] + (T % RG) * kRingStep;
   o.b0 = tr_fragment(tile, lane, 0);
   o.b1 = tr_fragment(tile, lane, 1);
 }
 template <int T>
 __device__ __forceinline__ void readout_step(const float (&x)[kD], const ReadoutOps& o, f32x16 (&acc)[2]) {
-  const float w[8] = {o.w0.x, o.w0.y, o.w0.z, o.w0.w, o.w1.x, o.w1.y, o.w1.z, o.w1.w};
-  const bf16x8 a = feature_fragment<T>(x, w);
+  const bf16x8 a = feature_fragment_row<T>(x, o.w);
   acc[0] = mfma32(a, o.b0, acc[0]);
   acc[1] = mfma32(a, o.b1, acc[1]);
 }
@@ -607,6 +607,10 @@ __global__ __launch_bounds__(128, 2) void k2_out_fwd(const T* __restrict__ q, co
 // chunk's state then leaves L2 twice, once per token half, instead of once per
 // query head, and the deeper ring keeps more of it in flight. The ring holds
 // kNSS stages of kRGS k-steps (48 KB): one ring barrier per eight k-steps.
+// The slot weights come from global memory (L2), a ring group ahead, one
+// register per k-step pair broadcast along each lane row (row_bcast), so the
+// block needs only the ring's LDS and two blocks (four waves per SIMD, 128
+// VGPRs) fit a CU.
 // ---------------------------------------------------------------------------
 constexpr int kNSS = 3;
 constexpr int kRGS = 8;  // k-steps per ring group of the shared readout
@@ -646,29 +650,54 @@ __device__ __forceinline__ void ring_produce(const uint16_t* pt, const LdsRing<k
   if constexpr (G + kNSS - 1 < kRingGroupsS) ring_issue_shared<G + kNSS - 1>(pt, ring, lane);
   if constexpr (G + 1 < kRingGroupsS) ring_produce<G + 1>(pt, ring, lane);
 }
+// Slot weights of ring group G of the shared readout, read from global memory
+// (L2) one group ahead: register p holds k-step pair 4 G + p, lane j of each
+// row the weight of slot 16 (2 (4 G + p) + j / 8) + 8 s + j % 8. The pair
+// index is clamped so that every load is issued.
 template <int G>
-__device__ __forceinline__ void readout_group_shared(const float (&x)[kD], const float* wl,
-                                                     const LdsRing<kNSS>& ring, int lane, f32x16 (&acc)[2]) {
+__device__ __forceinline__ void readout_weights_shared(const float* __restrict__ wg, int lane, float (&w)[kRGS / 2]) {
+  const int j = lane & 15, s = lane >> 5;
+#pragma unroll
+  for (int p = 0; p < kRGS / 2; ++p) {
+    constexpr int kPairs = kKS / 2;
+    const int pr = min(G * (kRGS / 2) + p, kPairs - 1);
+    w[p] = wg[32 * pr + 16 * (j >> 3) + 8 * s + (j & 7)];
+  }
+}
+template <int T>
+__device__ __forceinline__ void readout_tiles_shared(const LdsRing<kNSS>& ring, int lane, bf16x8 (&b)[2]) {
+  const __bf16* tile = ring.st[(T / kRGS) % kNSS] + (T % kRGS) * kRingStep;
+  b[0] = tr_fragment(tile, lane, 0);
+  b[1] = tr_fragment(tile, lane, 1);
+}
+template <int G>
+__device__ __forceinline__ void readout_group_shared(const float (&x)[kD], const float* __restrict__ wg,
+                                                     const LdsRing<kNSS>& ring, int lane, f32x16 (&acc)[2],
+                                                     const float (&wc)[kRGS / 2]) {
+  static_assert(kKS % 2 == 0 && kRGS % 2 == 0, "weights come in k-step pairs");
   ring_sync<shared_copies_in_flight<G>(std::make_integer_sequence<int, kNSS - 2>{})>();
+  float wn[kRGS / 2];
+  if constexpr (G + 1 < kRingGroupsS) readout_weights_shared<G + 1>(wg, lane, wn);
   constexpr int n = group_steps_shared<G>();
-  ReadoutOps o[2];
-  readout_read<G * kRGS, kNSS, kRGS>(wl, ring, lane, o[0]);
+  bf16x8 b[2][2];
+  readout_tiles_shared<G * kRGS>(ring, lane, b[0]);
   [&]<int... I>(std::integer_sequence<int, I...>) {
     (([&] {
-       if constexpr (I + 1 < n) readout_read<G * kRGS + I + 1, kNSS, kRGS>(wl, ring, lane, o[(I + 1) & 1]);
-       readout_step<G * kRGS + I>(x, o[I & 1], acc);
+       if constexpr (I + 1 < n) readout_tiles_shared<G * kRGS + I + 1>(ring, lane, b[(I + 1) & 1]);
+       const bf16x8 a = feature_fragment_row<G * kRGS + I, 8 * (I & 1)>(x, wc[I / 2]);
+       acc[0] = mfma32(a, b[I & 1][0], acc[0]);
+       acc[1] = mfma32(a, b[I & 1][1], acc[1]);
      }()),
      ...);
   }(std::make_integer_sequence<int, n>{});
-  if constexpr (G + 1 < kRingGroupsS) readout_group_shared<G + 1>(x, wl, ring, lane, acc);
+  if constexpr (G + 1 < kRingGroupsS) readout_group_shared<G + 1>(x, wg, ring, lane, acc, wn);
 }
 
 template <typename T>
-__global__ __launch_bounds__(64 * (kMaxRS + 1), 1) void k2_out_fwd_shared(
+__global__ __launch_bounds__(64 * (kMaxRS + 1), 4) void k2_out_fwd_shared(
     const T* __restrict__ q, const float* __restrict__ wqs, const uint16_t* __restrict__ PR, int Hq, int Hkv, int N,
     int NB, float floor, T* __restrict__ out, float* __restrict__ num, const float* __restrict__ den) {
   __shared__ __attribute__((aligned(16))) __bf16 rs[kNSS][kRGS * kRingStep];
-  __shared__ __attribute__((aligned(16))) float wl[kMaxRS][kS];
   LdsRing<kNSS> ring;
 #pragma unroll
   for (int i = 0; i < kNSS; ++i) ring.st[i] = rs[i];
@@ -690,8 +719,9 @@ __global__ __launch_bounds__(64 * (kMaxRS + 1), 1) void k2_out_fwd_shared(
   }
   const int h = kh * R + wv;
   const size_t qbase = (size_t)(b * Hq + h) * N * kD;
-  float* wlh = wl[wv];
-  stage_f4<64, kS / 4>(reinterpret_cast<float4*>(wlh), reinterpret_cast<const float4*>(wqs + (size_t)h * kS), l);
+  const float* wg = wqs + (size_t)h * kS;
+  float w0[kRGS / 2];
+  readout_weights_shared<0>(wg, l, w0);
   float x[kD];
   {
     const int tok = tok0 + row;
@@ -716,7 +746,7 @@ __global__ __launch_bounds__(64 * (kMaxRS + 1), 1) void k2_out_fwd_shared(
   // added in the epilogue, its loads sharing the denominators' round trip
   // (as the accumulators' initial value the first product waited for them)
   f32x16 acc[2] = {f32x16{}, f32x16{}};
-  readout_group_shared<0>(x, wlh, ring, l, acc);
+  readout_group_shared<0>(x, wg, ring, l, acc, w0);
 
   const size_t dbase = (size_t)(b * Hq + h) * N;
   // the row denominators are loaded together (rows clamped into range): a load
