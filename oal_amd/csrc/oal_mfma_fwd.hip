@@ -285,7 +285,7 @@ __device__ __forceinline__ f32x16 pair_score(const float (&xk)[kD], const float 
 // of the group sums; everything else is shared.
 // ---------------------------------------------------------------------------
 template <typename T, bool PAIRWISE>
-__global__ __launch_bounds__(256) void k2_intra_fwd(const T* __restrict__ q, const T* __restrict__ k,
+__global__ __launch_bounds__(256, PAIRWISE ? 2 : 3) void k2_intra_fwd(const T* __restrict__ q, const T* __restrict__ k,
                                                     const T* __restrict__ v, const float* __restrict__ PZ,
                                                     const float* __restrict__ PZm, const int32_t* __restrict__ labels,
                                                     const float* __restrict__ ic, const float* __restrict__ gm,
@@ -298,8 +298,11 @@ __global__ __launch_bounds__(256) void k2_intra_fwd(const T* __restrict__ q, con
   __shared__ __attribute__((aligned(16))) __bf16 VT[kD][LD];
   __shared__ __attribute__((aligned(16))) __bf16 Mz[kD][LD];
   __shared__ __attribute__((aligned(16))) uint32_t mk[4][8][2][4];
-  __shared__ float red[2][16][64];
   __shared__ float bz[kD], dsS[kC], dp2[32];
+  // wave 2's half of the i-tile 1 numerator, handed to wave 1 after the
+  // barrier that ends every read of Qs (8 KB of its 9 KB)
+  static_assert(sizeof(float) * 2 * 16 * 64 <= sizeof(Qs), "the reduction buffer fits Qs");
+  float (*red)[16][64] = reinterpret_cast<float (*)[16][64]>(&Qs[0][0]);
   __shared__ __attribute__((aligned(16))) __bf16 kapT[3][32][40];  // kappa^T tiles [j][i], bf16
   __shared__ __attribute__((aligned(16))) float wl[PAIRWISE ? kS : 4];  // the head's slot weights
 
@@ -437,13 +440,6 @@ __global__ __launch_bounds__(256) void k2_intra_fwd(const T* __restrict__ q, con
         acc[et] = mfma32(af, bfr, acc[et]);
       }
     }
-    if (wv == 2) {
-#pragma unroll
-      for (int et = 0; et < 2; ++et)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) red[et][r][l] = acc[et][r];
-      if (s == 0) dp2[row] = dsum;
-    }
   } else {
     // state part of the denominator: Z[d][i] = (Mz Q^T)[d][i]
     const float az = cf[0] * PZ[cbase * kFP];
@@ -472,6 +468,13 @@ __global__ __launch_bounds__(256) void k2_intra_fwd(const T* __restrict__ q, con
     }
   }
   __syncthreads();
+  if (wv == 2) {
+#pragma unroll
+    for (int et = 0; et < 2; ++et)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) red[et][r][l] = acc[et][r];
+    if (s == 0) dp2[row] = dsum;
+  }
   if (wv < 3) {
     // kappa for the backward's dv = kappa^T G (k2_local_dv): lane (key row j,
     // group s) holds kappa[i][j] for query rows i = 16 t + 8 s .. + 7, t = 0, 1
@@ -482,6 +485,7 @@ __global__ __launch_bounds__(256) void k2_intra_fwd(const T* __restrict__ q, con
     *reinterpret_cast<bf16x8*>(dst) = f0;
     *reinterpret_cast<bf16x8*>(dst + 8) = f1;
   }
+  __syncthreads();
   if (wv < 2) {
     const int i = 32 * wv + row, tok = tok0 + i;
     if (wv == 1) {
