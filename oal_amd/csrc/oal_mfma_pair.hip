@@ -114,15 +114,17 @@ __device__ __forceinline__ void stage_slots(uint8_t* sar, uint8_t* sac, float* w
     sar[i] = kSlot.ar[i];
     sac[i] = kSlot.ac[i];
   }
-  for (int i = tid; i < kS / 4; i += nthreads)
-    reinterpret_cast<float4*>(wl)[i] = reinterpret_cast<const float4*>(wqs + (size_t)h * kS)[i];
+  if (wl) {
+    for (int i = tid; i < kS / 4; i += nthreads)
+      reinterpret_cast<float4*>(wl)[i] = reinterpret_cast<const float4*>(wqs + (size_t)h * kS)[i];
+  }
 }
 
 // ---------------------------------------------------------------------------
 // k2p_local_dq: M-tile M of one wave (query tile), NKB k-blocks of 16 key tokens.
 // ---------------------------------------------------------------------------
 template <int NKB, bool COEF, int M>
-__device__ __forceinline__ void pdq_tile(const float* Kf, const uint8_t* sar, const uint8_t* sac, const float* wl,
+__device__ __forceinline__ void pdq_tile(const float* Kf, const uint8_t* sar, const uint8_t* sac, float wrow,
                                          const bf16x8 (&bds)[4], const float (&x)[kD], float (&dx)[kD], int lane,
                                          float* Ered, float* __restrict__ coef_out) {
   const int s = lane >> 5, row = lane & 31;
@@ -131,8 +133,6 @@ __device__ __forceinline__ void pdq_tile(const float* Kf, const uint8_t* sar, co
   f32x16 D = f32x16{};
 #pragma unroll
   for (int kb = 0; kb < NKB; ++kb) D = mfma32(lds_feature(Kf, ar, ac, 16 * kb + 8 * s, 1.f), bds[kb], D);
-  float w16[16];
-  fold_weights<M, true>(wl, s, w16);
   if constexpr (COEF) {
     // partial of slot 32 M + r: sum over this wave's 32 query tokens of
     // raw(q_i)[slot] D[slot][i], transposed through LDS (row = slot row,
@@ -153,14 +153,25 @@ __device__ __forceinline__ void pdq_tile(const float* Kf, const uint8_t* sar, co
     if (s == 0) coef_out[32 * M + row] = acc + __uint_as_float(r[1]);
     __builtin_amdgcn_wave_barrier();
   }
-  fold_tile<M>(D, x, dx, w16);
+  fold_tile_row<M>(D, x, dx, wrow);
 }
 
+// The slot weights of each M-tile (one register per lane, fold_weight_row)
+// come from global memory (L2), read two M-tiles ahead.
 template <int NKB, bool COEF, int... Ms>
-__device__ __forceinline__ void pdq_all_impl(const float* Kf, const uint8_t* sar, const uint8_t* sac, const float* wl,
-                                             const bf16x8 (&bds)[4], const float (&x)[kD], float (&dx)[kD], int lane,
-                                             float* Ered, float* coef_out, std::integer_sequence<int, Ms...>) {
-  ((pin64(dx), pdq_tile<NKB, COEF, Ms>(Kf, sar, sac, wl, bds, x, dx, lane, Ered, coef_out)), ...);
+__device__ __forceinline__ void pdq_all_impl(const float* Kf, const uint8_t* sar, const uint8_t* sac,
+                                             const float* __restrict__ wg, const bf16x8 (&bds)[4],
+                                             const float (&x)[kD], float (&dx)[kD], int lane, float* Ered,
+                                             float* coef_out, std::integer_sequence<int, Ms...>) {
+  constexpr int NT = kS / 32;
+  float w0 = fold_weight_row<0>(wg, lane), w1 = fold_weight_row<1>(wg, lane);
+  ((pin64(dx), [&] {
+     const float wc = w0;
+     w0 = w1;
+     if constexpr (Ms + 2 < NT) w1 = fold_weight_row<Ms + 2>(wg, lane);
+     pdq_tile<NKB, COEF, Ms>(Kf, sar, sac, wc, bds, x, dx, lane, Ered, coef_out);
+   }()),
+   ...);
 }
 
 // ---------------------------------------------------------------------------
@@ -207,10 +218,13 @@ __global__ __launch_bounds__(128, 2) void k2p_local_dq(const T* __restrict__ q, 
                                                       int Hq, int Hkv, int N, int NB, float* __restrict__ dqf,
                                                       float* __restrict__ dwql) {
   __shared__ __attribute__((aligned(16))) float Kf[kPRows * kPRow];
-  __shared__ __attribute__((aligned(16))) float wl[kS];
   __shared__ uint8_t sar[kS], sac[kS];
-  __shared__ __attribute__((aligned(16))) __bf16 Mz[kD][LD];
   __shared__ float bz[kD];
+  // Mz is staged into Kf's LDS once the fold has ended every read of Kf (the
+  // block then needs 32 KB of LDS, so that the register limit, four blocks per
+  // CU, binds instead of the LDS)
+  static_assert(sizeof(__bf16) * kD * LD <= sizeof(float) * kPRows * kPRow, "Mz fits Kf");
+  __bf16 (*Mz)[LD] = reinterpret_cast<__bf16 (*)[LD]>(Kf);
   __shared__ __attribute__((aligned(16))) float Ered[COEF ? 2 : 1][COEF ? 32 * kERow : 4];
 
   int hh, ch, u;
@@ -229,13 +243,7 @@ __global__ __launch_bounds__(128, 2) void k2p_local_dq(const T* __restrict__ q, 
     Kf[kD * kPRow + i] = 1.f;
     Kf[(kD + 1) * kPRow + i] = 0.f;
   }
-  stage_slots(sar, sac, wl, wqs, h, tid, 128);
-  // Mz = gm o PZm (bf16), row r holding dimension mz_dim(r / 32, r % 32)
-  for (int e = tid; e < kD * kD; e += 128) {
-    const int r = e >> 6, c = e & 63;
-    const int d = mz_dim(r >> 5, r & 31);
-    Mz[r][c] = (__bf16)(gm[((size_t)h * kD + d) * kD + c] * PZm[(cbase * kD + d) * kD + c]);
-  }
+  stage_slots(sar, sac, nullptr, wqs, h, tid, 128);
   if (tid < kD) bz[tid] = lb[(size_t)h * kD + tid] * PZ[cbase * kFP + 1 + tid];
   __syncthreads();
 
@@ -278,10 +286,19 @@ __global__ __launch_bounds__(128, 2) void k2p_local_dq(const T* __restrict__ q, 
   const int R2 = (int)(gridDim.x / (R * NB) / Hkv) * NB * 2;  // partial rows per head
   float* coef_out = COEF ? dwql + ((size_t)h * R2 + ((size_t)b * NB + ch) * 2 + it) * kS : nullptr;
   float* ered = COEF ? &Ered[COEF ? wv : 0][0] : nullptr;
+  const float* wg = wqs + (size_t)h * kS;
   if (it == 0)
-    pdq_all_impl<2, COEF>(Kf, sar, sac, wl, bds, x, dx, l, ered, coef_out, std::make_integer_sequence<int, kS / 32>{});
+    pdq_all_impl<2, COEF>(Kf, sar, sac, wg, bds, x, dx, l, ered, coef_out, std::make_integer_sequence<int, kS / 32>{});
   else
-    pdq_all_impl<4, COEF>(Kf, sar, sac, wl, bds, x, dx, l, ered, coef_out, std::make_integer_sequence<int, kS / 32>{});
+    pdq_all_impl<4, COEF>(Kf, sar, sac, wg, bds, x, dx, l, ered, coef_out, std::make_integer_sequence<int, kS / 32>{});
+  __syncthreads();  // every read of Kf has ended
+  // Mz = gm o PZm (bf16), row r holding dimension mz_dim(r / 32, r % 32)
+  for (int e = tid; e < kD * kD; e += 128) {
+    const int r = e >> 6, c = e & 63;
+    const int d = mz_dim(r >> 5, r & 31);
+    Mz[r][c] = (__bf16)(gm[((size_t)h * kD + d) * kD + c] * PZm[(cbase * kD + d) * kD + c]);
+  }
+  __syncthreads();
 
   // lane group s: dimensions 32 s .. 32 s + 31 of its token
   float full[32];
