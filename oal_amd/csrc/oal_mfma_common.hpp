@@ -27,6 +27,14 @@ __device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
 __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
+// v_mfma_f32_16x16x16_bf16: lane l supplies A[l%16][4*(l/16) + j],
+// B[4*(l/16) + j][l%16] (j < 4); register i holds C[4*(l/16) + i][l%16], so a
+// 16x16 accumulator tile is, lane for lane, the A operand of a product whose K
+// index is the tile's row.
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ f32x4 mfma16k16(s16x4 a, s16x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+}
 __device__ __forceinline__ constexpr int c32_row(int i, int lane) { return 8 * (i / 4) + 4 * (lane / 32) + (i % 4); }
 __device__ __forceinline__ constexpr int c16_row(int i, int lane) { return 4 * (lane / 16) + i; }
 
@@ -151,6 +159,12 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
   bf16x2 v = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
   return __builtin_bit_cast(uint32_t, v);
+}
+
+__device__ __forceinline__ s16x4 pack4(const float (&v)[4]) {
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+  u32x2 u = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+  return __builtin_bit_cast(s16x4, u);
 }
 
 __device__ __forceinline__ bf16x8 pack8(const float (&v)[8]) {

@@ -831,6 +831,20 @@ __global__ __launch_bounds__(64) void k2_selftest(int* __restrict__ errors) {
       bad += (c[i] != ref);
     }
   }
+  {  // 16x16x16 with K = 16
+    float fa[4], fb[4];
+    for (int j = 0; j < 4; ++j) {
+      fa[j] = A[l % 16][4 * (l / 16) + j];
+      fb[j] = B[4 * (l / 16) + j][l % 16];
+    }
+    f32x4 c = mfma16k16(pack4(fa), pack4(fb), f32x4{});
+    for (int i = 0; i < 4; ++i) {
+      const int r = c16_row(i, l), col = l % 16;
+      float ref = 0.f;
+      for (int kk = 0; kk < 16; ++kk) ref += A[r][kk] * B[kk][col];
+      bad += (c[i] != ref);
+    }
+  }
   {  // transposed LDS reads (tr_fragment) of a staged k-step tile: entry
      // (slot, value) holds the bits slot * 64 + value
     __shared__ __attribute__((aligned(16))) uint16_t tile[4 * 16 * 16];

@@ -8,16 +8,18 @@
 //   dc0 += sum ds,  dlam_g += sum ds s_g,  dGam_gh += sum ds s_g s_h
 // (reference: closed-form state VJP grouped_reference.py:214-318 and the local
 // score terms of hd_block_gemm_backward_wave.py:253-477, here in group-sum form).
-// The 64x64 chunk is covered by three lower 32x32 tiles (key tile jt, query
-// tile it) = (0,0), (0,1), (1,1). Group sums and ds come from
-// v_mfma_f32_32x32x16_bf16 on row-major operands; their accumulators are fed
-// straight back into the MFMA as the K-major operand of the dq / dk / dv
-// products, whose other operand is the transposed bf16 copy of K, q or G.
+// k2_local_dk and k2_local_dv cover the 64x64 chunk with three lower 32x32
+// tiles (key tile jt, query tile it) = (0,0), (0,1), (1,1); k2_local_dq covers
+// its causal triangle with ten 16x16 sub-tiles. Group sums and ds come from
+// the MFMA on row-major operands; their accumulators are fed straight back
+// into the MFMA as the K-major operand of the dq / dk / dv products, whose
+// other operand is the transposed bf16 copy of K, q or G.
 //
-// k2_local_dq    one block per (query head, chunk): dq local part and the state
-//                part of the denominator's dq (gz_i (bz + 2 Mz q_i)). With the
-//                coefficient gradients requested it also writes the per-(head,
-//                chunk) coefficient partials from the same group sums.
+// k2_local_dq    one block of two waves per (query head, chunk): dq local part
+//                and the state part of the denominator's dq (gz_i (bz + 2 Mz
+//                q_i)). With the coefficient gradients requested it also writes
+//                the per-(head, chunk) coefficient partials from the same group
+//                sums.
 // k2_local_dk    one block per (unit, chunk): dk local part summed over the
 //                unit's query heads in registers (group sums one at a time).
 // k2_local_dv    one block per (unit, chunk): the dv local part from the
@@ -88,267 +90,210 @@ __device__ __forceinline__ int tile_it(int tp) { return tp == 0 ? 0 : 1; }
 }  // namespace
 
 // ---------------------------------------------------------------------------
-// dq local part + denominator-state dq, one block per (query head, chunk),
-// grid R * NB * U (XCD-ordered), 3 waves = tile pairs 0..2 (orientation
-// C[j][i] for the group sums; dq accumulators C[i][d], lane = d):
-//   dq[i][d] = sum_h coef_h(d) sum_j X_h[i][j] K[j][d], X_h = ds o s'_h, X_8 = ds
-// with s'_h the unscaled group sum (s_h = scale s'_h), computed one group at a
-// time, coef_h(d) = 2 scale^2 Gam[g(d)][h], coef_8(d) = scale lam[g(d)];
-// waves 0 and 1 (query tiles 0, 1) add
-// gz_i (bz_d + 2 (Mz q_i)_d), Mz = gm o PZm, and write dqf.
-// COEF: the eight group sums are kept (two waves per SIMD instead of three),
-// the block also writes the coefficient partials from them (with ds[i][j] =
-// g_i . v_j + gz_i on live entries: [0] sum ds, [1 + g] sum ds s_g,
-// [9 + 8 g + h] sum ds s_g s_h in the full symmetric 8 x 8 layout, each a
-// fixed-order sum over the block's 192 lanes), and the dq products take s_h
-// from those registers.
+// dq local part + denominator-state dq on 16 x 16 sub-tiles, one block of two
+// waves per (query head, chunk), grid R * NB * U (XCD-ordered). The chunk's
+// causal lower triangle is 10 sub-tiles (key block jb <= query block ib, 16
+// tokens each); wave 0 owns query blocks 3 and 0, wave 1 blocks 2 and 1 (five
+// sub-tiles each), so each query row's dq is formed by one wave. Per sub-tile,
+// on v_mfma_f32_16x16x32_bf16 (lane column = query i, rows = key j):
+//   ds^T = V G^T (+ gz_i, j <= i), the eight group sums s'^T_g from masked key
+//   fragments, the coefficient partials over the lane's four entries, and
+//   dq[i][d] += coef_h(d) sum_j X_h[i][j] k_j[d], X_h = ds o s'_h (X_8 = ds),
+//   on v_mfma_f32_16x16x16_bf16 with the 16 x 16 accumulator tile X_h as the
+//   A operand as it stands (no exchange between lanes).
+// Then, per query block, gz_i (bz_d + 2 (Mz q_i)_d), Mz = gm o PZm, and the
+// dq rows. Against the 32 x 32 form: 10 sub-tiles instead of 12, and eight
+// group-sum registers per lane instead of 128, so three blocks' worth of
+// waves per SIMD fit. COEF: the partials ([0] sum ds, [1 + g] sum ds s_g,
+// [9 + packed (g <= h)] sum ds s_g s_h), summed over each 16-lane row by DPP
+// (fixed order), then over the block's eight rows in order.
 // ---------------------------------------------------------------------------
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float x) {
+  return x + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, true));
+}
+
 template <typename T, bool COEF>
-__global__ __launch_bounds__(192, COEF ? 2 : 3) void k2_local_dq(const T* __restrict__ q, const T* __restrict__ k,
-                                                   const T* __restrict__ v, const uint16_t* __restrict__ G16,
-                                                   const float* __restrict__ Gz, const uint16_t* __restrict__ KT16,
-                                                   const float* __restrict__ PZ, const float* __restrict__ PZm,
-                                                   const int32_t* __restrict__ labels, const float* __restrict__ lam,
-                                                   const float* __restrict__ gam, const float* __restrict__ gm,
-                                                   const float* __restrict__ lb, int G, int Hq, int Hkv, int N,
-                                                   int NB, float scale, float* __restrict__ dqf,
-                                                   float* __restrict__ coefl) {
+__global__ __launch_bounds__(128, 3) void k2_local_dq(const T* __restrict__ q, const T* __restrict__ k,
+                                                       const T* __restrict__ v, const uint16_t* __restrict__ G16,
+                                                       const float* __restrict__ Gz, const uint16_t* __restrict__ KT16,
+                                                       const float* __restrict__ PZ, const float* __restrict__ PZm,
+                                                       const int32_t* __restrict__ labels, const float* __restrict__ lam,
+                                                       const float* __restrict__ gam, const float* __restrict__ gm,
+                                                       const float* __restrict__ lb, int G, int Hq, int Hkv, int N,
+                                                       int NB, float scale, float* __restrict__ dqf,
+                                                       float* __restrict__ coefl) {
   constexpr int LD = kD + 8;
-  __shared__ __attribute__((aligned(16))) uint32_t mk[4][8][2][4];
-  __shared__ __attribute__((aligned(16))) __bf16 Mz[kD][LD];
+  // masks of the key fragments: [k-step][group][lane group][word], word w of
+  // lane group lg covers dims 32 ks + 8 lg + 2 w, + 1
+  __shared__ __attribute__((aligned(16))) uint32_t mk[2][8][4][4];
   __shared__ __attribute__((aligned(16))) uint16_t kts[kD][LD];  // k^T of the chunk
-  __shared__ float cft[9][kD];  // coef_h(d), h = 0..8
+  __shared__ __attribute__((aligned(16))) __bf16 Mz[kD][LD];
+  __shared__ float cft[9][kD];  // coef_h(d)
   __shared__ float bz[kD];
   __shared__ float gzs[kC];
-  __shared__ float red[2][16][64];  // wave 2's dq (query tile 1)
-  __shared__ float cp[COEF ? 3 * 64 : 1][45];  // per-lane coefficient partials
-  __shared__ float cred[COEF ? 4 * 45 : 1];
+  __shared__ float cp[COEF ? 8 : 1][45];  // row sums of the partials
 
   int hh, ch, u;
   head_chunk_unit(Hq / Hkv, NB, (int)(gridDim.x / ((Hq / Hkv) * NB)), hh, ch, u);
   const int R = Hq / Hkv, b = u / Hkv, kh = u % Hkv, h = kh * R + hh;
-  const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, s = l >> 5, row = l & 31;
+  const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, lr = l & 15, lg = l >> 4;
   const int tok0 = ch * kC;
   const size_t qbase = (size_t)(b * Hq + h) * N * kD;
   const size_t kbase = (size_t)u * N * kD;
   const size_t cbase = (size_t)u * NB + ch;
   const size_t np = (size_t)NB * kC;
 
-  // The prologue's global loads are issued together, labels first (the
-  // coefficient rows depend on them), and the lane's operand rows right after
-  // the Mz stores: two round trips in all instead of one per loop. Loads and
-  // LDS stores are unconditional: a thread past an item count wraps onto an
-  // item another thread also holds and stores the same value there.
-  // masks: thread t = tid & 31 covers dims d, d + 1, d = 16 kk + 8 ss + 2 w
-  const int mt = tid & 31, mkk = mt >> 3, mss = (mt >> 2) & 1, mw = mt & 3;
-  const int md = 16 * mkk + 8 * mss + 2 * mw;
-  const int ml0 = labels[h * kD + md], ml1 = labels[h * kD + md + 1];
-  const int cd = tid & 63;  // dim of the coefficient table, bz and token of gzs
-  const int cl = clamp_label(labels[h * kD + cd], G);
-  // Mz = gm o PZm (bf16): items e = tid, tid + 192 (< 256): row e / 4, columns 16 (e % 4) .. + 15
-  float4 mg[2][4], mz[2][4];
-#pragma unroll
-  for (int x = 0; x < 2; ++x) {
-    const int e = (tid + 192 * x) & 255, r = e >> 2, qq = e & 3;
-    const float4* gp = reinterpret_cast<const float4*>(gm + ((size_t)h * kD + r) * kD + 16 * qq);
-    const float4* zp = reinterpret_cast<const float4*>(PZm + (cbase * kD + r) * kD + 16 * qq);
-#pragma unroll
-    for (int y = 0; y < 4; ++y) {
-      mg[x][y] = gp[y];
-      mz[x][y] = zp[y];
-    }
+  for (int e = tid; e < 256; e += 128) {
+    const int ks = e >> 7, g = (e >> 4) & 7, lgm = (e >> 2) & 3, w = e & 3;
+    const int d = 32 * ks + 8 * lgm + 2 * w;
+    const int g0 = clamp_label(labels[h * kD + d], G), g1 = clamp_label(labels[h * kD + d + 1], G);
+    mk[ks][g][lgm][w] = (g0 == g ? 0x0000ffffu : 0u) | (g1 == g ? 0xffff0000u : 0u);
   }
-  const float lbv = lb[(size_t)h * kD + cd], pzv = PZ[cbase * kFP + 1 + cd];
-  const float gzv = Gz[(size_t)(b * Hq + h) * N + min(tok0 + cd, N - 1)];
-  // k^T of the chunk: 512 pieces of 8 tokens, pieces tid, tid + 192, tid + 384 (< 512)
-  bf16x8 ktv[3];
-#pragma unroll
-  for (int x = 0; x < 3; ++x) {
-    const int pc = (tid + 192 * x) & 511, d = pc >> 3, c = 8 * (pc & 7);
-    ktv[x] = *reinterpret_cast<const bf16x8*>(KT16 + ((size_t)u * kD + d) * np + tok0 + c);
+  for (int pc = tid; pc < 512; pc += 128) {
+    const int d = pc >> 3, c = 8 * (pc & 7);
+    *reinterpret_cast<bf16x8*>(&kts[d][c]) =
+        *reinterpret_cast<const bf16x8*>(KT16 + ((size_t)u * kD + d) * np + tok0 + c);
+    const float4* gp = reinterpret_cast<const float4*>(gm + ((size_t)h * kD + d) * kD + c);
+    const float4* zp = reinterpret_cast<const float4*>(PZm + (cbase * kD + d) * kD + c);
+    const float4 g0 = gp[0], g1 = gp[1], z0 = zp[0], z1 = zp[1];
+    float y[8] = {g0.x * z0.x, g0.y * z0.y, g0.z * z0.z, g0.w * z0.w,
+                  g1.x * z1.x, g1.y * z1.y, g1.z * z1.z, g1.w * z1.w};
+    *reinterpret_cast<bf16x8*>(&Mz[d][c]) = pack8(y);
   }
-  // coefficient rows of dim cd: gam[g(cd)][0..7], lam[g(cd)] (group index clamped)
-  float cg[9];
-#pragma unroll
-  for (int h2 = 0; h2 < 8; ++h2) cg[h2] = gam[((size_t)h * G + cl) * G + min(h2, G - 1)];
-  cg[8] = lam[(size_t)h * G + cl];
-
   {
-    const int g0 = clamp_label(ml0, G), g1 = clamp_label(ml1, G);
+    const int d = l;
+    const int cl = clamp_label(labels[h * kD + d], G);
+    if (wv == 0) {
 #pragma unroll
-    for (int g = 0; g < 8; ++g) mk[mkk][g][mss][mw] = (g0 == g ? 0x0000ffffu : 0u) | (g1 == g ? 0xffff0000u : 0u);
-  }
-#pragma unroll
-  for (int x = 0; x < 2; ++x) {
-    const int e = (tid + 192 * x) & 255, r = e >> 2, qq = e & 3;
-#pragma unroll
-    for (int i2 = 0; i2 < 2; ++i2) {
-      const float4 g0 = mg[x][2 * i2], g1 = mg[x][2 * i2 + 1], z0 = mz[x][2 * i2], z1 = mz[x][2 * i2 + 1];
-      float y[8] = {g0.x * z0.x, g0.y * z0.y, g0.z * z0.z, g0.w * z0.w,
-                    g1.x * z1.x, g1.y * z1.y, g1.z * z1.z, g1.w * z1.w};
-      *reinterpret_cast<bf16x8*>(&Mz[r][16 * qq + 8 * i2]) = pack8(y);
-    }
-  }
-  const int tp = wv, jt = tile_jt(tp), it = tile_it(tp);
-  const int jr = tok0 + 32 * jt + row, ir = tok0 + 32 * it + row;  // this lane's operand rows
-  const bool jok = jr < N, iok = ir < N;
-  const size_t jo = (size_t)(jok ? jr : N - 1) * kD, io = (size_t)(iok ? ir : N - 1) * kD;
-  bf16x8 kf[4], qf[4], vf[4], gf[4];
-#pragma unroll
-  for (int kk = 0; kk < 4; ++kk) {
-    const int c = 16 * kk + 8 * s;
-    kf[kk] = row8(k + kbase + jo + c, jok);
-    qf[kk] = row8(q + qbase + io + c, iok);
-    vf[kk] = row8(v + kbase + jo + c, jok);
-    gf[kk] = row8(G16 + qbase + io + c, iok);
-  }
-#pragma unroll
-  for (int x = 0; x < 3; ++x) {
-    const int pc = (tid + 192 * x) & 511;
-    *reinterpret_cast<bf16x8*>(&kts[pc >> 3][8 * (pc & 7)]) = ktv[x];
-  }
-  bz[cd] = lbv * pzv;
-  gzs[cd] = tok0 + cd < N ? gzv : 0.f;
-#pragma unroll
-  for (int h2 = 0; h2 < 8; ++h2) cft[h2][cd] = h2 < G ? 2.f * scale * scale * cg[h2] : 0.f;
-  cft[8][cd] = scale * cg[8];
-  lds_sync();
-
-  f32x16 ds = f32x16{};
-#pragma unroll
-  for (int kk = 0; kk < 4; ++kk) ds = mfma32(vf[kk], gf[kk], ds);
-  // lane column i = 32 it + row; register rows j = 32 jt + c32_row(r)
-  const int i = 32 * it + row;
-  const float gzi = gzs[i];  // zero past N
-  float dsv[16];
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int j = 32 * jt + c32_row(r, l);
-    dsv[r] = j <= i ? ds[r] + gzi : 0.f;
-  }
-  f32x16 sgs[COEF ? 8 : 1];
-  if constexpr (COEF) {
-    // all eight group sums, then the partials [0] sum ds, [1 + g] sum ds s_g,
-    // [9 + packed (g <= h)] sum ds s_g s_h over this lane's 16 entries
-#pragma unroll
-    for (int g = 0; g < 8; ++g) sgs[g] = f32x16{};
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk)
-#pragma unroll
-      for (int g = 0; g < 8; ++g) sgs[g] = mfma32(masked(kf[kk], &mk[kk][g][s][0]), qf[kk], sgs[g]);
-    float ca[45];
-#pragma unroll
-    for (int e = 0; e < 45; ++e) ca[e] = 0.f;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      float sv[8], tv[8];
-#pragma unroll
-      for (int g = 0; g < 8; ++g) {
-        sv[g] = sgs[g][r];  // unscaled; the sums are scaled once below
-        tv[g] = dsv[r] * sv[g];
-      }
-      ca[0] += dsv[r];
-      int e = 9;
-#pragma unroll
-      for (int g = 0; g < 8; ++g) {
-        ca[1 + g] += tv[g];
-#pragma unroll
-        for (int h2 = g; h2 < 8; ++h2) {
-          ca[e] = fmaf(tv[g], sv[h2], ca[e]);
-          ++e;
-        }
-      }
-    }
-#pragma unroll
-    for (int e = 0; e < 45; ++e) cp[tid][e] = ca[e] * (e == 0 ? 1.f : e < 9 ? scale : scale * scale);
-  }
-  bf16x8 kt[2][2];
-#pragma unroll
-  for (int dt = 0; dt < 2; ++dt)
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-      kt[dt][t] = *reinterpret_cast<const bf16x8*>(&kts[32 * dt + row][32 * jt + 16 * t + 8 * s]);
-  // this lane's query row again for the den-state term: the prologue's copy
-  // would stay live across the partials and spill. The pointer goes through an
-  // empty asm so that the compiler cannot fold the reload into the first load.
-  const T* qre = q;
-  asm volatile("" : "+s"(qre));
-  bf16x8 qz[4];
-#pragma unroll
-  for (int kk = 0; kk < 4; ++kk) qz[kk] = row8(qre + qbase + io + 16 * kk + 8 * s, iok);
-  f32x16 dq[2] = {f32x16{}, f32x16{}};
-#pragma unroll
-  for (int h2 = 0; h2 < 9; ++h2) {
-    float x[16];
-    if (h2 < 8) {
-      f32x16 sh;
-      if constexpr (COEF) {
-        sh = sgs[h2];
-      } else {
-        sh = f32x16{};
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk) sh = mfma32(masked(kf[kk], &mk[kk][h2][s][0]), qf[kk], sh);
-      }
-#pragma unroll
-      for (int r = 0; r < 16; ++r) x[r] = dsv[r] * sh[r];  // the scale of s_h is in cft
+      for (int h2 = 0; h2 < 8; ++h2)
+        cft[h2][d] = h2 < G ? 2.f * scale * scale * gam[((size_t)h * G + cl) * G + min(h2, G - 1)] : 0.f;
     } else {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) x[r] = dsv[r];
-    }
-    const bf16x8 f0 = acc_kfrag(x, 0, s), f1 = acc_kfrag(x, 1, s);
-#pragma unroll
-    for (int dt = 0; dt < 2; ++dt) {
-      f32x16 p = mfma32(f0, kt[dt][0], f32x16{});
-      p = mfma32(f1, kt[dt][1], p);
-      const float cf = cft[h2][32 * dt + row];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) dq[dt][r] = fmaf(cf, p[r], dq[dt][r]);
-    }
-  }
-  if (wv == 2) {
-#pragma unroll
-    for (int dt = 0; dt < 2; ++dt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) red[dt][r][l] = dq[dt][r];
-  } else {
-    // den-state dq of query tile it = wv: gz_i (bz_d + 2 Z[i][d]), Z = q Mz; the
-    // query fragments qz are this lane's row i = 32 it + row
-    float gzr[16];
-#pragma unroll
-    for (int a = 0; a < 4; ++a)
-#pragma unroll
-      for (int vv = 0; vv < 4; ++vv) gzr[4 * a + vv] = gzs[32 * it + 8 * a + 4 * s + vv];
-#pragma unroll
-    for (int dt = 0; dt < 2; ++dt) {
-      f32x16 z = f32x16{};
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk)
-        z = mfma32(qz[kk], *reinterpret_cast<const bf16x8*>(&Mz[32 * dt + row][16 * kk + 8 * s]), z);
-      const float bzd = bz[32 * dt + row];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) dq[dt][r] = fmaf(gzr[r], bzd + 2.f * z[r], dq[dt][r]);
+      cft[8][d] = scale * lam[(size_t)h * G + cl];
+      bz[d] = lb[(size_t)h * kD + d] * PZ[cbase * kFP + 1 + d];
+      gzs[d] = tok0 + d < N ? Gz[(size_t)(b * Hq + h) * N + tok0 + d] : 0.f;
     }
   }
   __syncthreads();
-  if (wv < 2) {
+
+  float ca[COEF ? 45 : 1];
 #pragma unroll
-    for (int dt = 0; dt < 2; ++dt)
+  for (int e = 0; e < (COEF ? 45 : 1); ++e) ca[e] = 0.f;
+#pragma unroll 1
+  for (int bi = 0; bi < 2; ++bi) {
+    const int ib = wv == 0 ? (bi == 0 ? 3 : 0) : (bi == 0 ? 2 : 1);
+    const int il = 16 * ib + lr;  // this lane's query column (and its operand row)
+    const int ir = tok0 + il;
+    const bool iok = ir < N;
+    const size_t io = (size_t)(iok ? ir : N - 1) * kD;
+    bf16x8 qf[2], gf[2];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float x = dq[dt][r];
-        if (wv == 1) x += red[dt][r][l];
-        const int tok = tok0 + 32 * wv + c32_row(r, l);
-        if (tok < N) dqf[qbase + (size_t)tok * kD + 32 * dt + row] = x;
+    for (int ks = 0; ks < 2; ++ks) {
+      qf[ks] = row8(q + qbase + io + 32 * ks + 8 * lg, iok);
+      gf[ks] = row8(G16 + qbase + io + 32 * ks + 8 * lg, iok);
+    }
+    const float gzi = gzs[il];  // zero past N
+    f32x4 dq[4] = {f32x4{}, f32x4{}, f32x4{}, f32x4{}};
+#pragma unroll 1
+    for (int jb = 0; jb <= ib; ++jb) {
+      const int jr = tok0 + 16 * jb + lr;
+      const bool jok = jr < N;
+      const size_t jo = (size_t)(jok ? jr : N - 1) * kD;
+      bf16x8 kf[2], vf[2];
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        kf[ks] = row8(k + kbase + jo + 32 * ks + 8 * lg, jok);
+        vf[ks] = row8(v + kbase + jo + 32 * ks + 8 * lg, jok);
       }
+      // ds^T[j][i], j = 16 jb + 4 lg + r, i = il
+      f32x4 ds = f32x4{};
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) ds = mfma16(vf[ks], gf[ks], ds);
+      float dsv[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) dsv[r] = 16 * jb + 4 * lg + r <= il ? ds[r] + gzi : 0.f;
+      f32x4 sg[8];
+#pragma unroll
+      for (int g = 0; g < 8; ++g) {
+        sg[g] = f32x4{};
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) sg[g] = mfma16(masked(kf[ks], &mk[ks][g][lg][0]), qf[ks], sg[g]);
+      }
+      if constexpr (COEF) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float tv[8];
+#pragma unroll
+          for (int g = 0; g < 8; ++g) tv[g] = dsv[r] * sg[g][r];
+          ca[0] += dsv[r];
+          int e = 9;
+#pragma unroll
+          for (int g = 0; g < 8; ++g) {
+            ca[1 + g] += tv[g];
+#pragma unroll
+            for (int h2 = g; h2 < 8; ++h2) {
+              ca[e] = fmaf(tv[g], sg[h2][r], ca[e]);
+              ++e;
+            }
+          }
+        }
+      }
+      // B operands k[j][d], j = 16 jb + 4 lg + (0..3), d = 16 db + lr
+      s16x4 kb[4];
+#pragma unroll
+      for (int db = 0; db < 4; ++db) kb[db] = *reinterpret_cast<const s16x4*>(&kts[16 * db + lr][16 * jb + 4 * lg]);
+#pragma unroll
+      for (int h2 = 0; h2 < 9; ++h2) {
+        float x[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) x[r] = h2 < 8 ? dsv[r] * sg[h2][r] : dsv[r];
+        const s16x4 xa = pack4(x);
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+          const f32x4 p = mfma16k16(xa, kb[db], f32x4{});
+          const float cf = cft[h2][16 * db + lr];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) dq[db][r] = fmaf(cf, p[r], dq[db][r]);
+        }
+        // one group's four products in flight at a time (the scheduler would
+        // otherwise issue all 36 first and hold their results)
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    // denominator state: Z[i][d] = sum_e q_i[e] Mz[d][e], i = 16 ib + 4 lg + r
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      f32x4 z = f32x4{};
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+        z = mfma16(qf[ks], *reinterpret_cast<const bf16x8*>(&Mz[16 * db + lr][32 * ks + 8 * lg]), z);
+      const float bzd = bz[16 * db + lr];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) dq[db][r] = fmaf(gzs[16 * ib + 4 * lg + r], bzd + 2.f * z[r], dq[db][r]);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int tok = tok0 + 16 * ib + 4 * lg + r;
+      if (tok < N) {
+#pragma unroll
+        for (int db = 0; db < 4; ++db) dqf[qbase + (size_t)tok * kD + 16 * db + lr] = dq[db][r];
+      }
+    }
   }
   if constexpr (COEF) {
-    // column sums over the 192 lanes (4 interleaved partial sums per column,
-    // then their sum), expanded to the symmetric [1 + 8 + 8 x 8] layout
-    if (tid < 180) {
-      const int e = tid % 45, part = tid / 45;
-      float x = 0.f;
-      for (int r = part; r < 192; r += 4) x += cp[r][e];
-      cred[tid] = x;
+    // sums over each 16-lane row (quad pairs, then quads, then half rows)
+#pragma unroll
+    for (int e = 0; e < 45; ++e) {
+      float x = ca[e];
+      x = dpp_add<0xB1>(x);   // quad_perm [1, 0, 3, 2]
+      x = dpp_add<0x4E>(x);   // quad_perm [2, 3, 0, 1]
+      x = dpp_add<0x124>(x);  // row_ror:4
+      x = dpp_add<0x128>(x);  // row_ror:8
+      ca[e] = x;
+    }
+    if (lr == 0) {
+#pragma unroll
+      for (int e = 0; e < 45; ++e) cp[4 * wv + lg][e] = ca[e];
     }
     __syncthreads();
     if (tid < 73) {
@@ -362,9 +307,12 @@ __global__ __launch_bounds__(192, COEF ? 2 : 3) void k2_local_dq(const T* __rest
         }
         e = 9 + g * 8 - g * (g - 1) / 2 + (h2 - g);
       }
+      float x = 0.f;
+#pragma unroll
+      for (int rw = 0; rw < 8; ++rw) x += cp[rw][e];
+      const float sc = e == 0 ? 1.f : e < 9 ? scale : scale * scale;
       const size_t bn = (size_t)(gridDim.x / (R * NB) / Hkv) * NB;
-      coefl[((size_t)h * 73 + tid) * bn + (size_t)b * NB + ch] =
-          (cred[e] + cred[45 + e]) + (cred[90 + e] + cred[135 + e]);
+      coefl[((size_t)h * 73 + tid) * bn + (size_t)b * NB + ch] = x * sc;
     }
   }
 }
@@ -587,13 +535,13 @@ void launch_local_bwd(const LaunchGeom& g, const T* q, const T* k, const T* v, c
   if (!a.pairwise && (need_dq || coef) && (parts & kLocalDq)) {
     timed("k2_local_dq", st, [&] {
       if (coef)
-        hipLaunchKernelGGL((k2_local_dq<T, true>), dim3(g.R * g.NB * g.U), dim3(192), 0, st, q, k, v, a.G16, a.Gz,
+        hipLaunchKernelGGL((k2_local_dq<T, true>), dim3(g.R * g.NB * g.U), dim3(128), 0, st, q, k, v, a.G16, a.Gz,
                            a.KT16, a.PZ, a.PZm, a.labels, a.lam, a.gam, a.gm, a.lb, a.groups, g.Hq, g.Hkv, g.N, g.NB,
                            a.scale, a.dqf, a.coefl);
       else
-        hipLaunchKernelGGL((k2_local_dq<T, false>), dim3(g.R * g.NB * g.U), dim3(192), 0, st, q, k, v, a.G16, a.Gz,
-                           a.KT16, a.PZ, a.PZm, a.labels, a.lam, a.gam, a.gm, a.lb, a.groups, g.Hq, g.Hkv, g.N, g.NB,
-                           a.scale, a.dqf, nullptr);
+        hipLaunchKernelGGL((k2_local_dq<T, false>), dim3(g.R * g.NB * g.U), dim3(128), 0, st, q, k, v, a.G16,
+                           a.Gz, a.KT16, a.PZ, a.PZm, a.labels, a.lam, a.gam, a.gm, a.lb, a.groups, g.Hq, g.Hkv, g.N,
+                           g.NB, a.scale, a.dqf, nullptr);
     });
   }
   if (!a.pairwise && need_dkv && (parts & kLocalDkv)) {
