@@ -250,7 +250,7 @@ template <typename T>
 __global__ __launch_bounds__(128, 2) void k2_q_fold(const T* __restrict__ q, const uint16_t* __restrict__ G16,
                                                  const float* __restrict__ wqs, const uint16_t* __restrict__ PR,
                                                  const float* __restrict__ dqf, int Hq, int Hkv, int N, int NB,
-                                                 T* __restrict__ dq) {
+                                                 int u0, T* __restrict__ dq) {
   __shared__ __attribute__((aligned(16))) __bf16 ring0[kTileElems], ring1[kTileElems], ring2[kTileElems],
       ring3[kTileElems], ring4[kTileElems], ring5[kTileElems];
   __shared__ __attribute__((aligned(16))) float wl[kS];
@@ -258,6 +258,7 @@ __global__ __launch_bounds__(128, 2) void k2_q_fold(const T* __restrict__ q, con
 
   int hh, ch, u;
   head_chunk_unit(Hq / Hkv, NB, (int)(gridDim.x / ((Hq / Hkv) * NB)), hh, ch, u);
+  u += u0;  // the launch covers units u0 ..
   const int R = Hq / Hkv, b = u / Hkv, kh = u % Hkv, h = kh * R + hh;
   const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, s = l >> 5, row = l & 31;
   const int tok0 = ch * kC;
@@ -767,37 +768,48 @@ int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, cons
     hipLaunchKernelGGL(k2_bwd_prep<T>, dim3(g.B * g.Hq * g.NB), dim3(256), 0, st, qt, static_cast<const T*>(dout),
                        dnum, dden, num, den, g.N, g.NB, floor, w.G16, w.Gz, w.GT16, w.QT16);
   });
-  // Two streams, joined only at the end. The second stream: the intra-chunk
-  // VJP (dk and dv first: their blocks, 35 KB and 8 KB of LDS, fit on a CU
-  // beside two blocks of the backward scan, 62.5 KB each; the dq kernel's
-  // 66 KB do not), then the query-side fold, which needs only the dq kernel's
-  // local part and what k2_bwd_prep and the forward wrote. The caller's stream:
-  // the state scan, its carry and the denominator kernels, then the key-side
-  // fold after an event that the dk and dv kernels recorded (long past by
-  // then), then the coefficient reductions after the dq kernel's event.
-  // (Measured, per config-2 step: 0.9263-0.9266 -> 0.9035-0.9077 ms against a
-  // join before the two folds, whose cross-stream wait left the GPU idle about
-  // 18 us; moving the denominator kernels or the coefficient reductions to the
-  // second stream was slower.)
+  // Two streams, joined only at the end. The second stream: the denominator
+  // kernels (they need only what k2_bwd_prep and the forward wrote), the
+  // intra-chunk VJP (dk and dv, then dq), then the query-side fold of three
+  // quarters of the units. The caller's stream: the state scan and its carry,
+  // the key-side fold after an event recorded behind the dk and dv kernels and
+  // the denominator scan, then the query-side fold of the remaining units and
+  // the coefficient reductions after the dq kernel's event. (Measured, per
+  // config-2 step, same box: 0.8505 ms with the denominator kernels on the
+  // caller's stream and the whole query-side fold on the second stream, 0.8441
+  // with the denominator kernels moved, 0.8363 with the fold also split 6/2
+  // over the 8 units; a 4/4 or 5/3 split: 0.844 and 0.849.)
   const LocalBwdArgs la{w.G16, w.Gz, w.QT16, w.GT16, sv.KT16, sv.KAP, sv.PZ, sv.PZm, labels, lam, gam, sv.ic, sv.gm,
                         sv.lb, groups, scale, w.dqf, w.dkl, w.dvl, (need_coef && !pairwise) ? w.coefl : nullptr,
                         pairwise, sv.wqs, w.dkp, (need_coef && pairwise) ? w.dwql : nullptr};
-  auto q_fold = [&](hipStream_t s) {
-    if (dq) {
+  // the query-side fold of units u0 .. u0 + nu - 1
+  auto q_fold = [&](hipStream_t s, int u0, int nu) {
+    if (dq && nu > 0) {
       timed("k2_q_fold", s, [&] {
-        hipLaunchKernelGGL(k2_q_fold<T>, dim3(g.R * g.NB * g.U), dim3(128), 0, s, qt, w.G16, sv.wqs, sv.PR, w.dqf,
-                           g.Hq, g.Hkv, g.N, g.NB, static_cast<T*>(dq));
+        hipLaunchKernelGGL(k2_q_fold<T>, dim3(g.R * g.NB * nu), dim3(128), 0, s, qt, w.G16, sv.wqs, sv.PR, w.dqf,
+                           g.Hq, g.Hkv, g.N, g.NB, u0, static_cast<T*>(dq));
       });
     }
   };
+  // denominator state (pair-matrix form): per-chunk dCarry and coefficient
+  // partials, then dTz as the exclusive chunk suffix
+  auto den_state = [&](hipStream_t s) {
+    launch_den_bwd(g, w.QT16, w.GT16, kTRows, sv.gm, sv.lb, sv.ic, kIC, sv.PZ, sv.PZm, w.dCt,
+                   need_coef ? w.dwz : nullptr, s, timed);
+    launch_den_scan(false, g, w.dCt, w.dTz, nullptr, s, timed);
+  };
   hipEvent_t ev_dkv = nullptr, ev_dq = nullptr;
+  // units whose query-side fold runs on the second stream (three quarters,
+  // rounded up); the rest follows the key-side fold on the caller's stream
+  const int ua = forked ? (3 * g.U + 3) / 4 : g.U;
   if (forked) {
     stream_wait(aux, st);
+    den_state(aux);
     launch_local_bwd<T>(g, qt, kt, vt, la, dq != nullptr, dk != nullptr, kLocalDkv, aux, timed);
     ev_dkv = record_event(aux);
     launch_local_bwd<T>(g, qt, kt, vt, la, dq != nullptr, dk != nullptr, kLocalDq, aux, timed);
     ev_dq = record_event(aux);
-    q_fold(aux);
+    q_fold(aux, 0, ua);
   }
   {
     const ScanPlan plan{w.S, w.SL, 0};
@@ -805,11 +817,7 @@ int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, cons
     ScanArgs a{w.QT16, kTRows, w.GT16, kTRows, sv.wqs, sv.PR, g.U, g.Hq, g.Hkv, g.N, g.NB,
                w.dTR, w.segtot, need_coef ? w.dwqs : nullptr, w.dCR};
     launch_scan<false>(plan, a, st, timed);
-    // denominator state (pair-matrix form): per-chunk dCarry and coefficient
-    // partials, then dTz as the exclusive chunk suffix
-    launch_den_bwd(g, w.QT16, w.GT16, kTRows, sv.gm, sv.lb, sv.ic, kIC, sv.PZ, sv.PZm, w.dCt,
-                   need_coef ? w.dwz : nullptr, st, timed);
-    launch_den_scan(false, g, w.dCt, w.dTz, nullptr, st, timed);
+    if (!forked) den_state(st);
   }
   if (!forked) {
     // one stream (the allocation-free entry point, the profiling mode, a call
@@ -818,7 +826,7 @@ int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, cons
     // stream 0.950-0.951 ms per config-2 step, against 0.955 with the
     // intra-chunk VJP first)
     launch_local_bwd<T>(g, qt, kt, vt, la, dq != nullptr, dk != nullptr, kLocalDq | kLocalDkv, st, timed);
-    q_fold(st);
+    q_fold(st, 0, g.U);
   }
   if (dk) {
     // the per-pair path forms its local dk in the dq part's launch
@@ -834,7 +842,8 @@ int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, cons
                            static_cast<T*>(dv));
     });
   }
-  if (forked && need_coef) wait_event(st, ev_dq);
+  if (forked && (need_coef || ua < g.U)) wait_event(st, ev_dq);
+  if (forked) q_fold(st, ua, g.U - ua);
   if (need_coef) {
     // group-sum path: the 73 local coefficient columns; per-pair path: the
     // local slot partials added to the state's
