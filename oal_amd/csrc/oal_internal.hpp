@@ -137,7 +137,7 @@ void launch_pair_coef_grad(const LaunchGeom& g, const float* dwq, const float* d
 
 // Parts of the intra-chunk VJP that one call of launch_local_bwd launches:
 // the dq kernel (which also forms the coefficient partials), the dk and dv kernels.
-constexpr unsigned kLocalDq = 1, kLocalDkv = 2;
+constexpr unsigned kLocalDq = 1, kLocalDk = 2, kLocalDv = 4, kLocalDkv = kLocalDk | kLocalDv;
 template <typename T>
 void launch_local_bwd(const LaunchGeom& g, const T* q, const T* k, const T* v, const LocalBwdArgs& a, bool need_dq,
                       bool need_dkv, unsigned parts, hipStream_t st, const Timer& timed);

@@ -770,15 +770,16 @@ int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, cons
   });
   // Two streams, joined only at the end. The second stream: the denominator
   // kernels (they need only what k2_bwd_prep and the forward wrote), the
-  // intra-chunk VJP (dk and dv, then dq), then the query-side fold of three
-  // quarters of the units. The caller's stream: the state scan and its carry,
-  // the key-side fold after an event recorded behind the dk and dv kernels and
-  // the denominator scan, then the query-side fold of the remaining units and
-  // the coefficient reductions after the dq kernel's event. (Measured, per
+  // intra-chunk dk, then dq, then the query-side fold of three quarters of the
+  // units. The caller's stream: the state scan and its carry, the intra-chunk
+  // dv, the key-side fold after an event recorded behind the dk kernel and the
+  // denominator scan, then the query-side fold of the remaining units and the
+  // coefficient reductions after the dq kernel's event. (Measured, per
   // config-2 step, same box: 0.8505 ms with the denominator kernels on the
   // caller's stream and the whole query-side fold on the second stream, 0.8441
   // with the denominator kernels moved, 0.8363 with the fold also split 6/2
-  // over the 8 units; a 4/4 or 5/3 split: 0.844 and 0.849.)
+  // over the 8 units (a 4/4 or 5/3 split: 0.844 and 0.849); on another box
+  // 0.8090 -> 0.7954 ms with the dv kernel moved to the caller's stream.)
   const LocalBwdArgs la{w.G16, w.Gz, w.QT16, w.GT16, sv.KT16, sv.KAP, sv.PZ, sv.PZm, labels, lam, gam, sv.ic, sv.gm,
                         sv.lb, groups, scale, w.dqf, w.dkl, w.dvl, (need_coef && !pairwise) ? w.coefl : nullptr,
                         pairwise, sv.wqs, w.dkp, (need_coef && pairwise) ? w.dwql : nullptr};
@@ -805,7 +806,7 @@ int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, cons
   if (forked) {
     stream_wait(aux, st);
     den_state(aux);
-    launch_local_bwd<T>(g, qt, kt, vt, la, dq != nullptr, dk != nullptr, kLocalDkv, aux, timed);
+    launch_local_bwd<T>(g, qt, kt, vt, la, dq != nullptr, dk != nullptr, kLocalDk, aux, timed);
     ev_dkv = record_event(aux);
     launch_local_bwd<T>(g, qt, kt, vt, la, dq != nullptr, dk != nullptr, kLocalDq, aux, timed);
     ev_dq = record_event(aux);
@@ -819,6 +820,9 @@ int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, cons
     launch_scan<false>(plan, a, st, timed);
     if (!forked) den_state(st);
   }
+  // the dv kernel (it needs only the forward's kappa and k2_bwd_prep's G^T) on
+  // the caller's stream, which would otherwise wait for the dk kernel's event
+  if (forked) launch_local_bwd<T>(g, qt, kt, vt, la, dq != nullptr, dk != nullptr, kLocalDv, st, timed);
   if (!forked) {
     // one stream (the allocation-free entry point, the profiling mode, a call
     // made during a graph capture before the second stream exists): the state

@@ -527,7 +527,8 @@ void launch_local_bwd(const LaunchGeom& g, const T* q, const T* k, const T* v, c
   // The coefficient partials come from the dq kernel's group sums, also when
   // dq itself is not requested (its dq then goes to the workspace unused), so
   // that every requested gradient is bit-identical whatever else is requested.
-  // parts: kLocalDq (with the per-pair path's whole local VJP), kLocalDkv.
+  // parts: kLocalDq (with the per-pair path's whole local VJP), kLocalDk,
+  // kLocalDv.
   if (a.pairwise && (parts & kLocalDq)) {
     launch_pair_local_bwd<T>(g, q, k, v, a, need_dq, need_dkv, st, timed);
   }
@@ -544,13 +545,13 @@ void launch_local_bwd(const LaunchGeom& g, const T* q, const T* k, const T* v, c
                            g.NB, a.scale, a.dqf, nullptr);
     });
   }
-  if (!a.pairwise && need_dkv && (parts & kLocalDkv)) {
+  if (!a.pairwise && need_dkv && (parts & kLocalDk)) {
     timed("k2_local_dk", st, [&] {
       hipLaunchKernelGGL(k2_local_dk<T>, dim3(g.NB * g.U), dim3(192), 0, st, q, k, v, a.G16, a.Gz, a.QT16,
                          a.labels, a.lam, a.gam, a.groups, g.Hq, g.Hkv, g.N, g.NB, a.scale, a.dkl);
     });
   }
-  if (need_dkv && (parts & kLocalDkv)) {
+  if (need_dkv && (parts & kLocalDv)) {
     timed("k2_local_dv", st, [&] {
       hipLaunchKernelGGL(k2_local_dv, dim3(g.NB * g.U), dim3(192), 0, st, a.KAP, a.GT16, g.Hq, g.Hkv, g.N, g.NB,
                          a.dvl);
