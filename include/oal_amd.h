@@ -118,7 +118,7 @@ int oal_forward(const void* q, const void* k, const void* v,
  * [g(r)][g(c)] only; gradients reaching a factor L with gam = L L^T, or a
  * per-pair coefficient, are the same under both.) Invalid combinations are
  * refused before anything is enqueued. On the matrix-core paths (bf16, and fp32
- * with up to 8 groups) the intra-chunk VJP and (most of) the query-side fold
+ * with up to 8 groups) most of the intra-chunk VJP and of the query-side fold
  * run on a second stream, on the bf16 path with the denominator kernels
  * (one per device, default
  * priority, created with its fork/join events on the first call; not created
