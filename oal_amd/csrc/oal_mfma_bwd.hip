@@ -250,15 +250,23 @@ template <typename T>
 __global__ __launch_bounds__(128, 2) void k2_q_fold(const T* __restrict__ q, const uint16_t* __restrict__ G16,
                                                  const float* __restrict__ wqs, const uint16_t* __restrict__ PR,
                                                  const float* __restrict__ dqf, int Hq, int Hkv, int N, int NB,
-                                                 int u0, T* __restrict__ dq) {
+                                                 int i0, int ni, T* __restrict__ dq) {
   __shared__ __attribute__((aligned(16))) __bf16 ring0[kTileElems], ring1[kTileElems], ring2[kTileElems],
       ring3[kTileElems], ring4[kTileElems], ring5[kTileElems];
   __shared__ __attribute__((aligned(16))) float wl[kS];
   const LdsRing<6> ring{{ring0, ring1, ring2, ring3, ring4, ring5}};
 
   int hh, ch, u;
-  head_chunk_unit(Hq / Hkv, NB, (int)(gridDim.x / ((Hq / Hkv) * NB)), hh, ch, u);
-  u += u0;  // the launch covers units u0 ..
+  {
+    // the launch covers items i0 .. i0 + ni - 1 of (unit, chunk, head), head
+    // fastest; block ids are dealt to the 8 XCDs round-robin (see head_chunk_unit)
+    const int id = blockIdx.x;
+    const int w = i0 + ((ni & 7) == 0 ? (id & 7) * (ni >> 3) + (id >> 3) : id);
+    const int R0 = Hq / Hkv;
+    hh = w % R0;
+    ch = (w / R0) % NB;
+    u = w / (R0 * NB);
+  }
   const int R = Hq / Hkv, b = u / Hkv, kh = u % Hkv, h = kh * R + hh;
   const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, s = l >> 5, row = l & 31;
   const int tok0 = ch * kC;
@@ -768,30 +776,32 @@ int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, cons
     hipLaunchKernelGGL(k2_bwd_prep<T>, dim3(g.B * g.Hq * g.NB), dim3(256), 0, st, qt, static_cast<const T*>(dout),
                        dnum, dden, num, den, g.N, g.NB, floor, w.G16, w.Gz, w.GT16, w.QT16);
   });
-  // Two streams, joined only at the end. The second stream: the denominator
-  // kernels (they need only what k2_bwd_prep and the forward wrote), the
-  // intra-chunk dk, then dq, then the query-side fold of three quarters of the
-  // units. The caller's stream: the state scan and its carry, the intra-chunk
-  // dv, the key-side fold after an event recorded behind the dk kernel and the
-  // denominator scan, then the query-side fold of the remaining units and the
-  // coefficient reductions after the dq kernel's event. (Measured, per
-  // config-2 step, same box: 0.8505 ms with the denominator kernels on the
-  // caller's stream and the whole query-side fold on the second stream, 0.8441
-  // with the denominator kernels moved, 0.8363 with the fold also split 6/2
-  // over the 8 units (a 4/4 or 5/3 split: 0.844 and 0.849); on another box
-  // 0.8090 -> 0.7954 ms with the dv kernel moved to the caller's stream.)
+  // Two streams, joined only at the end. The second stream: (at up to 128
+  // chunks per unit) the denominator kernels, which need only what
+  // k2_bwd_prep and the forward wrote; the intra-chunk dk, then dq, then the
+  // query-side fold of three quarters of its items. The caller's stream: the
+  // state scan and its carry, (otherwise the denominator kernels,) the
+  // intra-chunk dv, the key-side fold after an event recorded behind the dk
+  // kernel, then the rest of the query-side fold and the coefficient
+  // reductions after the dq kernel's event. (Measured, per config-2 step, same
+  // box: 0.8505 ms with the denominator kernels on the caller's stream and the
+  // whole query-side fold on the second stream, 0.8441 with the denominator
+  // kernels moved, 0.8363 with the fold also split 6/2 over the 8 units (a 4/4
+  // or 5/3 split: 0.844 and 0.849); on another box 0.8090 -> 0.7954 ms with
+  // the dv kernel moved to the caller's stream.)
   const LocalBwdArgs la{w.G16, w.Gz, w.QT16, w.GT16, sv.KT16, sv.KAP, sv.PZ, sv.PZm, labels, lam, gam, sv.ic, sv.gm,
                         sv.lb, groups, scale, w.dqf, w.dkl, w.dvl, (need_coef && !pairwise) ? w.coefl : nullptr,
                         pairwise, sv.wqs, w.dkp, (need_coef && pairwise) ? w.dwql : nullptr};
-  // the query-side fold of units u0 .. u0 + nu - 1
-  auto q_fold = [&](hipStream_t s, int u0, int nu) {
-    if (dq && nu > 0) {
+  // the query-side fold of items i0 .. i0 + ni - 1 of (unit, chunk, head)
+  auto q_fold = [&](hipStream_t s, int i0, int ni) {
+    if (dq && ni > 0) {
       timed("k2_q_fold", s, [&] {
-        hipLaunchKernelGGL(k2_q_fold<T>, dim3(g.R * g.NB * nu), dim3(128), 0, s, qt, w.G16, sv.wqs, sv.PR, w.dqf,
-                           g.Hq, g.Hkv, g.N, g.NB, u0, static_cast<T*>(dq));
+        hipLaunchKernelGGL(k2_q_fold<T>, dim3(ni), dim3(128), 0, s, qt, w.G16, sv.wqs, sv.PR, w.dqf, g.Hq, g.Hkv,
+                           g.N, g.NB, i0, ni, static_cast<T*>(dq));
       });
     }
   };
+  const int nq = g.R * g.NB * g.U;  // query-side fold items
   // denominator state (pair-matrix form): per-chunk dCarry and coefficient
   // partials, then dTz as the exclusive chunk suffix
   auto den_state = [&](hipStream_t s) {
@@ -800,17 +810,25 @@ int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, cons
     launch_den_scan(false, g, w.dCt, w.dTz, nullptr, s, timed);
   };
   hipEvent_t ev_dkv = nullptr, ev_dq = nullptr;
-  // units whose query-side fold runs on the second stream (three quarters,
-  // rounded up); the rest follows the key-side fold on the caller's stream
-  const int ua = forked ? (3 * g.U + 3) / 4 : g.U;
+  // Three quarters (rounded up) of the query-side fold items go to the second
+  // stream, the rest follows the key-side fold on the caller's stream. The dv
+  // kernel runs on the caller's stream after the scan. The denominator kernels
+  // go to the head of the second stream for the group-sum path at up to 128
+  // chunks per unit, and follow the scan on the caller's stream otherwise:
+  // measured at N = 4096 (64 chunks) the second stream is 22 us per step
+  // faster, at N = 32768 (512 chunks) 50 us slower, and on the per-pair path
+  // (whose key-side fold waits for the dq part) no faster.
+  const bool den_aux = forked && !pairwise && g.NB <= 128;
+  const bool dv_main = forked;
+  const int na = forked ? (3 * nq + 3) / 4 : nq;
   if (forked) {
     stream_wait(aux, st);
-    den_state(aux);
-    launch_local_bwd<T>(g, qt, kt, vt, la, dq != nullptr, dk != nullptr, kLocalDk, aux, timed);
+    if (den_aux) den_state(aux);
+    launch_local_bwd<T>(g, qt, kt, vt, la, dq != nullptr, dk != nullptr, dv_main ? kLocalDk : kLocalDkv, aux, timed);
     ev_dkv = record_event(aux);
     launch_local_bwd<T>(g, qt, kt, vt, la, dq != nullptr, dk != nullptr, kLocalDq, aux, timed);
     ev_dq = record_event(aux);
-    q_fold(aux, 0, ua);
+    q_fold(aux, 0, na);
   }
   {
     const ScanPlan plan{w.S, w.SL, 0};
@@ -818,11 +836,11 @@ int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, cons
     ScanArgs a{w.QT16, kTRows, w.GT16, kTRows, sv.wqs, sv.PR, g.U, g.Hq, g.Hkv, g.N, g.NB,
                w.dTR, w.segtot, need_coef ? w.dwqs : nullptr, w.dCR};
     launch_scan<false>(plan, a, st, timed);
-    if (!forked) den_state(st);
+    if (!den_aux) den_state(st);
   }
   // the dv kernel (it needs only the forward's kappa and k2_bwd_prep's G^T) on
   // the caller's stream, which would otherwise wait for the dk kernel's event
-  if (forked) launch_local_bwd<T>(g, qt, kt, vt, la, dq != nullptr, dk != nullptr, kLocalDv, st, timed);
+  if (dv_main) launch_local_bwd<T>(g, qt, kt, vt, la, dq != nullptr, dk != nullptr, kLocalDv, st, timed);
   if (!forked) {
     // one stream (the allocation-free entry point, the profiling mode, a call
     // made during a graph capture before the second stream exists): the state
@@ -830,7 +848,7 @@ int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, cons
     // stream 0.950-0.951 ms per config-2 step, against 0.955 with the
     // intra-chunk VJP first)
     launch_local_bwd<T>(g, qt, kt, vt, la, dq != nullptr, dk != nullptr, kLocalDq | kLocalDkv, st, timed);
-    q_fold(st, 0, g.U);
+    q_fold(st, 0, nq);
   }
   if (dk) {
     // the per-pair path forms its local dk in the dq part's launch
@@ -846,8 +864,8 @@ int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, cons
                            static_cast<T*>(dv));
     });
   }
-  if (forked && (need_coef || ua < g.U)) wait_event(st, ev_dq);
-  if (forked) q_fold(st, ua, g.U - ua);
+  if (forked && (need_coef || na < nq)) wait_event(st, ev_dq);
+  if (forked) q_fold(st, na, nq - na);
   if (need_coef) {
     // group-sum path: the 73 local coefficient columns; per-pair path: the
     // local slot partials added to the state's
