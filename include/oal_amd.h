@@ -119,8 +119,8 @@ int oal_forward(const void* q, const void* k, const void* v,
  * per-pair coefficient, are the same under both.) Invalid combinations are
  * refused before anything is enqueued. On the matrix-core paths (bf16, and fp32
  * with up to 8 groups) most of the intra-chunk VJP and of the query-side fold
- * run on a second stream, on the bf16 path with the denominator kernels
- * (one per device, default
+ * run on a second stream, on the bf16 group-sum path at up to 128 chunks per
+ * unit with the denominator kernels (one per device, default
  * priority, created with its fork/join events on the first call; not created
  * while the caller's stream is capturing a graph, whose call then stays on the
  * caller's stream). Every kernel on it waits for an event recorded on the
