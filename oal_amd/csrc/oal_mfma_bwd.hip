@@ -779,11 +779,11 @@ int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, cons
   // Two streams, joined only at the end. The second stream: (at up to 128
   // chunks per unit) the denominator kernels, which need only what
   // k2_bwd_prep and the forward wrote; the intra-chunk dk, then dq, then the
-  // query-side fold of three quarters of its items. The caller's stream: the
-  // state scan and its carry, (otherwise the denominator kernels,) the
-  // intra-chunk dv, the key-side fold after an event recorded behind the dk
-  // kernel, then the rest of the query-side fold and the coefficient
-  // reductions after the dq kernel's event. (Measured, per config-2 step, same
+  // query-side fold (per pair: three quarters of its items). The caller's
+  // stream: the state scan and its carry, (otherwise the denominator kernels,)
+  // the intra-chunk dv, the key-side fold after an event recorded behind the
+  // dk kernel, then (per pair) the rest of the query-side fold and the
+  // coefficient reductions after the dq kernel's event. (Measured, per config-2 step, same
   // box: 0.8505 ms with the denominator kernels on the caller's stream and the
   // whole query-side fold on the second stream, 0.8441 with the denominator
   // kernels moved, 0.8363 with the fold also split 6/2 over the 8 units (a 4/4
@@ -810,17 +810,21 @@ int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, cons
     launch_den_scan(false, g, w.dCt, w.dTz, nullptr, s, timed);
   };
   hipEvent_t ev_dkv = nullptr, ev_dq = nullptr;
-  // Three quarters (rounded up) of the query-side fold items go to the second
-  // stream, the rest follows the key-side fold on the caller's stream. The dv
-  // kernel runs on the caller's stream after the scan. The denominator kernels
-  // go to the head of the second stream for the group-sum path at up to 128
-  // chunks per unit, and follow the scan on the caller's stream otherwise:
-  // measured at N = 4096 (64 chunks) the second stream is 22 us per step
-  // faster, at N = 32768 (512 chunks) 50 us slower, and on the per-pair path
-  // (whose key-side fold waits for the dq part) no faster.
+  // The query-side fold runs on the second stream: all of it on the group-sum
+  // path, three quarters (rounded up) of its items on the per-pair path, whose
+  // remaining quarter follows the key-side fold on the caller's stream (on the
+  // group-sum path a split costs one more event wait on the caller's stream:
+  // 0.800 against 0.786 ms per config-2 step with 15/16 of the items on the
+  // second stream, 0.789 with 3/4). The dv kernel runs on the caller's stream
+  // after the scan. The denominator kernels go to the head of the second
+  // stream for the group-sum path at up to 128 chunks per unit, and follow the
+  // scan on the caller's stream otherwise: measured at N = 4096 (64 chunks)
+  // the second stream is 22 us per step faster, at N = 32768 (512 chunks)
+  // 50 us slower, and on the per-pair path (whose key-side fold waits for the
+  // dq part) no faster.
   const bool den_aux = forked && !pairwise && g.NB <= 128;
   const bool dv_main = forked;
-  const int na = forked ? (3 * nq + 3) / 4 : nq;
+  const int na = forked && pairwise ? (3 * nq + 3) / 4 : nq;
   if (forked) {
     stream_wait(aux, st);
     if (den_aux) den_state(aux);

@@ -1,10 +1,11 @@
 """The backward's second stream as the caller sees it: one stream.
 
 ``oal_backward`` forks the denominator kernels, most of the intra-chunk VJP and
-most of the query-side fold onto a stream of the library's own, makes the caller's
-stream wait for events the second stream recorded before the key-side fold
-and before the rest of the query-side fold and the coefficient reductions, and
-joins it back into the caller's stream before it returns.
+the query-side fold (all of it on the group-sum path, most of it per pair) onto a
+stream of the library's own, makes the caller's stream wait for events the second
+stream recorded before the key-side fold and before the rest of the query-side
+fold and the coefficient reductions, and joins it back into the caller's stream
+before it returns.
 These tests call it on caller-created streams (not the default one), from two
 streams in turn, and consume the gradients on the caller's stream right after
 the call with no synchronization in between. Every result must be bitwise
