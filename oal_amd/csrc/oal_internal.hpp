@@ -1,10 +1,12 @@
 // Declarations shared by the translation units of liboal_amd.so.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 #include <functional>
+#include <tuple>
 
 namespace oal {
 
@@ -89,6 +91,35 @@ void stream_wait(hipStream_t waiter, hipStream_t signaller);
 // on waiter later (stream_wait is the two at once).
 hipEvent_t record_event(hipStream_t s);
 void wait_event(hipStream_t waiter, hipEvent_t ev);
+// The next event of the device's ring, not recorded: a launch_signal stop
+// event. capturing(s): s is capturing a graph (or its state is unknown).
+hipEvent_t next_event();
+bool capturing(hipStream_t s);
+// Launch of kernel k on s; with stop given, the launch itself records stop
+// when the kernel completes (hipExtLaunchKernel's stop event), instead of a
+// marker of its own behind it on s, which leaves s idle for several
+// microseconds before its next kernel.
+// If that launch is refused, the kernel is launched as usual and stop
+// recorded behind it.
+template <typename... KA, typename... A>
+void launch_signal(void (*k)(KA...), dim3 grid, dim3 block, hipStream_t s, hipEvent_t stop, A... args) {
+  static_assert(sizeof...(KA) == sizeof...(A), "one argument per kernel parameter");
+  if (!stop) {
+    hipLaunchKernelGGL(k, grid, block, 0, s, args...);
+    return;
+  }
+  std::tuple<KA...> t{static_cast<KA>(args)...};
+  void* ptrs[sizeof...(KA)];
+  std::apply([&](auto&... e) {
+    int i = 0;
+    ((ptrs[i++] = static_cast<void*>(&e)), ...);
+  }, t);
+  if (hipExtLaunchKernel(reinterpret_cast<const void*>(k), grid, block, ptrs, 0, s, nullptr, stop, 0) != hipSuccess) {
+    (void)hipGetLastError();
+    hipLaunchKernelGGL(k, grid, block, 0, s, args...);
+    (void)hipEventRecord(stop, s);
+  }
+}
 
 // aux: a second stream for the kernels that do not depend on each other (the
 // intra-chunk VJP beside the state scan, the key-side fold beside the query
@@ -137,10 +168,13 @@ void launch_pair_coef_grad(const LaunchGeom& g, const float* dwq, const float* d
 
 // Parts of the intra-chunk VJP that one call of launch_local_bwd launches:
 // the dq kernel (which also forms the coefficient partials), the dk and dv kernels.
+// With stop given and parts naming one kernel of the group-sum path, that
+// kernel's launch records stop (launch_signal); the return value says whether
+// it did (if not, the caller records its own event).
 constexpr unsigned kLocalDq = 1, kLocalDk = 2, kLocalDv = 4, kLocalDkv = kLocalDk | kLocalDv;
 template <typename T>
-void launch_local_bwd(const LaunchGeom& g, const T* q, const T* k, const T* v, const LocalBwdArgs& a, bool need_dq,
-                      bool need_dkv, unsigned parts, hipStream_t st, const Timer& timed);
+bool launch_local_bwd(const LaunchGeom& g, const T* q, const T* k, const T* v, const LocalBwdArgs& a, bool need_dq,
+                      bool need_dkv, unsigned parts, hipStream_t st, const Timer& timed, hipEvent_t stop = nullptr);
 
 // Segmentation of a chunk-state scan: S segments of SL chunks, a function of
 // the geometry alone. The forward runs more than one segment as totals, carry,

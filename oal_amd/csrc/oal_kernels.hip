@@ -851,17 +851,27 @@ hipStream_t aux_stream(hipStream_t st) {
   return a.stream;
 }
 
-hipEvent_t record_event(hipStream_t s) {
+hipEvent_t next_event() {
   int dev = -1;
   (void)hipGetDevice(&dev);
-  hipEvent_t ev = nullptr;
-  {
-    std::lock_guard<std::mutex> lock(g_aux_mu);
-    AuxState& a = g_aux[dev];
-    ev = a.events[a.next++ % kAuxEvents];
-  }
+  std::lock_guard<std::mutex> lock(g_aux_mu);
+  AuxState& a = g_aux[dev];
+  return a.events[a.next++ % kAuxEvents];
+}
+
+hipEvent_t record_event(hipStream_t s) {
+  hipEvent_t ev = next_event();
   (void)hipEventRecord(ev, s);
   return ev;
+}
+
+bool capturing(hipStream_t s) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &cs) != hipSuccess) {
+    (void)hipGetLastError();
+    return true;
+  }
+  return cs != hipStreamCaptureStatusNone;
 }
 
 void wait_event(hipStream_t waiter, hipEvent_t ev) { (void)hipStreamWaitEvent(waiter, ev, 0); }

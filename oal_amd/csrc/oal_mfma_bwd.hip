@@ -772,9 +772,13 @@ int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, cons
   const T* kt = static_cast<const T*>(k);
   const T* vt = static_cast<const T*>(v);
   const bool forked = aux != st;
+  // the fork, the second stream's mid-call events and the join are recorded
+  // by the launches of the kernels they follow (not while st is capturing)
+  const bool sig = forked && !capturing(st);
+  const hipEvent_t ev_fork = sig ? next_event() : nullptr;
   timed("k2_bwd_prep", st, [&] {
-    hipLaunchKernelGGL(k2_bwd_prep<T>, dim3(g.B * g.Hq * g.NB), dim3(256), 0, st, qt, static_cast<const T*>(dout),
-                       dnum, dden, num, den, g.N, g.NB, floor, w.G16, w.Gz, w.GT16, w.QT16);
+    launch_signal(k2_bwd_prep<T>, dim3(g.B * g.Hq * g.NB), dim3(256), st, ev_fork, qt, static_cast<const T*>(dout),
+                  dnum, dden, num, den, g.N, g.NB, floor, w.G16, w.Gz, w.GT16, w.QT16);
   });
   // Two streams, joined only at the end. The second stream: (at up to 128
   // chunks per unit) the denominator kernels, which need only what
@@ -793,11 +797,11 @@ int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, cons
                         sv.lb, groups, scale, w.dqf, w.dkl, w.dvl, (need_coef && !pairwise) ? w.coefl : nullptr,
                         pairwise, sv.wqs, w.dkp, (need_coef && pairwise) ? w.dwql : nullptr};
   // the query-side fold of items i0 .. i0 + ni - 1 of (unit, chunk, head)
-  auto q_fold = [&](hipStream_t s, int i0, int ni) {
+  auto q_fold = [&](hipStream_t s, int i0, int ni, hipEvent_t stop) {
     if (dq && ni > 0) {
       timed("k2_q_fold", s, [&] {
-        hipLaunchKernelGGL(k2_q_fold<T>, dim3(ni), dim3(128), 0, s, qt, w.G16, sv.wqs, sv.PR, w.dqf, g.Hq, g.Hkv,
-                           g.N, g.NB, i0, ni, static_cast<T*>(dq));
+        launch_signal(k2_q_fold<T>, dim3(ni), dim3(128), s, stop, qt, w.G16, sv.wqs, sv.PR, w.dqf, g.Hq, g.Hkv, g.N,
+                      g.NB, i0, ni, static_cast<T*>(dq));
       });
     }
   };
@@ -825,14 +829,23 @@ int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, cons
   const bool den_aux = forked && !pairwise && g.NB <= 128;
   const bool dv_main = forked;
   const int na = forked && pairwise ? (3 * nq + 3) / 4 : nq;
+  hipEvent_t ev_join = nullptr;
   if (forked) {
-    stream_wait(aux, st);
+    if (ev_fork)
+      wait_event(aux, ev_fork);
+    else
+      stream_wait(aux, st);
     if (den_aux) den_state(aux);
-    launch_local_bwd<T>(g, qt, kt, vt, la, dq != nullptr, dk != nullptr, dv_main ? kLocalDk : kLocalDkv, aux, timed);
-    ev_dkv = record_event(aux);
-    launch_local_bwd<T>(g, qt, kt, vt, la, dq != nullptr, dk != nullptr, kLocalDq, aux, timed);
-    ev_dq = record_event(aux);
-    q_fold(aux, 0, na);
+    ev_dkv = sig ? next_event() : nullptr;
+    if (!launch_local_bwd<T>(g, qt, kt, vt, la, dq != nullptr, dk != nullptr, dv_main ? kLocalDk : kLocalDkv, aux,
+                             timed, ev_dkv))
+      ev_dkv = record_event(aux);
+    ev_dq = sig ? next_event() : nullptr;
+    if (!launch_local_bwd<T>(g, qt, kt, vt, la, dq != nullptr, dk != nullptr, kLocalDq, aux, timed, ev_dq))
+      ev_dq = record_event(aux);
+    // the fold is the second stream's last kernel: its launch records the join
+    ev_join = sig && dq && na > 0 ? next_event() : nullptr;
+    q_fold(aux, 0, na, ev_join);
   }
   {
     const ScanPlan plan{w.S, w.SL, 0};
@@ -852,7 +865,7 @@ int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, cons
     // stream 0.950-0.951 ms per config-2 step, against 0.955 with the
     // intra-chunk VJP first)
     launch_local_bwd<T>(g, qt, kt, vt, la, dq != nullptr, dk != nullptr, kLocalDq | kLocalDkv, st, timed);
-    q_fold(st, 0, nq);
+    q_fold(st, 0, nq, nullptr);
   }
   if (dk) {
     // the per-pair path forms its local dk in the dq part's launch
@@ -869,7 +882,7 @@ int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, cons
     });
   }
   if (forked && (need_coef || na < nq)) wait_event(st, ev_dq);
-  if (forked) q_fold(st, na, nq - na);
+  if (forked) q_fold(st, na, nq - na, nullptr);
   if (need_coef) {
     // group-sum path: the 73 local coefficient columns; per-pair path: the
     // local slot partials added to the state's
@@ -889,7 +902,10 @@ int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, cons
     }
   }
   // the caller's stream ends after every kernel of the call
-  if (forked) stream_wait(st, aux);
+  if (ev_join)
+    wait_event(st, ev_join);
+  else if (forked)
+    stream_wait(st, aux);
   return 0;
 }
 

@@ -522,8 +522,8 @@ __global__ __launch_bounds__(192, 2) void k2_local_dv(const uint16_t* __restrict
 }
 
 template <typename T>
-void launch_local_bwd(const LaunchGeom& g, const T* q, const T* k, const T* v, const LocalBwdArgs& a, bool need_dq,
-                      bool need_dkv, unsigned parts, hipStream_t st, const Timer& timed) {
+bool launch_local_bwd(const LaunchGeom& g, const T* q, const T* k, const T* v, const LocalBwdArgs& a, bool need_dq,
+                      bool need_dkv, unsigned parts, hipStream_t st, const Timer& timed, hipEvent_t stop) {
   // The coefficient partials come from the dq kernel's group sums, also when
   // dq itself is not requested (its dq then goes to the workspace unused), so
   // that every requested gradient is bit-identical whatever else is requested.
@@ -533,35 +533,45 @@ void launch_local_bwd(const LaunchGeom& g, const T* q, const T* k, const T* v, c
     launch_pair_local_bwd<T>(g, q, k, v, a, need_dq, need_dkv, st, timed);
   }
   const bool coef = a.coefl != nullptr;
+  // the one kernel of a single-part call records stop
+  hipEvent_t stop_dq = parts == kLocalDq ? stop : nullptr, stop_dk = parts == kLocalDk ? stop : nullptr,
+             stop_dv = parts == kLocalDv ? stop : nullptr;
+  bool signalled = false;
   if (!a.pairwise && (need_dq || coef) && (parts & kLocalDq)) {
     timed("k2_local_dq", st, [&] {
       if (coef)
-        hipLaunchKernelGGL((k2_local_dq<T, true>), dim3(g.R * g.NB * g.U), dim3(128), 0, st, q, k, v, a.G16, a.Gz,
-                           a.KT16, a.PZ, a.PZm, a.labels, a.lam, a.gam, a.gm, a.lb, a.groups, g.Hq, g.Hkv, g.N, g.NB,
-                           a.scale, a.dqf, a.coefl);
+        launch_signal(k2_local_dq<T, true>, dim3(g.R * g.NB * g.U), dim3(128), st, stop_dq, q, k, v, a.G16, a.Gz,
+                      a.KT16, a.PZ, a.PZm, a.labels, a.lam, a.gam, a.gm, a.lb, a.groups, g.Hq, g.Hkv, g.N, g.NB,
+                      a.scale, a.dqf, a.coefl);
       else
-        hipLaunchKernelGGL((k2_local_dq<T, false>), dim3(g.R * g.NB * g.U), dim3(128), 0, st, q, k, v, a.G16,
-                           a.Gz, a.KT16, a.PZ, a.PZm, a.labels, a.lam, a.gam, a.gm, a.lb, a.groups, g.Hq, g.Hkv, g.N,
-                           g.NB, a.scale, a.dqf, nullptr);
+        launch_signal(k2_local_dq<T, false>, dim3(g.R * g.NB * g.U), dim3(128), st, stop_dq, q, k, v, a.G16, a.Gz,
+                      a.KT16, a.PZ, a.PZm, a.labels, a.lam, a.gam, a.gm, a.lb, a.groups, g.Hq, g.Hkv, g.N, g.NB,
+                      a.scale, a.dqf, static_cast<float*>(nullptr));
     });
+    signalled = stop_dq != nullptr;
   }
   if (!a.pairwise && need_dkv && (parts & kLocalDk)) {
     timed("k2_local_dk", st, [&] {
-      hipLaunchKernelGGL(k2_local_dk<T>, dim3(g.NB * g.U), dim3(192), 0, st, q, k, v, a.G16, a.Gz, a.QT16,
-                         a.labels, a.lam, a.gam, a.groups, g.Hq, g.Hkv, g.N, g.NB, a.scale, a.dkl);
+      launch_signal(k2_local_dk<T>, dim3(g.NB * g.U), dim3(192), st, stop_dk, q, k, v, a.G16, a.Gz, a.QT16,
+                    a.labels, a.lam, a.gam, a.groups, g.Hq, g.Hkv, g.N, g.NB, a.scale, a.dkl);
     });
+    signalled = stop_dk != nullptr;
   }
   if (need_dkv && (parts & kLocalDv)) {
     timed("k2_local_dv", st, [&] {
-      hipLaunchKernelGGL(k2_local_dv, dim3(g.NB * g.U), dim3(192), 0, st, a.KAP, a.GT16, g.Hq, g.Hkv, g.N, g.NB,
-                         a.dvl);
+      launch_signal(k2_local_dv, dim3(g.NB * g.U), dim3(192), st, stop_dv, a.KAP, a.GT16, g.Hq, g.Hkv, g.N, g.NB,
+                    a.dvl);
     });
+    signalled = stop_dv != nullptr;
   }
+  return signalled;
 }
 
-template void launch_local_bwd<float>(const LaunchGeom&, const float*, const float*, const float*,
-                                      const LocalBwdArgs&, bool, bool, unsigned, hipStream_t, const Timer&);
-template void launch_local_bwd<uint16_t>(const LaunchGeom&, const uint16_t*, const uint16_t*, const uint16_t*,
-                                         const LocalBwdArgs&, bool, bool, unsigned, hipStream_t, const Timer&);
+template bool launch_local_bwd<float>(const LaunchGeom&, const float*, const float*, const float*,
+                                      const LocalBwdArgs&, bool, bool, unsigned, hipStream_t, const Timer&,
+                                      hipEvent_t);
+template bool launch_local_bwd<uint16_t>(const LaunchGeom&, const uint16_t*, const uint16_t*, const uint16_t*,
+                                         const LocalBwdArgs&, bool, bool, unsigned, hipStream_t, const Timer&,
+                                         hipEvent_t);
 
 }  // namespace oal
