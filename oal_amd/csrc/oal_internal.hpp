@@ -264,9 +264,23 @@ struct ScanArgs {
 };
 template <bool FWD>
 void launch_scan(const ScanPlan& p, const ScanArgs& a, hipStream_t st, const Timer& timed);
+// Inputs and outputs of the per-head slot coefficients (wqs, ic, gm, lb of the
+// saved state), formed in blocks of k2_fwd_prep's launch.
+struct SlotCoefArgs {
+  const int32_t* labels;
+  const float* c0;
+  const float* lam;
+  const float* gam;
+  int G;
+  float scale;
+  float* wqs;
+  float* ic;
+  float* gm;
+  float* lb;
+};
 template <typename T>
 void launch_fwd_prep(const LaunchGeom& g, const T* k, const T* v, uint16_t* KT16, uint16_t* VT16, float* Zt,
-                     hipStream_t st, const Timer& timed);
+                     const SlotCoefArgs& sc, hipStream_t st, const Timer& timed);
 // Denominator state in pair-matrix form (oal_mfma_scan.hip): the chunk prefix
 // (forward: PZ natural order and PZm) or suffix (backward: dTz) of per-chunk
 // totals, and the backward's per-chunk totals and coefficient partials.

@@ -1,8 +1,8 @@
 // bf16 matrix-core (MFMA) forward for gfx950.
 //
-// k2_slot_coefficients : per query head, the feature coefficient of every slot
-//                        and the intra-chunk coefficient packs.
-// (k2_fwd_prep and the chunk-state scan producing P_c are in oal_mfma_scan.hip)
+// (k2_fwd_prep, which also forms the per-head slot coefficients and the
+// intra-chunk coefficient packs of oal_slot_coef.hpp in blocks of its own, and
+// the chunk-state scan producing P_c are in oal_mfma_scan.hip)
 // k2_intra_fwd         : per (query head, chunk, unit): intra-chunk kernel from
 //                        MFMA group sums, kappa . V, and the denominator's state
 //                        term as a 64x64 quadratic form; writes num, den.
@@ -26,71 +26,11 @@
 
 #include "oal_internal.hpp"
 #include "oal_mfma_common.hpp"
+#include "oal_slot_coef.hpp"
 
 namespace oal {
 
 static __constant__ SlotTable kSlot = make_slot_table();
-
-// Per-head coefficients, grid (query head, 8 parts):
-//   wqs[h][slot]  wq of natural feature nat(slot) (0 for invalid slots);
-//   ic[h]         c0, scale*lam[g], scale^2*Gam[g][g'] padded to 8 groups (the
-//                 group-sum intra-chunk kernels; G > 8 keeps only c0);
-//   gm[h][r][c]   scale^2 * Gam[g(r)][g(c)]  (denominator quadratic form);
-//   lb[h][d]      scale * lam[g(d)].
-// Any group count up to 64: labels d -> d with G = 64 gives per-pair coefficients.
-__global__ __launch_bounds__(256) void k2_slot_coefficients(const int32_t* __restrict__ labels,
-                                                            const float* __restrict__ c0,
-                                                            const float* __restrict__ lam,
-                                                            const float* __restrict__ gam, int G, float scale,
-                                                            float* __restrict__ wqs, float* __restrict__ ic,
-                                                            float* __restrict__ gm, float* __restrict__ lb) {
-  // the head's coefficients are read once into LDS; every output then comes
-  // from LDS (no dependent global gathers)
-  __shared__ int lab[kD];
-  __shared__ float cg[kD * kD], cl[kD], cc;
-  // block (h, part): slots and gm rows of one eighth; part 0 also writes ic, lb
-  const int h = blockIdx.x, part = blockIdx.y, t = threadIdx.x;
-  if (t < kD) {
-    const int g = labels[h * kD + t];
-    lab[t] = g < 0 ? 0 : (g >= G ? G - 1 : g);
-  }
-  for (int e = t; e < G * G; e += blockDim.x) cg[e] = scale * scale * gam[(size_t)h * G * G + e];
-  if (t < G) cl[t] = scale * lam[(size_t)h * G + t];
-  if (t == 0) cc = c0[h];
-  __syncthreads();
-  constexpr int kSlotsPerPart = kS / 8;
-  static_assert(kSlotsPerPart * 8 == kS, "slot parts");
-  for (int s = part * kSlotsPerPart + t; s < (part + 1) * kSlotsPerPart; s += blockDim.x) {
-    const int n = kSlot.nat[s];
-    const int r = kSlot.ar[s], c = kSlot.ac[s];
-    float w = 0.f;
-    if (n == 0) {
-      w = cc;
-    } else if (n > 0 && n <= kD) {
-      w = cl[lab[r]];
-    } else if (n > kD) {
-      w = (r == c ? 1.f : 2.f) * cg[lab[r] * G + lab[c]];
-    }
-    wqs[(size_t)h * kS + s] = w;
-  }
-  if (part == 0 && t < kIC) {
-    float x = 0.f;
-    if (t == 0) {
-      x = cc;
-    } else if (G <= 8 && t < kIcGam) {
-      x = t - kIcLam < G ? cl[t - kIcLam] : 0.f;
-    } else if (G <= 8 && t < kIcGam + 64) {
-      const int g = (t - kIcGam) >> 3, g2 = (t - kIcGam) & 7;
-      x = (g < G && g2 < G) ? cg[g * G + g2] : 0.f;
-    }
-    ic[(size_t)h * kIC + t] = x;
-  }
-  for (int e = part * (kD * kD / 8) + t; e < (part + 1) * (kD * kD / 8); e += blockDim.x) {
-    const int r = e >> 6, c = e & 63;
-    gm[(size_t)h * kD * kD + e] = cg[lab[r] * G + lab[c]];
-  }
-  if (part == 0 && t < kD) lb[(size_t)h * kD + t] = cl[lab[t]];
-}
 
 template <typename T>
 __device__ __forceinline__ float ldf(const T* p, size_t i) {
@@ -905,11 +845,9 @@ void launch_mfma_forward(const LaunchGeom& g, const void* q, const void* k, cons
   const T* qt = static_cast<const T*>(q);
   const T* kt = static_cast<const T*>(k);
   const T* vt = static_cast<const T*>(v);
-  timed("k2_slot_coefficients", st, [&] {
-    hipLaunchKernelGGL(k2_slot_coefficients, dim3(g.Hq, 8), dim3(256), 0, st, labels, c0, lam, gam, groups, scale,
-                       sv.wqs, sv.ic, sv.gm, sv.lb);
-  });
-  launch_fwd_prep<T>(g, kt, vt, sv.KT16, sv.VT16, sv.Zt, st, timed);
+  // the per-head slot coefficients in blocks of the same launch
+  launch_fwd_prep<T>(g, kt, vt, sv.KT16, sv.VT16, sv.Zt,
+                     SlotCoefArgs{labels, c0, lam, gam, groups, scale, sv.wqs, sv.ic, sv.gm, sv.lb}, st, timed);
   // denominator state (pair-matrix form): PZ, PZm as exclusive chunk prefixes
   launch_den_scan(true, g, sv.Zt, sv.PZ, sv.PZm, st, timed);
   {

@@ -56,6 +56,7 @@
 
 #include "oal_internal.hpp"
 #include "oal_mfma_common.hpp"
+#include "oal_slot_coef.hpp"
 
 namespace oal {
 
@@ -508,8 +509,15 @@ __global__ __launch_bounds__(64 * NW, (NW + 1) / 2) void k2_scan(const uint16_t*
 // [4096 + d] = sum_j k_jd.
 template <typename T>
 __global__ __launch_bounds__(256) void k2_fwd_prep(const T* __restrict__ k, const T* __restrict__ v, int N, int NB,
-                                                   uint16_t* __restrict__ KT16, uint16_t* __restrict__ VT16,
-                                                   float* __restrict__ Zt) {
+                                                   int nprep, uint16_t* __restrict__ KT16,
+                                                   uint16_t* __restrict__ VT16, float* __restrict__ Zt,
+                                                   SlotCoefArgs sc) {
+  // blocks nprep .. nprep + 8 Hq - 1: the slot coefficients (query head, part)
+  if ((int)blockIdx.x >= nprep) {
+    const int i = (int)blockIdx.x - nprep;
+    slot_coefficients_part(kSlot, sc, i >> 3, i & 7);
+    return;
+  }
   __shared__ __attribute__((aligned(16))) __bf16 kT[kD][kC + 8];
   __shared__ __attribute__((aligned(16))) __bf16 vT[kD + 1][kC + 8];
   const int u = blockIdx.x / NB, ch = blockIdx.x % NB;
@@ -721,14 +729,16 @@ template void launch_scan<false>(const ScanPlan&, const ScanArgs&, hipStream_t, 
 
 template <typename T>
 void launch_fwd_prep(const LaunchGeom& g, const T* k, const T* v, uint16_t* KT16, uint16_t* VT16, float* Zt,
-                     hipStream_t st, const Timer& timed) {
+                     const SlotCoefArgs& sc, hipStream_t st, const Timer& timed) {
+  const int nprep = g.U * g.NB;
   timed("k2_fwd_prep", st, [&] {
-    hipLaunchKernelGGL(k2_fwd_prep<T>, dim3(g.U * g.NB), dim3(256), 0, st, k, v, g.N, g.NB, KT16, VT16, Zt);
+    hipLaunchKernelGGL(k2_fwd_prep<T>, dim3(nprep + 8 * g.Hq), dim3(256), 0, st, k, v, g.N, g.NB, nprep, KT16, VT16,
+                       Zt, sc);
   });
 }
 template void launch_fwd_prep<float>(const LaunchGeom&, const float*, const float*, uint16_t*, uint16_t*, float*,
-                                     hipStream_t, const Timer&);
+                                     const SlotCoefArgs&, hipStream_t, const Timer&);
 template void launch_fwd_prep<uint16_t>(const LaunchGeom&, const uint16_t*, const uint16_t*, uint16_t*, uint16_t*,
-                                        float*, hipStream_t, const Timer&);
+                                        float*, const SlotCoefArgs&, hipStream_t, const Timer&);
 
 }  // namespace oal
