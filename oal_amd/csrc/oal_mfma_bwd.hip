@@ -780,14 +780,16 @@ int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, cons
     launch_signal(k2_bwd_prep<T>, dim3(g.B * g.Hq * g.NB), dim3(256), st, ev_fork, qt, static_cast<const T*>(dout),
                   dnum, dden, num, den, g.N, g.NB, floor, w.G16, w.Gz, w.GT16, w.QT16);
   });
-  // Two streams, joined only at the end. The second stream: (at up to 128
-  // chunks per unit) the denominator kernels, which need only what
-  // k2_bwd_prep and the forward wrote; the intra-chunk dk, then dq, then the
-  // query-side fold (per pair: three quarters of its items). The caller's
-  // stream: the state scan and its carry, (otherwise the denominator kernels,)
-  // the intra-chunk dv, the key-side fold after an event recorded behind the
-  // dk kernel, then (per pair) the rest of the query-side fold and the
-  // coefficient reductions after the dq kernel's event. (Measured, per config-2 step, same
+  // Two streams, joined only at the end. The second stream: (group-sum path)
+  // the intra-chunk dv, whose small footprint (58 VGPRs, 8 KB of LDS) fits
+  // beside the state scan's blocks; (at up to 128 chunks per unit) the
+  // denominator kernels, which need only what k2_bwd_prep and the forward
+  // wrote; the intra-chunk dk, then dq, then the query-side fold (or the
+  // first 7/8 or 3/4 of its items). The caller's stream: the state scan and
+  // its carry, (otherwise the denominator kernels,) (per pair) the intra-chunk
+  // dv, the key-side fold after an event recorded behind the dk kernel, then
+  // the rest of the query-side fold and the coefficient reductions after the
+  // dq kernel's event. (Measured, per config-2 step, same
   // box: 0.8505 ms with the denominator kernels on the caller's stream and the
   // whole query-side fold on the second stream, 0.8441 with the denominator
   // kernels moved, 0.8363 with the fold also split 6/2 over the 8 units (a 4/4
@@ -814,31 +816,32 @@ int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, cons
     launch_den_scan(false, g, w.dCt, w.dTz, nullptr, s, timed);
   };
   hipEvent_t ev_dkv = nullptr, ev_dq = nullptr;
-  // The query-side fold runs on the second stream: all of it on the group-sum
-  // path, three quarters (rounded up) of its items on the per-pair path, whose
-  // remaining quarter follows the key-side fold on the caller's stream (on the
-  // group-sum path a split costs one more event wait on the caller's stream:
-  // 0.800 against 0.786 ms per config-2 step with 15/16 of the items on the
-  // second stream, 0.789 with 3/4). The dv kernel runs on the caller's stream
-  // after the scan. The denominator kernels go to the head of the second
-  // stream for the group-sum path at up to 128 chunks per unit, and follow the
-  // scan on the caller's stream otherwise: measured at N = 4096 (64 chunks)
-  // the second stream is 22 us per step faster, at N = 32768 (512 chunks)
-  // 50 us slower, and on the per-pair path (whose key-side fold waits for the
-  // dq part) no faster.
+  // The denominator kernels go to the second stream for the group-sum path at
+  // up to 128 chunks per unit, and follow the scan on the caller's stream
+  // otherwise: measured at N = 4096 (64 chunks) the second stream is 22 us per
+  // step faster, at N = 32768 (512 chunks) 50 us slower, and on the per-pair
+  // path (whose key-side fold waits for the dq part) no faster. The dv kernel
+  // heads the second stream on the group-sum path (config 2 0.8015 -> 0.7886
+  // ms per step with the fold split 7/8, config 3 1.660 -> 1.640 ms with the
+  // fold whole; on the caller's stream after the scan before). The second
+  // stream runs the query-side fold's first items: 7/8 of them (rounded up)
+  // where it also has the denominator kernels, all of them on the group-sum
+  // path otherwise, 3/4 on the per-pair path; the rest follows the key-side
+  // fold on the caller's stream.
   const bool den_aux = forked && !pairwise && g.NB <= 128;
-  const bool dv_main = forked;
-  const int na = forked && pairwise ? (3 * nq + 3) / 4 : nq;
+  const bool dv_aux = forked && !pairwise;
+  const bool dv_main = forked && !dv_aux;
+  const int na = !forked ? nq : pairwise ? (3 * nq + 3) / 4 : den_aux ? (7 * nq + 7) / 8 : nq;
   hipEvent_t ev_join = nullptr;
   if (forked) {
     if (ev_fork)
       wait_event(aux, ev_fork);
     else
       stream_wait(aux, st);
+    if (dv_aux) launch_local_bwd<T>(g, qt, kt, vt, la, dq != nullptr, dk != nullptr, kLocalDv, aux, timed);
     if (den_aux) den_state(aux);
     ev_dkv = sig ? next_event() : nullptr;
-    if (!launch_local_bwd<T>(g, qt, kt, vt, la, dq != nullptr, dk != nullptr, dv_main ? kLocalDk : kLocalDkv, aux,
-                             timed, ev_dkv))
+    if (!launch_local_bwd<T>(g, qt, kt, vt, la, dq != nullptr, dk != nullptr, kLocalDk, aux, timed, ev_dkv))
       ev_dkv = record_event(aux);
     ev_dq = sig ? next_event() : nullptr;
     if (!launch_local_bwd<T>(g, qt, kt, vt, la, dq != nullptr, dk != nullptr, kLocalDq, aux, timed, ev_dq))
@@ -855,8 +858,9 @@ int launch_mfma_backward(const LaunchGeom& g, const void* q, const void* k, cons
     launch_scan<false>(plan, a, st, timed);
     if (!den_aux) den_state(st);
   }
-  // the dv kernel (it needs only the forward's kappa and k2_bwd_prep's G^T) on
-  // the caller's stream, which would otherwise wait for the dk kernel's event
+  // per pair, the dv kernel (it needs only the forward's kappa and
+  // k2_bwd_prep's G^T) on the caller's stream, which would otherwise wait for
+  // the dq part's event
   if (dv_main) launch_local_bwd<T>(g, qt, kt, vt, la, dq != nullptr, dk != nullptr, kLocalDv, st, timed);
   if (!forked) {
     // one stream (the allocation-free entry point, the profiling mode, a call

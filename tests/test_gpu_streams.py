@@ -1,8 +1,7 @@
 """The backward's second stream as the caller sees it: one stream.
 
 ``oal_backward`` forks the denominator kernels, most of the intra-chunk VJP and
-the query-side fold (all of it on the group-sum path, most of it per pair) onto a
-stream of the library's own, makes the caller's stream wait for events the second
+most or all of the query-side fold onto a stream of the library's own, makes the caller's stream wait for events the second
 stream recorded before the key-side fold and before the rest of the query-side
 fold and the coefficient reductions, and joins it back into the caller's stream
 before it returns.
