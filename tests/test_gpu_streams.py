@@ -27,9 +27,9 @@ def _dev():
     return torch.device("cuda:0")
 
 
-def _inputs(dev, n=1000, seed=43):
+def _inputs(dev, n=1000, seed=43, b=2, g=8):
     gen = torch.Generator().manual_seed(seed)
-    b, hq, hkv, g = 2, 14, 2, 8
+    hq, hkv = 14, 2
     dt = torch.bfloat16
     q = (torch.randn(b, hq, n, 64, generator=gen) * 0.5).to(dt).to(dev)
     k = (torch.randn(b, hkv, n, 64, generator=gen) * 0.5).to(dt).to(dev)
@@ -76,6 +76,33 @@ def test_backward_on_caller_streams_is_joined_before_the_next_work(precision):
         for name, a, r in zip(names, res, ref):
             assert torch.equal(a, r), f"call {rep}: {name} differs from the default-stream call"
         assert torch.equal(res[-1], ref[3].float().sum())
+
+
+@pytest.mark.parametrize("n, b, groups", [(8300, 1, 8), (1000, 2, 12)])
+def test_other_stream_arrangements_are_joined(n, b, groups):
+    """Above 128 chunks per unit (N = 8300: 130) the denominator kernels follow
+    the scan on the caller's stream and the query-side fold runs whole on the
+    second stream; with more than 8 groups (per-pair coefficients) the dv
+    kernel and a quarter of the fold stay on the caller's stream. Each call on
+    a caller-created stream must equal the default-stream call bitwise."""
+    dev = _dev()
+    inp = _inputs(dev, n=n, seed=7, b=b, g=groups)
+    ref = _step(inp)
+    torch.cuda.synchronize()
+    st = torch.cuda.Stream(dev)
+    results = []
+    for _ in range(2):
+        st.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(st):
+            res = _step(inp)
+            res.append(res[4].float().sum())
+        results.append(res)
+    torch.cuda.synchronize()
+    names = ["out", "num", "den", "dq", "dk", "dv", "dc0", "dlam", "dgam"]
+    for rep, res in enumerate(results):
+        for name, a, r in zip(names, res, ref):
+            assert torch.equal(a, r), f"call {rep}: {name} differs from the default-stream call"
+        assert torch.equal(res[-1], ref[4].float().sum())
 
 
 def test_two_caller_streams_with_their_own_inputs():
